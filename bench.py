@@ -1,0 +1,177 @@
+"""Benchmark: triangle attention (starting node) at N=768 on one MI355X.
+
+Workload (the headline configuration): z bf16 [768, 768, 128] ~ N(0,1), 4 heads x 32,
+bias [4, 768, 768] from LN(z) W_b, sigmoid gate, output projection and residual -- one
+call of GridSelfAttention.forward through the HIP backend.  A "step" is one such call with
+z already resident in HBM.
+
+Reports ms/call and the fraction of dense bf16 MFMA peak on the module's algorithmic FLOP
+(4*H*D*N^3 attention + 2*N^2*C*(4*H*D + H) projections + 2*N^2*H*D*C output projection), a
+roofline object for the dominant kernel (the attention core, timed live with HIP events on
+the stream it runs on), and the host-CPU Torch math path (oracle restatement of the reference
+composite in bf16, 128-row chunks) timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+N, C, H, D = 768, 128, 4, 32
+PEAK_BF16_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def module_flop(n=N, c=C, h=H, d=D) -> float:
+  attn = 4.0 * h * d * n ** 3
+  proj = 2.0 * n * n * c * (4 * h * d + h)
+  out = 2.0 * n * n * h * d * c
+  return attn + proj + out
+
+
+def core_flop(n=N, h=H, d=D) -> float:
+  return 4.0 * h * d * n ** 3
+
+
+def parse():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--gpus", type=int, default=1)
+  ap.add_argument("--steps", type=int, default=20)
+  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--cpu-baseline", type=int, default=1, help="time the host-CPU math path (rank 0)")
+  ap.add_argument("--cpu-rows", type=int, default=128, help="rows in the CPU-baseline sample")
+  return ap.parse_args()
+
+
+def _events_time(fn, iters: int, stream) -> float:
+  start = torch.cuda.Event(enable_timing=True)
+  end = torch.cuda.Event(enable_timing=True)
+  start.record(stream)
+  for _ in range(iters):
+    fn()
+  end.record(stream)
+  end.synchronize()
+  return start.elapsed_time(end) / iters
+
+
+def attention_core_ms(z, seq, mod, iters: int) -> float:
+  """Average duration of the attention kernel alone, launched exactly as the triangle module
+  launches it (same strides, shared bias planes, masks), timed with HIP events."""
+  from sparsefold_amd.backends.hip import ops
+  HD = H * D
+  x = ops.layer_norm(z, mod._hip_ln_w, mod._hip_ln_b)
+  bias = torch.empty(H, N * N, dtype=torch.bfloat16, device=z.device)
+  y = ops.linear(x, mod._hip_w_qkvgb, ycols=4 * HD, yt=bias, tcol0=4 * HD)        # [N, N, 4HD]
+  y5 = y.view(N, 1, N, 4 * HD)
+
+  def view(i):
+    return y5[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D))
+
+  q, k, v, g = view(0), view(1), view(2), view(3)
+  b5 = bias.view(1, 1, H, N, N).expand(N, 1, H, N, N)
+  m8 = seq.to(torch.uint8)
+  mq = m8.view(N, 1, 1).expand(N, 1, N)
+  mk = m8.view(1, 1, N).expand(N, 1, N)
+  out = torch.empty(N, 1, N, H, D, dtype=torch.bfloat16, device=z.device)
+  fn = lambda: ops.attention(q, k, v, scale=1 / math.sqrt(D), bias=b5, mask_q=mq, mask_k=mk, gate=g, out=out)
+  fn()
+  torch.cuda.synchronize()
+  return _events_time(fn, iters, torch.cuda.current_stream())
+
+
+def cpu_baseline(rows: int) -> dict:
+  """Host-CPU Torch math path (oracle restatement of blocks.py:293-366 in bf16, SDPA MATH,
+  128-row chunks as configs/cpu.toml's runtime.sharding): the shared prologue (LN + bias)
+  once, plus `rows` attention rows, scaled to the full N rows."""
+  from oracle import modules as OM
+  from oracle.primitives import layer_norm, linear
+  from sparsefold_amd import workloads as W
+  cores = len(os.sched_getaffinity(0))
+  torch.set_num_threads(cores)
+  mod, z, seq = W.make_triangle(N, seed=3)
+  p = {k: v.to(torch.bfloat16) for k, v in W.state_dict_f32(mod).items()}
+  with torch.inference_mode():
+    t0 = time.perf_counter()
+    x = layer_norm(z, p["act_norm.weight"], p["act_norm.bias"])
+    bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
+    t1 = time.perf_counter()
+    OM.grid_self_attention_rows(z, seq, p, transpose=False, rows=range(rows), bias=bias)   # warm-up
+    reps = []
+    for _ in range(2):
+      t2 = time.perf_counter()
+      OM.grid_self_attention_rows(z, seq, p, transpose=False, rows=range(rows), bias=bias)
+      reps.append(time.perf_counter() - t2)
+  chunk = min(reps)
+  total_s = (t1 - t0) + chunk * (N / rows)
+  return {"value": total_s * 1e3, "unit": "ms/call", "cores": cores, "kind": "port",
+          "sample": f"bf16 Torch math (oracle restatement), prologue once + {rows} of {N} rows "
+                    f"(min of 2 after 1 warm-up), scaled x{N / rows:g}"}
+
+
+def main():
+  args = parse()
+  if args.gpus != 1:
+    print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only",
+                      "n_gpus": args.gpus}))
+    sys.exit(2)
+  from sparsefold_amd import backends
+  from sparsefold_amd import workloads as W
+  from sparsefold_amd.runtime import config
+
+  config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda")
+  backends.init()
+  dev = torch.device("cuda:0")
+  mod, z, seq = W.make_triangle(N, seed=3)
+  mod = mod.to(dev)
+  backends.prepare(mod)
+  z, seq = z.to(dev), seq.to(dev)
+  stream = torch.cuda.current_stream()
+  print(f"[bench] triangle start N={N} C={C} H={H} D={D} warmup={args.warmup} steps={args.steps}", flush=True)
+  for _ in range(args.warmup):
+    mod(z, seq)
+  torch.cuda.synchronize()
+  ms = _events_time(lambda: mod(z, seq), args.steps, stream)
+  torch.cuda.synchronize()
+  core_ms = attention_core_ms(z, seq, mod, max(args.steps, 10))
+  flop = module_flop()
+  tflops = flop / (ms * 1e-3) / 1e12
+  core_tflops = core_flop() / (core_ms * 1e-3) / 1e12
+  print(f"[bench] module {ms:.3f} ms ({tflops:.1f} TFLOP/s); attention kernel {core_ms:.3f} ms "
+        f"({core_tflops:.1f} TFLOP/s)", flush=True)
+  cpu = None
+  if args.cpu_baseline:
+    print("[bench] timing host-CPU math path sample...", flush=True)
+    cpu = cpu_baseline(args.cpu_rows)
+    print(f"[bench] cpu baseline {cpu['value']:.1f} ms/call on {cpu['cores']} threads", flush=True)
+  line = {
+      "metric": "ms/call + % bf16 MFMA peak, triangle attention N=768; vs host-CPU math path",
+      "value": round(ms, 4),
+      "unit": "ms/call",
+      "n_gpus": 1,
+      "steps": args.steps,
+      "warmup": args.warmup,
+      "ms_per_step": round(ms, 4),
+      "higher_is_better": False,
+      "scaling": "weak",
+      "vs_baseline": None,
+      "dtype": "bf16",
+      "data": "synthetic (seeded N(0,1) z, N(0,0.02^2) weights)",
+      "config": {"workload": "triangle attention, starting node, N=768, C=128, H=4, D=32, all-ones mask",
+                 "module_flop": flop, "tflops": round(tflops, 2),
+                 "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2)},
+      "roofline": {"bound": "mfma", "kernel": "attention_fwd_kernel", "achieved": round(core_tflops, 2),
+                   "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(core_tflops / PEAK_BF16_TFLOPS, 4),
+                   "traffic": None, "kernel_ms": round(core_ms, 4), "flop_per_launch": core_flop()},
+      "cpu_baseline": cpu,
+      "speedup_vs_cpu": None if cpu is None else round(cpu["value"] / ms, 1),
+  }
+  print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+  main()

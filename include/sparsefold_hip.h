@@ -1,0 +1,174 @@
+/*
+ * sparsefold_hip.h -- C ABI of the MI355X (gfx950) gated pair-biased attention library.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, and a
+ * hipStream_t (passed as void*; NULL = default stream).  Calls are asynchronous on that
+ * stream.  The caller owns all memory: outputs and workspaces are allocated by the caller
+ * (sizes from the *_workspace_bytes queries).  Return value 0 = success; non-zero = error,
+ * with a message from sf_hip_last_error().  No entry point synchronises the device.
+ *
+ * Element types: "bf16" = IEEE bfloat16 bit patterns (uint16_t), "f32" = float,
+ * "u8" = bool as one byte (0 = masked / invalid).
+ *
+ * Reference interfaces replaced (SparseFold, paths relative to src/sparsefold/):
+ *   sf_hip_attention_fwd        backends/torch/attention/sdpa.py:22-121  dot_product_attention
+ *   sf_hip_layer_norm_fwd       model/layers/primitives.py:471-497        LayerNorm.forward
+ *                               model/diffusion/transformer.py:80-96      AdaptiveLayerNorm.forward
+ *   sf_hip_linear_fwd           model/layers/primitives.py:328-372        Linear.forward (einsum,
+ *                               bias, residual, sigmoid post-op)
+ *   sf_hip_triangle_attn_fwd    model/trunk/blocks.py:293-366             GridSelfAttention.forward
+ *                               (vecops op sparsefold_native::grid_self_attention,
+ *                                backends/vecops/kernels/registry.py:1188-1233, dense form)
+ *   sf_hip_pair_logits_fwd      model/trunk/blocks.py:745-749             SingleActUpdate pair logits
+ *                               model/diffusion/transformer.py:430-447    Transformer pair-logit pack
+ *   sf_hip_window_gather_fwd    schema/atom_layout.py:61-83               convert (queries_to_keys,
+ *                               CrossAttTransformer block key gather, transformer.py:671-673)
+ */
+#ifndef SPARSEFOLD_HIP_H_
+#define SPARSEFOLD_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SF_HIP_ABI_VERSION 1
+
+/* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
+int sf_hip_abi_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated to n).
+ * Returns the full message length. */
+size_t sf_hip_last_error(char* buf, size_t n);
+
+/* ---------------------------------------------------------------------------------------
+ * Gated pair-biased attention (flash-style, bf16 MFMA, fp32 softmax / accumulation).
+ *
+ *   out[b,i,h,:] = softmax_j( scale * q[b,i,h,:].k[b,j,h,:] + bias[b,h,i,j] , masked ) v[b,j,h,:]
+ *                  (* sigmoid(gate[b,i,h,:]) when gate != NULL)
+ *
+ * Batch is two-level, b = (b0, b1) with b0 < B0, b1 < B1; every tensor carries its own
+ * element strides for b0 and b1 (0 = broadcast), so a bias shared by all rows / samples
+ * costs nothing.  The last dimension of q, k, v, gate and out is contiguous (stride 1);
+ * bias is contiguous along keys.  Masks: masked key j for query i <=> !mask_q[b,i] or
+ * !mask_k[b,j]; a query whose every key is masked returns the mean of v over all K keys
+ * (the reference's -finfo.max additive mask, sdpa.py:62-80).  D, Dv <= 64.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_attention_args {
+  int32_t B0, B1, Q, K, H, D, Dv;
+  float scale;                                  /* logits scale (1/sqrt(D) if unspecified) */
+  const void* q;    int64_t q_s[4];             /* bf16, strides [b0, b1, q, h]            */
+  const void* k;    int64_t k_s[4];             /* bf16, strides [b0, b1, k, h]            */
+  const void* v;    int64_t v_s[4];             /* bf16, strides [b0, b1, k, h]            */
+  const void* bias; int64_t bias_s[4];          /* bf16 or NULL, strides [b0, b1, h, q]    */
+  const uint8_t* mask_q; int64_t mq_s[3];       /* u8 or NULL, strides [b0, b1, q]         */
+  const uint8_t* mask_k; int64_t mk_s[3];       /* u8 or NULL, strides [b0, b1, k]         */
+  const void* gate; int64_t g_s[4];             /* bf16 or NULL (sigmoid gate logits)      */
+  void* out;        int64_t o_s[4];             /* bf16, strides [b0, b1, q, h]            */
+} sf_attention_args;
+
+int sf_hip_attention_fwd(const sf_attention_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Row LayerNorm, optionally adaptive (AdaLN):
+ *   y[m,:] = LN(x[m,:]) * gamma + beta                       (gamma/beta f32 or NULL)
+ *   y[m,:] = LN(x[m,:]) * scale[m % cond_rows,:] + shift[m % cond_rows,:]   (AdaLN)
+ * x, y bf16 row-major with row strides; eps as given (reference 1e-5).  C <= 2048.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_layer_norm_args {
+  int64_t M; int32_t C; float eps;
+  const void* x; int64_t x_rs;                  /* bf16 */
+  const float* gamma; const float* beta;        /* f32 [C] or NULL */
+  const void* scale; const void* shift;         /* bf16 [cond_rows, C] or NULL (AdaLN) */
+  int64_t cond_rows; int64_t cond_rs;
+  void* y; int64_t y_rs;                        /* bf16 */
+} sf_layer_norm_args;
+
+int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * y[m,n] = post( sum_k x[m,k] * wt[n,k] + bias[n] ) * mul[m % mul_rows, n] + residual[m,n]
+ * x bf16 [M,K] (row stride x_rs), wt bf16 [N,K] contiguous (weight pre-transposed so K is
+ * contiguous), bias f32 [N] or NULL, residual bf16 or NULL, post = identity | sigmoid,
+ * mul bf16 or NULL (multiplier applied after post, rows broadcast modulo mul_rows).
+ * Only columns [0, ycols) go to y (ycols = 0 means all N).  Optional second output:
+ * columns [tcol0, tcol0+tcols) are also written transposed, yt[n - tcol0, m] (bf16, row
+ * stride yt_rs) -- used to emit [H, rows] bias planes.  K % 8 == 0.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_linear_args {
+  int64_t M; int32_t N, K;
+  const void* x; int64_t x_rs;
+  const void* wt;
+  const float* bias;
+  const void* residual; int64_t r_rs;
+  const void* mul; int64_t mul_rows, mul_rs;
+  int32_t post_sigmoid;
+  void* y; int64_t y_rs; int32_t ycols;        /* y may be NULL when only yt is wanted */
+  int32_t tcol0, tcols; void* yt; int64_t yt_rs;
+} sf_linear_args;
+
+int sf_hip_linear_fwd(const sf_linear_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Triangle attention, starting (transpose = 0) or ending (transpose = 1) node, whole module:
+ *   x = LN(z); bias[h,a,b] = (x W_b)[a,b,h] (untransposed); rows r of x (x^T for ending);
+ *   per row: q,k,v,g projections, attention with mask_k = seq[r] & seq[k] and the shared
+ *   bias, sigmoid gate, output projection; out = z + update (or update only).
+ * z bf16 [N, N, C] contiguous; seq_mask u8 [N]; weights bf16 packed by the host:
+ *   w_qkvgb [4*H*D + H, C]  rows: q (h,d), k (h,d), v (h,d), g (h,d), bias (h)
+ *   w_o     [C, H*D]        (transposed output projection)
+ * ln_w / ln_b f32 [C] (ln_b may be NULL).  Workspace from sf_hip_triangle_workspace_bytes.
+ * out may not alias z.  Constraints: C % 8 == 0, H*D <= 1024, D <= 64.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_triangle_args {
+  int32_t N, C, H, D;
+  int32_t transpose;                            /* 0 starting node, 1 ending node */
+  int32_t add_residual;                         /* 1: out = z + update (module output) */
+  const void* z;
+  const uint8_t* seq_mask;
+  const float* ln_w; const float* ln_b;
+  const void* w_qkvgb;
+  const void* w_o;
+  void* out;
+} sf_triangle_args;
+
+size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t D);
+int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Pair logits: out[h, p] = (LN(z[p,:]) W)[h] for H <= 64 planes; z bf16 [P, C] contiguous
+ * (C <= 128, C % 8 == 0), ln_w/ln_b f32 [C] (either may be NULL), w_t bf16 [H, C],
+ * out bf16 [H, P].
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_pair_logits_args {
+  int64_t P; int32_t C, H;                      /* P = number of pair positions */
+  const void* z;
+  const float* ln_w; const float* ln_b;
+  const void* w_t;
+  void* out;                                    /* [H, P] */
+} sf_pair_logits_args;
+
+int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Key-window gather (atom_layout.convert with layout axes (-3,-2)):
+ *   keys[s, u, j, :] = gather_mask[u,j] ? src[s, idx[u,j], :] : 0      (idx flat over U*Qw)
+ * src bf16 [S, rows, C] contiguous, idx int32 [U*Kw], mask u8 [U*Kw], keys bf16 [S,U*Kw,C].
+ * Indices are bounds-checked on the device: an index outside [0, rows) is treated as masked.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_window_gather_args {
+  int32_t S, rows, C, UK;
+  const void* src; const int32_t* idx; const uint8_t* mask;
+  void* keys;
+} sf_window_gather_args;
+
+int sf_hip_window_gather_fwd(const sf_window_gather_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSEFOLD_HIP_H_ */

@@ -1,0 +1,140 @@
+"""ctypes binding of ``libsparsefold_hip.so`` (the C ABI declared in include/sparsefold_hip.h).
+
+The structures below mirror the header field for field; ``tests/test_abi.py`` compiles the
+header with gcc and checks every size and offset against these definitions.  Loading fails
+loudly: there is no fallback implementation behind this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
+ABI_VERSION = 1
+
+_i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+_u8p = C.POINTER(C.c_uint8)
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+
+
+class AttentionArgs(C.Structure):
+  _fields_ = [
+      ("B0", _i32), ("B1", _i32), ("Q", _i32), ("K", _i32), ("H", _i32), ("D", _i32), ("Dv", _i32),
+      ("scale", _f32),
+      ("q", _vp), ("q_s", _i64 * 4),
+      ("k", _vp), ("k_s", _i64 * 4),
+      ("v", _vp), ("v_s", _i64 * 4),
+      ("bias", _vp), ("bias_s", _i64 * 4),
+      ("mask_q", _vp), ("mq_s", _i64 * 3),
+      ("mask_k", _vp), ("mk_s", _i64 * 3),
+      ("gate", _vp), ("g_s", _i64 * 4),
+      ("out", _vp), ("o_s", _i64 * 4),
+  ]
+
+
+class LayerNormArgs(C.Structure):
+  _fields_ = [
+      ("M", _i64), ("C", _i32), ("eps", _f32),
+      ("x", _vp), ("x_rs", _i64),
+      ("gamma", _vp), ("beta", _vp),
+      ("scale", _vp), ("shift", _vp),
+      ("cond_rows", _i64), ("cond_rs", _i64),
+      ("y", _vp), ("y_rs", _i64),
+  ]
+
+
+class LinearArgs(C.Structure):
+  _fields_ = [
+      ("M", _i64), ("N", _i32), ("K", _i32),
+      ("x", _vp), ("x_rs", _i64),
+      ("wt", _vp),
+      ("bias", _vp),
+      ("residual", _vp), ("r_rs", _i64),
+      ("mul", _vp), ("mul_rows", _i64), ("mul_rs", _i64),
+      ("post_sigmoid", _i32),
+      ("y", _vp), ("y_rs", _i64), ("ycols", _i32),
+      ("tcol0", _i32), ("tcols", _i32), ("yt", _vp), ("yt_rs", _i64),
+  ]
+
+
+class TriangleArgs(C.Structure):
+  _fields_ = [
+      ("N", _i32), ("C", _i32), ("H", _i32), ("D", _i32),
+      ("transpose", _i32), ("add_residual", _i32),
+      ("z", _vp), ("seq_mask", _vp),
+      ("ln_w", _vp), ("ln_b", _vp),
+      ("w_qkvgb", _vp), ("w_o", _vp),
+      ("out", _vp),
+  ]
+
+
+class PairLogitsArgs(C.Structure):
+  _fields_ = [
+      ("P", _i64), ("C", _i32), ("H", _i32),
+      ("z", _vp), ("ln_w", _vp), ("ln_b", _vp), ("w_t", _vp), ("out", _vp),
+  ]
+
+
+class WindowGatherArgs(C.Structure):
+  _fields_ = [
+      ("S", _i32), ("rows", _i32), ("C", _i32), ("UK", _i32),
+      ("src", _vp), ("idx", _vp), ("mask", _vp), ("keys", _vp),
+  ]
+
+
+STRUCTS = {
+    "sf_attention_args": AttentionArgs,
+    "sf_layer_norm_args": LayerNormArgs,
+    "sf_linear_args": LinearArgs,
+    "sf_triangle_args": TriangleArgs,
+    "sf_pair_logits_args": PairLogitsArgs,
+    "sf_window_gather_args": WindowGatherArgs,
+}
+
+# (name, restype, argtypes) of every exported entry point.
+SIGNATURES = [
+    ("sf_hip_abi_version", C.c_int, []),
+    ("sf_hip_last_error", C.c_size_t, [C.c_char_p, C.c_size_t]),
+    ("sf_hip_attention_fwd", C.c_int, [C.POINTER(AttentionArgs), _vp]),
+    ("sf_hip_layer_norm_fwd", C.c_int, [C.POINTER(LayerNormArgs), _vp]),
+    ("sf_hip_linear_fwd", C.c_int, [C.POINTER(LinearArgs), _vp]),
+    ("sf_hip_triangle_workspace_bytes", C.c_size_t, [_i32, _i32, _i32, _i32]),
+    ("sf_hip_triangle_attn_fwd", C.c_int, [C.POINTER(TriangleArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_pair_logits_fwd", C.c_int, [C.POINTER(PairLogitsArgs), _vp]),
+    ("sf_hip_window_gather_fwd", C.c_int, [C.POINTER(WindowGatherArgs), _vp]),
+]
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+  """Loads the HIP library once; raises RuntimeError when it is missing or mismatched."""
+  global _lib
+  if _lib is not None:
+    return _lib
+  if not LIB_PATH.exists():
+    raise RuntimeError(f"{LIB_PATH.name} is not built; run __graft_entry__.build() or "
+                       "python -m sparsefold_amd._build (no fallback implementation exists)")
+  lib = C.CDLL(str(LIB_PATH))
+  for name, res, args in SIGNATURES:
+    fn = getattr(lib, name)
+    fn.restype = res
+    fn.argtypes = args
+  ver = lib.sf_hip_abi_version()
+  if ver != ABI_VERSION:
+    raise RuntimeError(f"libsparsefold_hip ABI version {ver} != expected {ABI_VERSION}")
+  _lib = lib
+  return lib
+
+
+def last_error() -> str:
+  lib = load()
+  buf = C.create_string_buffer(1024)
+  lib.sf_hip_last_error(buf, len(buf))
+  return buf.value.decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+  if rc != 0:
+    raise RuntimeError(f"{what} failed (status {rc}): {last_error()}")

@@ -1,0 +1,98 @@
+"""Lifecycle hooks of the HIP (MI355X / gfx950) backend.
+
+Same hook set as the reference backends (``src/sparsefold/backends/__init__.py:25``):
+``apply`` replaces the attention module factories before model construction (selected by
+``native_ops`` names from ``src/sparsefold/config.py:24-35``, as
+``backends/vecops/backend.py:187-248`` does), ``unapply`` restores them, ``prepare`` packs
+weights into non-persistent buffers after strict loading, and the remaining hooks are
+trivial because nothing is JIT-compiled (the kernels are built ahead of time into
+``libsparsefold_hip.so``).  ``apply`` loads that library first, so a missing build fails here,
+before any model exists.
+"""
+from __future__ import annotations
+
+import importlib
+from contextlib import nullcontext
+
+import torch
+
+from sparsefold_amd import _lib
+from sparsefold_amd import modules as _modules
+from sparsefold_amd.runtime import config
+
+_PATCHED_FACTORIES: list[tuple[object, str, object]] = []
+
+# native.ops name -> (factory attribute, HIP class attribute in backends.hip.modules)
+_REPLACE_MAP = {
+    "grid_self_attn": ("GridSelfAttention", "GridSelfAttentionHip"),
+    "evoformer_single_act_update": ("SingleActUpdate", "SingleActUpdateHip"),
+    "diffusion_self_attention": ("SelfAttention", "SelfAttentionHip"),
+    "diffusion_cross_attention": ("CrossAttention", "CrossAttentionHip"),
+}
+
+
+def _replace_factory(module, name: str, implementation) -> None:
+  if not any(owner is module and attr == name for owner, attr, _ in _PATCHED_FACTORIES):
+    _PATCHED_FACTORIES.append((module, name, getattr(module, name)))
+  setattr(module, name, implementation)
+
+
+def unapply() -> None:
+  for module, name, original in reversed(_PATCHED_FACTORIES):
+    setattr(module, name, original)
+  _PATCHED_FACTORIES.clear()
+
+
+def apply() -> None:
+  _lib.load()
+  hip_modules = importlib.import_module("sparsefold_amd.backends.hip.modules")
+  selected = list(config.native_ops)
+  if "*" in selected or "all" in selected:
+    selected = list(_REPLACE_MAP)
+  for key, (factory, impl) in _REPLACE_MAP.items():
+    if key in selected:
+      _replace_factory(_modules, factory, getattr(hip_modules, impl))
+
+
+def manual_seed(seed: int) -> None:
+  torch.manual_seed(seed)
+
+
+def prepare(module: torch.nn.Module) -> dict[str, int]:
+  """Prepare every HIP module once (children of a prepared fused module are covered)."""
+  hip_modules = importlib.import_module("sparsefold_amd.backends.hip.modules")
+  counts = {"packed": 0, "fallback": 0, "opaque": 0}
+  visited: set[int] = set()
+
+  def visit(current: torch.nn.Module) -> None:
+    if id(current) in visited:
+      return
+    visited.add(id(current))
+    if isinstance(current, hip_modules.HIP_TYPES):
+      current.prepare_native()
+      counts["opaque"] += 1
+      for child in current.modules():
+        visited.add(id(child))
+      return
+    for child in current.children():
+      visit(child)
+
+  visit(module)
+  return counts
+
+
+def materialize(*, parallelism: int | None = None) -> int:
+  _lib.load()
+  return 0
+
+
+def precompile(module, *args, **kwargs):
+  return None
+
+
+def is_precompiling() -> bool:
+  return False
+
+
+def execution_context():
+  return nullcontext()

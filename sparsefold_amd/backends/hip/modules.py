@@ -1,0 +1,276 @@
+"""HIP module replacements for the four gated pair-biased attention forms.
+
+Each replacement is a mixin over a module with the reference's parameter layout (this
+package's ``sparsefold_amd.modules`` classes, or -- when integrated -- the reference classes
+themselves).  ``prepare_native()`` runs after strict checkpoint loading and packs bf16 /
+fp32 copies of the weights into *non-persistent* buffers; parameters and ``state_dict`` are
+untouched (as ``backends/vecops/modules.py:436-444`` / ``tests/test_native_preparation.py:107-132``
+require).  ``forward`` before ``prepare_native`` raises the reference's "not prepared" error
+(``backends/vecops/modules.py:88-94``).  Every numeric step runs in libsparsefold_hip.
+
+Replaced reference forwards:
+* ``GridSelfAttentionHip.forward``   blocks.py:293-366
+* ``SelfAttentionHip.forward``       transformer.py:306-345 (with AdaLN :80-96, AdaLN-zero :138-154)
+* ``CrossAttentionHip.forward``      transformer.py:549-585; ``forward_indexed`` additionally
+                                     gathers the key windows (transformer.py:671-673)
+* ``SingleActUpdateHip.forward``     blocks.py:739-763 (attention half)
+"""
+from __future__ import annotations
+
+import functools
+
+import torch
+
+from sparsefold_amd import modules as base
+from sparsefold_amd.backends.hip import ops
+from sparsefold_amd.backends.hip.attention import dot_product_attention
+
+BF16 = torch.bfloat16
+
+
+def _begin_preparation(module: torch.nn.Module) -> None:
+  module._native_prepared = False
+  devices = {p.device.type for p in module.parameters()}
+  if devices - {"cuda"}:
+    raise RuntimeError("HIP kernels need the module's parameters on the GPU; move the model to 'cuda' first")
+
+
+def _require_native_preparation(function):
+  @functools.wraps(function)
+  def wrapped(self, *args, **kwargs):
+    if not getattr(self, "_native_prepared", False):
+      raise RuntimeError("Native buffers are not prepared; call backends.prepare(model) after strict checkpoint loading")
+    return function(self, *args, **kwargs)
+  return wrapped
+
+
+def _buf(module: torch.nn.Module, name: str, value: torch.Tensor | None) -> None:
+  module.register_buffer(name, None if value is None else value.detach().contiguous(), persistent=False)
+
+
+def _bf(t: torch.Tensor) -> torch.Tensor:
+  return t.detach().to(BF16).contiguous()
+
+
+def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
+  return None if t is None else t.detach().to(torch.float32).contiguous()
+
+
+# ---------------------------------------------------------------------------------------
+# Triangle attention
+# ---------------------------------------------------------------------------------------
+
+class GridSelfAttentionHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    H, C, D = self.config.num_head, self.num_channels, self.qkv_dim
+    HD = H * D
+    wq = self.q_projection.weight.reshape(HD, C)                       # [H, D, C]
+    wk = self.k_projection.weight.reshape(HD, C)
+    wv = self.v_projection.weight.reshape(C, HD).t()                   # [C, H, D]
+    wg = self.gating_query.weight.reshape(HD, C)                       # [H*D, C]
+    wb = self.pair_bias_projection.weight.t()                          # [C, H]
+    _buf(self, "_hip_w_qkvgb", _bf(torch.cat([wq, wk, wv, wg, wb], 0)))
+    _buf(self, "_hip_w_o", _bf(self.output_projection.weight.t()))      # [H*D, C] -> [C, H*D]
+    _buf(self, "_hip_ln_w", _f32(self.act_norm.weight))
+    _buf(self, "_hip_ln_b", _f32(getattr(self.act_norm, "bias", None)))
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def forward(self, act: torch.Tensor, seq_mask: torch.Tensor, *, add_residual: bool = True) -> torch.Tensor:
+    assert act.ndim >= 3
+    N = act.shape[-2]
+    assert act.shape[-1] == self.num_channels
+    assert seq_mask.shape == (N,) and seq_mask.dtype == torch.bool
+    assert act.shape[-3] == N, "triangle attention needs the full [N, N] pair block on one GPU"
+    flat = act.reshape(-1, N, N, act.shape[-1])
+    outs = [ops.triangle_attention(z, seq_mask, self._hip_ln_w, self._hip_ln_b, self._hip_w_qkvgb, self._hip_w_o,
+                                   num_head=self.config.num_head, transpose=self.transpose,
+                                   add_residual=add_residual) for z in flat]
+    out = outs[0].unsqueeze(0) if len(outs) == 1 else torch.stack(outs)
+    return out.reshape(act.shape).to(act.dtype)
+
+
+# ---------------------------------------------------------------------------------------
+# AdaLN helpers shared by SelfAttention and CrossAttention
+# ---------------------------------------------------------------------------------------
+
+def _prepare_adaln(module: torch.nn.Module, ada: base.AdaptiveLayerNorm, prefix: str) -> None:
+  if ada.single_cond:
+    _buf(module, prefix + "lnc_w", _f32(ada.single_cond_layer_norm.weight))
+    _buf(module, prefix + "lnc_b", _f32(getattr(ada.single_cond_layer_norm, "bias", None)))
+    _buf(module, prefix + "w_scale", _bf(ada.single_cond_scale.weight.t()))   # [S, C] -> [C, S]
+    _buf(module, prefix + "b_scale", _f32(ada.single_cond_scale.bias))
+    _buf(module, prefix + "w_shift", _bf(ada.single_cond_bias.weight.t()))
+  else:
+    _buf(module, prefix + "ln_w", _f32(ada.layer_norm.weight))
+    _buf(module, prefix + "ln_b", _f32(getattr(ada.layer_norm, "bias", None)))
+
+
+def _adaln(module, prefix: str, x: torch.Tensor, cond: torch.Tensor | None) -> torch.Tensor:
+  if cond is None:
+    return ops.layer_norm(x, getattr(module, prefix + "ln_w"), getattr(module, prefix + "ln_b"))
+  c = ops.layer_norm(cond, getattr(module, prefix + "lnc_w"), getattr(module, prefix + "lnc_b"))
+  scale = ops.linear(c, getattr(module, prefix + "w_scale"), getattr(module, prefix + "b_scale"), post_sigmoid=True)
+  shift = ops.linear(c, getattr(module, prefix + "w_shift"))
+  return ops.layer_norm(x, scale=scale.reshape(-1, scale.shape[-1]), shift=shift.reshape(-1, shift.shape[-1]))
+
+
+def _prepare_zero_init(module: torch.nn.Module, zi: base.AdaptiveZeroInit) -> None:
+  _buf(module, "_hip_w_t2", _bf(zi.transition2.weight.t()))            # [HD, C] -> [C, HD]
+  if zi.single_cond:
+    _buf(module, "_hip_w_zc", _bf(zi.adaptive_zero_cond.weight.t()))  # [S, C] -> [C, S]
+    _buf(module, "_hip_b_zc", _f32(zi.adaptive_zero_cond.bias))
+
+
+def _zero_init_residual(module, o: torch.Tensor, cond: torch.Tensor | None, residual: torch.Tensor) -> torch.Tensor:
+  mul = None
+  if cond is not None:
+    mul = ops.linear(cond, module._hip_w_zc, module._hip_b_zc, post_sigmoid=True)
+    mul = mul.reshape(-1, mul.shape[-1])
+  return ops.linear(o, module._hip_w_t2, mul=mul, residual=residual)
+
+
+# ---------------------------------------------------------------------------------------
+# SelfAttention (single representation with pair bias; diffusion token attention)
+# ---------------------------------------------------------------------------------------
+
+class SelfAttentionHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    H, D = self.num_head, self.key_dim
+    C = self.q_projection.weight.shape[0]
+    HD = H * D
+    wq = self.q_projection.weight.reshape(C, HD).t()
+    wk = self.k_projection.weight.reshape(C, HD).t()
+    wv = self.v_projection.weight.reshape(C, HD).t()
+    wg = self.gating_query.weight.reshape(C, HD).t()
+    _buf(self, "_hip_w_qkvg", _bf(torch.cat([wq, wk, wv, wg], 0)))    # [4HD, C]
+    b = torch.zeros(4 * HD, dtype=torch.float32, device=wq.device)
+    b[:HD] = self.q_projection.bias.detach().reshape(HD).float()
+    _buf(self, "_hip_b_qkvg", b)
+    _prepare_adaln(self, self.layer_norm, "_hip_ada_")
+    _prepare_zero_init(self, self.zero_init)
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def forward(self, x: torch.Tensor, mask: torch.Tensor, *, pair_logits: torch.Tensor | None = None,
+              single_cond: torch.Tensor | None = None) -> torch.Tensor:
+    H, D = self.num_head, self.key_dim
+    HD = H * D
+    lead, N = x.shape[:-2], x.shape[-2]
+    xh = _adaln(self, "_hip_ada_", x, single_cond)
+    y = ops.linear(xh, self._hip_w_qkvg, self._hip_b_qkvg)              # [..., N, 4HD]
+    q, k, v, g = (y[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D)) for i in range(4))
+    o = dot_product_attention(q, k, v, mask_k=mask, bias=pair_logits, gate=g)
+    o = o.reshape(*lead, N, HD)
+    return _zero_init_residual(self, o, single_cond, x).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------------------
+# CrossAttention (windowed atom attention)
+# ---------------------------------------------------------------------------------------
+
+class CrossAttentionHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    H, D = self.num_head, self.key_dim
+    C = self.q_projection.weight.shape[0]
+    HD = H * D
+    wq = self.q_projection.weight.reshape(C, HD).t()
+    wg = self.gating_query.weight.reshape(C, HD).t()
+    wk = self.k_projection.weight.reshape(C, HD).t()
+    wv = self.v_projection.weight.reshape(C, HD).t()
+    _buf(self, "_hip_w_qg", _bf(torch.cat([wq, wg], 0)))               # [2HD, C]
+    b = torch.zeros(2 * HD, dtype=torch.float32, device=wq.device)
+    b[:HD] = self.q_projection.bias.detach().reshape(HD).float()
+    _buf(self, "_hip_b_qg", b)
+    _buf(self, "_hip_w_kv", _bf(torch.cat([wk, wv], 0)))               # [2HD, C]
+    _prepare_adaln(self, self.q_layernorm, "_hip_adq_")
+    _prepare_adaln(self, self.k_layernorm, "_hip_adk_")
+    _prepare_zero_init(self, self.zero_init)
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def forward(self, x_q: torch.Tensor, x_k: torch.Tensor, mask_q: torch.Tensor, mask_k: torch.Tensor,
+              pair_logits: torch.Tensor | None = None, single_cond_q: torch.Tensor | None = None,
+              single_cond_k: torch.Tensor | None = None) -> torch.Tensor:
+    H, D = self.num_head, self.key_dim
+    HD = H * D
+    hq = _adaln(self, "_hip_adq_", x_q, single_cond_q)
+    hk = _adaln(self, "_hip_adk_", x_k, single_cond_k)
+    yq = ops.linear(hq, self._hip_w_qg, self._hip_b_qg)                 # [..., Q, 2HD]
+    yk = ops.linear(hk, self._hip_w_kv)                                 # [..., K, 2HD]
+    q, g = yq[..., :HD].unflatten(-1, (H, D)), yq[..., HD:].unflatten(-1, (H, D))
+    k, v = yk[..., :HD].unflatten(-1, (H, D)), yk[..., HD:].unflatten(-1, (H, D))
+    o = dot_product_attention(q, k, v, mask_q=mask_q, mask_k=mask_k, bias=pair_logits, gate=g)
+    o = o.reshape(*o.shape[:-2], HD)
+    return _zero_init_residual(self, o, single_cond_q, x_q).to(x_q.dtype)
+
+  @_require_native_preparation
+  def forward_indexed(self, queries_act: torch.Tensor, queries_mask: torch.Tensor, gather_idxs: torch.Tensor,
+                      gather_mask: torch.Tensor, keys_mask: torch.Tensor, queries_single_cond: torch.Tensor,
+                      keys_single_cond: torch.Tensor, pair_logits: torch.Tensor | None = None) -> torch.Tensor:
+    """CrossAttTransformer block attention (transformer.py:668-682): keys are gathered from
+    the queries by ``queries_to_keys`` (flat index over ``[U, Qw]``, masked -> 0)."""
+    lead = queries_act.shape[:-3]
+    U, Qw, Cn = queries_act.shape[-3:]
+    S = 1
+    for s in lead:
+      S *= s
+    keys = ops.window_gather(queries_act.reshape(S, U * Qw, Cn), gather_idxs, gather_mask)
+    keys = keys.view(*lead, U, gather_idxs.shape[-1], Cn)
+    return self.forward(queries_act, keys, queries_mask, keys_mask, pair_logits, queries_single_cond,
+                        keys_single_cond)
+
+
+# ---------------------------------------------------------------------------------------
+# SingleActUpdate: pair-logit prologue + single attention
+# ---------------------------------------------------------------------------------------
+
+class SingleActUpdateHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    _buf(self, "_hip_pl_ln_w", _f32(self.single_pair_logits_norm.weight))
+    _buf(self, "_hip_pl_ln_b", _f32(getattr(self.single_pair_logits_norm, "bias", None)))
+    _buf(self, "_hip_pl_w", _bf(self.single_pair_logits_projection.weight.t()))   # [Cz, H] -> [H, Cz]
+    prep = getattr(self.single_attention, "prepare_native", None)
+    if prep is None:
+      raise RuntimeError("single_attention is not a HIP module; select backend 'hip' before construction")
+    prep()
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def forward(self, pair_act: torch.Tensor, single_act: torch.Tensor, seq_mask: torch.Tensor) -> torch.Tensor:
+    N = pair_act.shape[-2]
+    pl = ops.pair_logits(pair_act, self._hip_pl_ln_w, self._hip_pl_ln_b, self._hip_pl_w)
+    pl = pl.view(self.num_head, *pair_act.shape[:-1])                   # [H, B, N]
+    out = self.single_attention(single_act, seq_mask, pair_logits=pl)
+    transition = getattr(self, "single_transition", None)
+    if transition is not None:                                          # reference transition, when present
+      out = transition(out, broadcast_dim=None)
+    assert out.shape[-2] == N
+    return out
+
+
+class GridSelfAttentionHip(GridSelfAttentionHipMixin, base.GridSelfAttention):
+  pass
+
+
+class SelfAttentionHip(SelfAttentionHipMixin, base.SelfAttention):
+  pass
+
+
+class CrossAttentionHip(CrossAttentionHipMixin, base.CrossAttention):
+  pass
+
+
+class SingleActUpdateHip(SingleActUpdateHipMixin, base.SingleActUpdate):
+  pass
+
+
+HIP_TYPES = (GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin)

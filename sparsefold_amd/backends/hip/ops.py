@@ -1,0 +1,257 @@
+"""Tensor-level wrappers over the C ABI (include/sparsefold_hip.h).
+
+Each wrapper checks devices, shapes and dtypes in Python (ValueError, as the reference's
+native wrappers do, ``backends/vecops/kernels/registry.py:2910-2929``), allocates outputs and
+workspaces with torch on the input's device, and launches on torch's current HIP stream.
+Nothing here computes on the host: every numeric result comes from libsparsefold_hip.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+
+from sparsefold_amd import _lib
+
+BF16 = torch.bfloat16
+
+
+def _vp(t: torch.Tensor | None):
+  return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+  return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_cuda(*ts: torch.Tensor | None) -> torch.device:
+  dev = None
+  for t in ts:
+    if t is None:
+      continue
+    if t.device.type != "cuda":
+      raise ValueError(f"HIP kernels need device tensors, got a tensor on {t.device}")
+    if dev is None:
+      dev = t.device
+    elif t.device != dev:
+      raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+  if dev is None:
+    raise ValueError("no device tensor given")
+  return dev
+
+
+def _require(cond: bool, msg: str) -> None:
+  if not cond:
+    raise ValueError(msg)
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+  return t if t.dtype == BF16 else t.to(BF16)
+
+
+def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
+  return None if t is None else t.to(torch.float32).contiguous()
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+  return t if t.dtype == torch.uint8 else t.to(torch.uint8)
+
+
+def _rows(t: torch.Tensor, last: int) -> torch.Tensor:
+  """2-D row view ``[M, last]`` with unit last stride and 16-byte aligned rows."""
+  t2 = t.reshape(-1, last)
+  if t2.stride(-1) != 1 or t2.stride(0) % 8 != 0 or t2.data_ptr() % 16 != 0:
+    t2 = t2.contiguous()
+  return t2
+
+
+# ---------------------------------------------------------------------------------------
+# attention core
+# ---------------------------------------------------------------------------------------
+
+def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gate=None, out=None):
+  """Core launch on 2-level batched views.
+
+  q ``[B0,B1,Q,H,D]``, k ``[B0,B1,K,H,D]``, v ``[B0,B1,K,H,Dv]``, gate like the output
+  ``[B0,B1,Q,H,Dv]``; bias ``[B0,B1,H,Q,K]`` (zero strides allowed), masks ``[B0,B1,Q]`` /
+  ``[B0,B1,K]`` uint8.  All bf16 with unit last stride.  Returns ``out``.
+  """
+  dev = _require_cuda(q, k, v, bias, mask_q, mask_k, gate, out)
+  _require(q.ndim == 5 and k.ndim == 5 and v.ndim == 5, "attention: q/k/v must be [B0,B1,L,H,D]")
+  B0, B1, Q, H, D = q.shape
+  K, Dv = k.shape[2], v.shape[-1]
+  _require(tuple(k.shape) == (B0, B1, K, H, D), f"attention: k shape {tuple(k.shape)} vs q {tuple(q.shape)}")
+  _require(tuple(v.shape[:4]) == (B0, B1, K, H), f"attention: v shape {tuple(v.shape)}")
+  for name, t in (("q", q), ("k", k), ("v", v), ("gate", gate), ("bias", bias)):
+    if t is not None:
+      _require(t.dtype == BF16, f"attention: {name} must be bfloat16, got {t.dtype}")
+      _require(t.stride(-1) == 1, f"attention: {name} needs a unit last stride")
+  if out is None:
+    out = torch.empty((B0, B1, Q, H, Dv), dtype=BF16, device=dev)
+  _require(tuple(out.shape) == (B0, B1, Q, H, Dv) and out.stride(-1) == 1, "attention: bad out")
+  a = _lib.AttentionArgs()
+  a.B0, a.B1, a.Q, a.K, a.H, a.D, a.Dv = B0, B1, Q, K, H, D, Dv
+  a.scale = float(scale)
+  a.q, a.q_s = _vp(q), (C.c_int64 * 4)(*q.stride()[:4])
+  a.k, a.k_s = _vp(k), (C.c_int64 * 4)(*k.stride()[:4])
+  a.v, a.v_s = _vp(v), (C.c_int64 * 4)(*v.stride()[:4])
+  if bias is not None:
+    _require(tuple(bias.shape) == (B0, B1, H, Q, K), f"attention: bias shape {tuple(bias.shape)}")
+    a.bias, a.bias_s = _vp(bias), (C.c_int64 * 4)(*bias.stride()[:4])
+  if mask_q is not None:
+    _require(tuple(mask_q.shape) == (B0, B1, Q) and mask_q.dtype == torch.uint8, "attention: bad mask_q")
+    a.mask_q, a.mq_s = _vp(mask_q), (C.c_int64 * 3)(*mask_q.stride())
+  if mask_k is not None:
+    _require(tuple(mask_k.shape) == (B0, B1, K) and mask_k.dtype == torch.uint8, "attention: bad mask_k")
+    a.mask_k, a.mk_s = _vp(mask_k), (C.c_int64 * 3)(*mask_k.stride())
+  if gate is not None:
+    _require(tuple(gate.shape) == (B0, B1, Q, H, Dv), f"attention: gate shape {tuple(gate.shape)}")
+    a.gate, a.g_s = _vp(gate), (C.c_int64 * 4)(*gate.stride()[:4])
+  a.out, a.o_s = _vp(out), (C.c_int64 * 4)(*out.stride()[:4])
+  lib = _lib.load()
+  _lib.check(lib.sf_hip_attention_fwd(C.byref(a), _stream(q)), "sf_hip_attention_fwd")
+  return out
+
+
+# ---------------------------------------------------------------------------------------
+# row kernels
+# ---------------------------------------------------------------------------------------
+
+def layer_norm(x: torch.Tensor, gamma=None, beta=None, *, eps: float = 1e-5, scale=None, shift=None):
+  """LN over the last dim (bf16 in / out).  With ``scale``/``shift`` ([R, C] bf16) this is
+  the AdaLN modulation, row m using condition row ``m % R``."""
+  _require_cuda(x, gamma, beta, scale, shift)
+  Cn = x.shape[-1]
+  x2 = _rows(_bf16(x), Cn)
+  y = torch.empty(x2.shape, dtype=BF16, device=x.device)
+  a = _lib.LayerNormArgs()
+  a.M, a.C, a.eps = x2.shape[0], Cn, float(eps)
+  a.x, a.x_rs = _vp(x2), x2.stride(0)
+  g, b = _f32(gamma), _f32(beta)
+  a.gamma, a.beta = _vp(g), _vp(b)
+  if scale is not None:
+    s2, h2 = _rows(_bf16(scale), Cn), _rows(_bf16(shift), Cn)
+    _require(s2.shape == h2.shape, "layer_norm: scale/shift shapes differ")
+    a.scale, a.shift, a.cond_rows, a.cond_rs = _vp(s2), _vp(h2), s2.shape[0], s2.stride(0)
+  a.y, a.y_rs = _vp(y), y.stride(0)
+  _lib.check(_lib.load().sf_hip_layer_norm_fwd(C.byref(a), _stream(x)), "sf_hip_layer_norm_fwd")
+  return y.view(*x.shape[:-1], Cn)
+
+
+def linear(x: torch.Tensor, wt: torch.Tensor, bias=None, *, residual=None, mul=None,
+           post_sigmoid: bool = False, ycols: int | None = None, yt=None, tcol0: int = 0,
+           want_y: bool = True):
+  """``post(x @ wt.T + bias) * mul + residual`` with ``wt`` ``[N, K]`` bf16 (K contiguous).
+
+  ``mul`` ``[R, N]`` multiplies row m by ``mul[m % R]``.  ``yt`` (``[T, M]`` bf16) receives
+  columns ``[tcol0, tcol0+T)`` transposed.  Returns ``y`` ``[..., ycols or N]`` or None."""
+  _require_cuda(x, wt, bias, residual, mul, yt)
+  N, K = wt.shape
+  _require(x.shape[-1] == K, f"linear: x last dim {x.shape[-1]} != weight K {K}")
+  _require(K % 8 == 0, "linear: K must be a multiple of 8")
+  _require(wt.dtype == BF16 and wt.is_contiguous(), "linear: wt must be contiguous bf16 [N, K]")
+  x2 = _rows(_bf16(x), K)
+  M = x2.shape[0]
+  a = _lib.LinearArgs()
+  a.M, a.N, a.K = M, N, K
+  a.x, a.x_rs, a.wt = _vp(x2), x2.stride(0), _vp(wt)
+  bias_f = _f32(bias)
+  a.bias = _vp(bias_f)
+  ycols = N if ycols is None else ycols
+  y = None
+  if want_y:
+    y = torch.empty((M, ycols), dtype=BF16, device=x.device)
+    a.y, a.y_rs, a.ycols = _vp(y), y.stride(0), ycols
+  if residual is not None:
+    r2 = _bf16(residual).reshape(M, -1)
+    _require(r2.shape[1] == ycols and r2.stride(-1) == 1, "linear: residual shape")
+    a.residual, a.r_rs = _vp(r2), r2.stride(0)
+  if mul is not None:
+    m2 = _bf16(mul).reshape(-1, N)
+    _require(m2.stride(-1) == 1, "linear: mul needs a unit last stride")
+    a.mul, a.mul_rows, a.mul_rs = _vp(m2), m2.shape[0], m2.stride(0)
+  else:
+    a.mul_rows = 1
+  a.post_sigmoid = int(bool(post_sigmoid))
+  if yt is not None:
+    _require(yt.dtype == BF16 and yt.shape[-1] == M and yt.stride(-1) == 1, "linear: yt shape")
+    a.tcol0, a.tcols, a.yt, a.yt_rs = tcol0, yt.shape[0], _vp(yt), yt.stride(0)
+  _lib.check(_lib.load().sf_hip_linear_fwd(C.byref(a), _stream(x)), "sf_hip_linear_fwd")
+  return None if y is None else y.view(*x.shape[:-1], ycols)
+
+
+def pair_logits(z: torch.Tensor, ln_w, ln_b, w_t: torch.Tensor) -> torch.Tensor:
+  """``[..., C]`` pair activations -> ``[H, P]`` logits planes (LN + projection)."""
+  _require_cuda(z, ln_w, ln_b, w_t)
+  H, Cn = w_t.shape
+  z2 = _rows(_bf16(z), Cn)
+  P = z2.shape[0]
+  _require(z2.stride(0) == Cn, "pair_logits: z rows must be contiguous")
+  out = torch.empty((H, P), dtype=BF16, device=z.device)
+  lw, lb = _f32(ln_w), _f32(ln_b)
+  wt = _bf16(w_t).contiguous()
+  a = _lib.PairLogitsArgs()
+  a.P, a.C, a.H = P, Cn, H
+  a.z, a.ln_w, a.ln_b, a.w_t, a.out = _vp(z2), _vp(lw), _vp(lb), _vp(wt), _vp(out)
+  _lib.check(_lib.load().sf_hip_pair_logits_fwd(C.byref(a), _stream(z)), "sf_hip_pair_logits_fwd")
+  return out
+
+
+def window_gather(src: torch.Tensor, idx: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+  """``src [S, rows, C]`` -> ``[S, UK, C]`` by flat index ``idx [UK]`` (masked -> 0)."""
+  _require_cuda(src, idx, mask)
+  S, rows, Cn = src.shape
+  src = _bf16(src).contiguous()
+  idx32 = idx.reshape(-1).to(torch.int32).contiguous()
+  m8 = _u8(mask.reshape(-1)).contiguous()
+  _require(idx32.numel() == m8.numel(), "window_gather: idx / mask sizes differ")
+  UK = idx32.numel()
+  keys = torch.empty((S, UK, Cn), dtype=BF16, device=src.device)
+  a = _lib.WindowGatherArgs()
+  a.S, a.rows, a.C, a.UK = S, rows, Cn, UK
+  a.src, a.idx, a.mask, a.keys = _vp(src), _vp(idx32), _vp(m8), _vp(keys)
+  _lib.check(_lib.load().sf_hip_window_gather_fwd(C.byref(a), _stream(src)), "sf_hip_window_gather_fwd")
+  return keys
+
+
+# ---------------------------------------------------------------------------------------
+# triangle attention module
+# ---------------------------------------------------------------------------------------
+
+def triangle_workspace_bytes(N: int, C_: int, H: int, D: int) -> int:
+  return int(_lib.load().sf_hip_triangle_workspace_bytes(N, C_, H, D))
+
+
+def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qkvgb: torch.Tensor,
+                       w_o: torch.Tensor, *, num_head: int, transpose: bool, add_residual: bool = True,
+                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+  """GridSelfAttention on ``z [N, N, C]`` (bf16).  Weights packed as the C ABI documents."""
+  _require_cuda(z, seq_mask, ln_w, ln_b, w_qkvgb, w_o, workspace)
+  _require(z.ndim == 3 and z.shape[0] == z.shape[1], f"triangle: z must be [N, N, C], got {tuple(z.shape)}")
+  N, _, Cn = z.shape
+  HD = w_o.shape[1]
+  _require(HD % num_head == 0, "triangle: output projection width not divisible by heads")
+  D = HD // num_head
+  _require(tuple(w_qkvgb.shape) == (4 * HD + num_head, Cn), f"triangle: w_qkvgb shape {tuple(w_qkvgb.shape)}")
+  _require(tuple(w_o.shape) == (Cn, HD), f"triangle: w_o shape {tuple(w_o.shape)}")
+  _require(seq_mask.shape == (N,), "triangle: seq_mask must be [N]")
+  zc = _bf16(z).contiguous()
+  m8 = _u8(seq_mask).contiguous()
+  lw, lb = _f32(ln_w), _f32(ln_b)
+  need = triangle_workspace_bytes(N, Cn, num_head, D)
+  if workspace is None or workspace.numel() < need:
+    workspace = torch.empty(need, dtype=torch.uint8, device=z.device)
+  out = torch.empty_like(zc)
+  a = _lib.TriangleArgs()
+  a.N, a.C, a.H, a.D = N, Cn, num_head, D
+  a.transpose, a.add_residual = int(bool(transpose)), int(bool(add_residual))
+  a.z, a.seq_mask, a.ln_w, a.ln_b = _vp(zc), _vp(m8), _vp(lw), _vp(lb)
+  a.w_qkvgb, a.w_o, a.out = _vp(w_qkvgb), _vp(w_o), _vp(out)
+  _lib.check(_lib.load().sf_hip_triangle_attn_fwd(C.byref(a), _vp(workspace), workspace.numel(), _stream(z)),
+             "sf_hip_triangle_attn_fwd")
+  return out
+
+
+def default_scale(d: int) -> float:
+  return 1.0 / math.sqrt(d)

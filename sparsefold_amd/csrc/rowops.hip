@@ -1,0 +1,334 @@
+// Row-wise kernels around the attention core on gfx950:
+//   layer_norm_kernel   LayerNorm / AdaLN rows (primitives.py:471-497, transformer.py:80-96)
+//   linear_kernel       bf16 MFMA GEMM with fused bias / sigmoid / row-broadcast multiplier /
+//                       residual epilogue and an optional transposed second output
+//                       (primitives.py:328-372 Linear.forward; the transposed output emits
+//                       pair-bias planes [H, rows] as blocks.py:329 rearranges them)
+//   pair_logits_kernel  LN(z) . W -> [H, P] in one pass over z (blocks.py:745-749,
+//                       transformer.py:430-447); HBM-bound on z
+//   window_gather_kernel key-window gather of atom_layout.convert (atom_layout.py:61-83)
+#include "sf_common.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------
+// LayerNorm / AdaLN: one wave per row, 16-byte chunks, fp32 statistics.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const int C = a.C, nch = C / 8;
+  const uint16_t* xp = (const uint16_t*)a.x + row * a.x_rs;
+  u32x4 w[4];
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int ch = lane + 64 * t;
+    w[t] = (ch < nch) ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += bflo(w[t][e]) + bfhi(w[t][e]);
+  }
+  const float mean = wave_sum(sum) / (float)C;
+  float sq = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (lane + 64 * t < nch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d0 = bflo(w[t][e]) - mean, d1 = bfhi(w[t][e]) - mean;
+        sq += d0 * d0 + d1 * d1;
+      }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(sq) / (float)C + a.eps);
+  const uint16_t* scp = nullptr;
+  const uint16_t* shp = nullptr;
+  if (a.scale != nullptr) {
+    const int64_t crow = row % a.cond_rows;
+    scp = (const uint16_t*)a.scale + crow * a.cond_rs;
+    shp = (const uint16_t*)a.shift + crow * a.cond_rs;
+  }
+  uint16_t* yp = (uint16_t*)a.y + row * a.y_rs;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int ch = lane + 64 * t;
+    if (ch >= nch) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = (bflo(w[t][e]) - mean) * rstd;
+      v[2 * e + 1] = (bfhi(w[t][e]) - mean) * rstd;
+    }
+    const int c0 = 8 * ch;
+    if (a.gamma != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = v[e] * a.gamma[c0 + e] + (a.beta ? a.beta[c0 + e] : 0.f);
+    }
+    if (scp != nullptr) {
+      const u32x4 sw = ld16(scp + c0), hw = ld16(shp + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = v[2 * e] * bflo(sw[e]) + bflo(hw[e]);
+        v[2 * e + 1] = v[2 * e + 1] * bfhi(sw[e]) + bfhi(hw[e]);
+      }
+    }
+    st16(yp + c0, u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]),
+                        pack_bf2(v[6], v[7])});
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Linear: Y[M,N] = epi(X[M,K] . Wt[N,K]^T).  128x128 block tile, 4 waves of 64x64,
+// K in steps of 32 through LDS, v_mfma_f32_32x32x16_bf16.
+// ------------------------------------------------------------------------------------
+constexpr int kBM = 128, kBN = 128, kBK = 32, kLD = kBK + 8;
+
+__global__ __launch_bounds__(256) void linear_kernel(const sf_linear_args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[kBM * kLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[kBN * kLD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, li = lane & 31;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * kBM;
+  const int n0 = blockIdx.y * kBN;
+  const uint16_t* xp = (const uint16_t*)a.x;
+  const uint16_t* wp = (const uint16_t*)a.wt;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.f;
+
+  for (int k0 = 0; k0 < a.K; k0 += kBK) {
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int t = tid + 256 * it;
+      const int r = t >> 2, c8 = (t & 3) * 8;
+      const int kk = k0 + c8;
+      const int64_t gm = m0 + r;
+      const int gn = n0 + r;
+      st16(&sA[r * kLD + c8], (gm < a.M && kk < a.K) ? ld16(xp + gm * a.x_rs + kk) : u32x4{0, 0, 0, 0});
+      st16(&sB[r * kLD + c8], (gn < a.N && kk < a.K) ? ld16(wp + (int64_t)gn * a.K + kk) : u32x4{0, 0, 0, 0});
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      bf16x8 av[2], bv[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        av[mb] = as_bf16x8(ld16(&sA[(64 * wm + 32 * mb + li) * kLD + 16 * kk + 8 * half]));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        bv[nb] = as_bf16x8(ld16(&sB[(64 * wn + 32 * nb + li) * kLD + 16 * kk + 8 * half]));
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = mfma32(av[mb], bv[nb], acc[mb][nb]);
+    }
+  }
+
+  uint16_t* yp = (uint16_t*)a.y;
+  uint16_t* ytp = (uint16_t*)a.yt;
+  const uint16_t* rp = (const uint16_t*)a.residual;
+  const uint16_t* mp = (const uint16_t*)a.mul;
+  const int ycols = a.ycols > 0 ? a.ycols : a.N;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int n = n0 + 64 * wn + 32 * nb + li;
+    if (n >= a.N) continue;
+    const float bn = a.bias ? a.bias[n] : 0.f;
+    const bool tcol = ytp != nullptr && n >= a.tcol0 && n < a.tcol0 + a.tcols;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+        const int64_t mbase = m0 + 64 * wm + 32 * mb + 8 * g + 4 * half;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t m = mbase + e;
+          float x = acc[mb][nb][4 * g + e] + bn;
+          if (m < a.M) {
+            if (a.post_sigmoid) x = sigmoidf_(x);
+            if (mp) x *= bf2f(mp[(m % a.mul_rows) * a.mul_rs + n]);
+            if (rp) x += bf2f(rp[m * a.r_rs + n]);
+            if (yp && n < ycols) yp[m * a.y_rs + n] = f2bf(x);
+          }
+          v[e] = x;
+        }
+        if (tcol) {
+          uint16_t* tp = ytp + (int64_t)(n - a.tcol0) * a.yt_rs;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (mbase + e < a.M) tp[mbase + e] = f2bf(v[e]);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Pair logits: one thread per pair position; the position's C channels stay in
+// registers as packed bf16, LN statistics in fp32, then H dot products against
+// gamma-folded weights held in LDS ([c][h] so every thread reads the same words).
+// ------------------------------------------------------------------------------------
+constexpr int kPLMaxC = 128, kPLMaxH = 64;
+
+template <int H>  // H = compile-time capacity; a.H <= H planes are produced
+__global__ __launch_bounds__(256) void pair_logits_kernel(const sf_pair_logits_args a) {
+  __shared__ float sG[kPLMaxC * H];   // gamma[c] * w[h][c]   (zero for h >= a.H)
+  __shared__ float sS2[H];            // sum_c beta[c] * w[h][c]
+  const int C = a.C, Hr = a.H;
+  const uint16_t* wt = (const uint16_t*)a.w_t;
+  for (int t = threadIdx.x; t < C * H; t += 256) {
+    const int c = t / H, h = t % H;
+    sG[t] = h < Hr ? bf2f(wt[h * C + c]) * (a.ln_w ? a.ln_w[c] : 1.f) : 0.f;
+  }
+  if (threadIdx.x < H) {
+    float s = 0.f;
+    if (a.ln_b && (int)threadIdx.x < Hr)
+      for (int c = 0; c < C; ++c) s += a.ln_b[c] * bf2f(wt[threadIdx.x * C + c]);
+    sS2[threadIdx.x] = s;
+  }
+  __syncthreads();
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= a.P) return;
+  const uint16_t* zp = (const uint16_t*)a.z + p * C;
+  uint32_t xw[kPLMaxC / 2];
+  float sum = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < kPLMaxC / 8; ++ch) {
+    if (8 * ch < C) {
+      const u32x4 w = ld16(zp + 8 * ch);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xw[4 * ch + e] = w[e];
+        sum += bflo(w[e]) + bfhi(w[e]);
+      }
+    }
+  }
+  const float mean = sum / (float)C;
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPLMaxC / 2; ++e) {
+    if (2 * e < C) {
+      const float d0 = bflo(xw[e]) - mean, d1 = bfhi(xw[e]) - mean;
+      sq += d0 * d0 + d1 * d1;
+    }
+  }
+  const float rstd = rsqrtf(sq / (float)C + 1e-5f);
+  float acc[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) acc[h] = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPLMaxC / 2; ++e) {
+    if (2 * e < C) {
+      const float x0 = bflo(xw[e]) - mean, x1 = bfhi(xw[e]) - mean;
+#pragma unroll
+      for (int h = 0; h < H; ++h) acc[h] += x0 * sG[(2 * e) * H + h] + x1 * sG[(2 * e + 1) * H + h];
+    }
+  }
+  uint16_t* op = (uint16_t*)a.out;
+#pragma unroll
+  for (int h = 0; h < H; ++h)
+    if (h < Hr) op[(int64_t)h * a.P + p] = f2bf(acc[h] * rstd + sS2[h]);
+}
+
+// ------------------------------------------------------------------------------------
+// Window gather: one thread per 16-byte chunk of a gathered key row.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void window_gather_kernel(const sf_window_gather_args a) {
+  const int nch = a.C / 8;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)a.S * a.UK * nch;
+  if (t >= total) return;
+  const int ch = (int)(t % nch);
+  const int64_t rowo = t / nch;                 // s * UK + uk
+  const int uk = (int)(rowo % a.UK);
+  const int s = (int)(rowo / a.UK);
+  const int idx = a.idx[uk];
+  const bool ok = a.mask[uk] != 0 && idx >= 0 && idx < a.rows;
+  u32x4 w = u32x4{0, 0, 0, 0};
+  if (ok) w = ld16((const uint16_t*)a.src + ((int64_t)s * a.rows + idx) * a.C + 8 * ch);
+  st16((uint16_t*)a.keys + rowo * a.C + 8 * ch, w);
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+extern "C" int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream) {
+  if (a == nullptr || a->x == nullptr || a->y == nullptr) { sf_set_error("layer_norm: null x/y"); return 1; }
+  if (a->M <= 0 || a->C <= 0 || a->C % 8 != 0 || a->C > 2048) {
+    sf_set_error("layer_norm: need M > 0 and C a multiple of 8 in [8, 2048] (M=%lld C=%d)", (long long)a->M, a->C);
+    return 1;
+  }
+  if ((a->scale == nullptr) != (a->shift == nullptr) || (a->scale && a->cond_rows <= 0)) {
+    sf_set_error("layer_norm: scale and shift must be given together with cond_rows > 0"); return 1;
+  }
+  if (!al16(a->x) || !al16(a->y) || a->x_rs % 8 || a->y_rs % 8 ||
+      (a->scale && (!al16(a->scale) || !al16(a->shift) || a->cond_rs % 8))) {
+    sf_set_error("layer_norm: rows must be 16-byte aligned"); return 1;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)((a->M + 3) / 4)), dim3(256), 0, st, *a);
+  return sf_check_launch("layer_norm_kernel");
+}
+
+extern "C" int sf_hip_linear_fwd(const sf_linear_args* a, void* stream) {
+  if (a == nullptr || a->x == nullptr || a->wt == nullptr || (a->y == nullptr && a->yt == nullptr)) {
+    sf_set_error("linear: null x / wt / outputs"); return 1;
+  }
+  if (a->M <= 0 || a->N <= 0 || a->K <= 0 || a->K % 8 != 0) {
+    sf_set_error("linear: need M, N > 0 and K a positive multiple of 8 (M=%lld N=%d K=%d)", (long long)a->M, a->N, a->K);
+    return 1;
+  }
+  if (!al16(a->x) || !al16(a->wt) || a->x_rs % 8) { sf_set_error("linear: x / wt rows must be 16-byte aligned"); return 1; }
+  if (a->mul && a->mul_rows <= 0) { sf_set_error("linear: mul_rows must be positive"); return 1; }
+  if (a->yt && (a->tcol0 < 0 || a->tcols < 0 || a->tcol0 + a->tcols > a->N)) {
+    sf_set_error("linear: transposed column range out of bounds"); return 1;
+  }
+  const int64_t gm = (a->M + kBM - 1) / kBM;
+  if (gm > 0x7fffffff) { sf_set_error("linear: M too large"); return 1; }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(linear_kernel, dim3((unsigned)gm, (a->N + kBN - 1) / kBN), dim3(256), 0, st, *a);
+  return sf_check_launch("linear_kernel");
+}
+
+extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream) {
+  if (a == nullptr || a->z == nullptr || a->w_t == nullptr || a->out == nullptr) {
+    sf_set_error("pair_logits: null pointers"); return 1;
+  }
+  if (a->P <= 0 || a->C <= 0 || a->C % 8 != 0 || a->C > kPLMaxC || a->H <= 0 || a->H > kPLMaxH) {
+    sf_set_error("pair_logits: need C a multiple of 8 <= %d and 0 < H <= %d (C=%d H=%d)", kPLMaxC, kPLMaxH, a->C, a->H);
+    return 1;
+  }
+  if (!al16(a->z)) { sf_set_error("pair_logits: z must be 16-byte aligned"); return 1; }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((a->P + 255) / 256));
+  if (a->H <= 4) hipLaunchKernelGGL(pair_logits_kernel<4>, grid, dim3(256), 0, st, *a);
+  else if (a->H <= 8) hipLaunchKernelGGL(pair_logits_kernel<8>, grid, dim3(256), 0, st, *a);
+  else if (a->H <= 16) hipLaunchKernelGGL(pair_logits_kernel<16>, grid, dim3(256), 0, st, *a);
+  else if (a->H <= 32) hipLaunchKernelGGL(pair_logits_kernel<32>, grid, dim3(256), 0, st, *a);
+  else hipLaunchKernelGGL(pair_logits_kernel<64>, grid, dim3(256), 0, st, *a);
+  return sf_check_launch("pair_logits_kernel");
+}
+
+extern "C" int sf_hip_window_gather_fwd(const sf_window_gather_args* a, void* stream) {
+  if (a == nullptr || a->src == nullptr || a->idx == nullptr || a->mask == nullptr || a->keys == nullptr) {
+    sf_set_error("window_gather: null pointers"); return 1;
+  }
+  if (a->S <= 0 || a->rows <= 0 || a->UK <= 0 || a->C <= 0 || a->C % 8 != 0) {
+    sf_set_error("window_gather: bad sizes (S=%d rows=%d UK=%d C=%d)", a->S, a->rows, a->UK, a->C); return 1;
+  }
+  if (!al16(a->src) || !al16(a->keys)) { sf_set_error("window_gather: src/keys must be 16-byte aligned"); return 1; }
+  const int64_t total = (int64_t)a->S * a->UK * (a->C / 8);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(window_gather_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, *a);
+  return sf_check_launch("window_gather_kernel");
+}

@@ -1,0 +1,73 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels: bf16 packing, 16-byte vector
+// loads, MFMA wrappers and wave-level reductions.  Written for wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sparsefold_hip.h"
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+#define SF_LOG2E 1.4426950408889634f
+// Logit (log2 domain) of a masked key.  Finite, so a query whose keys are all masked
+// sees identical logits and weighs every key equally -- the reference's -finfo.max rule.
+#define SF_MASKED_LOGIT (-1.0e30f)
+
+__device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  __bf16 b = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// D(32x32) += A(32x16) * B(16x32), bf16 inputs, fp32 accumulation.
+// Lane l: A row l%32 / B column l%32, k = 8*(l/32) .. +7; D row 8*(r/4)+4*(l/32)+r%4, col l%32.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// Logistic sigmoid from exp2: 1 / (1 + 2^(-x log2 e)).
+__device__ __forceinline__ float sigmoidf_(float x) { return fast_rcp(1.0f + fast_exp2(-x * SF_LOG2E)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Load 8 bf16 starting at element `d0` of a row with `n` valid elements; elements past n
+// read as 0.  `vec` selects the 16-byte path (caller guarantees alignment and n % 8 == 0).
+__device__ __forceinline__ u32x4 load8_guard(const uint16_t* row, int d0, int n, bool vec) {
+  if (vec) {
+    if (d0 < n) return ld16(row + d0);
+    return u32x4{0, 0, 0, 0};
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t lo = (d0 + 2 * e < n) ? row[d0 + 2 * e] : 0;
+    uint32_t hi = (d0 + 2 * e + 1 < n) ? row[d0 + 2 * e + 1] : 0;
+    w[e] = lo | (hi << 16);
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Thread-local last-error plumbing shared by all C entry points.
+void sf_set_error(const char* fmt, ...);
+int sf_check_launch(const char* what);

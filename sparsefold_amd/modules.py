@@ -1,0 +1,228 @@
+"""Parameter-layout mirrors of the reference attention modules.
+
+Each class has the reference constructor signature and registers the same sub-modules and
+parameters (names and shapes), so a reference ``state_dict`` loads strictly.  They carry no
+compute of their own: ``forward`` is provided by the HIP backend, which ``backends.init()``
+installs over these factories (exactly as the reference's vecops ``apply()`` replaces module
+factories, ``src/sparsefold/backends/vecops/backend.py:187-248``).  Calling ``forward`` on an
+unreplaced class raises.
+
+Mirrored layouts (reference file:line):
+* ``Linear``            primitives.py:178-280 -- weight ``[*in, *out]``, or ``[*out, *in]``
+                        with ``transpose_weights``; optional bias ``[*out]``
+* ``LayerNorm``         primitives.py:375-430 -- weight ``[C]``, optional bias ``[C]``
+* ``GridSelfAttention`` blocks.py:188-267
+* ``AdaptiveLayerNorm`` / ``AdaptiveZeroInit`` / ``SelfAttention`` transformer.py:27-304
+* ``CrossAttention``    transformer.py:480-547
+* ``SingleActUpdate``   blocks.py:692-737 (attention half; the transition is outside the
+                        attention path)
+"""
+from __future__ import annotations
+
+import dataclasses
+import numbers
+from collections.abc import Sequence
+
+import torch
+
+
+@dataclasses.dataclass
+class GlobalConfig:
+  """model/config.py:15-27 (the fields the attention modules read)."""
+  bfloat16: str = "all"
+  final_init: str = "zeros"
+  pair_attention_chunk_size: Sequence = ((1536, 128), (None, 32))
+
+
+def _shape(x) -> tuple[int, ...]:
+  return (int(x),) if isinstance(x, numbers.Integral) else tuple(int(v) for v in x)
+
+
+class Linear(torch.nn.Module):
+  def __init__(self, num_input, num_output, *, bias: bool = False, transpose_weights: bool = False,
+               dtype: torch.dtype | None = None, device=None, name: str | None = None, **_):
+    super().__init__()
+    self.name = name
+    self.input_shape, self.output_shape = _shape(num_input), _shape(num_output)
+    self.transpose_weights = transpose_weights
+    self.use_bias = bias
+    ws = self.output_shape + self.input_shape if transpose_weights else self.input_shape + self.output_shape
+    self.weight = torch.nn.Parameter(torch.empty(ws, dtype=dtype or torch.float32, device=device))
+    if bias:
+      self.bias = torch.nn.Parameter(torch.empty(self.output_shape, dtype=dtype or torch.float32, device=device))
+    else:
+      self.register_parameter("bias", None)
+
+
+class LayerNorm(torch.nn.Module):
+  def __init__(self, normalized_shape: int, *, eps: float = 1e-5, elementwise_affine: bool = True,
+               bias: bool = True, dtype=None, device=None, name: str | None = None):
+    super().__init__()
+    self.name = name
+    self.eps = eps
+    self.normalized_shape = _shape(normalized_shape)
+    if elementwise_affine:
+      self.weight = torch.nn.Parameter(torch.empty(self.normalized_shape, dtype=dtype or torch.float32, device=device))
+      if bias:
+        self.bias = torch.nn.Parameter(torch.empty(self.normalized_shape, dtype=dtype or torch.float32, device=device))
+      else:
+        self.register_parameter("bias", None)
+    else:
+      self.register_parameter("weight", None)
+      self.register_parameter("bias", None)
+
+
+class _NoTorchPath:
+  def forward(self, *args, **kwargs):
+    raise RuntimeError(f"{type(self).__name__} has no Torch compute path in this package; "
+                       "configure_runtime(backend='hip') and backends.init() before constructing it")
+
+
+class GridSelfAttention(_NoTorchPath, torch.nn.Module):
+  """blocks.py:188-267: triangle attention, starting (transpose=False) / ending node."""
+
+  @dataclasses.dataclass
+  class Config:
+    num_head: int = 4
+
+  def __init__(self, config: Config, global_config: GlobalConfig, transpose: bool, *, num_channels: int,
+               distributed: bool = False, name: str = "", **kwargs):
+    super().__init__()
+    self.name = name
+    self.distributed = False
+    if distributed:
+      raise ValueError("GridSelfAttention: the multi-rank path is not part of this build")
+    self.transpose = transpose
+    self.config = config
+    self.num_channels = num_channels
+    self.pair_attention_chunk_size = global_config.pair_attention_chunk_size
+    assert num_channels % config.num_head == 0
+    qkv_dim = max(num_channels // config.num_head, 16)
+    self.qkv_dim = qkv_dim
+    H = config.num_head
+    self.q_projection = Linear(num_channels, (H, qkv_dim), transpose_weights=True, name="q_projection")
+    self.k_projection = Linear(num_channels, (H, qkv_dim), transpose_weights=True, name="k_projection")
+    self.v_projection = Linear(num_channels, (H, qkv_dim), name="v_projection")
+    self.gating_query = Linear(num_channels, H * qkv_dim, transpose_weights=True, name="gating_query")
+    self.output_projection = Linear(H * qkv_dim, num_channels, name="output_projection")
+    self.act_norm = LayerNorm(num_channels, bias=kwargs.pop("act_norm_bias", True), name="act_norm")
+    self.pair_bias_projection = Linear(num_channels, H, name="pair_bias_projection")
+
+
+class AdaptiveLayerNorm(torch.nn.Module):
+  """transformer.py:27-78."""
+
+  def __init__(self, hidden_size, single_cond_size, *, dtype=None, name: str = ""):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    self.single_cond = single_cond_size is not None
+    if self.single_cond:
+      self.layer_norm = LayerNorm(hidden_size, elementwise_affine=False, dtype=torch.float32, name="layer_norm")
+      self.single_cond_layer_norm = LayerNorm(single_cond_size, bias=False, dtype=torch.float32,
+                                              name="single_cond_layer_norm")
+      self.single_cond_scale = Linear(single_cond_size, hidden_size, bias=True, dtype=dtype, name="single_cond_scale")
+      self.single_cond_bias = Linear(single_cond_size, hidden_size, bias=False, dtype=dtype, name="single_cond_bias")
+    else:
+      self.layer_norm = LayerNorm(hidden_size, dtype=torch.float32, name="layer_norm")
+
+
+class AdaptiveZeroInit(torch.nn.Module):
+  """transformer.py:99-136."""
+
+  def __init__(self, global_config, *, num_channels: int, hidden_size: int, single_cond_size, dtype=None,
+               name: str = ""):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    self.single_cond = single_cond_size is not None
+    self.transition2 = Linear(hidden_size, num_channels, bias=False, dtype=dtype, name="transition2")
+    if self.single_cond:
+      self.adaptive_zero_cond = Linear(single_cond_size, num_channels, bias=True, dtype=dtype,
+                                       name="adaptive_zero_cond")
+
+
+class SelfAttention(_NoTorchPath, torch.nn.Module):
+  """transformer.py:234-304: single-representation / diffusion token attention."""
+
+  @dataclasses.dataclass
+  class Config:
+    num_head: int = 16
+    key_dim: int | None = None
+    value_dim: int | None = None
+
+  def __init__(self, config: Config, global_config: GlobalConfig, *, num_channels: int,
+               single_cond_size: int | None = None, dtype: torch.dtype | None = None,
+               distributed: bool = False, name: str = ""):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    if distributed:
+      raise ValueError("SelfAttention: the multi-rank path is not part of this build")
+    self.distributed = False
+    self.layer_norm = AdaptiveLayerNorm(num_channels, single_cond_size, dtype=dtype, name="")
+    key_dim = config.key_dim if config.key_dim is not None else num_channels
+    value_dim = config.value_dim if config.value_dim is not None else num_channels
+    H = config.num_head
+    assert key_dim % H == 0 and value_dim % H == 0
+    self.num_head = H
+    self.key_dim = key_dim = key_dim // H
+    self.value_dim = value_dim = value_dim // H
+    assert key_dim == value_dim
+    self.q_projection = Linear(num_channels, (H, key_dim), bias=True, dtype=dtype, name="q_projection")
+    self.k_projection = Linear(num_channels, (H, key_dim), bias=False, dtype=dtype, name="k_projection")
+    self.v_projection = Linear(num_channels, (H, value_dim), bias=False, dtype=dtype, name="v_projection")
+    self.gating_query = Linear(num_channels, H * value_dim, bias=False, dtype=dtype, name="gating_query")
+    self.zero_init = AdaptiveZeroInit(global_config, num_channels=num_channels, hidden_size=num_channels,
+                                      single_cond_size=single_cond_size, dtype=dtype, name="")
+
+
+class CrossAttention(_NoTorchPath, torch.nn.Module):
+  """transformer.py:480-547: windowed atom cross attention."""
+
+  @dataclasses.dataclass
+  class Config:
+    num_head: int = 4
+    key_dim: int = 128
+    value_dim: int = 128
+
+  def __init__(self, config: Config, global_config: GlobalConfig, *, num_channels: int,
+               dtype: torch.dtype | None = None, name: str = ""):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    self.q_layernorm = AdaptiveLayerNorm(num_channels, num_channels, dtype=dtype, name="q")
+    self.k_layernorm = AdaptiveLayerNorm(num_channels, num_channels, dtype=dtype, name="k")
+    assert config.key_dim % config.num_head == 0 and config.value_dim % config.num_head == 0
+    H = config.num_head
+    self.num_head = H
+    self.key_dim = key_dim = config.key_dim // H
+    self.value_dim = value_dim = config.value_dim // H
+    assert key_dim == value_dim
+    self.q_projection = Linear(num_channels, (H, key_dim), bias=True, dtype=dtype, name="q_projection")
+    self.k_projection = Linear(num_channels, (H, key_dim), bias=False, dtype=dtype, name="k_projection")
+    self.v_projection = Linear(num_channels, (H, value_dim), bias=False, dtype=dtype, name="v_projection")
+    self.gating_query = Linear(num_channels, H * value_dim, bias=False, dtype=dtype, name="gating_query")
+    self.zero_init = AdaptiveZeroInit(global_config, num_channels=num_channels, hidden_size=num_channels,
+                                      single_cond_size=num_channels, dtype=dtype, name="")
+
+
+class SingleActUpdate(_NoTorchPath, torch.nn.Module):
+  """blocks.py:692-737: pair-logit prologue + single attention with pair bias."""
+
+  def __init__(self, global_config: GlobalConfig, num_channels: int, seq_channels: int,
+               attn_config: SelfAttention.Config, transition_config=None, distributed: bool = False, **kwargs):
+    super().__init__()
+    self.name = "<none>"
+    if distributed:
+      raise ValueError("SingleActUpdate: the multi-rank path is not part of this build")
+    self.distributed = False
+    self.num_channels = num_channels
+    self.seq_channels = seq_channels
+    self.num_head = attn_config.num_head
+    self.qkv_dim = seq_channels // self.num_head
+    self.single_pair_logits_norm = LayerNorm(num_channels, name="single_pair_logits_norm")
+    self.single_pair_logits_projection = Linear(num_channels, attn_config.num_head,
+                                                name="single_pair_logits_projection")
+    self.single_attention = SelfAttention(attn_config, global_config, num_channels=seq_channels,
+                                          name="single_attention_")

@@ -1,0 +1,135 @@
+"""Seeded synthetic workloads for the five attention configurations.
+
+All tensors are drawn on the CPU from a seeded ``torch.Generator`` in float32 and then cast,
+so every consumer (parity tests, benchmark, CPU baseline) sees identical values.
+Weights: Linear ~ N(0, std^2) (std 0.02 by default; ``sharp=True`` uses std = 1/sqrt(fan_in)
+so the softmax is far from uniform); LayerNorm gamma = 1 + N(0, 0.02^2), beta ~ N(0, 0.02^2).
+
+Configurations (sizes as used by the benchmark):
+  triangle   z [N, N, 128], H=4, D=32; padded variant masks the last N//10 tokens
+  single     s [N, 384], z [N, N, 128] -> bias [16, N, N]; H=16, D=24
+  diffusion  act [S, N, 768], single_cond [N, 384], bias [16, N, N] shared by the S samples;
+             H=16, D=48
+  window     act [S, U, 32, 128] (U = atoms/32 windows), keys = 128 atoms starting at 32u-48,
+             indices outside [0, atoms) masked, last `pad` atoms padded; bias [U, 4, 32, 128];
+             H=4, D=32
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+
+from sparsefold_amd import modules as M
+
+
+def _gen(seed: int) -> torch.Generator:
+  return torch.Generator().manual_seed(int(seed))
+
+
+def fill_parameters(module: torch.nn.Module, seed: int, std: float = 0.02, sharp: bool = False) -> torch.nn.Module:
+  """Deterministically fills every parameter (sorted by name) of ``module`` in place."""
+  g = _gen(seed)
+  linears = {id(m.weight): m for m in module.modules() if isinstance(m, M.Linear)}
+  norms = {id(m.weight): m for m in module.modules() if isinstance(m, M.LayerNorm) and m.weight is not None}
+  norm_biases = {id(m.bias) for m in module.modules() if isinstance(m, M.LayerNorm) and m.bias is not None}
+  with torch.no_grad():
+    for name, p in sorted(module.named_parameters(), key=lambda kv: kv[0]):
+      r = torch.randn(p.shape, generator=g, dtype=torch.float32)
+      if id(p) in norms:
+        val = 1.0 + 0.02 * r
+      elif id(p) in norm_biases:
+        val = 0.02 * r
+      elif id(p) in linears and sharp:
+        fan_in = 1
+        for s in linears[id(p)].input_shape:
+          fan_in *= s
+        val = r / fan_in ** 0.5
+      else:
+        val = std * r
+      p.copy_(val.to(p.dtype))
+  return module
+
+
+def state_dict_f32(module: torch.nn.Module) -> dict[str, torch.Tensor]:
+  return {k: v.detach().to("cpu", torch.float32) for k, v in module.state_dict().items()}
+
+
+# ---------------------------------------------------------------------------------------
+
+def make_triangle(N: int, *, C: int = 128, H: int = 4, transpose: bool = False, padded: bool = False,
+                  seed: int = 1, sharp: bool = False, dtype=torch.bfloat16):
+  g = _gen(seed)
+  z = torch.randn(N, N, C, generator=g).to(dtype)
+  seq = torch.ones(N, dtype=torch.bool)
+  if padded:
+    seq[N - N // 10:] = False
+  mod = M.GridSelfAttention(M.GridSelfAttention.Config(num_head=H), M.GlobalConfig(), transpose,
+                            num_channels=C, name="pair_attention")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, z, seq
+
+
+def make_single(N: int, *, C_s: int = 384, C_z: int = 128, H: int = 16, seed: int = 3, sharp: bool = False,
+                padded: bool = False, dtype=torch.bfloat16):
+  g = _gen(seed)
+  s = torch.randn(N, C_s, generator=g).to(dtype)
+  z = torch.randn(N, N, C_z, generator=g).to(dtype)
+  seq = torch.ones(N, dtype=torch.bool)
+  if padded:
+    seq[N - N // 10:] = False
+  mod = M.SingleActUpdate(M.GlobalConfig(), C_z, C_s, M.SelfAttention.Config(num_head=H))
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, z, s, seq
+
+
+def make_diffusion(N: int, *, S: int = 5, C: int = 768, C_cond: int = 384, H: int = 16, seed: int = 4,
+                   sharp: bool = False, padded: bool = False, dtype=torch.bfloat16):
+  g = _gen(seed)
+  act = torch.randn(S, N, C, generator=g).to(dtype)
+  cond = torch.randn(N, C_cond, generator=g).to(dtype)
+  bias = torch.randn(H, N, N, generator=g).to(dtype)
+  mask = torch.ones(N, dtype=torch.bool)
+  if padded:
+    mask[N - N // 10:] = False
+  mod = M.SelfAttention(M.SelfAttention.Config(num_head=H), M.GlobalConfig(), num_channels=C,
+                        single_cond_size=C_cond, name="diffusion_transformer")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, act, cond, bias, mask
+
+
+@dataclasses.dataclass
+class WindowLayout:
+  """Key windows for 32-atom query blocks: window u covers atoms [32u - 48, 32u + 80)."""
+  gather_idxs: torch.Tensor   # [U, Kw] int32, flat index into [U, Qw]
+  gather_mask: torch.Tensor   # [U, Kw] bool, index inside [0, atoms)
+  queries_mask: torch.Tensor  # [U, Qw] bool, atom present
+  keys_mask: torch.Tensor     # [U, Kw] bool, key present
+
+
+def window_layout(atoms: int, *, Qw: int = 32, Kw: int = 128, pad: int = 0) -> WindowLayout:
+  U = atoms // Qw
+  present = torch.ones(atoms, dtype=torch.bool)
+  if pad:
+    present[atoms - pad:] = False
+  start = torch.arange(U) * Qw + Qw // 2 - Kw // 2
+  idx = start[:, None] + torch.arange(Kw)[None, :]
+  inside = (idx >= 0) & (idx < atoms)
+  idx_c = idx.clamp(0, atoms - 1)
+  return WindowLayout(gather_idxs=idx_c.to(torch.int32), gather_mask=inside,
+                      queries_mask=present.view(U, Qw).clone(), keys_mask=inside & present[idx_c])
+
+
+def make_window(atoms: int, *, S: int = 5, C: int = 128, H: int = 4, pad: int = 192, seed: int = 5,
+                sharp: bool = False, dtype=torch.bfloat16):
+  g = _gen(seed)
+  lay = window_layout(atoms, pad=pad)
+  U = atoms // 32
+  act = torch.randn(S, U, 32, C, generator=g).to(dtype)
+  qcond = torch.randn(U, 32, C, generator=g).to(dtype)
+  kcond = torch.randn(U, 128, C, generator=g).to(dtype)
+  bias = torch.randn(U, H, 32, 128, generator=g).to(dtype)
+  mod = M.CrossAttention(M.CrossAttention.Config(num_head=H, key_dim=C, value_dim=C), M.GlobalConfig(),
+                         num_channels=C, name="atom_transformer")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, act, lay, qcond, kcond, bias

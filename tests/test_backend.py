@@ -1,0 +1,99 @@
+"""Plugin boundary on the CPU: runtime selection keys, backend lifecycle, factory
+replacement, preparation guards (mirrors tests/test_runtime_reference.py and
+tests/test_native_preparation.py of the reference)."""
+import pytest
+import torch
+
+from sparsefold_amd import backends
+from sparsefold_amd import modules as M
+from sparsefold_amd.runtime import config
+
+
+def test_configure_runtime_accepts_hip_selection_keys(reset_runtime):
+  config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda")
+  assert config.acclib_implementation == "hip" and config.sdpa_implementation == "hip"
+  config.configure_runtime(backend="none")
+  assert config.acclib_implementation == "torch"
+  with pytest.raises(ValueError, match="SDPA"):
+    config.configure_runtime(sdpa_implementation="triton")
+  with pytest.raises(TypeError, match="Unknown runtime settings"):
+    config.configure_runtime(not_a_setting=1)
+  with pytest.raises(ValueError, match="either backend"):
+    config.configure_runtime(backend="hip", acclib_implementation="hip")
+  opts = config.get_runtime_options()
+  opts["native_ops"].append("x")
+  assert "x" not in config.native_ops
+
+
+def test_environment_selection(monkeypatch, reset_runtime):
+  monkeypatch.setenv("SPARSEFOLD_ACCLIB_IMPLEMENTATION", "hip")
+  monkeypatch.setenv("SPARSEFOLD_SDPA_IMPLEMENTATION", "hip")
+  config.reset()
+  assert config.acclib_implementation == "hip" and config.sdpa_implementation == "hip"
+
+
+def test_hip_backend_requires_gpu_device(reset_runtime):
+  config.configure_runtime(backend="hip", device="cpu")
+  with pytest.raises(RuntimeError, match="GPU only"):
+    backends.init()
+
+
+def test_unknown_native_op_rejected(reset_runtime):
+  config.configure_runtime(backend="hip", device="cuda", native_ops=["not_an_op"])
+  with pytest.raises(ValueError, match="Unknown native operators"):
+    backends.init()
+
+
+def test_apply_replaces_and_restores_factories(reset_runtime):
+  original = M.GridSelfAttention
+  config.configure_runtime(backend="hip", device="cuda", native_ops=["grid_self_attn"])
+  backends.init()
+  assert M.GridSelfAttention is not original and issubclass(M.GridSelfAttention, original)
+  assert M.SelfAttention.__name__ == "SelfAttention"          # not selected
+  config.configure_runtime(backend="torch")
+  backends.init()
+  assert M.GridSelfAttention is original
+  assert backends.prepare(torch.nn.Linear(2, 2)) == {"packed": 0, "fallback": 0, "opaque": 0}
+
+
+def test_vecops_is_declared_but_unavailable(reset_runtime):
+  assert "vecops" in backends.available_libraries() and "hip" in backends.available_libraries()
+  config.configure_runtime(backend="vecops", device="cpu")
+  with pytest.raises(RuntimeError, match="vecops"):
+    backends.init()
+
+
+def test_unreplaced_modules_have_no_torch_path(reset_runtime):
+  mod = M.GridSelfAttention(M.GridSelfAttention.Config(), M.GlobalConfig(), False, num_channels=32, name="x")
+  with pytest.raises(RuntimeError, match="no Torch compute path"):
+    mod(torch.zeros(4, 4, 32), torch.ones(4, dtype=torch.bool))
+
+
+def test_reference_parameter_layouts():
+  g = M.GridSelfAttention(M.GridSelfAttention.Config(num_head=4), M.GlobalConfig(), False, num_channels=128, name="t")
+  shapes = {k: tuple(v.shape) for k, v in g.state_dict().items()}
+  assert shapes == {
+      "q_projection.weight": (4, 32, 128), "k_projection.weight": (4, 32, 128), "v_projection.weight": (128, 4, 32),
+      "gating_query.weight": (128, 128), "output_projection.weight": (128, 128), "act_norm.weight": (128,),
+      "act_norm.bias": (128,), "pair_bias_projection.weight": (128, 4)}
+  s = M.SelfAttention(M.SelfAttention.Config(num_head=16), M.GlobalConfig(), num_channels=768, single_cond_size=384)
+  shapes = {k: tuple(v.shape) for k, v in s.state_dict().items()}
+  assert shapes["layer_norm.single_cond_scale.weight"] == (384, 768)
+  assert shapes["q_projection.weight"] == (768, 16, 48) and shapes["q_projection.bias"] == (16, 48)
+  assert shapes["zero_init.adaptive_zero_cond.weight"] == (384, 768)
+  assert "layer_norm.layer_norm.weight" not in shapes
+  c = M.CrossAttention(M.CrossAttention.Config(), M.GlobalConfig(), num_channels=128)
+  assert tuple(c.state_dict()["k_layernorm.single_cond_scale.weight"].shape) == (128, 128)
+  u = M.SingleActUpdate(M.GlobalConfig(), 128, 384, M.SelfAttention.Config(num_head=16))
+  assert u.single_attention.key_dim == 24
+  assert tuple(u.state_dict()["single_pair_logits_projection.weight"].shape) == (128, 16)
+
+
+def test_prepare_rejects_host_parameters_and_forward_requires_prepare(reset_runtime):
+  config.configure_runtime(backend="hip", device="cuda")
+  backends.init()
+  mod = M.GridSelfAttention(M.GridSelfAttention.Config(), M.GlobalConfig(), False, num_channels=32, name="x")
+  with pytest.raises(RuntimeError, match="not prepared"):
+    mod(torch.zeros(4, 4, 32), torch.ones(4, dtype=torch.bool))
+  with pytest.raises(RuntimeError, match="on the GPU"):
+    backends.prepare(mod)

@@ -1,0 +1,103 @@
+"""HIP dot_product_attention vs the oracle (float32 restatement of sdpa.py:22-121)."""
+import pytest
+import torch
+
+from oracle.sdpa import dot_product_attention as oracle_dpa
+from sparsefold_amd.backends.hip.attention import dot_product_attention as hip_dpa
+from tests._metrics import assert_close_bf16, bf16_round
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _run(q, k, v, **kw):
+  """HIP on bf16 inputs; oracle in float32 on the same (bf16-rounded) values."""
+  cast = lambda t: None if t is None else t.to(DEV, torch.bfloat16)
+  mq, mk = kw.pop("mask_q", None), kw.pop("mask_k", None)
+  bias = kw.pop("bias", None)
+  gate = kw.pop("gate", None)
+  out = hip_dpa(cast(q), cast(k), cast(v), mask_q=None if mq is None else mq.to(DEV),
+                mask_k=None if mk is None else mk.to(DEV), bias=cast(bias), gate=cast(gate), **kw)
+  torch.cuda.synchronize()
+  ref = oracle_dpa(bf16_round(q), bf16_round(k), bf16_round(v), mask_q=mq, mask_k=mk,
+                   bias=None if bias is None else bf16_round(bias), **kw)
+  if gate is not None:
+    ref = ref * torch.sigmoid(bf16_round(gate))
+  return out.float().cpu(), ref
+
+
+@pytest.mark.parametrize("batch_shape", [(), (2,), (2, 3)])
+@pytest.mark.parametrize("with_masks", [False, True])
+def test_reference_spec_seed808(batch_shape, with_masks):
+  """Shapes / masks of tests/test_runtime_reference.py:117-138 (incl. a fully masked query, D=4, Dv=6)."""
+  gen = torch.Generator().manual_seed(808)
+  q = torch.randn(*batch_shape, 3, 2, 4, generator=gen)
+  k = torch.randn(*batch_shape, 5, 2, 4, generator=gen)
+  v = torch.randn(*batch_shape, 5, 2, 6, generator=gen)
+  bias = torch.randn(*batch_shape, 2, 3, 5, generator=gen)
+  mq = torch.tensor([True, False, True]).expand(*batch_shape, 3) if with_masks else None
+  mk = torch.tensor([True, False, True, True, False]).expand(*batch_shape, 5) if with_masks else None
+  out, ref = _run(q, k, v, scale=0.4, mask_q=mq, mask_k=mk, bias=bias)
+  assert_close_bf16(out, ref, f"seed808 {batch_shape} masks={with_masks}")
+
+
+def test_reference_gpu_spec_seed610():
+  """tests/test_runtime_gpu.py:28-41 shapes (Dv=12 != D=16, bias per batch, key mask)."""
+  gen = torch.Generator().manual_seed(610)
+  q = torch.randn(2, 7, 3, 16, generator=gen)
+  k = torch.randn(2, 9, 3, 16, generator=gen)
+  v = torch.randn(2, 9, 3, 12, generator=gen)
+  bias = torch.randn(2, 3, 7, 9, generator=gen)
+  mk = torch.tensor([[True, False, True, True, True, False, True, False, True]]).expand(2, 9)
+  out, ref = _run(q, k, v, mask_k=mk, bias=bias, scale=0.3)
+  assert_close_bf16(out, ref, "seed610")
+
+
+@pytest.mark.parametrize("D", [16, 24, 32, 48, 64])
+@pytest.mark.parametrize("QK", [(77, 133), (128, 64), (200, 300)])
+def test_head_dims_tails_masks_bias_gate(D, QK):
+  Q, K = QK
+  g = torch.Generator().manual_seed(1000 + D + Q)
+  B, H = 2, 3
+  q, k = torch.randn(B, Q, H, D, generator=g), torch.randn(B, K, H, D, generator=g)
+  v = torch.randn(B, K, H, D, generator=g)
+  bias = torch.randn(H, Q, K, generator=g)            # broadcast over the batch (stride 0)
+  gate = torch.randn(B, Q, H, D, generator=g)
+  mq = torch.rand(B, Q, generator=g) > 0.1
+  mk = torch.rand(B, K, generator=g) > 0.3
+  mk[1, :] = False                                    # batch 1: every query fully masked
+  out, ref = _run(q, k, v, mask_q=mq, mask_k=mk, bias=bias, gate=gate)
+  assert_close_bf16(out, ref, f"D={D} Q={Q} K={K}")
+
+
+def test_fully_masked_rows_are_exact_means():
+  g = torch.Generator().manual_seed(5)
+  q, k = torch.randn(1, 70, 2, 32, generator=g), torch.randn(1, 150, 2, 32, generator=g)
+  v = torch.randn(1, 150, 2, 32, generator=g)
+  bias = 5 * torch.randn(1, 2, 70, 150, generator=g)
+  mq = torch.ones(1, 70, dtype=torch.bool)
+  mq[0, ::3] = False
+  out, _ = _run(q, k, v, mask_q=mq, bias=bias)
+  mean = bf16_round(v).mean(1)                         # [1, 2, 32] over all 150 keys
+  rows = out[0, ~mq[0]]                               # [n_masked, 2, 32]
+  diff = (rows - mean).abs().max().item()
+  print(f"[parity] fully masked rows: max |out - mean(v)| = {diff:.3e}")
+  assert diff <= 2 ** -8 * mean.abs().max().item() + 1e-6
+
+
+def test_no_mask_no_bias_and_known_answer():
+  g = torch.Generator().manual_seed(6)
+  q, k, v = (torch.randn(3, 40, 4, 32, generator=g) for _ in range(3))
+  out, ref = _run(q, k, v)
+  assert_close_bf16(out, ref, "plain")
+  ones = torch.ones(2, 1, 3, device=DEV, dtype=torch.bfloat16)
+  torch.testing.assert_close(hip_dpa(ones, ones, ones).float(), ones.float())
+
+
+def test_fp32_inputs_round_trip_dtype():
+  g = torch.Generator().manual_seed(7)
+  q, k, v = (torch.randn(2, 33, 2, 32, generator=g).to(DEV) for _ in range(3))
+  out = hip_dpa(q, k, v)
+  assert out.dtype == torch.float32
+  ref = oracle_dpa(bf16_round(q.cpu()), bf16_round(k.cpu()), bf16_round(v.cpu()))
+  assert_close_bf16(out, ref, "fp32 in/out")

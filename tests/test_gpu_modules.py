@@ -1,0 +1,127 @@
+"""Module-level parity: the HIP backend's four attention forms vs the oracle composites,
+through the reference lifecycle (configure_runtime -> backends.init -> construct ->
+load weights -> backends.prepare -> forward)."""
+import pytest
+import torch
+
+from oracle import modules as OM
+from sparsefold_amd import backends
+from sparsefold_amd import workloads as W
+from sparsefold_amd.runtime import config
+from tests._metrics import assert_close_bf16, bf16_round
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def hip_backend():
+  config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda")
+  backends.init()
+  yield
+  config.configure_runtime(backend="torch")
+  backends.init()
+  config.reset()
+
+
+def _prepared(mod):
+  mod = mod.to(DEV)
+  counts = backends.prepare(mod)
+  assert counts["opaque"] >= 1
+  return mod
+
+
+def _params(mod):
+  """float32 copies of the weights as the HIP path sees them: projection matrices rounded
+  to bf16 (the kernels' MFMA operands), norm parameters and biases kept in float32."""
+  from sparsefold_amd import modules as M
+  rounded = {f"{name}.weight" if name else "weight" for name, m in mod.named_modules() if isinstance(m, M.Linear)}
+  return {k: (bf16_round(v.float().cpu()) if k in rounded else v.float().cpu()) for k, v in mod.state_dict().items()}
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_c1_n20_fp32(transpose):
+  mod, z, seq = W.make_triangle(20, transpose=transpose, seed=1, dtype=torch.float32)
+  hip = _prepared(mod)
+  out = hip(z.to(DEV), seq.to(DEV))
+  assert out.dtype == torch.float32
+  p = _params(hip)
+  ref = OM.grid_self_attention(z, seq, p, transpose=transpose)
+  assert_close_bf16(out, ref, f"C1 triangle N=20 transpose={transpose}")
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref_u = OM.grid_self_attention(bf16_round(z), seq, p, transpose=transpose, return_update=True)
+  assert_close_bf16(upd, ref_u, "C1 update", max_abs=2e-2 * ref_u.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("N", [64, 97])
+def test_triangle_sharp_update_padded(transpose, N):
+  mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=7, sharp=True)
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert_close_bf16(upd, ref, f"triangle sharp N={N} transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_c2_n384_padded(transpose):
+  mod, z, seq = W.make_triangle(384, transpose=transpose, padded=True, seed=2)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  out = hip(zd, sd)
+  p = _params(hip)
+  ref = OM.grid_self_attention(z.float(), seq, p, transpose=transpose, chunk_size=128)
+  assert_close_bf16(out, ref, f"C2 triangle N=384 transpose={transpose}")
+  upd = hip(zd, sd, add_residual=False)
+  ref_u = ref - z.float()
+  assert_close_bf16(upd, ref_u, "C2 update", max_abs=2e-2 * ref_u.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_c3_n768_sampled_rows(transpose):
+  mod, z, seq = W.make_triangle(768, transpose=transpose, seed=3)
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False).float().cpu()
+  rows = [0, 1, 255, 383, 384, 511, 700, 767]
+  ref = OM.grid_self_attention_rows(z.float(), seq, _params(hip), transpose=transpose, rows=rows)
+  got = upd[:, rows].transpose(0, 1) if transpose else upd[rows]
+  assert_close_bf16(got, ref, f"C3 triangle N=768 rows transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("N,padded,sharp", [(96, True, True), (768, False, False)])
+def test_single_attention_with_pair_bias(N, padded, sharp):
+  mod, z, s, seq = W.make_single(N, seed=3, padded=padded, sharp=sharp)
+  hip = _prepared(mod)
+  out = hip(z.to(DEV), s.to(DEV), seq.to(DEV))
+  ref = OM.single_act_update_attention(z.float(), s.float(), seq, _params(hip))
+  assert_close_bf16(out, ref, f"single N={N}")
+  assert_close_bf16(out.float().cpu() - s.float(), ref - s.float(), f"single N={N} update",
+                    max_abs=2e-2 * (ref - s.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("N,S,padded,sharp", [(100, 2, True, True), (1024, 5, False, False)])
+def test_diffusion_token_attention(N, S, padded, sharp):
+  mod, act, cond, bias, mask = W.make_diffusion(N, S=S, seed=4, padded=padded, sharp=sharp)
+  hip = _prepared(mod)
+  out = hip(act.to(DEV), mask.to(DEV), pair_logits=bias.to(DEV), single_cond=cond.to(DEV))
+  ref = OM.self_attention(act.float(), mask, _params(hip), pair_logits=bias.float(), single_cond=cond.float())
+  assert_close_bf16(out, ref, f"diffusion N={N} S={S}")
+  d_ref = ref - act.float()
+  assert_close_bf16(out.float().cpu() - act.float(), d_ref, "diffusion update",
+                    max_abs=2e-2 * d_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False)])
+def test_windowed_atom_attention(atoms, S, sharp):
+  mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5, sharp=sharp)
+  hip = _prepared(mod)
+  out = hip.forward_indexed(act.to(DEV), lay.queries_mask.to(DEV), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV),
+                            lay.keys_mask.to(DEV), qc.to(DEV), kc.to(DEV), bias.to(DEV))
+  ref = OM.windowed_cross_attention(act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask,
+                                    qc.float(), kc.float(), bias.float(), _params(hip))
+  assert_close_bf16(out, ref, f"window atoms={atoms}")
+  d_ref = ref - act.float()
+  assert_close_bf16(out.float().cpu() - act.float(), d_ref, "window update",
+                    max_abs=2e-2 * d_ref.abs().max().item())

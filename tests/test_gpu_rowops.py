@@ -1,0 +1,83 @@
+"""HIP row kernels (LayerNorm / AdaLN, linear epilogues, pair logits, window gather) vs
+float32 torch on the same bf16 inputs."""
+import pytest
+import torch
+
+from oracle.modules import atom_layout_convert
+from oracle.primitives import layer_norm as oracle_ln
+from sparsefold_amd.backends.hip import ops
+from sparsefold_amd import workloads as W
+from tests._metrics import assert_close_bf16, bf16_round
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("M,C", [(1, 8), (37, 128), (300, 384), (65, 768), (9, 2048)])
+def test_layer_norm_affine(M, C):
+  g = torch.Generator().manual_seed(M + C)
+  x = (torch.randn(M, C, generator=g) * 2 + 0.5).to(torch.bfloat16)
+  w, b = 1 + 0.1 * torch.randn(C, generator=g), 0.1 * torch.randn(C, generator=g)
+  out = ops.layer_norm(x.to(DEV), w.to(DEV), b.to(DEV))
+  ref = oracle_ln(x.float(), w, b)
+  assert_close_bf16(out, ref, f"layer_norm {M}x{C}")
+
+
+def test_layer_norm_adaptive_rows_broadcast():
+  g = torch.Generator().manual_seed(3)
+  x = torch.randn(3, 50, 64, generator=g).to(torch.bfloat16)
+  scale = torch.rand(50, 64, generator=g).to(torch.bfloat16)
+  shift = torch.randn(50, 64, generator=g).to(torch.bfloat16)
+  out = ops.layer_norm(x.to(DEV), scale=scale.to(DEV), shift=shift.to(DEV))
+  ref = oracle_ln(x.float(), None, None) * scale.float() + shift.float()
+  assert_close_bf16(out, ref, "adaln")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (100, 96, 128), (257, 516, 128), (1030, 384, 384), (64, 3072, 768)])
+def test_linear_plain(M, N, K):
+  g = torch.Generator().manual_seed(M * 7 + N)
+  x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+  w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+  out = ops.linear(x.to(DEV), w.to(DEV))
+  ref = x.float() @ w.float().t()
+  assert_close_bf16(out, ref, f"linear {M}x{N}x{K}")
+
+
+def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns():
+  g = torch.Generator().manual_seed(9)
+  M, N, K = 300, 72, 64
+  x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+  w = (torch.randn(N, K, generator=g) / 8).to(torch.bfloat16)
+  bias = torch.randn(N, generator=g)
+  mul = torch.randn(100, N, generator=g).to(torch.bfloat16)
+  res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+  yt = torch.empty(8, M, dtype=torch.bfloat16, device=DEV)
+  out = ops.linear(x.to(DEV), w.to(DEV), bias.to(DEV), post_sigmoid=True, mul=mul.to(DEV), residual=res.to(DEV),
+                   yt=yt, tcol0=64)
+  pre = torch.sigmoid(x.float() @ w.float().t() + bias)
+  ref = pre * mul.float().repeat(3, 1) + res.float()
+  assert_close_bf16(out, ref, "linear epilogue")
+  assert_close_bf16(yt, ref[:, 64:72].t(), "linear transposed columns")
+  y2 = ops.linear(x.to(DEV), w.to(DEV), ycols=64)
+  assert y2.shape == (M, 64)
+  assert_close_bf16(y2, x.float() @ w.float()[:64].t(), "linear ycols")
+
+
+@pytest.mark.parametrize("H,C,with_b", [(4, 128, True), (16, 128, True), (12, 16, False), (64, 128, False)])
+def test_pair_logits(H, C, with_b):
+  g = torch.Generator().manual_seed(H * C)
+  z = torch.randn(33, 40, C, generator=g).to(torch.bfloat16)
+  lw, lb = 1 + 0.1 * torch.randn(C, generator=g), 0.1 * torch.randn(C, generator=g)
+  w = (torch.randn(H, C, generator=g) / C ** 0.5).to(torch.bfloat16)
+  out = ops.pair_logits(z.to(DEV), lw.to(DEV), lb.to(DEV) if with_b else None, w.to(DEV))
+  ref = torch.einsum("abc,hc->hab", oracle_ln(z.float(), lw, lb if with_b else None), w.float()).reshape(H, -1)
+  assert_close_bf16(out, ref, f"pair_logits H={H} C={C}")
+
+
+def test_window_gather_exact():
+  lay = W.window_layout(256, pad=20)
+  g = torch.Generator().manual_seed(4)
+  act = torch.randn(3, 8, 32, 16, generator=g).to(torch.bfloat16)
+  keys = ops.window_gather(act.reshape(3, 256, 16).to(DEV), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV))
+  ref = atom_layout_convert(lay.gather_idxs, lay.gather_mask, (8, 32), act, layout_axes=(-3, -2))
+  assert torch.equal(keys.view(3, 8, 128, 16).cpu(), ref)

@@ -1,0 +1,181 @@
+"""Pins the oracle's module composites (blocks.py / transformer.py restatements)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+from oracle import modules as OM
+from oracle.primitives import cpu_bounded_sigmoid, layer_norm
+from sparsefold_amd import workloads as W
+
+
+def _sd(mod):
+  return W.state_dict_f32(mod)
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("padded", [False, True])
+def test_triangle_matches_brute_force(transpose, padded):
+  mod, z, seq = W.make_triangle(6, C=16, H=2, transpose=transpose, seed=11, sharp=True, dtype=torch.float32)
+  if padded:
+    seq[-2:] = False
+  p = _sd(mod)
+  out = OM.grid_self_attention(z, seq, p, transpose=transpose)
+  ref, upd = brute.grid_self_attention(z.numpy(), seq.numpy(), {k: v.numpy() for k, v in p.items()}, transpose)
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=1e-5)
+  got_upd = OM.grid_self_attention(z, seq, p, transpose=transpose, return_update=True)
+  np.testing.assert_allclose(got_upd.numpy(), upd, rtol=1e-4, atol=1e-5)
+
+
+def test_ending_node_is_starting_node_on_transpose_with_untransposed_bias():
+  mod, z, seq = W.make_triangle(7, C=16, H=2, seed=12, sharp=True, dtype=torch.float32)
+  seq[-1] = False
+  p = _sd(mod)
+  end = OM.grid_self_attention(z, seq, p, transpose=True, return_update=True)
+  x = layer_norm(z, p["act_norm.weight"], p["act_norm.bias"])
+  bias_untransposed = torch.einsum("abc,ch->hab", x, p["pair_bias_projection.weight"])
+  start_rows = OM.grid_self_attention_rows(z.transpose(0, 1).contiguous(), seq, p, transpose=False,
+                                           rows=range(7), bias=bias_untransposed)
+  torch.testing.assert_close(end, start_rows.transpose(0, 1), rtol=1e-5, atol=1e-6)
+  # with the bias rebuilt from z^T (a transposed bias) the identity must fail
+  wrong = OM.grid_self_attention(z.transpose(0, 1).contiguous(), seq, p, transpose=False, return_update=True)
+  assert not torch.allclose(end, wrong.transpose(0, 1), rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_row_chunking_and_row_subsets_are_neutral(transpose):
+  mod, z, seq = W.make_triangle(9, C=16, H=2, transpose=transpose, seed=13, sharp=True, dtype=torch.float32)
+  seq[-3:] = False
+  p = _sd(mod)
+  full = OM.grid_self_attention(z, seq, p, transpose=transpose, return_update=True)
+  chunked = OM.grid_self_attention(z, seq, p, transpose=transpose, chunk_size=4, return_update=True)
+  torch.testing.assert_close(full, chunked, rtol=1e-5, atol=1e-6)
+  rows = [0, 4, 8]
+  sub = OM.grid_self_attention_rows(z, seq, p, transpose=transpose, rows=rows)
+  exp = full[:, rows].transpose(0, 1) if transpose else full[rows]
+  torch.testing.assert_close(sub, exp, rtol=1e-5, atol=1e-6)
+
+
+def test_triangle_zero_output_projection_is_identity():
+  mod, z, seq = W.make_triangle(5, C=16, H=2, seed=14, dtype=torch.float32)
+  p = _sd(mod)
+  p["output_projection.weight"] = torch.zeros_like(p["output_projection.weight"])
+  torch.testing.assert_close(OM.grid_self_attention(z, seq, p, transpose=False), z)
+
+
+def _np(t):
+  return t.detach().double().numpy()
+
+
+def _brute_self_attention(x, mask, p, pair_logits=None, single_cond=None):
+  """transformer.py:306-345 in float64 numpy (independent of the torch restatement)."""
+  x = _np(x)
+  if single_cond is None:
+    h = brute.layer_norm(x, _np(p["layer_norm.layer_norm.weight"]), _np(p["layer_norm.layer_norm.bias"]))
+  else:
+    c = brute.layer_norm(_np(single_cond), _np(p["layer_norm.single_cond_layer_norm.weight"]))
+    scale = brute.sigmoid(c @ _np(p["layer_norm.single_cond_scale.weight"]) + _np(p["layer_norm.single_cond_scale.bias"]))
+    h = scale * brute.layer_norm(x) + c @ _np(p["layer_norm.single_cond_bias.weight"])
+  wq = _np(p["q_projection.weight"])
+  q = np.einsum("...c,chd->...hd", h, wq) + _np(p["q_projection.bias"])
+  k = np.einsum("...c,chd->...hd", h, _np(p["k_projection.weight"]))
+  v = np.einsum("...c,chd->...hd", h, _np(p["v_projection.weight"]))
+  lead = x.shape[:-2]
+  B = int(np.prod(lead)) if lead else 1
+  N, H, D = q.shape[-3:]
+  bias = None
+  if pair_logits is not None:
+    bias = np.broadcast_to(_np(pair_logits), lead + (H, N, N)).reshape(B, H, N, N)
+  mk = np.broadcast_to(mask.numpy(), lead + (N,)).reshape(B, N)
+  o = brute.attention(q.reshape(B, N, H, D), k.reshape(B, N, H, D), v.reshape(B, N, H, D), None, None, mk, bias)
+  o = o.reshape(lead + (N, H * D)) * brute.sigmoid(h @ _np(p["gating_query.weight"]))
+  out = o @ _np(p["zero_init.transition2.weight"])
+  if single_cond is not None:
+    out = out * brute.sigmoid(_np(single_cond) @ _np(p["zero_init.adaptive_zero_cond.weight"])
+                              + _np(p["zero_init.adaptive_zero_cond.bias"]))
+  return x + out
+
+
+@pytest.mark.parametrize("cond", [False, True])
+def test_self_attention_matches_brute_force(cond):
+  if cond:
+    mod, act, c, bias, mask = W.make_diffusion(6, S=2, C=16, C_cond=8, H=2, seed=21, sharp=True, dtype=torch.float32)
+    mask[-1] = False
+  else:
+    mod_s, z, s, mask = W.make_single(6, C_s=16, C_z=8, H=2, seed=22, sharp=True, dtype=torch.float32)
+    mod, act, c = mod_s.single_attention, s, None
+    bias = torch.randn(2, 6, 6, generator=torch.Generator().manual_seed(5))
+  p = _sd(mod)
+  out = OM.self_attention(act, mask, p, pair_logits=bias, single_cond=c)
+  ref = _brute_self_attention(act, mask, p, pair_logits=bias, single_cond=c)
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=1e-5)
+
+
+def test_adaln_without_condition_is_layer_norm_and_zero_gate_is_identity():
+  mod, act, c, bias, mask = W.make_diffusion(5, S=1, C=16, C_cond=8, H=2, seed=23, dtype=torch.float32)
+  p = _sd(mod)
+  x = torch.randn(3, 16)
+  pp = {"layer_norm.weight": torch.ones(16), "layer_norm.bias": torch.zeros(16)}
+  torch.testing.assert_close(OM.adaptive_layer_norm(x, None, pp, "", None),
+                             torch.nn.functional.layer_norm(x, (16,)))
+  p["zero_init.adaptive_zero_cond.weight"] = torch.zeros_like(p["zero_init.adaptive_zero_cond.weight"])
+  p["zero_init.adaptive_zero_cond.bias"] = torch.full_like(p["zero_init.adaptive_zero_cond.bias"], -1e4)
+  torch.testing.assert_close(OM.self_attention(act, mask, p, pair_logits=bias, single_cond=c), act)
+
+
+def test_single_act_update_pair_logits():
+  mod, z, s, seq = W.make_single(5, C_s=16, C_z=8, H=2, seed=24, dtype=torch.float32)
+  p = _sd(mod)
+  pl = OM.pair_logits_from_pair(z, p["single_pair_logits_norm.weight"], p["single_pair_logits_norm.bias"],
+                                p["single_pair_logits_projection.weight"])
+  x = brute.layer_norm(z.numpy(), p["single_pair_logits_norm.weight"].numpy(), p["single_pair_logits_norm.bias"].numpy())
+  ref = np.einsum("abc,ch->hab", x, p["single_pair_logits_projection.weight"].numpy())
+  np.testing.assert_allclose(pl.numpy(), ref, rtol=1e-4, atol=1e-5)
+  sub = {k[len("single_attention."):]: v for k, v in p.items() if k.startswith("single_attention.")}
+  torch.testing.assert_close(OM.single_act_update_attention(z, s, seq, p),
+                             OM.self_attention(s, seq, sub, pair_logits=pl))
+
+
+def test_windowed_attention_equals_dense_masked_attention():
+  """Window attention over gathered keys == attention over all atoms with a mask that keeps
+  exactly the window's keys (window keys are distinct atoms, so the sets coincide)."""
+  mod, act, lay, qc, kc, bias = W.make_window(128, S=2, C=16, H=2, pad=20, seed=25, sharp=True, dtype=torch.float32)
+  p = _sd(mod)
+  win = OM.windowed_cross_attention(act, lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc, kc,
+                                    bias, p, return_update=True)
+  U = 4
+  atoms = act.reshape(2, 128, 16)
+  kcond_all = torch.zeros(128, 16)
+  bias_all = torch.zeros(U, 2, 32, 128)
+  mask_all = torch.zeros(U, 128, dtype=torch.bool)
+  for u in range(U):
+    for j in range(128):
+      if lay.gather_mask[u, j]:
+        a = int(lay.gather_idxs[u, j])
+        kcond_all[a] = kc[u, j]          # the per-key conditioning depends on the atom only here
+        bias_all[u, :, :, a] = bias[u, :, :, j]
+        mask_all[u, a] = bool(lay.keys_mask[u, j])
+  kc_win = OM.atom_layout_convert(lay.gather_idxs, lay.gather_mask, (U, 32), kcond_all.view(U, 32, 16), layout_axes=(0, 1))
+  win2 = OM.windowed_cross_attention(act, lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc, kc_win,
+                                     bias, p, return_update=True)
+  dense = OM.cross_attention(act, atoms[:, None].expand(2, U, 128, 16), lay.queries_mask, mask_all, p,
+                             pair_logits=bias_all, single_cond_q=qc,
+                             single_cond_k=kcond_all[None].expand(U, 128, 16), return_update=True)
+  valid_q = lay.queries_mask[None, :, :, None].expand_as(dense)
+  torch.testing.assert_close(win2[valid_q], dense[valid_q], rtol=1e-4, atol=1e-5)
+  assert win.shape == dense.shape
+
+
+def test_bounded_sigmoid_closed_form():
+  x = torch.linspace(-30, 30, 2001)
+  s = cpu_bounded_sigmoid(x)
+  assert (s - torch.sigmoid(x)).abs().max() < 5e-6          # far below a bf16 ulp (~4e-3 at 1)
+  assert s[0] == cpu_bounded_sigmoid(torch.tensor(-20.0)) and s[-1] == cpu_bounded_sigmoid(torch.tensor(20.0))
+  torch.testing.assert_close(cpu_bounded_sigmoid(torch.zeros(1)), torch.full((1,), 0.5))
+
+
+def test_layer_norm_matches_numpy():
+  x = torch.randn(4, 33, generator=torch.Generator().manual_seed(7)) * 3 + 1
+  w, b = torch.randn(33), torch.randn(33)
+  np.testing.assert_allclose(layer_norm(x, w, b).numpy(), brute.layer_norm(x.numpy(), w.numpy(), b.numpy()),
+                             rtol=1e-5, atol=1e-5)
