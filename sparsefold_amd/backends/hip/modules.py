@@ -124,7 +124,8 @@ def _prepare_zero_init(module: torch.nn.Module, zi: base.AdaptiveZeroInit) -> No
     _buf(module, "_hip_b_zc", _f32(zi.adaptive_zero_cond.bias))
 
 
-def _zero_init_residual(module, o: torch.Tensor, cond: torch.Tensor | None, residual: torch.Tensor) -> torch.Tensor:
+def _zero_init_residual(module, o: torch.Tensor, cond: torch.Tensor | None, residual: torch.Tensor | None) -> torch.Tensor:
+  """AdaLN-zero output (transformer.py:138-154) plus the caller's residual add, one GEMM."""
   mul = None
   if cond is not None:
     mul = ops.linear(cond, module._hip_w_zc, module._hip_b_zc, post_sigmoid=True)
@@ -157,7 +158,7 @@ class SelfAttentionHipMixin:
 
   @_require_native_preparation
   def forward(self, x: torch.Tensor, mask: torch.Tensor, *, pair_logits: torch.Tensor | None = None,
-              single_cond: torch.Tensor | None = None) -> torch.Tensor:
+              single_cond: torch.Tensor | None = None, add_residual: bool = True) -> torch.Tensor:
     H, D = self.num_head, self.key_dim
     HD = H * D
     lead, N = x.shape[:-2], x.shape[-2]
@@ -166,7 +167,7 @@ class SelfAttentionHipMixin:
     q, k, v, g = (y[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D)) for i in range(4))
     o = dot_product_attention(q, k, v, mask_k=mask, bias=pair_logits, gate=g)
     o = o.reshape(*lead, N, HD)
-    return _zero_init_residual(self, o, single_cond, x).to(x.dtype)
+    return _zero_init_residual(self, o, single_cond, x if add_residual else None).to(x.dtype)
 
 
 # ---------------------------------------------------------------------------------------
@@ -197,7 +198,7 @@ class CrossAttentionHipMixin:
   @_require_native_preparation
   def forward(self, x_q: torch.Tensor, x_k: torch.Tensor, mask_q: torch.Tensor, mask_k: torch.Tensor,
               pair_logits: torch.Tensor | None = None, single_cond_q: torch.Tensor | None = None,
-              single_cond_k: torch.Tensor | None = None) -> torch.Tensor:
+              single_cond_k: torch.Tensor | None = None, *, add_residual: bool = True) -> torch.Tensor:
     H, D = self.num_head, self.key_dim
     HD = H * D
     hq = _adaln(self, "_hip_adq_", x_q, single_cond_q)
@@ -208,12 +209,13 @@ class CrossAttentionHipMixin:
     k, v = yk[..., :HD].unflatten(-1, (H, D)), yk[..., HD:].unflatten(-1, (H, D))
     o = dot_product_attention(q, k, v, mask_q=mask_q, mask_k=mask_k, bias=pair_logits, gate=g)
     o = o.reshape(*o.shape[:-2], HD)
-    return _zero_init_residual(self, o, single_cond_q, x_q).to(x_q.dtype)
+    return _zero_init_residual(self, o, single_cond_q, x_q if add_residual else None).to(x_q.dtype)
 
   @_require_native_preparation
   def forward_indexed(self, queries_act: torch.Tensor, queries_mask: torch.Tensor, gather_idxs: torch.Tensor,
                       gather_mask: torch.Tensor, keys_mask: torch.Tensor, queries_single_cond: torch.Tensor,
-                      keys_single_cond: torch.Tensor, pair_logits: torch.Tensor | None = None) -> torch.Tensor:
+                      keys_single_cond: torch.Tensor, pair_logits: torch.Tensor | None = None, *,
+                      add_residual: bool = True) -> torch.Tensor:
     """CrossAttTransformer block attention (transformer.py:668-682): keys are gathered from
     the queries by ``queries_to_keys`` (flat index over ``[U, Qw]``, masked -> 0)."""
     lead = queries_act.shape[:-3]
@@ -224,7 +226,7 @@ class CrossAttentionHipMixin:
     keys = ops.window_gather(queries_act.reshape(S, U * Qw, Cn), gather_idxs, gather_mask)
     keys = keys.view(*lead, U, gather_idxs.shape[-1], Cn)
     return self.forward(queries_act, keys, queries_mask, keys_mask, pair_logits, queries_single_cond,
-                        keys_single_cond)
+                        keys_single_cond, add_residual=add_residual)
 
 
 # ---------------------------------------------------------------------------------------
@@ -245,13 +247,14 @@ class SingleActUpdateHipMixin:
     return True
 
   @_require_native_preparation
-  def forward(self, pair_act: torch.Tensor, single_act: torch.Tensor, seq_mask: torch.Tensor) -> torch.Tensor:
+  def forward(self, pair_act: torch.Tensor, single_act: torch.Tensor, seq_mask: torch.Tensor, *,
+              add_residual: bool = True) -> torch.Tensor:
     N = pair_act.shape[-2]
     pl = ops.pair_logits(pair_act, self._hip_pl_ln_w, self._hip_pl_ln_b, self._hip_pl_w)
     pl = pl.view(self.num_head, *pair_act.shape[:-1])                   # [H, B, N]
-    out = self.single_attention(single_act, seq_mask, pair_logits=pl)
+    out = self.single_attention(single_act, seq_mask, pair_logits=pl, add_residual=add_residual)
     transition = getattr(self, "single_transition", None)
-    if transition is not None:                                          # reference transition, when present
+    if transition is not None and add_residual:                         # reference transition, when present
       out = transition(out, broadcast_dim=None)
     assert out.shape[-2] == N
     return out

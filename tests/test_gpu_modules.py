@@ -97,31 +97,39 @@ def test_single_attention_with_pair_bias(N, padded, sharp):
   out = hip(z.to(DEV), s.to(DEV), seq.to(DEV))
   ref = OM.single_act_update_attention(z.float(), s.float(), seq, _params(hip))
   assert_close_bf16(out, ref, f"single N={N}")
-  assert_close_bf16(out.float().cpu() - s.float(), ref - s.float(), f"single N={N} update",
-                    max_abs=2e-2 * (ref - s.float()).abs().max().item())
+  upd = hip(z.to(DEV), s.to(DEV), seq.to(DEV), add_residual=False)
+  d_ref = OM.single_act_update_attention(z.float(), s.float(), seq, _params(hip), return_update=True)
+  assert_close_bf16(upd, d_ref, f"single N={N} update", max_abs=2e-2 * d_ref.abs().max().item())
 
 
 @pytest.mark.parametrize("N,S,padded,sharp", [(100, 2, True, True), (1024, 5, False, False)])
 def test_diffusion_token_attention(N, S, padded, sharp):
   mod, act, cond, bias, mask = W.make_diffusion(N, S=S, seed=4, padded=padded, sharp=sharp)
   hip = _prepared(mod)
-  out = hip(act.to(DEV), mask.to(DEV), pair_logits=bias.to(DEV), single_cond=cond.to(DEV))
-  ref = OM.self_attention(act.float(), mask, _params(hip), pair_logits=bias.float(), single_cond=cond.float())
+  args = (act.to(DEV), mask.to(DEV))
+  kw = dict(pair_logits=bias.to(DEV), single_cond=cond.to(DEV))
+  out = hip(*args, **kw)
+  p = _params(hip)
+  ref = OM.self_attention(act.float(), mask, p, pair_logits=bias.float(), single_cond=cond.float())
   assert_close_bf16(out, ref, f"diffusion N={N} S={S}")
-  d_ref = ref - act.float()
-  assert_close_bf16(out.float().cpu() - act.float(), d_ref, "diffusion update",
-                    max_abs=2e-2 * d_ref.abs().max().item())
+  upd = hip(*args, **kw, add_residual=False)
+  d_ref = OM.self_attention(act.float(), mask, p, pair_logits=bias.float(), single_cond=cond.float(),
+                            return_update=True)
+  assert_close_bf16(upd, d_ref, "diffusion update", max_abs=2e-2 * d_ref.abs().max().item())
 
 
 @pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False)])
 def test_windowed_atom_attention(atoms, S, sharp):
   mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5, sharp=sharp)
   hip = _prepared(mod)
-  out = hip.forward_indexed(act.to(DEV), lay.queries_mask.to(DEV), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV),
-                            lay.keys_mask.to(DEV), qc.to(DEV), kc.to(DEV), bias.to(DEV))
-  ref = OM.windowed_cross_attention(act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask,
-                                    qc.float(), kc.float(), bias.float(), _params(hip))
+  args = (act.to(DEV), lay.queries_mask.to(DEV), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV),
+          lay.keys_mask.to(DEV), qc.to(DEV), kc.to(DEV), bias.to(DEV))
+  out = hip.forward_indexed(*args)
+  p = _params(hip)
+  oargs = (act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc.float(), kc.float(),
+           bias.float(), p)
+  ref = OM.windowed_cross_attention(*oargs)
   assert_close_bf16(out, ref, f"window atoms={atoms}")
-  d_ref = ref - act.float()
-  assert_close_bf16(out.float().cpu() - act.float(), d_ref, "window update",
-                    max_abs=2e-2 * d_ref.abs().max().item())
+  upd = hip.forward_indexed(*args, add_residual=False)
+  d_ref = OM.windowed_cross_attention(*oargs, return_update=True)
+  assert_close_bf16(upd, d_ref, "window update", max_abs=2e-2 * d_ref.abs().max().item())
