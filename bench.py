@@ -59,29 +59,24 @@ def _events_time(fn, iters: int, stream) -> float:
   return start.elapsed_time(end) / iters
 
 
-def attention_core_ms(z, seq, mod, iters: int) -> float:
-  """Average duration of the attention kernel alone, launched exactly as the triangle module
-  launches it (same strides, shared bias planes, masks), timed with HIP events."""
+def stage_ms(z, seq, mod, iters: int) -> dict:
+  """Average duration of each triangle stage (projection, attention core, output projection),
+  launched through sf_hip_triangle_stage_fwd on the current stream and timed with HIP events
+  recorded on that same stream."""
+  from sparsefold_amd import _lib
   from sparsefold_amd.backends.hip import ops
-  HD = H * D
-  x = ops.layer_norm(z, mod._hip_ln_w, mod._hip_ln_b)
-  bias = torch.empty(H, N * N, dtype=torch.bfloat16, device=z.device)
-  y = ops.linear(x, mod._hip_w_qkvgb, ycols=4 * HD, yt=bias, tcol0=4 * HD)        # [N, N, 4HD]
-  y5 = y.view(N, 1, N, 4 * HD)
-
-  def view(i):
-    return y5[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D))
-
-  q, k, v, g = view(0), view(1), view(2), view(3)
-  b5 = bias.view(1, 1, H, N, N).expand(N, 1, H, N, N)
-  m8 = seq.to(torch.uint8)
-  mq = m8.view(N, 1, 1).expand(N, 1, N)
-  mk = m8.view(1, 1, N).expand(N, 1, N)
-  out = torch.empty(N, 1, N, H, D, dtype=torch.bfloat16, device=z.device)
-  fn = lambda: ops.attention(q, k, v, scale=1 / math.sqrt(D), bias=b5, mask_q=mq, mask_k=mk, gate=g, out=out)
-  fn()
+  ws = torch.empty(ops.triangle_workspace_bytes(N, C, H, D), dtype=torch.uint8, device=z.device)
+  out = torch.empty_like(z)
+  args = (z, seq, mod._hip_ln_w, mod._hip_ln_b, mod._hip_w_qkvgb, mod._hip_w_o)
+  kw = dict(num_head=H, transpose=False, workspace=ws, out=out)
+  ops.triangle_attention(*args, **kw, stages=_lib.TRI_STAGE_ALL)
   torch.cuda.synchronize()
-  return _events_time(fn, iters, torch.cuda.current_stream())
+  res = {}
+  for name, st in (("project", _lib.TRI_STAGE_PROJECT), ("attend", _lib.TRI_STAGE_ATTEND),
+                   ("output", _lib.TRI_STAGE_OUTPUT)):
+    res[name] = _events_time(lambda: ops.triangle_attention(*args, **kw, stages=st), iters,
+                             torch.cuda.current_stream())
+  return res
 
 
 def cpu_baseline(rows: int) -> dict:
@@ -137,12 +132,14 @@ def main():
   torch.cuda.synchronize()
   ms = _events_time(lambda: mod(z, seq), args.steps, stream)
   torch.cuda.synchronize()
-  core_ms = attention_core_ms(z, seq, mod, max(args.steps, 10))
+  stages = stage_ms(z, seq, mod, max(args.steps, 10))
+  core_ms = stages["attend"]
   flop = module_flop()
   tflops = flop / (ms * 1e-3) / 1e12
   core_tflops = core_flop() / (core_ms * 1e-3) / 1e12
-  print(f"[bench] module {ms:.3f} ms ({tflops:.1f} TFLOP/s); attention kernel {core_ms:.3f} ms "
-        f"({core_tflops:.1f} TFLOP/s)", flush=True)
+  print(f"[bench] module {ms:.3f} ms ({tflops:.1f} TFLOP/s); stages "
+        + ", ".join(f"{k} {v:.3f} ms" for k, v in stages.items())
+        + f"; attention core {core_tflops:.1f} TFLOP/s", flush=True)
   cpu = None
   if args.cpu_baseline:
     print("[bench] timing host-CPU math path sample...", flush=True)
@@ -164,7 +161,8 @@ def main():
       "config": {"workload": "triangle attention, starting node, N=768, C=128, H=4, D=32, all-ones mask",
                  "module_flop": flop, "tflops": round(tflops, 2),
                  "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2)},
-      "roofline": {"bound": "mfma", "kernel": "attention_fwd_kernel", "achieved": round(core_tflops, 2),
+      "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+      "roofline": {"bound": "mfma", "kernel": "tri_attn_kernel", "achieved": round(core_tflops, 2),
                    "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(core_tflops / PEAK_BF16_TFLOPS, 4),
                    "traffic": None, "kernel_ms": round(core_ms, 4), "flop_per_launch": core_flop()},
       "cpu_baseline": cpu,

@@ -138,6 +138,21 @@ size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t 
 int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* The same module as separate stages sharing one workspace (head dim 32 path), mirroring the
+ * reference's projection / attention split of the row-sharded triangle attention
+ * (backends/vecops/kernels/registry.py:1236-1309, grid_distributed_projection and
+ * grid_distributed_attention):
+ *   SF_TRI_STAGE_PROJECT  LN + q/k/v/g/bias projections into the workspace
+ *   SF_TRI_STAGE_ATTEND   attention core + sigmoid gate (reads the projected operands)
+ *   SF_TRI_STAGE_OUTPUT   output projection (+ residual) into out
+ * Stages run in that order when several bits are set; sf_hip_triangle_attn_fwd == all three. */
+#define SF_TRI_STAGE_PROJECT 1
+#define SF_TRI_STAGE_ATTEND 2
+#define SF_TRI_STAGE_OUTPUT 4
+#define SF_TRI_STAGE_ALL 7
+int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Pair logits: out[h, p] = (LN(z[p,:]) W)[h] for H <= 64 planes; z bf16 [P, C] contiguous
  * (C <= 128, C % 8 == 0), ln_w/ln_b f32 [C] (either may be NULL), w_t bf16 [H, C],

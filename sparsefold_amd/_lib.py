@@ -11,6 +11,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
 ABI_VERSION = 1
+TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 _u8p = C.POINTER(C.c_uint8)
@@ -101,6 +102,7 @@ SIGNATURES = [
     ("sf_hip_linear_fwd", C.c_int, [C.POINTER(LinearArgs), _vp]),
     ("sf_hip_triangle_workspace_bytes", C.c_size_t, [_i32, _i32, _i32, _i32]),
     ("sf_hip_triangle_attn_fwd", C.c_int, [C.POINTER(TriangleArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_triangle_stage_fwd", C.c_int, [C.POINTER(TriangleArgs), _i32, _vp, C.c_size_t, _vp]),
     ("sf_hip_pair_logits_fwd", C.c_int, [C.POINTER(PairLogitsArgs), _vp]),
     ("sf_hip_window_gather_fwd", C.c_int, [C.POINTER(WindowGatherArgs), _vp]),
 ]

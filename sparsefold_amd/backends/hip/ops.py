@@ -225,8 +225,11 @@ def triangle_workspace_bytes(N: int, C_: int, H: int, D: int) -> int:
 
 def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qkvgb: torch.Tensor,
                        w_o: torch.Tensor, *, num_head: int, transpose: bool, add_residual: bool = True,
-                       workspace: torch.Tensor | None = None) -> torch.Tensor:
-  """GridSelfAttention on ``z [N, N, C]`` (bf16).  Weights packed as the C ABI documents."""
+                       workspace: torch.Tensor | None = None, stages: int = _lib.TRI_STAGE_ALL,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+  """GridSelfAttention on ``z [N, N, C]`` (bf16).  Weights packed as the C ABI documents.
+  ``stages`` selects a subset of the pipeline (projection / attention / output projection)
+  against a caller-held ``workspace``."""
   _require_cuda(z, seq_mask, ln_w, ln_b, w_qkvgb, w_o, workspace)
   _require(z.ndim == 3 and z.shape[0] == z.shape[1], f"triangle: z must be [N, N, C], got {tuple(z.shape)}")
   N, _, Cn = z.shape
@@ -242,14 +245,18 @@ def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qk
   need = triangle_workspace_bytes(N, Cn, num_head, D)
   if workspace is None or workspace.numel() < need:
     workspace = torch.empty(need, dtype=torch.uint8, device=z.device)
-  out = torch.empty_like(zc)
+  if out is None:
+    out = torch.empty_like(zc)
   a = _lib.TriangleArgs()
   a.N, a.C, a.H, a.D = N, Cn, num_head, D
   a.transpose, a.add_residual = int(bool(transpose)), int(bool(add_residual))
   a.z, a.seq_mask, a.ln_w, a.ln_b = _vp(zc), _vp(m8), _vp(lw), _vp(lb)
   a.w_qkvgb, a.w_o, a.out = _vp(w_qkvgb), _vp(w_o), _vp(out)
-  _lib.check(_lib.load().sf_hip_triangle_attn_fwd(C.byref(a), _vp(workspace), workspace.numel(), _stream(z)),
-             "sf_hip_triangle_attn_fwd")
+  if stages == _lib.TRI_STAGE_ALL:
+    rc = _lib.load().sf_hip_triangle_attn_fwd(C.byref(a), _vp(workspace), workspace.numel(), _stream(z))
+  else:
+    rc = _lib.load().sf_hip_triangle_stage_fwd(C.byref(a), stages, _vp(workspace), workspace.numel(), _stream(z))
+  _lib.check(rc, "sf_hip_triangle_attn_fwd")
   return out
 
 
