@@ -12,11 +12,14 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
 
 #define SF_LOG2E 1.4426950408889634f
 // Logit (log2 domain) of a masked key.  Finite, so a query whose keys are all masked
 // sees identical logits and weighs every key equally -- the reference's -finfo.max rule.
-#define SF_MASKED_LOGIT (-1.0e30f)
+// -2^99: exact in bf16 and fp32, and any |q.k| logit is absorbed when added to it.
+#define SF_MASKED_LOGIT (-6.338253001141147e29f)
 
 __device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {
@@ -27,6 +30,16 @@ __device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 
 __device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Two floats -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ bf16x2 cvt_bf2(float lo, float hi) {
+  return __builtin_convertvector(f32x2{lo, hi}, bf16x2);
+}
+// acc + lo + hi of a packed bf16 pair, fp32 accumulation (v_dot2c_f32_bf16 against ones).
+__device__ __forceinline__ float add_bf2(bf16x2 v, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
 }
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

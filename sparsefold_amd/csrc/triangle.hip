@@ -4,15 +4,17 @@
 // per-chunk _attention of :270-291).
 //
 // Fast path (head dim 32, the trunk's C=128 / H=4 configuration), three kernels:
-//   1. tri_proj_kernel   one workgroup per (attention row r, 128 positions): LN(z) in LDS
-//                        (blocks.py:317), then one MFMA GEMM against [Wq|Wk|Wv|Wg|Wb]
-//                        (blocks.py:276-278, :286, :320) whose epilogue writes every operand
-//                        in the layout the attention kernel consumes:
+//   1. tri_proj_kernel   persistent workgroups with [Wq|Wk|Wv|Wg|Wb] resident in LDS (LN gamma
+//                        folded into the weight, beta into a per-column offset); each wave
+//                        normalises 32 positions of an attention row straight into MFMA
+//                        operand registers (blocks.py:317) and runs the projections
+//                        (blocks.py:276-278, :286, :320), writing every operand in the layout
+//                        the attention kernel consumes:
 //                          Qs  [r][i][h][d]  q * scale * log2(e)   (logits land in log2 units)
 //                          Ks  [r][j][h][d]
 //                          Vt  [r][h][d][j'] V transposed, keys in PV-MFMA slot order
 //                          Gs  [r][i][h][d]  gate logits
-//                          Bs  [h][i][j'']   bias * log2(e) in the untransposed orientation
+//                          Bs  [h][i][j'']   bias * log2(e), fp32, in the untransposed orientation
 //                                            (blocks.py:329), masked keys = SF_MASKED_LOGIT,
 //                                            keys past N = -inf, keys in S^T register order
 //                        For the ending node the workgroup walks z's column instead of its row,
@@ -23,7 +25,7 @@
 //                        -- identical for every row -- as the accumulator input of the S^T MFMA,
 //                        so bias loads and conversion are paid once per 4 rows; sigmoid gate in
 //                        the epilogue, output written at its pair position.
-//   3. linear_kernel     out = z + o W_o (blocks.py:291, :366).
+//   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
 
@@ -47,7 +49,8 @@ __host__ __device__ inline int v_pos64(int j) {
 }
 
 struct FastWs {
-  uint16_t *q, *k, *vt, *g, *bias, *o;
+  uint16_t *q, *k, *vt, *g, *o;
+  float* bias;
   size_t bytes;
 };
 
@@ -60,7 +63,7 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.k = (uint16_t*)(p + off); off += round_up(E * 2);
   w.vt = (uint16_t*)(p + off); off += round_up(E * 2);
   w.g = (uint16_t*)(p + off); off += round_up(E * 2);
-  w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
+  w.bias = (float*)(p + off); off += round_up(NP * NP * H * 4);
   w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
   w.bytes = off;
   return w;
@@ -70,128 +73,194 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
 // 1. LN + projection
 // ---------------------------------------------------------------------------------------
 struct TriProjArgs {
-  int N, NP, C, H, transpose;
+  int N, NP, H, transpose;
   float qscale;                       // softmax scale * log2(e)
   const uint16_t* z; const uint8_t* seq;
   const float* ln_w; const float* ln_b;
   const uint16_t* w;                  // [4*H*32 + H, C]
-  uint16_t *q, *k, *vt, *g, *bias;
+  uint16_t *q, *k, *vt, *g;
+  float* bias;
+  int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
 
-constexpr int kPB = 128;              // positions per projection workgroup
 constexpr int kPC = 128;              // channels (C) handled by the fast path
-constexpr int kXP = kPC + 8;          // LDS pitch (elements) of the normalised tile / weight tile
+constexpr int kWP = kPC + 8;          // LDS pitch (elements) of weight rows
+constexpr int kPWaves = 8;            // waves per projection / output workgroup
+constexpr int kPCols = 17 * 32;       // q k v g (4 x 128) + bias block (32, 4 used)
 
-__global__ __launch_bounds__(256) void tri_proj_kernel(const TriProjArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sX[kPB * kXP];
-  __shared__ __attribute__((aligned(16))) uint16_t sW[128 * kXP];
+// LN of the 32 positions of a block, straight into MFMA operand registers: lane (li, half)
+// holds channels 16*kk + 8*half .. +7 of position li for kk = 0..7 -- the same registers serve
+// as A operand (rows = positions) and as B operand (columns = positions).
+__device__ __forceinline__ void ln_operands(const u32x4 (&x)[8], bool valid, bf16x8 (&xo)[8]) {
+  float sum = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
+  sum += __shfl_xor(sum, 32);
+  const float mean = sum * (1.0f / kPC);
+  float sq = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
+      sq += d0 * d0 + d1 * d1;
+    }
+  sq += __shfl_xor(sq, 32);
+  const float rstd = valid ? rsqrtf(sq * (1.0f / kPC) + 1e-5f) : 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd, (bfhi(x[kk][e]) - mean) * rstd);
+      xo[kk][2 * e] = v[0];
+      xo[kk][2 * e + 1] = v[1];
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// 1. LN + projection.  Persistent: each workgroup keeps the packed weight (gamma folded in,
+//    beta folded into a per-column offset) in LDS and walks 32-position blocks; positions of
+//    attention row r are z[r, p] (starting node) or z[p, r] (ending node).
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[kPCols * kWP];
+  __shared__ float sOff[kPCols];                        // beta . W per output column
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
-  const int r = blockIdx.y, p0 = blockIdx.x * kPB;
   const int N = a.N, NP = a.NP, H = a.H;
-  const int HD = H * 32;
+  const int HD = H * 32;                                // 128
+  const int nrows = 4 * HD + H;                         // 516 valid weight rows
 
-  // ---- LN of 128 positions; two threads per position, 64 channels each ----
-  {
-    const int pl = tid >> 1, hc = tid & 1;
-    const int p = p0 + pl;
-    const int za = a.transpose ? p : r, zb = a.transpose ? r : p;
-    const bool valid = za < N && zb < N;
-    u32x4 w[8];
-    float sum = 0.f;
+  for (int t = tid; t < kPCols * (kPC / 8); t += 64 * kPWaves) {
+    const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    u32x4 w = u32x4{0, 0, 0, 0};
+    if (n < nrows) {
+      const u32x4 raw = ld16(a.w + (int64_t)n * kPC + c8);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      w[t] = valid ? ld16(a.z + ((int64_t)za * N + zb) * kPC + 64 * hc + 8 * t) : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sum += bflo(w[t][e]) + bfhi(w[t][e]);
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf2(bflo(raw[e]) * a.ln_w[c8 + 2 * e], bfhi(raw[e]) * a.ln_w[c8 + 2 * e + 1]);
     }
-    sum += __shfl_xor(sum, 1);
-    const float mean = sum * (1.0f / kPC);
-    float sq = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float d0 = bflo(w[t][e]) - mean, d1 = bfhi(w[t][e]) - mean;
-        sq += d0 * d0 + d1 * d1;
-      }
-    sq += __shfl_xor(sq, 1);
-    const float rstd = rsqrtf(sq * (1.0f / kPC) + 1e-5f);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int c0 = 64 * hc + 8 * t;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] = (bflo(w[t][e]) - mean) * rstd;
-        v[2 * e + 1] = (bfhi(w[t][e]) - mean) * rstd;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = v[e] * a.ln_w[c0 + e] + (a.ln_b ? a.ln_b[c0 + e] : 0.f);
-      u32x4 o = u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
-      if (!valid) o = u32x4{0, 0, 0, 0};
-      st16(&sX[pl * kXP + c0], o);
-    }
+    st16(&sW[n * kWP + c8], w);
   }
+  for (int n = tid; n < kPCols; n += 64 * kPWaves) {
+    float off = 0.f;
+    if (n < nrows && a.ln_b != nullptr)
+      for (int c = 0; c < kPC; ++c) off += a.ln_b[c] * bf2f(a.w[(int64_t)n * kPC + c]);
+    sOff[n] = off;
+  }
+  __syncthreads();
 
-  // ---- GEMM over 5 column tiles: q, k, v, g (128 columns each = 4 heads x 32), bias ----
-  for (int nt = 0; nt < 5; ++nt) {
-    const int ncols = nt < 4 ? HD : 32;          // bias tile: H valid rows, rest zero
-    __syncthreads();
-    for (int t = tid; t < ncols * (kPC / 8); t += 256) {
-      const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-      u32x4 w = u32x4{0, 0, 0, 0};
-      if (nt < 4) w = ld16(a.w + (int64_t)(nt * HD + n) * kPC + c8);
-      else if (n < H) w = ld16(a.w + (int64_t)(4 * HD + n) * kPC + c8);
-      st16(&sW[n * kXP + c8], w);
+  const int bpr = NP / 32;                              // position blocks per attention row
+  auto block_load = [&](int item, u32x4 (&x)[8], bool& valid, int& r, int& p) {
+    r = item / bpr;
+    p = (item - r * bpr) * 32 + li;
+    const int za = a.transpose ? p : r, zb = a.transpose ? r : p;
+    valid = za < N && zb < N;
+    const uint16_t* zp = a.z + ((int64_t)(valid ? za : 0) * N + (valid ? zb : 0)) * kPC + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+  };
+
+  const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
+  const int last = min(first + a.items_per_wave, a.items);
+  u32x4 xn[8];
+  bool vn = false;
+  int rn = 0, pn = 0;
+  if (first < last) block_load(first, xn, vn, rn, pn);
+  for (int item = first; item < last; ++item) {
+    bf16x8 xo[8];
+    const bool valid = vn;
+    const int r = rn, p = pn;                            // this lane's position p (= p0 + li)
+    ln_operands(xn, valid, xo);
+    if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
+    const int p0 = p - li;
+
+    // q, k, g: D^T = W . X^T -> lane = position, 4 consecutive columns per register group
+#pragma unroll
+    for (int which = 0; which < 4; ++which) {
+      if (which == 2) continue;
+      uint16_t* dst = which == 0 ? a.q : (which == 1 ? a.k : a.g);
+      const float sc = which == 0 ? a.qscale : 1.0f;
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        const int nb = 4 * which + hh;
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+          acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xo[kk], acc);
+        uint16_t* op = dst + ((int64_t)r * NP + p) * HD + 32 * hh;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int n0 = 8 * c + 4 * half;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = valid ? (acc[4 * c + e] + sOff[32 * nb + n0 + e]) * sc : 0.f;
+          *reinterpret_cast<u32x2*>(op + n0) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        }
+      }
     }
-    __syncthreads();
-    const int nblk = ncols / 32;
-    f32x16 acc[4];
+    // v: D = X . W^T -> lane = column d, 4 consecutive positions -> V^T rows
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int hh = 0; hh < 4; ++hh) {
+      const int nb = 8 + hh;
+      f32x16 acc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[nb][e] = 0.f;
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < kPC / 16; ++kk) {
-      const bf16x8 av = as_bf16x8(ld16(&sX[(32 * wave + li) * kXP + 16 * kk + 8 * half]));
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        if (nb < nblk) acc[nb] = mfma32(av, as_bf16x8(ld16(&sW[(32 * nb + li) * kXP + 16 * kk + 8 * half])), acc[nb]);
-    }
-    // ---- epilogue: lane owns column n = 32*nb + li; rows m = 32*wave + 8*(e/4) + 4*half + e%4 ----
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      if (nb >= nblk) continue;
-      const int n = 32 * nb + li;               // within the tile: head nb, dim li (q/k/v/g)
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
+      const float off = sOff[32 * nb + li];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int pb = p0 + 32 * wave + 8 * c + 4 * half;   // 4 consecutive positions pb..pb+3
-        if (pb >= NP) continue;                              // NP % 4 == 0: all four past the end
+        const int pb = p0 + 8 * c + 4 * half;
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[nb][4 * c + e];
-        if (nt == 0 || nt == 1 || nt == 3) {
-          uint16_t* dst = nt == 0 ? a.q : (nt == 1 ? a.k : a.g);
-          const float sc = nt == 0 ? a.qscale : 1.0f;
+        for (int e = 0; e < 4; ++e) {
+          const int pe = pb + e;
+          const int za = a.transpose ? pe : r, zb = a.transpose ? r : pe;
+          v[e] = (za < N && zb < N) ? acc[4 * c + e] + off : 0.f;
+        }
+        const int64_t base = (((int64_t)r * H + hh) * 32 + li) * NP + (pb & ~63) + v_pos64(pb & 63);
+        *reinterpret_cast<u32x2*>(a.vt + base) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      }
+    }
+    // bias planes: D = X . Wb^T, lane = head li (< H), 4 consecutive positions
+    {
+      const int nb = 16;
+      f32x16 acc;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            dst[((int64_t)r * NP + pb + e) * HD + n] = f2bf(v[e] * sc);
-        } else if (nt == 2) {
-          // V^T[r][h][d][v_pos(p)]: 4 consecutive positions stay contiguous
-          const int64_t base = (((int64_t)r * H + nb) * 32 + li) * NP + (pb & ~63) + v_pos64(pb & 63);
-          *reinterpret_cast<u32x2*>(a.vt + base) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-        } else if (li < H) {
-          // bias plane of head li at untransposed (za, zb)
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
+      if (li < H) {
+        const float off = sOff[4 * HD + li];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int pb = p0 + 8 * c + 4 * half;
+          float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int p = pb + e;
-            const int za = a.transpose ? p : r, zb = a.transpose ? r : p;
-            float b = v[e] * SF_LOG2E;
+            const int pe = pb + e;
+            const int za = a.transpose ? pe : r, zb = a.transpose ? r : pe;
+            float b = (acc[4 * c + e] + off) * SF_LOG2E;
             if (zb >= N) b = -INFINITY;
             else if (za >= N) b = 0.f;
             else if (a.seq[zb] == 0) b = SF_MASKED_LOGIT;
-            a.bias[((int64_t)li * NP + za) * NP + (zb & ~63) + bias_pos64(zb & 63)] = f2bf(b);
+            v[e] = b;
+          }
+          if (!a.transpose) {   // za = r: four consecutive keys of one bias row
+            const int64_t base = ((int64_t)li * NP + r) * NP + (pb & ~63) + bias_pos64(pb & 63);
+            st16(a.bias + base, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                      __float_as_uint(v[3])});
+          } else {              // zb = r: one key of four bias rows
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              a.bias[((int64_t)li * NP + pb + e) * NP + (r & ~63) + bias_pos64(r & 63)] = v[e];
           }
         }
       }
@@ -200,11 +269,75 @@ __global__ __launch_bounds__(256) void tri_proj_kernel(const TriProjArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// 2. attention
+// 3. output projection + residual: out[p] = z[p] + o[p] . W_o^T over the N*N pair positions,
+//    W_o resident in LDS; lane = position, 4 consecutive output channels per register group.
 // ---------------------------------------------------------------------------------------
+struct TriOutArgs {
+  int64_t P;                          // N * N
+  const uint16_t* o;                  // [P, 128]
+  const uint16_t* wo;                 // [128 out, 128 in]
+  const uint16_t* z;                  // residual or nullptr
+  uint16_t* out;
+  int items, items_per_wave;          // 32-position blocks
+};
+
+__global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, li = lane & 31;
+  for (int t = tid; t < kPC * (kPC / 8); t += 64 * kPWaves) {
+    const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    st16(&sW[n * kWP + c8], ld16(a.wo + (int64_t)n * kPC + c8));
+  }
+  __syncthreads();
+  const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
+  const int last = min(first + a.items_per_wave, a.items);
+  auto load = [&](int item, bf16x8 (&x)[8], int64_t& p) {
+    p = (int64_t)item * 32 + li;
+    const bool ok = p < a.P;
+    const uint16_t* op = a.o + (ok ? p : 0) * kPC + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) x[kk] = as_bf16x8(ok ? ld16(op + 16 * kk) : u32x4{0, 0, 0, 0});
+  };
+  bf16x8 xn[8];
+  int64_t pn = 0;
+  if (first < last) load(first, xn, pn);
+  for (int item = first; item < last; ++item) {
+    bf16x8 x[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) x[kk] = xn[kk];
+    const int64_t p = pn;
+    const bool ok = p < a.P;                             // only the last block has idle lanes
+    if (item + 1 < last) load(item + 1, xn, pn);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), x[kk], acc);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int n0 = 32 * nb + 8 * c + 4 * half;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
+        if (!ok) continue;
+        if (a.z != nullptr) {
+          const u32x2 zw = *reinterpret_cast<const u32x2*>(a.z + p * kPC + n0);
+          v[0] += bflo(zw[0]); v[1] += bfhi(zw[0]); v[2] += bflo(zw[1]); v[3] += bfhi(zw[1]);
+        }
+        *reinterpret_cast<u32x2*>(a.out + p * kPC + n0) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      }
+    }
+  }
+}
+
 struct TriAttnArgs {
   int N, NP, H, transpose;
-  const uint16_t *q, *k, *vt, *g, *bias;
+  const uint16_t *q, *k, *vt, *g;
+  const float* bias;
   const uint8_t* seq;
   uint16_t* o;                        // [N][N][H][32] at pair positions
 };
@@ -238,27 +371,37 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
   const int i = qb * 32 * W + 32 * wave + li;      // this lane's query
   const int iq = min(i, NP - 1);                    // operand row for loads (results of i >= N unused)
 
-  // Q operands (B of S^T = K Q^T) for the 4 rows, row masks
+  // Q operands (B of S^T = K Q^T) for the 4 rows; row validity and padding are uniform.
   bf16x8 qb8[kTR][2];
   bool rvalid[kTR], rmasked[kTR];
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
     const int r = r0 + rr;
     rvalid[rr] = r < N;
-    rmasked[rr] = rvalid[rr] && a.seq[r] == 0;
+    rmasked[rr] = rvalid[rr] && __builtin_amdgcn_readfirstlane((int)a.seq[min(r, N - 1)]) == 0;
     const uint16_t* qp = a.q + (((int64_t)r * NP + iq) * H + h) * 32;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(qp + 16 * kk + 8 * half));
   }
+  // Online softmax state.  m is the reference point of the exponentials (shared by the two
+  // lanes holding the same query), kept bf16-exact because it enters the S^T MFMA through an
+  // extra k-step: [K | 1] . [Q | -m]^T + bias = logit - m, so after tile 0 the weights are
+  // exp2 of the MFMA output directly.  Tile 0 sets m to its row maximum; later tiles move it
+  // only when a tile's probability mass exceeds kMassLimit (all weights are >= 0, so the sum
+  // bounds every single weight and nothing can overflow unnoticed).
+  constexpr float kMassLimit = 1.152921504606847e18f;   // 2^60
   f32x16 o[kTR];
   float m[kTR], l[kTR];
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[rr][e] = 0.f;
-    m[rr] = -INFINITY;
+    m[rr] = 0.f;
     l[rr] = 0.f;
   }
+  bf16x8 ones_k;                                         // A operand: 1 at k = 0 (lanes of half 0)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones_k[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
 
   // tile loader: 4 rows x (K 64x32 + V^T 32x64) bf16 = 2 x 2048 16-byte chunks
   constexpr int CH = 2 * kTR * 256;
@@ -290,76 +433,155 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
       else st16(&sV[buf * kVTile + (rr * 32 + (w >> 3)) * kVP + 8 * (w & 7)], stage[u]);
     }
   };
-  const uint16_t* bp = a.bias + ((int64_t)h * NP + iq) * NP + 16 * half;
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  const int ntiles = NP / kKT;
-  for (int tt = 0; tt < ntiles; ++tt) {
-    const int buf = tt & 1;
-    const int j0 = tt * kKT;
-    if (tt + 1 < ntiles) load_tile(j0 + kKT);
-    // bias tile -> fp32 accumulator seed, shared by the 4 rows
-    f32x16 bseed[2];
+  // bias tile (fp32, key order of the S^T registers): this lane's 16 keys of each 32-key half
+  const float* bp = a.bias + ((int64_t)h * NP + iq) * NP + 16 * half;
+  f32x16 bseed[2];
+  auto load_bias = [&](int j0) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 w = ld16(bp + j0 + 32 * kb + 4 * u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bseed[kb][4 * u + e] = __uint_as_float(w[e]);
+      }
+  };
+  // S^T of row rr (64 keys x 32 queries) from the K tile in LDS, seeded with the bias tile;
+  // with_m adds the k-step that subtracts the row's reference point.
+  auto qk = [&](int rr, int buf, f32x16 (&s)[2], bool with_m) {
+    const uint16_t* kt = &sK[buf * kKTile + rr * kKT * kKP];
+    bf16x8 mq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
+    mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const u32x4 b0 = ld16(bp + j0 + 32 * kb), b1 = ld16(bp + j0 + 32 * kb + 8);
+      const bf16x8 k0 = as_bf16x8(ld16(&kt[(32 * kb + li) * kKP + 8 * half]));
+      const bf16x8 k1 = as_bf16x8(ld16(&kt[(32 * kb + li) * kKP + 16 + 8 * half]));
+      s[kb] = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
+      if (with_m) s[kb] = mfma32(ones_k, mq, s[kb]);
+    }
+  };
+  // padded token: every key masked, weights uniform over the keys below N (relative logit 0)
+  auto masked_logits = [&](f32x16 (&s)[2]) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        bseed[kb][2 * e] = bflo(b0[e]);
-        bseed[kb][2 * e + 1] = bfhi(b0[e]);
-        bseed[kb][8 + 2 * e] = bflo(b1[e]);
-        bseed[kb][8 + 2 * e + 1] = bfhi(b1[e]);
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[kb][e] = (bseed[kb][e] == -INFINITY) ? -INFINITY : 0.0f;
+  };
+  // weights 2^(s - shift) as packed bf16 pairs in PV slot order; returns their sum
+  auto weights = [&](const f32x16 (&s)[2], float shift, bf16x2 (&pw)[16]) {
+    float ts = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pw[8 * kb + e] = cvt_bf2(fast_exp2(s[kb][2 * e] - shift), fast_exp2(s[kb][2 * e + 1] - shift));
+        ts = add_bf2(pw[8 * kb + e], ts);
+      }
+    return ts;
+  };
+  auto tile_max = [&](const f32x16 (&s)[2]) {
+    float v = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v = fmaxf(v, s[kb][e]);
+    return fmaxf(v, __shfl_xor(v, 32));
+  };
+  // rare path: this tile's mass passed the limit; s holds logit - m exactly (|m| stays
+  // moderate), so move m up to the tile maximum and rescale what is accumulated
+  auto move_reference = [&](int rr, const f32x16 (&s)[2], bf16x2 (&pw)[16]) {
+    const float mnew = (float)(__bf16)(m[rr] + fmaxf(tile_max(s), 0.f));
+    const float shift = mnew - m[rr];
+    const float alpha = fast_exp2(-shift);
+    m[rr] = mnew;
+    l[rr] *= alpha;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
+    return weights(s, shift, pw);
+  };
+  auto pv = [&](int rr, int buf, const bf16x2 (&pw)[16]) {
+    const uint16_t* vt = &sV[buf * kVTile + rr * 32 * kVP];
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) {
+      bf16x8 pb;                     // P^T chunk c2: pairs 4*c2 .. 4*c2+3
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        pb[2 * q2] = pw[4 * c2 + q2][0];
+        pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
+      }
+      o[rr] = mfma32(as_bf16x8(ld16(&vt[li * kVP + 16 * c2 + 8 * half])), pb, o[rr]);
+    }
+  };
+  // one row of a tile after tile 0: weights against m, rare rescale, accumulate
+  auto step = [&](int rr, int buf, const f32x16 (&s)[2]) {
+    bf16x2 pw[16];
+    float ts = weights(s, 0.0f, pw);
+    if (__any(!(ts <= kMassLimit))) ts = move_reference(rr, s, pw);
+    l[rr] += ts;
+    pv(rr, buf, pw);
+  };
+
+  const int ntiles = NP / kKT;
+  const int last_rr = min(kTR - 1, N - 1 - r0);            // last row of this group below N
+  // The software-pipelined row order needs S^T of two rows live at once, which does not fit the
+  // register budget together with 4 rows of state; every row group takes the row-by-row path.
+  constexpr bool plain = false;
+
+  load_tile(0);
+  load_bias(0);
+  store_tile(0);
+  __syncthreads();
+  // ---- tile 0: the reference point starts at the tile's row maximum ----
+  if (ntiles > 1) load_tile(kKT);
+#pragma unroll
+  for (int rr = 0; rr < kTR; ++rr) {
+    if (!rvalid[rr]) continue;
+    f32x16 s[2];
+    qk(rr, 0, s, false);
+    if (rmasked[rr]) masked_logits(s);
+    const float smax = tile_max(s);
+    // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
+    const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
+    m[rr] = m0;
+    if (rr == last_rr && ntiles > 1) load_bias(kKT);
+    bf16x2 pw[16];
+    l[rr] = weights(s, m0, pw);
+    pv(rr, 0, pw);
+  }
+  if (ntiles > 1) store_tile(1);
+  __syncthreads();
+
+  for (int tt = 1; tt < ntiles; ++tt) {
+    const int buf = tt & 1;
+    const int j0 = tt * kKT;
+    const bool more = tt + 1 < ntiles;
+    if (more) load_tile(j0 + kKT);
+    if (plain) {
+      // software-pipelined: the next row's S^T MFMAs are issued before this row's weights
+      f32x16 sa[2], sb[2];
+      qk(0, buf, sa, true);
+      qk(1, buf, sb, true);
+      step(0, buf, sa);
+      qk(2, buf, sa, true);
+      step(1, buf, sb);
+      qk(3, buf, sb, true);
+      if (more) load_bias(j0 + kKT);                       // seed consumed by all rows
+      step(2, buf, sa);
+      step(3, buf, sb);
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < kTR; ++rr) {
+        if (!rvalid[rr]) continue;
+        f32x16 s[2];
+        qk(rr, buf, s, true);
+        if (rmasked[rr]) masked_logits(s);
+        if (rr == last_rr && more) load_bias(j0 + kKT);
+        step(rr, buf, s);
       }
     }
-#pragma unroll
-    for (int rr = 0; rr < kTR; ++rr) {
-      if (!rvalid[rr]) continue;
-      const uint16_t* kt = &sK[buf * kKTile + rr * kKT * kKP];
-      f32x16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = bseed[kb];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          s[kb] = mfma32(as_bf16x8(ld16(&kt[(32 * kb + li) * kKP + 16 * kk + 8 * half])), qb8[rr][kk], s[kb]);
-      }
-      if (rmasked[rr]) {   // padded token: every key of this row is masked (uniform weights)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) s[kb][e] = (bseed[kb][e] == -INFINITY) ? -INFINITY : SF_MASKED_LOGIT;
-      }
-      float tmax = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[kb][e]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float mnew = fmaxf(m[rr], tmax);
-      const float alpha = fast_exp2(m[rr] - mnew);
-      m[rr] = mnew;
-      l[rr] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
-      const uint16_t* vt = &sV[buf * kVTile + rr * 32 * kVP];
-#pragma unroll
-      for (int c2 = 0; c2 < 4; ++c2) {
-        const int kb = c2 >> 1, base = 8 * (c2 & 1);
-        bf16x8 pb;
-#pragma unroll
-        for (int sl = 0; sl < 8; ++sl) {
-          const float p = fast_exp2(s[kb][base + sl] - mnew);
-          l[rr] += p;
-          pb[sl] = (__bf16)p;
-        }
-        o[rr] = mfma32(as_bf16x8(ld16(&vt[li * kVP + 16 * c2 + 8 * half])), pb, o[rr]);
-      }
-    }
-    if (tt + 1 < ntiles) {
-      store_tile(buf ^ 1);
-    }
+    if (more) store_tile(buf ^ 1);
     __syncthreads();
   }
 
@@ -370,7 +592,7 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
     const int r = r0 + rr;
     if (r >= N) continue;
     const float lt = l[rr] + __shfl_xor(l[rr], 32);
-    const float inv = 1.0f / lt;
+    const float inv = fast_rcp(lt);
     const uint16_t* gp = a.g + (((int64_t)r * NP + i) * H + h) * 32;
     const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
     uint16_t* op = a.o + (((int64_t)za * N + zb) * H + h) * 32;
@@ -418,6 +640,17 @@ extern "C" size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t 
 }
 
 namespace {
+// Persistent launch size: enough waves to cover every CU a few times, each wave walking a
+// contiguous run of items so that neighbouring waves touch neighbouring memory.
+int persistent_groups(int items, int* items_per_wave) {
+  const int target_waves = 256 * 4 * 2;               // 256 CUs x 4 SIMDs x 2 waves
+  int ipw = (items + target_waves - 1) / target_waves;
+  if (ipw < 1) ipw = 1;
+  *items_per_wave = ipw;
+  const int waves = (items + ipw - 1) / ipw;
+  return (waves + kPWaves - 1) / kPWaves;
+}
+
 int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_bytes, hipStream_t st, int stages) {
   const int32_t N = a->N, H = a->H;
   const FastWs ws = carve_fast(workspace, N, H);
@@ -427,13 +660,15 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   }
   const int NP = round64(N);
   TriProjArgs pa{};
-  pa.N = N; pa.NP = NP; pa.C = kPC; pa.H = H; pa.transpose = a->transpose;
+  pa.N = N; pa.NP = NP; pa.H = H; pa.transpose = a->transpose;
   pa.qscale = (1.0f / sqrtf(32.0f)) * SF_LOG2E;
   pa.z = (const uint16_t*)a->z; pa.seq = a->seq_mask; pa.ln_w = a->ln_w; pa.ln_b = a->ln_b;
   pa.w = (const uint16_t*)a->w_qkvgb;
   pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.g = ws.g; pa.bias = ws.bias;
+  pa.items = NP * (NP / 32);
+  const int pgroups = persistent_groups(pa.items, &pa.items_per_wave);
   if (stages & SF_TRI_STAGE_PROJECT) {
-    hipLaunchKernelGGL(tri_proj_kernel, dim3((NP + kPB - 1) / kPB, NP), dim3(256), 0, st, pa);
+    hipLaunchKernelGGL(tri_proj_kernel, dim3(pgroups), dim3(64 * kPWaves), 0, st, pa);
     if (int rc = sf_check_launch("tri_proj_kernel")) return rc;
   }
 
@@ -452,14 +687,15 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
 
-  sf_linear_args op{};
-  const int64_t HD = (int64_t)H * 32;
-  op.M = (int64_t)N * N; op.N = a->C; op.K = (int32_t)HD;
-  op.x = ws.o; op.x_rs = HD; op.wt = a->w_o;
-  if (a->add_residual) { op.residual = a->z; op.r_rs = a->C; }
-  op.mul_rows = 1;
-  op.y = a->out; op.y_rs = a->C;
-  return sf_hip_linear_fwd(&op, st);
+  TriOutArgs oa{};
+  oa.P = (int64_t)N * N;
+  oa.o = ws.o; oa.wo = (const uint16_t*)a->w_o;
+  oa.z = a->add_residual ? (const uint16_t*)a->z : nullptr;
+  oa.out = (uint16_t*)a->out;
+  oa.items = (int)((oa.P + 31) / 32);
+  const int ogroups = persistent_groups(oa.items, &oa.items_per_wave);
+  hipLaunchKernelGGL(tri_out_kernel, dim3(ogroups), dim3(64 * kPWaves), 0, st, oa);
+  return sf_check_launch("tri_out_kernel");
 }
 }  // namespace
 
