@@ -133,3 +133,24 @@ def test_windowed_atom_attention(atoms, S, sharp):
   upd = hip.forward_indexed(*args, add_residual=False)
   d_ref = OM.windowed_cross_attention(*oargs, return_update=True)
   assert_close_bf16(upd, d_ref, "window update", max_abs=2e-2 * d_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_against_committed_fixture(transpose):
+  """tests/golden/oracle_small.npz: sharp-weight, padded triangle attention at N=20 (float32)."""
+  import os
+  import numpy as np
+  from sparsefold_amd import modules as M
+  f = np.load(os.path.join(os.path.dirname(__file__), "golden", "oracle_small.npz"))
+  tag = "end" if transpose else "start"
+  pre = f"tri20_{tag}_param_"
+  params = {k[len(pre):]: torch.from_numpy(f[k]) for k in f.files if k.startswith(pre)}
+  mod = M.GridSelfAttention(M.GridSelfAttention.Config(num_head=4), M.GlobalConfig(), transpose,
+                            num_channels=128, name="fixture")
+  mod.load_state_dict(params, strict=True)
+  hip = _prepared(mod)
+  z = torch.from_numpy(f[f"tri20_{tag}_z"])
+  seq = torch.from_numpy(f[f"tri20_{tag}_seq"])
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref = torch.from_numpy(f[f"tri20_{tag}_update"])
+  assert_close_bf16(upd, ref, f"fixture triangle N=20 {tag}", max_abs=2e-2 * ref.abs().max().item())
