@@ -14,7 +14,7 @@
 //                          Ks  [r][j][h][d]
 //                          Vt  [r][h][d][j'] V transposed, keys in PV-MFMA slot order
 //                          Gs  [r][i][h][d]  gate logits
-//                          Bs  [h][i][j'']   bias * log2(e), fp32, in the untransposed orientation
+//                          Bs  [h][i][j'']   bias * log2(e), bf16, in the untransposed orientation
 //                                            (blocks.py:329), masked keys = SF_MASKED_LOGIT,
 //                                            keys past N = -inf, keys in S^T register order
 //                        For the ending node the workgroup walks z's column instead of its row,
@@ -28,6 +28,7 @@
 //   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
+#include <type_traits>
 
 #include "sf_common.h"
 
@@ -49,8 +50,7 @@ __host__ __device__ inline int v_pos64(int j) {
 }
 
 struct FastWs {
-  uint16_t *q, *k, *vt, *g, *o;
-  float* bias;
+  uint16_t *q, *k, *vt, *g, *bias, *o;
   size_t bytes;
 };
 
@@ -63,7 +63,7 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.k = (uint16_t*)(p + off); off += round_up(E * 2);
   w.vt = (uint16_t*)(p + off); off += round_up(E * 2);
   w.g = (uint16_t*)(p + off); off += round_up(E * 2);
-  w.bias = (float*)(p + off); off += round_up(NP * NP * H * 4);
+  w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
   w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
   w.bytes = off;
   return w;
@@ -78,8 +78,7 @@ struct TriProjArgs {
   const uint16_t* z; const uint8_t* seq;
   const float* ln_w; const float* ln_b;
   const uint16_t* w;                  // [4*H*32 + H, C]
-  uint16_t *q, *k, *vt, *g;
-  float* bias;
+  uint16_t *q, *k, *vt, *g, *bias;
   int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
 
@@ -255,12 +254,11 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
           }
           if (!a.transpose) {   // za = r: four consecutive keys of one bias row
             const int64_t base = ((int64_t)li * NP + r) * NP + (pb & ~63) + bias_pos64(pb & 63);
-            st16(a.bias + base, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                                      __float_as_uint(v[3])});
+            *reinterpret_cast<u32x2*>(a.bias + base) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
           } else {              // zb = r: one key of four bias rows
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              a.bias[((int64_t)li * NP + pb + e) * NP + (r & ~63) + bias_pos64(r & 63)] = v[e];
+              a.bias[((int64_t)li * NP + pb + e) * NP + (r & ~63) + bias_pos64(r & 63)] = f2bf(v[e]);
           }
         }
       }
@@ -317,18 +315,20 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), x[kk], acc);
+      if (ok) {
+        const uint16_t* zp = a.z != nullptr ? a.z + p * kPC + 32 * nb + 4 * half : nullptr;
+        uint16_t* outp = a.out + p * kPC + 32 * nb + 4 * half;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int n0 = 32 * nb + 8 * c + 4 * half;
-        float v[4];
+        for (int c = 0; c < 4; ++c) {
+          float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
-        if (!ok) continue;
-        if (a.z != nullptr) {
-          const u32x2 zw = *reinterpret_cast<const u32x2*>(a.z + p * kPC + n0);
-          v[0] += bflo(zw[0]); v[1] += bfhi(zw[0]); v[2] += bflo(zw[1]); v[3] += bfhi(zw[1]);
+          for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
+          if (zp != nullptr) {
+            const u32x2 zw = *reinterpret_cast<const u32x2*>(zp + 8 * c);
+            v[0] += bflo(zw[0]); v[1] += bfhi(zw[0]); v[2] += bflo(zw[1]); v[3] += bfhi(zw[1]);
+          }
+          *reinterpret_cast<u32x2*>(outp + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
         }
-        *reinterpret_cast<u32x2*>(a.out + p * kPC + n0) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
       }
     }
   }
@@ -336,27 +336,41 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 
 struct TriAttnArgs {
   int N, NP, H, transpose;
-  const uint16_t *q, *k, *vt, *g;
-  const float* bias;
+  const uint16_t *q, *k, *vt, *g, *bias;
   const uint8_t* seq;
   uint16_t* o;                        // [N][N][H][32] at pair positions
 };
 
 constexpr int kTR = 4;                // rows per workgroup
 constexpr int kKT = 64;               // keys per tile
-constexpr int kKP = 40;               // K tile row pitch (elements): 32 + 8
-constexpr int kVP = 72;               // V^T tile row pitch (elements): 64 + 8
-constexpr int kKTile = kTR * kKT * kKP;   // elements per K tile buffer
-constexpr int kVTile = kTR * 32 * kVP;    // elements per V^T tile buffer
+
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
+// One LDS tile buffer (all 16-byte slots, XOR-swizzled so that the MFMA operand reads of any
+// 8 consecutive lanes hit 8 distinct slot positions of a 128-byte window):
+//   K    [row rr][key 0..63][slot 0..3]   slot = d-chunk ^ ((key >> 1) & 3)      16 KB
+//   V^T  [row rr][d 0..31][slot 0..7]     slot = key-chunk ^ (d & 7)             16 KB
+//   bias [query 0..32W-1][slot 0..7]      slot = key-piece ^ (query & 7)   W x 4 KB
+// Every 1 KB of it is filled by one global_load_lds_dwordx4 (lane L -> bytes 16L..16L+15).
+template <int W>
+struct TileLayout {
+  static constexpr int kKBytes = kTR * kKT * 64;
+  static constexpr int kVBytes = kTR * 32 * 128;
+  static constexpr int kBBytes = 32 * W * 128;
+  static constexpr int kBytes = kKBytes + kVBytes + kBBytes;
+  static constexpr int kChunks = kBytes / 1024;
+  static constexpr int kChunksPerWave = kChunks / W;
+  static_assert(kChunks % W == 0, "tile chunks must split evenly over the waves");
+};
 
 template <int W>
 __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2 * kKTile];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2 * kVTile];
-  constexpr int NT = 64 * W;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  using TL = TileLayout<W>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar branches
   const int half = lane >> 5, li = lane & 31;
-  const int N = a.N, NP = a.NP, H = a.H, HD = H * 32;
+  const int N = a.N, NP = a.NP, H = a.H;
 
   // ---- workgroup -> (head, row group, query block); XCD-major so that the workgroups an XCD
   //      runs together share the head's bias plane and the row group's K/V tiles in its L2 ----
@@ -370,6 +384,44 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
   const int r0 = rg * kTR;
   const int i = qb * 32 * W + 32 * wave + li;      // this lane's query
   const int iq = min(i, NP - 1);                    // operand row for loads (results of i >= N unused)
+
+  // ---- tile loader: this wave's 1 KB chunks of the next tile, straight into LDS.  Every chunk
+  //      address is a wave-uniform base plus one of two per-lane offsets (the swizzle only
+  //      depends on the lane): K rows (lane/4 keys, slot lane%4) or 128-byte rows (V^T dims and
+  //      bias queries, lane/8 rows, slot lane%8). ----
+  const int koff = (lane >> 2) * H * 32 + 8 * ((lane & 3) ^ ((lane >> 3) & 3));
+  const int roff = (lane >> 3) * NP + 8 * ((lane & 7) ^ ((lane >> 3) & 7));
+  auto load_tile = [&](int j0, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < TL::kChunksPerWave; ++u) {
+      const int c = wave * TL::kChunksPerWave + u;             // uniform
+      const uint16_t* base;
+      int off;
+      if (c < 16) {                                            // K: row c/4, keys (c%4)*16 + lane/4
+        const int r = min(r0 + (c >> 2), NP - 1);
+        base = a.k + (((int64_t)r * NP + j0 + (c & 3) * 16) * H + h) * 32;
+        off = koff;
+      } else if (c < 32) {                                     // V^T: row (c-16)/4, dims ((c-16)%4)*8 + lane/8
+        const int r = min(r0 + ((c - 16) >> 2), NP - 1);
+        base = a.vt + (((int64_t)r * H + h) * 32 + ((c - 16) & 3) * 8) * NP + j0;
+        off = roff;
+      } else {                                                 // bias: query rows (c-32)*8 + lane/8
+        const int q0 = min(qb * 32 * W + (c - 32) * 8, NP - 8);
+        base = a.bias + ((int64_t)h * NP + q0) * NP + j0;
+        off = roff;
+      }
+      __builtin_amdgcn_global_load_lds(base + off, (lds_u32*)(smem + buf * TL::kBytes + c * 1024), 16, 0, 0);
+    }
+  };
+  auto kslot = [&](int buf, int rr, int key, int dc) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kBytes + ((rr * kKT + key) * 4 + (dc ^ ((key >> 1) & 3))) * 16;
+  };
+  auto vslot = [&](int buf, int rr, int d, int kc) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kBytes + TL::kKBytes + ((rr * 32 + d) * 8 + (kc ^ (d & 7))) * 16;
+  };
+  auto bslot = [&](int buf, int row, int pc) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kBytes + TL::kKBytes + TL::kVBytes + (row * 8 + (pc ^ (row & 7))) * 16;
+  };
 
   // Q operands (B of S^T = K Q^T) for the 4 rows; row validity and padding are uniform.
   bf16x8 qb8[kTR][2];
@@ -403,61 +455,34 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones_k[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
 
-  // tile loader: 4 rows x (K 64x32 + V^T 32x64) bf16 = 2 x 2048 16-byte chunks
-  constexpr int CH = 2 * kTR * 256;
-  constexpr int PER = CH / NT;
-  u32x4 stage[PER];
-  auto load_tile = [&](int j0) {
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int c = tid + u * NT;
-      const int isv = c >= kTR * 256;
-      const int cc = c - isv * kTR * 256;
-      const int rr = cc >> 8, w = cc & 255;
-      const int r = min(r0 + rr, NP - 1);
-      if (!isv) {   // K: key w/4, dims 8*(w%4)
-        stage[u] = ld16(a.k + (((int64_t)r * NP + j0 + (w >> 2)) * H + h) * 32 + 8 * (w & 3));
-      } else {      // V^T: dim w/8, keys 8*(w%8)
-        stage[u] = ld16(a.vt + (((int64_t)r * H + h) * 32 + (w >> 3)) * NP + j0 + 8 * (w & 7));
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int c = tid + u * NT;
-      const int isv = c >= kTR * 256;
-      const int cc = c - isv * kTR * 256;
-      const int rr = cc >> 8, w = cc & 255;
-      if (!isv) st16(&sK[buf * kKTile + (rr * kKT + (w >> 2)) * kKP + 8 * (w & 3)], stage[u]);
-      else st16(&sV[buf * kVTile + (rr * 32 + (w >> 3)) * kVP + 8 * (w & 7)], stage[u]);
-    }
-  };
-  // bias tile (fp32, key order of the S^T registers): this lane's 16 keys of each 32-key half
-  const float* bp = a.bias + ((int64_t)h * NP + iq) * NP + 16 * half;
+  // bias tile of this wave's 32 queries -> fp32 accumulator seed in S^T register order
   f32x16 bseed[2];
-  auto load_bias = [&](int j0) {
+  auto load_bias = [&](int buf) __attribute__((always_inline)) {
+    const int row = 32 * wave + li;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
+      const u32x4 b0 = ld16(bslot(buf, row, 4 * kb + 2 * half));
+      const u32x4 b1 = ld16(bslot(buf, row, 4 * kb + 2 * half + 1));
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const u32x4 w = ld16(bp + j0 + 32 * kb + 4 * u);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bseed[kb][4 * u + e] = __uint_as_float(w[e]);
+      for (int e = 0; e < 4; ++e) {
+        bseed[kb][2 * e] = bflo(b0[e]);
+        bseed[kb][2 * e + 1] = bfhi(b0[e]);
+        bseed[kb][8 + 2 * e] = bflo(b1[e]);
+        bseed[kb][8 + 2 * e + 1] = bfhi(b1[e]);
       }
+    }
   };
   // S^T of row rr (64 keys x 32 queries) from the K tile in LDS, seeded with the bias tile;
   // with_m adds the k-step that subtracts the row's reference point.
   auto qk = [&](int rr, int buf, f32x16 (&s)[2], bool with_m) {
-    const uint16_t* kt = &sK[buf * kKTile + rr * kKT * kKP];
     bf16x8 mq;
 #pragma unroll
     for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
     mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 k0 = as_bf16x8(ld16(&kt[(32 * kb + li) * kKP + 8 * half]));
-      const bf16x8 k1 = as_bf16x8(ld16(&kt[(32 * kb + li) * kKP + 16 + 8 * half]));
+      const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, 32 * kb + li, half)));
+      const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, 32 * kb + li, 2 + half)));
       s[kb] = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
       if (with_m) s[kb] = mfma32(ones_k, mq, s[kb]);
     }
@@ -502,7 +527,6 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
     return weights(s, shift, pw);
   };
   auto pv = [&](int rr, int buf, const bf16x2 (&pw)[16]) {
-    const uint16_t* vt = &sV[buf * kVTile + rr * 32 * kVP];
 #pragma unroll
     for (int c2 = 0; c2 < 4; ++c2) {
       bf16x8 pb;                     // P^T chunk c2: pairs 4*c2 .. 4*c2+3
@@ -511,7 +535,7 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
         pb[2 * q2] = pw[4 * c2 + q2][0];
         pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
       }
-      o[rr] = mfma32(as_bf16x8(ld16(&vt[li * kVP + 16 * c2 + 8 * half])), pb, o[rr]);
+      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, li, 2 * c2 + half))), pb, o[rr]);
     }
   };
   // one row of a tile after tile 0: weights against m, rare rescale, accumulate
@@ -525,16 +549,13 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
 
   const int ntiles = NP / kKT;
   const int last_rr = min(kTR - 1, N - 1 - r0);            // last row of this group below N
-  // The software-pipelined row order needs S^T of two rows live at once, which does not fit the
-  // register budget together with 4 rows of state; every row group takes the row-by-row path.
-  constexpr bool plain = false;
 
-  load_tile(0);
-  load_bias(0);
-  store_tile(0);
-  __syncthreads();
+  load_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
+  __syncthreads();                                         // ... and everybody else's
   // ---- tile 0: the reference point starts at the tile's row maximum ----
-  if (ntiles > 1) load_tile(kKT);
+  if (ntiles > 1) load_tile(kKT, 1);
+  load_bias(0);
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
     if (!rvalid[rr]) continue;
@@ -545,44 +566,33 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
     // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
     const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
     m[rr] = m0;
-    if (rr == last_rr && ntiles > 1) load_bias(kKT);
     bf16x2 pw[16];
     l[rr] = weights(s, m0, pw);
     pv(rr, 0, pw);
   }
-  if (ntiles > 1) store_tile(1);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int tt = 1; tt < ntiles; ++tt) {
-    const int buf = tt & 1;
+  // tiles 1.. : buffer index is a compile-time constant inside each half of the pair
+  auto tile_step = [&](int tt, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
     const int j0 = tt * kKT;
-    const bool more = tt + 1 < ntiles;
-    if (more) load_tile(j0 + kKT);
-    if (plain) {
-      // software-pipelined: the next row's S^T MFMAs are issued before this row's weights
-      f32x16 sa[2], sb[2];
-      qk(0, buf, sa, true);
-      qk(1, buf, sb, true);
-      step(0, buf, sa);
-      qk(2, buf, sa, true);
-      step(1, buf, sb);
-      qk(3, buf, sb, true);
-      if (more) load_bias(j0 + kKT);                       // seed consumed by all rows
-      step(2, buf, sa);
-      step(3, buf, sb);
-    } else {
+    if (tt + 1 < ntiles) load_tile(j0 + kKT, buf ^ 1);     // lands while this tile computes
+    load_bias(buf);
 #pragma unroll
-      for (int rr = 0; rr < kTR; ++rr) {
-        if (!rvalid[rr]) continue;
-        f32x16 s[2];
-        qk(rr, buf, s, true);
-        if (rmasked[rr]) masked_logits(s);
-        if (rr == last_rr && more) load_bias(j0 + kKT);
-        step(rr, buf, s);
-      }
+    for (int rr = 0; rr < kTR; ++rr) {
+      if (!rvalid[rr]) continue;
+      f32x16 s[2];
+      qk(rr, buf, s, true);
+      if (rmasked[rr]) masked_logits(s);
+      step(rr, buf, s);
     }
-    if (more) store_tile(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+  for (int tt = 1; tt < ntiles; tt += 2) {
+    tile_step(tt, std::integral_constant<int, 1>{});
+    if (tt + 1 < ntiles) tile_step(tt + 1, std::integral_constant<int, 0>{});
   }
 
   // ---- epilogue: normalise, gate, store at the pair position ----
