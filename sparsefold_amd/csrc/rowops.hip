@@ -173,6 +173,154 @@ __global__ __launch_bounds__(256) void linear_kernel(const sf_linear_args a) {
 }
 
 // ------------------------------------------------------------------------------------
+// Linear, K % 64 == 0: BMxBN tile, 4 waves (2x2), K in steps of 64 double-buffered in LDS
+// through direct-to-LDS loads (global_load_lds_dwordx4: lane L fills bytes 16L..16L+15 of a
+// 1 KB chunk = 8 rows x 64 k).  Rows are 128 bytes with their 16-byte slots XOR-swizzled by
+// (row & 7), so the operand reads of 8 consecutive lanes hit 8 distinct slots.  The product is
+// formed transposed (A operand = weight rows), so each lane owns one output row and 4
+// consecutive columns per register group: 8-byte epilogue loads and stores.
+// ------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
+  constexpr int ABYTES = BM * 128, BBYTES = BN * 128, BUF = ABYTES + BBYTES;
+  constexpr int CHUNKS = BUF / 1024, CPW = CHUNKS / 4;        // 1 KB chunks per wave per step
+  constexpr int WR = BM / 2, WC = BN / 2;                     // wave tile
+  constexpr int MB = WR / 32, NB = WC / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * BUF];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, li = lane & 31;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * BM;
+  const int n0 = blockIdx.y * BN;
+  const uint16_t* xp = (const uint16_t*)a.x;
+  const uint16_t* wp = (const uint16_t*)a.wt;
+  const int rsw = 8 * ((lane & 7) ^ ((lane >> 3) & 7));       // this lane's swizzled source piece
+  const int64_t mlast = a.M - 1;
+  const int nlast = a.N - 1;
+
+  auto load_step = [&](int k0, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int c = wave * CPW + u;                            // uniform
+      const uint16_t* src;
+      if (c < ABYTES / 1024) {
+        const int64_t row = min(m0 + c * 8 + (lane >> 3), mlast);
+        src = xp + row * a.x_rs + k0 + rsw;
+      } else {
+        const int row = min(n0 + (c - ABYTES / 1024) * 8 + (lane >> 3), nlast);
+        src = wp + (int64_t)row * a.K + k0 + rsw;
+      }
+      __builtin_amdgcn_global_load_lds(src, (lds_u32_t*)(smem + buf * BUF + c * 1024), 16, 0, 0);
+    }
+  };
+  auto slot = [&](int buf, int region, int row, int piece) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * BUF + region + (row * 8 + (piece ^ (row & 7))) * 16;
+  };
+
+  f32x16 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.f;
+
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8 xa[MB], wb[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        xa[mb] = as_bf16x8(ld16(slot(buf, 0, wm * WR + 32 * mb + li, 2 * kk + half)));
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        wb[nb] = as_bf16x8(ld16(slot(buf, ABYTES, wn * WC + 32 * nb + li, 2 * kk + half)));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma32(wb[nb], xa[mb], acc[mb][nb]);
+    }
+  };
+
+  const int nsteps = a.K / 64;
+  load_step(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int ks = 0; ks < nsteps; ks += 2) {
+    if (ks + 1 < nsteps) load_step((ks + 1) * 64, 1);
+    compute(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (ks + 1 >= nsteps) break;
+    if (ks + 2 < nsteps) load_step((ks + 2) * 64, 0);
+    compute(1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane = output row m, register group c = 4 consecutive columns ----
+  uint16_t* yp = (uint16_t*)a.y;
+  uint16_t* ytp = (uint16_t*)a.yt;
+  const uint16_t* rp = (const uint16_t*)a.residual;
+  const uint16_t* mp = (const uint16_t*)a.mul;
+  const int ycols = a.ycols > 0 ? a.ycols : a.N;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int64_t m = m0 + wm * WR + 32 * mb + li;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int n = n0 + wn * WC + 32 * nb + 8 * c + 4 * half;   // columns n .. n+3
+        if (n >= a.N) continue;
+        const bool full = n + 4 <= a.N;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[mb][nb][4 * c + e] + ((a.bias && n + e < a.N) ? a.bias[n + e] : 0.f);
+        if (a.post_sigmoid) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(v[e]);
+        }
+        if (mp) {
+          const uint16_t* mrow = mp + (m % a.mul_rows) * a.mul_rs + n;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) v[e] *= bf2f(mrow[e]);
+        }
+        if (rp) {
+          const uint16_t* rrow = rp + m * a.r_rs + n;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) v[e] += bf2f(rrow[e]);
+        }
+        if (yp && n < ycols) {
+          uint16_t* yrow = yp + m * a.y_rs + n;
+          if (full && n + 4 <= ycols && ((reinterpret_cast<uintptr_t>(yrow) & 7) == 0)) {
+            *reinterpret_cast<u32x2*>(yrow) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < a.N && n + e < ycols) yrow[e] = f2bf(v[e]);
+          }
+        }
+        if (ytp) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ne = n + e;
+            if (ne < a.N && ne >= a.tcol0 && ne < a.tcol0 + a.tcols)
+              ytp[(int64_t)(ne - a.tcol0) * a.yt_rs + m] = f2bf(v[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // Pair logits: one thread per pair position; the position's C channels stay in
 // registers as packed bf16, LN statistics in fp32, then H dot products against
 // gamma-folded weights held in LDS ([c][h] so every thread reads the same words).
@@ -293,9 +441,23 @@ extern "C" int sf_hip_linear_fwd(const sf_linear_args* a, void* stream) {
   if (a->yt && (a->tcol0 < 0 || a->tcols < 0 || a->tcol0 + a->tcols > a->N)) {
     sf_set_error("linear: transposed column range out of bounds"); return 1;
   }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->K % 64 == 0) {
+    // largest tile that still gives >= 512 workgroups (two per CU); else the smallest
+    auto tiles = [&](int bm, int bn) { return ((a->M + bm - 1) / bm) * (int64_t)((a->N + bn - 1) / bn); };
+    int bm = 64, bn = 64;
+    if (tiles(128, 128) >= 512) bm = 128, bn = 128;
+    else if (tiles(64, 128) >= 512) bm = 64, bn = 128;
+    const int64_t gm = (a->M + bm - 1) / bm;
+    if (gm > 0x7fffffff) { sf_set_error("linear: M too large"); return 1; }
+    const dim3 grid((unsigned)gm, (a->N + bn - 1) / bn);
+    if (bm == 128) hipLaunchKernelGGL((linear64_kernel<128, 128>), grid, dim3(256), 0, st, *a);
+    else if (bn == 128) hipLaunchKernelGGL((linear64_kernel<64, 128>), grid, dim3(256), 0, st, *a);
+    else hipLaunchKernelGGL((linear64_kernel<64, 64>), grid, dim3(256), 0, st, *a);
+    return sf_check_launch("linear64_kernel");
+  }
   const int64_t gm = (a->M + kBM - 1) / kBM;
   if (gm > 0x7fffffff) { sf_set_error("linear: M too large"); return 1; }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(linear_kernel, dim3((unsigned)gm, (a->N + kBN - 1) / kBN), dim3(256), 0, st, *a);
   return sf_check_launch("linear_kernel");
 }

@@ -33,7 +33,11 @@ def test_layer_norm_adaptive_rows_broadcast():
   assert_close_bf16(out, ref, "adaln")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (100, 96, 128), (257, 516, 128), (1030, 384, 384), (64, 3072, 768)])
+# Shapes cover both GEMM kernels (K % 64 != 0 and == 0), each tile size of the K % 64 == 0
+# kernel (64x64, 64x128 at >= 512 tiles, 128x128 at >= 512 tiles), odd K-step counts and
+# ragged M / N edges (N % 4 != 0 exercises the partial 4-column epilogue group).
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (100, 96, 128), (257, 516, 128), (1030, 384, 384), (64, 3072, 768),
+                                   (1, 8, 64), (130, 70, 64), (4100, 1030, 192), (32773, 256, 128), (77, 3, 320)])
 def test_linear_plain(M, N, K):
   g = torch.Generator().manual_seed(M * 7 + N)
   x = torch.randn(M, K, generator=g).to(torch.bfloat16)
@@ -43,9 +47,10 @@ def test_linear_plain(M, N, K):
   assert_close_bf16(out, ref, f"linear {M}x{N}x{K}")
 
 
-def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns():
+@pytest.mark.parametrize("K", [64, 72])
+def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns(K):
   g = torch.Generator().manual_seed(9)
-  M, N, K = 300, 72, 64
+  M, N = 300, 72
   x = torch.randn(M, K, generator=g).to(torch.bfloat16)
   w = (torch.randn(N, K, generator=g) / 8).to(torch.bfloat16)
   bias = torch.randn(N, generator=g)
