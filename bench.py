@@ -46,6 +46,9 @@ def parse():
   ap.add_argument("--cpu-baseline", type=int, default=1, help="time the host-CPU math path (rank 0)")
   ap.add_argument("--cpu-rows", type=int, default=128, help="rows in the CPU-baseline sample")
   ap.add_argument("--other-configs", type=int, default=1, help="also time the other four configurations")
+  ap.add_argument("--copy-mib", type=int, default=0,
+                  help="only run a plain device-to-device copy of this many MiB 5 times and exit "
+                       "(the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters)")
   return ap.parse_args()
 
 
@@ -78,6 +81,31 @@ def stage_ms(z, seq, mod, iters: int) -> dict:
     res[name] = _events_time(lambda: ops.triangle_attention(*args, **kw, stages=st), iters,
                              torch.cuda.current_stream())
   return res
+
+
+def copy_calibration(mib: int) -> None:
+  """A plain copy of `mib` MiB: reads and writes exactly mib MiB of HBM per launch."""
+  n = mib << 20
+  src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+  dst = torch.empty_like(src)
+  for _ in range(5):
+    dst.copy_(src)
+  torch.cuda.synchronize()
+  print(json.dumps({"copy_mib": mib, "launches": 5, "bytes_read_per_launch": n, "bytes_written_per_launch": n}))
+
+
+def traffic_from_profile() -> float | None:
+  """HBM bytes per tri_attn_kernel launch, as recorded from the FETCH_SIZE / WRITE_SIZE counter
+  runs (calibrated against a plain copy) in profiles/tri_attn_kernel_n768_traffic.md."""
+  path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tri_attn_kernel_n768_traffic.md")
+  try:
+    with open(path) as f:
+      for line in f:
+        if line.startswith("traffic_bytes_per_launch:"):
+          return float(line.split(":", 1)[1])
+  except OSError:
+    return None
+  return None
 
 
 def _time_call(fn, iters: int) -> float:
@@ -189,6 +217,9 @@ def main():
     print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only",
                       "n_gpus": args.gpus}))
     sys.exit(2)
+  if args.copy_mib:
+    copy_calibration(args.copy_mib)
+    return
   from sparsefold_amd import backends
   from sparsefold_amd import workloads as W
   from sparsefold_amd.runtime import config
@@ -245,7 +276,7 @@ def main():
       "stages_ms": {k: round(v, 4) for k, v in stages.items()},
       "roofline": {"bound": "mfma", "kernel": "tri_attn_kernel", "achieved": round(core_tflops, 2),
                    "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(core_tflops / PEAK_BF16_TFLOPS, 4),
-                   "traffic": None, "kernel_ms": round(core_ms, 4), "flop_per_launch": core_flop()},
+                   "traffic": traffic_from_profile(), "kernel_ms": round(core_ms, 4), "flop_per_launch": core_flop()},
       "other_configs": others,
       "cpu_baseline": cpu,
       "speedup_vs_cpu": None if cpu is None else round(cpu["value"] / ms, 1),
