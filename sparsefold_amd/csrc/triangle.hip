@@ -3,28 +3,32 @@
 // Replaces GridSelfAttention.forward (src/sparsefold/model/trunk/blocks.py:293-366 with the
 // per-chunk _attention of :270-291).
 //
-// Fast path (head dim 32, the trunk's C=128 / H=4 configuration), three kernels:
-//   1. tri_proj_kernel   persistent workgroups with [Wq|Wk|Wv|Wg|Wb] resident in LDS (LN gamma
-//                        folded into the weight, beta into a per-column offset); each wave
-//                        normalises 32 positions of an attention row straight into MFMA
-//                        operand registers (blocks.py:317) and runs the projections
-//                        (blocks.py:276-278, :286, :320), writing every operand in the layout
-//                        the attention kernel consumes:
-//                          Qs  [r][i][h][d]  q * scale * log2(e)   (logits land in log2 units)
-//                          Ks  [r][j][h][d]
-//                          Vt  [r][h][d][j'] V transposed, keys in PV-MFMA slot order
-//                          Gs  [r][i][h][d]  gate logits
-//                          Bs  [h][i][j'']   bias * log2(e), bf16, in the untransposed orientation
-//                                            (blocks.py:329), masked keys = SF_MASKED_LOGIT,
-//                                            keys past N = -inf, keys in S^T register order
+// Fast path (head dim 32, the trunk's C=128 / H=4 configuration):
+//   0. tri_fold_kernel   folds the LN gamma into the packed projection weight and beta into
+//                        a per-column offset (blocks.py:317 followed by :276-278, :286, :320).
+//   1. tri_proj_kernel   persistent workgroups with the folded [Wq|Wk|Wv|Wg|Wb] resident in
+//                        LDS; each wave normalises 32 positions of an attention row straight
+//                        into MFMA operand registers and runs the projections, storing every
+//                        operand head-major in the register order the attention MFMAs use, so
+//                        that each store instruction writes 1 KB of contiguous memory:
+//                          Q, K, G  per (row r, head h), 32-position blocks of
+//                                   [k-chunk 2][lane half 2][position 32][8 dims]; q carries
+//                                   scale * log2(e), so logits land in log2 units
+//                          V^T      per (row r, head h), 16-key chunks of
+//                                   [lane half 2][dim 32][8 keys in PV slot order]
+//                          bias     [h][i][j''] bias * log2(e), bf16, untransposed orientation
+//                                   (blocks.py:329), masked keys = SF_MASKED_LOGIT, keys past
+//                                   N = -inf, keys in S^T register order
 //                        For the ending node the workgroup walks z's column instead of its row,
 //                        so nothing is transposed in memory (blocks.py:345-346, :362-363).
-//   2. tri_attn_kernel   one workgroup per (4 rows, head, 32*W queries); K / V^T tiles of 64
+//   2. tri_attn_kernel   one workgroup per (4 rows, head, 256 queries); K / V^T tiles of 64
 //                        keys for the 4 rows double-buffered in LDS; each wave keeps the online
 //                        softmax state of its 32 queries for all 4 rows and feeds the bias tile
-//                        -- identical for every row -- as the accumulator input of the S^T MFMA,
-//                        so bias loads and conversion are paid once per 4 rows; sigmoid gate in
-//                        the epilogue, output written at its pair position.
+//                        -- identical for every row -- as the accumulator input of the S^T MFMA;
+//                        sigmoid gate in the epilogue, output written at its pair position.
+//      tri_masked_kernel rows whose token is masked attend uniformly to every key (the
+//                        reference's finite -finfo.max mask): gate * mean of V, written over
+//                        what the attention kernel stored for them.
 //   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
@@ -37,20 +41,34 @@ size_t round_up(size_t x) { return (x + 255) & ~(size_t)255; }
 int round64(int n) { return (n + 63) & ~63; }
 
 // ---------------------------------------------------------------------------------------
-// Key orders inside a 64-key tile.
+// Operand layouts.
 // S^T register order: lane half h', register a -> key 8*(a/4) + 4*h' + a%4 of a 32-key half.
 __host__ __device__ inline int bias_pos64(int j) {
   const int j32 = j & 31;
   return (j & 32) + 16 * ((j32 >> 2) & 1) + 4 * (j32 >> 3) + (j32 & 3);
 }
-// PV slot order: 16-key chunk c2, lane half h', slot s -> key 16*c2 + 8*(s/4) + 4*h' + s%4.
-__host__ __device__ inline int v_pos64(int j) {
-  const int k16 = j & 15;
-  return (j & 48) + 8 * ((k16 >> 2) & 1) + (k16 & 3) + 4 * (k16 >> 3);
+// Q / K / G of (row r, head h): position p, k-chunk kk, lane half hf.  The 8 values at the
+// returned offset are dims 16*kk + 8*(t/4) + 4*hf + t%4 for t = 0..7 -- what lane (p%32, hf)
+// of a 32x32x16 MFMA holds for k-chunk kk, both as the A operand of S^T = K Q^T and, for Q,
+// as its B operand, and what the D^T accumulator of the projection holds in registers
+// 8*kk .. 8*kk+7.  The dot product q.k is invariant under this common dim permutation.
+__host__ __device__ __forceinline__ int64_t ql_off(int r, int h, int H, int NP, int p, int kk, int hf) {
+  return ((((int64_t)r * H + h) * (NP >> 5) + (p >> 5)) * 4 + kk * 2 + hf) * 256 + (p & 31) * 8;
+}
+// V^T of (row r, head h): 16-key chunk c16, lane half hf, dim d.  The 8 values are keys
+// 16*c16 + 8*(t/4) + 4*hf + t%4 (PV slot order: the keys whose weights lane half hf holds).
+__host__ __device__ __forceinline__ int64_t vl_off(int r, int h, int H, int NP, int c16, int hf, int d) {
+  return ((((int64_t)r * H + h) * (NP >> 4) + c16) * 2 + hf) * 256 + d * 8;
 }
 
+constexpr int kPC = 128;              // channels (C) handled by the fast path
+constexpr int kWP = kPC + 8;          // LDS pitch (elements) of weight rows
+constexpr int kPWaves = 8;            // waves per projection / output workgroup
+constexpr int kPCols = 17 * 32;       // q k v g (4 x 128) + bias block (32, 4 used)
+
 struct FastWs {
-  uint16_t *q, *k, *vt, *g, *bias, *o;
+  uint16_t *q, *k, *vt, *g, *bias, *o, *wf;
+  float* off;
   size_t bytes;
 };
 
@@ -65,8 +83,37 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.g = (uint16_t*)(p + off); off += round_up(E * 2);
   w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
   w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
+  w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
+  w.off = (float*)(p + off); off += round_up((size_t)kPCols * 4);
   w.bytes = off;
   return w;
+}
+
+// ---------------------------------------------------------------------------------------
+// 0. weight fold: wf[n][c] = bf16(w[n][c] * gamma[c]), off[n] = sum_c beta[c] w[n][c];
+//    rows 516..543 (padding of the bias block) are zero.  One wave per weight row.
+// ---------------------------------------------------------------------------------------
+struct TriFoldArgs {
+  int nrows;                          // 4 * H * 32 + H
+  const uint16_t* w;                  // [nrows, 128]
+  const float* ln_w; const float* ln_b;
+  uint16_t* wf; float* off;           // [544, 128], [544]
+};
+
+__global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= kPCols) return;
+  const int c = 2 * lane;
+  float w0 = 0.f, w1 = 0.f;
+  if (n < a.nrows) {
+    const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.w + (int64_t)n * kPC + c);
+    w0 = bflo(raw); w1 = bfhi(raw);
+  }
+  *reinterpret_cast<uint32_t*>(a.wf + (int64_t)n * kPC + c) = pack_bf2(w0 * a.ln_w[c], w1 * a.ln_w[c + 1]);
+  const float part = a.ln_b != nullptr ? a.ln_b[c] * w0 + a.ln_b[c + 1] * w1 : 0.f;
+  const float tot = wave_sum(part);
+  if (lane == 0) a.off[n] = tot;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -76,16 +123,10 @@ struct TriProjArgs {
   int N, NP, H, transpose;
   float qscale;                       // softmax scale * log2(e)
   const uint16_t* z; const uint8_t* seq;
-  const float* ln_w; const float* ln_b;
-  const uint16_t* w;                  // [4*H*32 + H, C]
+  const uint16_t* wf; const float* off;   // folded weight [544, 128] and column offsets
   uint16_t *q, *k, *vt, *g, *bias;
   int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
-
-constexpr int kPC = 128;              // channels (C) handled by the fast path
-constexpr int kWP = kPC + 8;          // LDS pitch (elements) of weight rows
-constexpr int kPWaves = 8;            // waves per projection / output workgroup
-constexpr int kPCols = 17 * 32;       // q k v g (4 x 128) + bias block (32, 4 used)
 
 // LN of the 32 positions of a block, straight into MFMA operand registers: lane (li, half)
 // holds channels 16*kk + 8*half .. +7 of position li for kk = 0..7 -- the same registers serve
@@ -118,37 +159,20 @@ __device__ __forceinline__ void ln_operands(const u32x4 (&x)[8], bool valid, bf1
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// 1. LN + projection.  Persistent: each workgroup keeps the packed weight (gamma folded in,
-//    beta folded into a per-column offset) in LDS and walks 32-position blocks; positions of
-//    attention row r are z[r, p] (starting node) or z[p, r] (ending node).
-// ---------------------------------------------------------------------------------------
+// Persistent: each workgroup keeps the folded weight in LDS and walks 32-position blocks;
+// positions of attention row r are z[r, p] (starting node) or z[p, r] (ending node).
 __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[kPCols * kWP];
-  __shared__ float sOff[kPCols];                        // beta . W per output column
+  __shared__ __attribute__((aligned(16))) float sOff[kPCols];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
-  const int HD = H * 32;                                // 128
-  const int nrows = 4 * HD + H;                         // 516 valid weight rows
 
   for (int t = tid; t < kPCols * (kPC / 8); t += 64 * kPWaves) {
     const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    u32x4 w = u32x4{0, 0, 0, 0};
-    if (n < nrows) {
-      const u32x4 raw = ld16(a.w + (int64_t)n * kPC + c8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf2(bflo(raw[e]) * a.ln_w[c8 + 2 * e], bfhi(raw[e]) * a.ln_w[c8 + 2 * e + 1]);
-    }
-    st16(&sW[n * kWP + c8], w);
+    st16(&sW[n * kWP + c8], ld16(a.wf + (int64_t)n * kPC + c8));
   }
-  for (int n = tid; n < kPCols; n += 64 * kPWaves) {
-    float off = 0.f;
-    if (n < nrows && a.ln_b != nullptr)
-      for (int c = 0; c < kPC; ++c) off += a.ln_b[c] * bf2f(a.w[(int64_t)n * kPC + c]);
-    sOff[n] = off;
-  }
+  for (int n = tid; n < kPCols; n += 64 * kPWaves) sOff[n] = a.off[n];
   __syncthreads();
 
   const int bpr = NP / 32;                              // position blocks per attention row
@@ -161,6 +185,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
   };
+  auto pos_valid = [&](int r, int pe) { return a.transpose ? (pe < N && r < N) : (r < N && pe < N); };
 
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
@@ -176,7 +201,8 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
     if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
     const int p0 = p - li;
 
-    // q, k, g: D^T = W . X^T -> lane = position, 4 consecutive columns per register group
+    // q, k, g: D^T = W . X^T -> lane = position; registers 8*kk .. 8*kk+7 are the 16 bytes
+    // of k-chunk kk in the Q/K/G layout
 #pragma unroll
     for (int which = 0; which < 4; ++which) {
       if (which == 2) continue;
@@ -191,18 +217,25 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
           acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xo[kk], acc);
-        uint16_t* op = dst + ((int64_t)r * NP + p) * HD + 32 * hh;
+        uint16_t* op = dst + ql_off(r, hh, H, NP, p, 0, half);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int n0 = 8 * c + 4 * half;
-          float v[4];
+        for (int kk = 0; kk < 2; ++kk) {
+          const f32x4 o0 = *reinterpret_cast<const f32x4*>(&sOff[32 * nb + 16 * kk + 4 * half]);
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(&sOff[32 * nb + 16 * kk + 8 + 4 * half]);
+          uint32_t w[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = valid ? (acc[4 * c + e] + sOff[32 * nb + n0 + e]) * sc : 0.f;
-          *reinterpret_cast<u32x2*>(op + n0) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+          for (int e = 0; e < 2; ++e) {
+            w[e] = pack_bf2(valid ? (acc[8 * kk + 2 * e] + o0[2 * e]) * sc : 0.f,
+                            valid ? (acc[8 * kk + 2 * e + 1] + o0[2 * e + 1]) * sc : 0.f);
+            w[2 + e] = pack_bf2(valid ? (acc[8 * kk + 4 + 2 * e] + o1[2 * e]) * sc : 0.f,
+                                valid ? (acc[8 * kk + 4 + 2 * e + 1] + o1[2 * e + 1]) * sc : 0.f);
+          }
+          st16(op + kk * 512, u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
-    // v: D = X . W^T -> lane = column d, 4 consecutive positions -> V^T rows
+    // v: D = X . W^T -> lane = dim li; registers 8*cc .. 8*cc+7 are keys of 16-key chunk cc of
+    // this block in PV slot order for lane half `half`
 #pragma unroll
     for (int hh = 0; hh < 4; ++hh) {
       const int nb = 8 + hh;
@@ -214,17 +247,17 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
         acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
       const float off = sOff[32 * nb + li];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int pb = p0 + 8 * c + 4 * half;
-        float v[4];
+      for (int cc = 0; cc < 2; ++cc) {
+        uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int pe = pb + e;
-          const int za = a.transpose ? pe : r, zb = a.transpose ? r : pe;
-          v[e] = (za < N && zb < N) ? acc[4 * c + e] + off : 0.f;
+          const int t0 = 2 * e, t1 = 2 * e + 1;         // slot t -> key 16cc + 8(t/4) + 4half + t%4
+          const int k0 = p0 + 16 * cc + 8 * (t0 >> 2) + 4 * half + (t0 & 3);
+          const int k1 = p0 + 16 * cc + 8 * (t1 >> 2) + 4 * half + (t1 & 3);
+          w[e] = pack_bf2(pos_valid(r, k0) ? acc[8 * cc + t0] + off : 0.f,
+                          pos_valid(r, k1) ? acc[8 * cc + t1] + off : 0.f);
         }
-        const int64_t base = (((int64_t)r * H + hh) * 32 + li) * NP + (pb & ~63) + v_pos64(pb & 63);
-        *reinterpret_cast<u32x2*>(a.vt + base) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        st16(a.vt + vl_off(r, hh, H, NP, (p0 >> 4) + cc, half, li), u32x4{w[0], w[1], w[2], w[3]});
       }
     }
     // bias planes: D = X . Wb^T, lane = head li (< H), 4 consecutive positions
@@ -237,7 +270,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
       if (li < H) {
-        const float off = sOff[4 * HD + li];
+        const float off = sOff[4 * H * 32 + li];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int pb = p0 + 8 * c + 4 * half;
@@ -269,6 +302,9 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 // ---------------------------------------------------------------------------------------
 // 3. output projection + residual: out[p] = z[p] + o[p] . W_o^T over the N*N pair positions,
 //    W_o resident in LDS; lane = position, 4 consecutive output channels per register group.
+//    Within each head, o holds its 32 dims in the order the attention epilogue produces them
+//    (lane half hf, register group c, element e -> dim 8c + 4hf + e); W_o's columns are
+//    permuted to match when they are staged in LDS.
 // ---------------------------------------------------------------------------------------
 struct TriOutArgs {
   int64_t P;                          // N * N
@@ -285,7 +321,13 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   const int half = lane >> 5, li = lane & 31;
   for (int t = tid; t < kPC * (kPC / 8); t += 64 * kPWaves) {
     const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    st16(&sW[n * kWP + c8], ld16(a.wo + (int64_t)n * kPC + c8));
+    // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
+    // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head
+    const int hd = c8 & ~31, hf = (c8 >> 4) & 1, j = (c8 >> 3) & 1;
+    const uint16_t* src = a.wo + (int64_t)n * kPC + hd + 16 * j + 4 * hf;
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
+    st16(&sW[n * kWP + c8], u32x4{lo[0], lo[1], hi[0], hi[1]});
   }
   __syncthreads();
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
@@ -338,34 +380,41 @@ struct TriAttnArgs {
   int N, NP, H, transpose;
   const uint16_t *q, *k, *vt, *g, *bias;
   const uint8_t* seq;
-  uint16_t* o;                        // [N][N][H][32] at pair positions
+  uint16_t* o;                        // [N][N][H][32] at pair positions, dims in epilogue order
 };
 
 constexpr int kTR = 4;                // rows per workgroup
 constexpr int kKT = 64;               // keys per tile
+constexpr int kAW = 8;                // waves per attention workgroup (256 queries)
 
 typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
-// One LDS tile buffer (all 16-byte slots, XOR-swizzled so that the MFMA operand reads of any
-// 8 consecutive lanes hit 8 distinct slot positions of a 128-byte window):
-//   K    [row rr][key 0..63][slot 0..3]   slot = d-chunk ^ ((key >> 1) & 3)      16 KB
-//   V^T  [row rr][d 0..31][slot 0..7]     slot = key-chunk ^ (d & 7)             16 KB
-//   bias [query 0..32W-1][slot 0..7]      slot = key-piece ^ (query & 7)   W x 4 KB
-// Every 1 KB of it is filled by one global_load_lds_dwordx4 (lane L -> bytes 16L..16L+15).
-template <int W>
+// One LDS tile buffer, all in 16-byte slots; every 1 KB of it is filled by one
+// global_load_lds_dwordx4 (lane L -> bytes 16L..16L+15):
+//   K    [row rr][key block 2][k-chunk 2][lane half 2][key 32]   copied as stored     16 KB
+//   V^T  [row rr][16-key chunk 4][lane half 2][dim 32]          copied as stored     16 KB
+//   bias [query/8][key-piece 0..7][query%8]                                          32 KB
+// The operand reads of consecutive lanes are consecutive slots (bank-conflict free), and
+// every read of a lane is one per-lane base plus a compile-time offset.
 struct TileLayout {
-  static constexpr int kKBytes = kTR * kKT * 64;
-  static constexpr int kVBytes = kTR * 32 * 128;
-  static constexpr int kBBytes = 32 * W * 128;
-  static constexpr int kBytes = kKBytes + kVBytes + kBBytes;
+  static constexpr int kKBytes = kTR * kKT * 32 * 2;
+  static constexpr int kVBytes = kTR * kKT * 32 * 2;
+  static constexpr int kBBytes = kAW * 32 * kKT * 2;
+  static constexpr int kKVBytes = kKBytes + kVBytes;
+  static constexpr int kBytes = kKVBytes + kBBytes;
+  // K / V^T of both buffers first, then the two bias buffers: every operand read is one of
+  // two per-lane bases plus an offset that fits the 16-bit LDS immediate
+  static constexpr int kBiasBase = 2 * kKVBytes;
+  __device__ static constexpr int chunk_offset(int buf, int c) {
+    return c * 1024 < kKVBytes ? buf * kKVBytes + c * 1024 : kBiasBase + buf * kBBytes + c * 1024 - kKVBytes;
+  }
   static constexpr int kChunks = kBytes / 1024;
-  static constexpr int kChunksPerWave = kChunks / W;
-  static_assert(kChunks % W == 0, "tile chunks must split evenly over the waves");
+  static constexpr int kChunksPerWave = kChunks / kAW;
+  static_assert(kChunks % kAW == 0, "tile chunks must split evenly over the waves");
 };
 
-template <int W>
-__global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
-  using TL = TileLayout<W>;
+__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) {
+  using TL = TileLayout;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar branches
@@ -374,7 +423,7 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
 
   // ---- workgroup -> (head, row group, query block); XCD-major so that the workgroups an XCD
   //      runs together share the head's bias plane and the row group's K/V tiles in its L2 ----
-  const int QB = (NP + 32 * W - 1) / (32 * W), RG = NP / kTR;
+  const int QB = (NP + 32 * kAW - 1) / (32 * kAW), RG = NP / kTR;
   const int total = QB * RG * H;
   int t = blockIdx.x;
   if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
@@ -382,59 +431,49 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
   const int rg = (t / QB) % RG;
   const int h = t / (QB * RG);
   const int r0 = rg * kTR;
-  const int i = qb * 32 * W + 32 * wave + li;      // this lane's query
+  const int i = qb * 32 * kAW + 32 * wave + li;     // this lane's query
   const int iq = min(i, NP - 1);                    // operand row for loads (results of i >= N unused)
+  const bool active = qb * 32 * kAW + 32 * wave < NP;   // uniform: the wave has queries below NP
 
-  // ---- tile loader: this wave's 1 KB chunks of the next tile, straight into LDS.  Every chunk
-  //      address is a wave-uniform base plus one of two per-lane offsets (the swizzle only
-  //      depends on the lane): K rows (lane/4 keys, slot lane%4) or 128-byte rows (V^T dims and
-  //      bias queries, lane/8 rows, slot lane%8). ----
-  const int koff = (lane >> 2) * H * 32 + 8 * ((lane & 3) ^ ((lane >> 3) & 3));
-  const int roff = (lane >> 3) * NP + 8 * ((lane & 7) ^ ((lane >> 3) & 7));
+  // ---- tile loader: this wave's 1 KB chunks of the next tile, straight into LDS.  K and V^T
+  //      chunks are 1 KB of contiguous memory; bias chunks are 8 query rows of 128 bytes.
+  //      Every chunk address is a wave-uniform base plus one of two per-lane offsets. ----
+  const int64_t rstride = (int64_t)H * NP * 32;             // row stride of the Q/K/G and V^T layouts
+  const uint16_t* kbase = a.k + ql_off(r0, h, H, NP, 0, 0, 0);
+  const uint16_t* vbase = a.vt + vl_off(r0, h, H, NP, 0, 0, 0);
+  const uint16_t* bbase = a.bias + (int64_t)h * NP * NP;
+  const uint32_t lane16 = (uint32_t)lane * 16u;             // byte offsets: K / V^T chunks ...
+  const uint32_t roffb = (uint32_t)((lane & 7) * NP + 8 * (lane >> 3)) * 2u;   // ... bias: row L%8, piece L/8
   auto load_tile = [&](int j0, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerWave; ++u) {
       const int c = wave * TL::kChunksPerWave + u;             // uniform
-      const uint16_t* base;
-      int off;
-      if (c < 16) {                                            // K: row c/4, keys (c%4)*16 + lane/4
-        const int r = min(r0 + (c >> 2), NP - 1);
-        base = a.k + (((int64_t)r * NP + j0 + (c & 3) * 16) * H + h) * 32;
-        off = koff;
-      } else if (c < 32) {                                     // V^T: row (c-16)/4, dims ((c-16)%4)*8 + lane/8
-        const int r = min(r0 + ((c - 16) >> 2), NP - 1);
-        base = a.vt + (((int64_t)r * H + h) * 32 + ((c - 16) & 3) * 8) * NP + j0;
-        off = roff;
-      } else {                                                 // bias: query rows (c-32)*8 + lane/8
-        const int q0 = min(qb * 32 * W + (c - 32) * 8, NP - 8);
-        base = a.bias + ((int64_t)h * NP + q0) * NP + j0;
-        off = roff;
-      }
-      __builtin_amdgcn_global_load_lds(base + off, (lds_u32*)(smem + buf * TL::kBytes + c * 1024), 16, 0, 0);
+      const int cq = c & 15;                                    // K / V^T: row cq/4, quarter cq%4
+      const uint16_t* kv = (c < 16 ? kbase : vbase) + (cq >> 2) * rstride + (int64_t)j0 * 32 + (cq & 3) * 512;
+      const int q0 = min(qb * 32 * kAW + (c - 32) * 8, NP - 8);   // bias: query rows q0 .. q0+7
+      const char* base = (const char*)(c < 32 ? kv : bbase + (int64_t)q0 * NP + j0);
+      const uint32_t off = c < 32 ? lane16 : roffb;
+      __builtin_amdgcn_global_load_lds(base + off, (lds_u32*)(smem + TL::chunk_offset(buf, c)), 16, 0, 0);
     }
   };
-  auto kslot = [&](int buf, int rr, int key, int dc) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + buf * TL::kBytes + ((rr * kKT + key) * 4 + (dc ^ ((key >> 1) & 3))) * 16;
+  auto kslot = [&](int buf, int rr, int kb, int kk) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kKVBytes + rr * 4096 + (kb * 4 + kk * 2 + half) * 512 + li * 16;
   };
-  auto vslot = [&](int buf, int rr, int d, int kc) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + buf * TL::kBytes + TL::kKBytes + ((rr * 32 + d) * 8 + (kc ^ (d & 7))) * 16;
+  auto vslot = [&](int buf, int rr, int c2) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kKVBytes + TL::kKBytes + rr * 4096 + (c2 * 2 + half) * 512 + li * 16;
   };
   auto bslot = [&](int buf, int row, int pc) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + buf * TL::kBytes + TL::kKBytes + TL::kVBytes + (row * 8 + (pc ^ (row & 7))) * 16;
+    return smem + TL::kBiasBase + buf * TL::kBBytes + (row >> 3) * 1024 + pc * 128 + (row & 7) * 16;
   };
 
-  // Q operands (B of S^T = K Q^T) for the 4 rows; row validity and padding are uniform.
+  // Q operands (B of S^T = K Q^T) for the 4 rows.  Rows past N hold zeros and are never stored.
+  const int qlane = (int)(ql_off(0, 0, H, NP, iq, 0, half));   // lane offset within a (row, head)
+  const uint16_t* qbase = a.q + ql_off(r0, h, H, NP, 0, 0, 0);
   bf16x8 qb8[kTR][2];
-  bool rvalid[kTR], rmasked[kTR];
 #pragma unroll
-  for (int rr = 0; rr < kTR; ++rr) {
-    const int r = r0 + rr;
-    rvalid[rr] = r < N;
-    rmasked[rr] = rvalid[rr] && __builtin_amdgcn_readfirstlane((int)a.seq[min(r, N - 1)]) == 0;
-    const uint16_t* qp = a.q + (((int64_t)r * NP + iq) * H + h) * 32;
+  for (int rr = 0; rr < kTR; ++rr)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(qp + 16 * kk + 8 * half));
-  }
+    for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + qlane + kk * 512));
   // Online softmax state.  m is the reference point of the exponentials (shared by the two
   // lanes holding the same query), kept bf16-exact because it enters the S^T MFMA through an
   // extra k-step: [K | 1] . [Q | -m]^T + bias = logit - m, so after tile 0 the weights are
@@ -474,28 +513,21 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
   };
   // S^T of row rr (64 keys x 32 queries) from the K tile in LDS, seeded with the bias tile;
   // with_m adds the k-step that subtracts the row's reference point.
-  auto qk = [&](int rr, int buf, f32x16 (&s)[2], bool with_m) {
+  auto qk = [&](int rr, int buf, f32x16 (&s)[2], bool with_m) __attribute__((always_inline)) {
     bf16x8 mq;
 #pragma unroll
     for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
     mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, 32 * kb + li, half)));
-      const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, 32 * kb + li, 2 + half)));
+      const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
+      const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
       s[kb] = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
       if (with_m) s[kb] = mfma32(ones_k, mq, s[kb]);
     }
   };
-  // padded token: every key masked, weights uniform over the keys below N (relative logit 0)
-  auto masked_logits = [&](f32x16 (&s)[2]) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = (bseed[kb][e] == -INFINITY) ? -INFINITY : 0.0f;
-  };
   // weights 2^(s - shift) as packed bf16 pairs in PV slot order; returns their sum
-  auto weights = [&](const f32x16 (&s)[2], float shift, bf16x2 (&pw)[16]) {
+  auto weights = [&](const f32x16 (&s)[2], float shift, bf16x2 (&pw)[16]) __attribute__((always_inline)) {
     float ts = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -506,7 +538,7 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
       }
     return ts;
   };
-  auto tile_max = [&](const f32x16 (&s)[2]) {
+  auto tile_max = [&](const f32x16 (&s)[2]) __attribute__((always_inline)) {
     float v = s[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -526,7 +558,7 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
     for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
     return weights(s, shift, pw);
   };
-  auto pv = [&](int rr, int buf, const bf16x2 (&pw)[16]) {
+  auto pv = [&](int rr, int buf, const bf16x2 (&pw)[16]) __attribute__((always_inline)) {
 #pragma unroll
     for (int c2 = 0; c2 < 4; ++c2) {
       bf16x8 pb;                     // P^T chunk c2: pairs 4*c2 .. 4*c2+3
@@ -535,11 +567,11 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
         pb[2 * q2] = pw[4 * c2 + q2][0];
         pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
       }
-      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, li, 2 * c2 + half))), pb, o[rr]);
+      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, c2))), pb, o[rr]);
     }
   };
   // one row of a tile after tile 0: weights against m, rare rescale, accumulate
-  auto step = [&](int rr, int buf, const f32x16 (&s)[2]) {
+  auto step = [&](int rr, int buf, const f32x16 (&s)[2]) __attribute__((always_inline)) {
     bf16x2 pw[16];
     float ts = weights(s, 0.0f, pw);
     if (__any(!(ts <= kMassLimit))) ts = move_reference(rr, s, pw);
@@ -548,27 +580,26 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
   };
 
   const int ntiles = NP / kKT;
-  const int last_rr = min(kTR - 1, N - 1 - r0);            // last row of this group below N
 
   load_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
   // ---- tile 0: the reference point starts at the tile's row maximum ----
   if (ntiles > 1) load_tile(kKT, 1);
-  load_bias(0);
+  if (active) {
+    load_bias(0);
 #pragma unroll
-  for (int rr = 0; rr < kTR; ++rr) {
-    if (!rvalid[rr]) continue;
-    f32x16 s[2];
-    qk(rr, 0, s, false);
-    if (rmasked[rr]) masked_logits(s);
-    const float smax = tile_max(s);
-    // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
-    const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
-    m[rr] = m0;
-    bf16x2 pw[16];
-    l[rr] = weights(s, m0, pw);
-    pv(rr, 0, pw);
+    for (int rr = 0; rr < kTR; ++rr) {
+      f32x16 s[2];
+      qk(rr, 0, s, false);
+      const float smax = tile_max(s);
+      // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
+      const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
+      m[rr] = m0;
+      bf16x2 pw[16];
+      l[rr] = weights(s, m0, pw);
+      pv(rr, 0, pw);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -578,14 +609,14 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
     constexpr int buf = decltype(bufc)::value;
     const int j0 = tt * kKT;
     if (tt + 1 < ntiles) load_tile(j0 + kKT, buf ^ 1);     // lands while this tile computes
-    load_bias(buf);
+    if (active) {
+      load_bias(buf);
 #pragma unroll
-    for (int rr = 0; rr < kTR; ++rr) {
-      if (!rvalid[rr]) continue;
-      f32x16 s[2];
-      qk(rr, buf, s, true);
-      if (rmasked[rr]) masked_logits(s);
-      step(rr, buf, s);
+      for (int rr = 0; rr < kTR; ++rr) {
+        f32x16 s[2];
+        qk(rr, buf, s, true);
+        step(rr, buf, s);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -597,23 +628,68 @@ __global__ __launch_bounds__(64 * W) void tri_attn_kernel(const TriAttnArgs a) {
 
   // ---- epilogue: normalise, gate, store at the pair position ----
   if (i >= N) return;
+  const uint16_t* gbase = a.g + ql_off(r0, h, H, NP, 0, 0, 0);
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
     const int r = r0 + rr;
     if (r >= N) continue;
     const float lt = l[rr] + __shfl_xor(l[rr], 32);
     const float inv = fast_rcp(lt);
-    const uint16_t* gp = a.g + (((int64_t)r * NP + i) * H + h) * 32;
     const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-    uint16_t* op = a.o + (((int64_t)za * N + zb) * H + h) * 32;
+    uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * half;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d0 = 8 * c + 4 * half;
-      const u32x2 gw = *reinterpret_cast<const u32x2*>(gp + d0);
-      const float g0 = bflo(gw[0]), g1 = bfhi(gw[0]), g2 = bflo(gw[1]), g3 = bfhi(gw[1]);
-      const float v0 = o[rr][4 * c] * inv * sigmoidf_(g0), v1 = o[rr][4 * c + 1] * inv * sigmoidf_(g1);
-      const float v2 = o[rr][4 * c + 2] * inv * sigmoidf_(g2), v3 = o[rr][4 * c + 3] * inv * sigmoidf_(g3);
-      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack_bf2(v0, v1), pack_bf2(v2, v3)};
+    for (int kk = 0; kk < 2; ++kk) {
+      const u32x4 gw = ld16(gbase + rr * rstride + qlane + kk * 512);   // dims of registers 8kk..8kk+7
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv * sigmoidf_(bflo(gw[e])),
+                        o[rr][8 * kk + 2 * e + 1] * inv * sigmoidf_(bfhi(gw[e])));
+      st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
+// reference's softmax is uniform over the N keys: o = sigmoid(g) * mean_k V[r, k].
+// One workgroup per row; rows with seq[r] != 0 return at once.  Keys past N hold V = 0.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tri_masked_kernel(const TriAttnArgs a) {
+  const int r = blockIdx.x;
+  if (r >= a.N || a.seq[r] != 0) return;
+  __shared__ float mean[4 * 32];
+  const int tid = threadIdx.x, N = a.N, NP = a.NP, H = a.H;
+  if (tid < H * 32) {
+    const int h = tid >> 5, d = tid & 31;
+    float s = 0.f;
+    for (int c16 = 0; c16 < NP / 16; ++c16)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const u32x4 v = ld16(a.vt + vl_off(r, h, H, NP, c16, hf, d));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += bflo(v[e]) + bfhi(v[e]);
+      }
+    mean[tid] = s / (float)N;
+  }
+  __syncthreads();
+  // one (query, head, lane half) per thread: 16 dims in epilogue order
+  for (int t = tid; t < N * H * 2; t += 256) {
+    const int hf = t & 1, h = (t >> 1) % H, i = (t >> 1) / H;
+    const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
+    uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const u32x4 gw = ld16(a.g + ql_off(r, h, H, NP, i, kk, hf));
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t0 = 2 * e, t1 = 2 * e + 1;          // register 8kk + t -> dim 16kk + 8(t/4) + 4hf + t%4
+        const float m0 = mean[h * 32 + 16 * kk + 8 * (t0 >> 2) + 4 * hf + (t0 & 3)];
+        const float m1 = mean[h * 32 + 16 * kk + 8 * (t1 >> 2) + 4 * hf + (t1 & 3)];
+        w[e] = pack_bf2(m0 * sigmoidf_(bflo(gw[e])), m1 * sigmoidf_(bfhi(gw[e])));
+      }
+      st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
 }
@@ -669,31 +745,35 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     return 1;
   }
   const int NP = round64(N);
-  TriProjArgs pa{};
-  pa.N = N; pa.NP = NP; pa.H = H; pa.transpose = a->transpose;
-  pa.qscale = (1.0f / sqrtf(32.0f)) * SF_LOG2E;
-  pa.z = (const uint16_t*)a->z; pa.seq = a->seq_mask; pa.ln_w = a->ln_w; pa.ln_b = a->ln_b;
-  pa.w = (const uint16_t*)a->w_qkvgb;
-  pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.g = ws.g; pa.bias = ws.bias;
-  pa.items = NP * (NP / 32);
-  const int pgroups = persistent_groups(pa.items, &pa.items_per_wave);
   if (stages & SF_TRI_STAGE_PROJECT) {
+    TriFoldArgs fa{};
+    fa.nrows = 4 * H * 32 + H;
+    fa.w = (const uint16_t*)a->w_qkvgb; fa.ln_w = a->ln_w; fa.ln_b = a->ln_b;
+    fa.wf = ws.wf; fa.off = ws.off;
+    hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4), dim3(256), 0, st, fa);
+    if (int rc = sf_check_launch("tri_fold_kernel")) return rc;
+
+    TriProjArgs pa{};
+    pa.N = N; pa.NP = NP; pa.H = H; pa.transpose = a->transpose;
+    pa.qscale = (1.0f / sqrtf(32.0f)) * SF_LOG2E;
+    pa.z = (const uint16_t*)a->z; pa.seq = a->seq_mask;
+    pa.wf = ws.wf; pa.off = ws.off;
+    pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.g = ws.g; pa.bias = ws.bias;
+    pa.items = NP * (NP / 32);
+    const int pgroups = persistent_groups(pa.items, &pa.items_per_wave);
     hipLaunchKernelGGL(tri_proj_kernel, dim3(pgroups), dim3(64 * kPWaves), 0, st, pa);
     if (int rc = sf_check_launch("tri_proj_kernel")) return rc;
   }
 
-  TriAttnArgs aa{};
-  aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
-  aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.g = ws.g; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
   if (stages & SF_TRI_STAGE_ATTEND) {
-    if (NP % 256 == 0) {
-      const int total = (NP / 256) * (NP / kTR) * H;
-      hipLaunchKernelGGL(tri_attn_kernel<8>, dim3(total), dim3(512), 0, st, aa);
-    } else {
-      const int total = ((NP + 127) / 128) * (NP / kTR) * H;
-      hipLaunchKernelGGL(tri_attn_kernel<4>, dim3(total), dim3(256), 0, st, aa);
-    }
+    TriAttnArgs aa{};
+    aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
+    aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.g = ws.g; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
+    const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;
+    hipLaunchKernelGGL(tri_attn_kernel, dim3(total), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
+    hipLaunchKernelGGL(tri_masked_kernel, dim3(N), dim3(256), 0, st, aa);
+    if (int rc = sf_check_launch("tri_masked_kernel")) return rc;
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
 
