@@ -444,16 +444,30 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   const uint16_t* bbase = a.bias + (int64_t)h * NP * NP;
   const uint32_t lane16 = (uint32_t)lane * 16u;             // byte offsets: K / V^T chunks ...
   const uint32_t roffb = (uint32_t)((lane & 7) * NP + 8 * (lane >> 3)) * 2u;   // ... bias: row L%8, piece L/8
+  // Waves 0-1 fetch K (rows 2w, 2w+1), waves 2-3 V^T (rows 2(w-2), 2(w-2)+1), waves 4-7 the bias
+  // rows of queries 64(w-4) .. +63 of the block; chunk u of a wave is then a uniform base plus
+  // a compile-time multiple of the wave's two strides.
+  const char* wsrc;
+  int64_t wrow;                          // bytes between the wave's chunks 4 apart (K / V^T rows)
+  int wq, wj, wlim;                      // bytes per quarter / per key; bias: last chunk row offset
+  uint32_t woff;
+  if (wave < 4) {
+    const uint16_t* b0 = wave < 2 ? kbase + 2 * wave * rstride : vbase + 2 * (wave - 2) * rstride;
+    wsrc = (const char*)b0; wrow = rstride * 2; wq = 1024; wj = 64; wlim = 0; woff = lane16;
+  } else {
+    const int q0 = qb * 32 * kAW + (wave - 4) * 64;
+    wsrc = (const char*)(bbase + (int64_t)q0 * NP); wrow = 0; wq = 16 * NP; wj = 2;
+    wlim = NP - 8 - q0;                  // query rows past NP - 8 are clamped (idle waves only)
+    woff = roffb;
+  }
   auto load_tile = [&](int j0, int buf) __attribute__((always_inline)) {
+    const char* src = wsrc + (int64_t)j0 * wj;
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerWave; ++u) {
-      const int c = wave * TL::kChunksPerWave + u;             // uniform
-      const int cq = c & 15;                                    // K / V^T: row cq/4, quarter cq%4
-      const uint16_t* kv = (c < 16 ? kbase : vbase) + (cq >> 2) * rstride + (int64_t)j0 * 32 + (cq & 3) * 512;
-      const int q0 = min(qb * 32 * kAW + (c - 32) * 8, NP - 8);   // bias: query rows q0 .. q0+7
-      const char* base = (const char*)(c < 32 ? kv : bbase + (int64_t)q0 * NP + j0);
-      const uint32_t off = c < 32 ? lane16 : roffb;
-      __builtin_amdgcn_global_load_lds(base + off, (lds_u32*)(smem + TL::chunk_offset(buf, c)), 16, 0, 0);
+      const char* cs = wave < 4 ? src + (u >> 2) * wrow + (u & 3) * wq
+                                : src + (int64_t)min(8 * u, wlim) * (2 * NP);
+      __builtin_amdgcn_global_load_lds(cs + woff, (lds_u32*)(smem + TL::chunk_offset(buf, wave * TL::kChunksPerWave + u)),
+                                       16, 0, 0);
     }
   };
   auto kslot = [&](int buf, int rr, int kb, int kk) __attribute__((always_inline)) -> const uint8_t* {
@@ -478,8 +492,8 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   // lanes holding the same query), kept bf16-exact because it enters the S^T MFMA through an
   // extra k-step: [K | 1] . [Q | -m]^T + bias = logit - m, so after tile 0 the weights are
   // exp2 of the MFMA output directly.  Tile 0 sets m to its row maximum; later tiles move it
-  // only when a tile's probability mass exceeds kMassLimit (all weights are >= 0, so the sum
-  // bounds every single weight and nothing can overflow unnoticed).
+  // only when the probability mass of a 32-key half exceeds kMassLimit (all weights are >= 0,
+  // so the sum bounds every single weight and nothing can overflow unnoticed).
   constexpr float kMassLimit = 1.152921504606847e18f;   // 2^60
   f32x16 o[kTR];
   float m[kTR], l[kTR];
@@ -511,72 +525,48 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       }
     }
   };
-  // S^T of row rr (64 keys x 32 queries) from the K tile in LDS, seeded with the bias tile;
-  // with_m adds the k-step that subtracts the row's reference point.
-  auto qk = [&](int rr, int buf, f32x16 (&s)[2], bool with_m) __attribute__((always_inline)) {
-    bf16x8 mq;
+  // The work of a tile is split into units (row rr, 32-key half kb): S^T half = 32 keys x 32
+  // queries (3 MFMAs), its 32 weights per lane pair, and their P.V (2 MFMAs).  Units are
+  // software-pipelined: the S^T MFMAs of unit u+1 are issued before the exponentials of unit u.
+  auto qk_half = [&](int rr, int kb, int buf, bool with_m, f32x16& s) __attribute__((always_inline)) {
+    const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
+    const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
+    s = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
+    if (with_m) {
+      bf16x8 mq;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
-    mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
-      const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
-      s[kb] = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
-      if (with_m) s[kb] = mfma32(ones_k, mq, s[kb]);
+      for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
+      mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
+      s = mfma32(ones_k, mq, s);
     }
   };
   // weights 2^(s - shift) as packed bf16 pairs in PV slot order; returns their sum
-  auto weights = [&](const f32x16 (&s)[2], float shift, bf16x2 (&pw)[16]) __attribute__((always_inline)) {
+  auto weights_half = [&](const f32x16& s, float shift, bf16x2 (&pw)[8]) __attribute__((always_inline)) {
     float ts = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pw[8 * kb + e] = cvt_bf2(fast_exp2(s[kb][2 * e] - shift), fast_exp2(s[kb][2 * e + 1] - shift));
-        ts = add_bf2(pw[8 * kb + e], ts);
-      }
+    for (int e = 0; e < 8; ++e) {
+      pw[e] = cvt_bf2(fast_exp2(s[2 * e] - shift), fast_exp2(s[2 * e + 1] - shift));
+      ts = add_bf2(pw[e], ts);
+    }
     return ts;
   };
-  auto tile_max = [&](const f32x16 (&s)[2]) __attribute__((always_inline)) {
-    float v = s[0][0];
+  auto max_half = [&](const f32x16& s) __attribute__((always_inline)) {
+    float v = s[0];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) v = fmaxf(v, s[kb][e]);
+    for (int e = 1; e < 16; ++e) v = fmaxf(v, s[e]);
     return fmaxf(v, __shfl_xor(v, 32));
   };
-  // rare path: this tile's mass passed the limit; s holds logit - m exactly (|m| stays
-  // moderate), so move m up to the tile maximum and rescale what is accumulated
-  auto move_reference = [&](int rr, const f32x16 (&s)[2], bf16x2 (&pw)[16]) {
-    const float mnew = (float)(__bf16)(m[rr] + fmaxf(tile_max(s), 0.f));
-    const float shift = mnew - m[rr];
-    const float alpha = fast_exp2(-shift);
-    m[rr] = mnew;
-    l[rr] *= alpha;
+  auto pv_half = [&](int rr, int kb, int buf, const bf16x2 (&pw)[8]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
-    return weights(s, shift, pw);
-  };
-  auto pv = [&](int rr, int buf, const bf16x2 (&pw)[16]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int c2 = 0; c2 < 4; ++c2) {
-      bf16x8 pb;                     // P^T chunk c2: pairs 4*c2 .. 4*c2+3
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 pb;                     // P^T chunk 2kb+j: pairs 4j .. 4j+3 of the half
 #pragma unroll
       for (int q2 = 0; q2 < 4; ++q2) {
-        pb[2 * q2] = pw[4 * c2 + q2][0];
-        pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
+        pb[2 * q2] = pw[4 * j + q2][0];
+        pb[2 * q2 + 1] = pw[4 * j + q2][1];
       }
-      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, c2))), pb, o[rr]);
+      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, 2 * kb + j))), pb, o[rr]);
     }
-  };
-  // one row of a tile after tile 0: weights against m, rare rescale, accumulate
-  auto step = [&](int rr, int buf, const f32x16 (&s)[2]) __attribute__((always_inline)) {
-    bf16x2 pw[16];
-    float ts = weights(s, 0.0f, pw);
-    if (__any(!(ts <= kMassLimit))) ts = move_reference(rr, s, pw);
-    l[rr] += ts;
-    pv(rr, buf, pw);
   };
 
   const int ntiles = NP / kKT;
@@ -584,21 +574,24 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   load_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
-  // ---- tile 0: the reference point starts at the tile's row maximum ----
+  // ---- tile 0: the reference point starts at the row maximum over the tile ----
   if (ntiles > 1) load_tile(kKT, 1);
   if (active) {
     load_bias(0);
 #pragma unroll
     for (int rr = 0; rr < kTR; ++rr) {
-      f32x16 s[2];
-      qk(rr, 0, s, false);
-      const float smax = tile_max(s);
+      f32x16 s0, s1;
+      qk_half(rr, 0, 0, false, s0);
+      qk_half(rr, 1, 0, false, s1);
+      const float smax = fmaxf(max_half(s0), max_half(s1));
       // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
       const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
       m[rr] = m0;
-      bf16x2 pw[16];
-      l[rr] = weights(s, m0, pw);
-      pv(rr, 0, pw);
+      bf16x2 pw[8];
+      l[rr] = weights_half(s0, m0, pw);
+      pv_half(rr, 0, 0, pw);
+      l[rr] += weights_half(s1, m0, pw);
+      pv_half(rr, 1, 0, pw);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -611,11 +604,34 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     if (tt + 1 < ntiles) load_tile(j0 + kKT, buf ^ 1);     // lands while this tile computes
     if (active) {
       load_bias(buf);
+      f32x16 sc, sn;
+      qk_half(0, 0, buf, true, sc);
 #pragma unroll
-      for (int rr = 0; rr < kTR; ++rr) {
-        f32x16 s[2];
-        qk(rr, buf, s, true);
-        step(rr, buf, s);
+      for (int u = 0; u < 2 * kTR; ++u) {
+        const int rr = u >> 1, kb = u & 1;
+        if (u + 1 < 2 * kTR) qk_half((u + 1) >> 1, (u + 1) & 1, buf, true, sn);
+        bf16x2 pw[8];
+        float ts = weights_half(sc, 0.0f, pw);
+        if (__any(!(ts <= kMassLimit))) {
+          // rare: this half's mass passed the limit; sc holds logit - m exactly (|m| stays
+          // moderate), so move m up to the half's maximum and rescale what is accumulated.
+          // The next unit of the same row was issued against the old m: shift it too.
+          const float mnew = (float)(__bf16)(m[rr] + fmaxf(max_half(sc), 0.f));
+          const float shift = mnew - m[rr];
+          const float alpha = fast_exp2(-shift);
+          m[rr] = mnew;
+          l[rr] *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
+          ts = weights_half(sc, shift, pw);
+          if (kb == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sn[e] -= shift;
+          }
+        }
+        l[rr] += ts;
+        pv_half(rr, kb, buf, pw);
+        sc = sn;
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
