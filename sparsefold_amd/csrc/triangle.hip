@@ -32,6 +32,7 @@
 //   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "sf_common.h"
@@ -378,6 +379,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 
 struct TriAttnArgs {
   int N, NP, H, transpose;
+  float mass_limit;                   // probability mass of a 32-key half that moves the reference
   const uint16_t *q, *k, *vt, *g, *bias;
   const uint8_t* seq;
   uint16_t* o;                        // [N][N][H][32] at pair positions, dims in epilogue order
@@ -492,9 +494,8 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   // lanes holding the same query), kept bf16-exact because it enters the S^T MFMA through an
   // extra k-step: [K | 1] . [Q | -m]^T + bias = logit - m, so after tile 0 the weights are
   // exp2 of the MFMA output directly.  Tile 0 sets m to its row maximum; later tiles move it
-  // only when the probability mass of a 32-key half exceeds kMassLimit (all weights are >= 0,
-  // so the sum bounds every single weight and nothing can overflow unnoticed).
-  constexpr float kMassLimit = 1.152921504606847e18f;   // 2^60
+  // only when the probability mass of a 32-key half exceeds mass_limit (2^60; all weights are
+  // >= 0, so the sum bounds every single weight and nothing can overflow unnoticed).
   f32x16 o[kTR];
   float m[kTR], l[kTR];
 #pragma unroll
@@ -612,7 +613,7 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
         if (u + 1 < 2 * kTR) qk_half((u + 1) >> 1, (u + 1) & 1, buf, true, sn);
         bf16x2 pw[8];
         float ts = weights_half(sc, 0.0f, pw);
-        if (__any(!(ts <= kMassLimit))) {
+        if (__any(!(ts <= a.mass_limit))) {
           // rare: this half's mass passed the limit; sc holds logit - m exactly (|m| stays
           // moderate), so move m up to the half's maximum and rescale what is accumulated.
           // The next unit of the same row was issued against the old m: shift it too.
@@ -753,6 +754,18 @@ int persistent_groups(int items, int* items_per_wave) {
   return (waves + kPWaves - 1) / kPWaves;
 }
 
+// Mass of a 32-key half above which the attention kernel moves its reference point: 2^60, or
+// SPARSEFOLD_HIP_TRI_MASS_LIMIT (a positive finite float) so that tests can drive the rescale
+// path with ordinary logits.  The result does not depend on it beyond rounding.
+float mass_limit() {
+  float v = 1.152921504606847e18f;
+  if (const char* e = getenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT")) {
+    const float f = strtof(e, nullptr);
+    if (f > 0.f && f <= v) v = f;
+  }
+  return v;
+}
+
 int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_bytes, hipStream_t st, int stages) {
   const int32_t N = a->N, H = a->H;
   const FastWs ws = carve_fast(workspace, N, H);
@@ -784,6 +797,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   if (stages & SF_TRI_STAGE_ATTEND) {
     TriAttnArgs aa{};
     aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
+    aa.mass_limit = mass_limit();
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.g = ws.g; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;
     hipLaunchKernelGGL(tri_attn_kernel, dim3(total), dim3(64 * kAW), 0, st, aa);

@@ -65,6 +65,24 @@ def test_triangle_sharp_update_padded(transpose, N):
 
 
 @pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_reference_point_moves(transpose, monkeypatch):
+  """With the mass limit at 1, nearly every 32-key half after the first tile moves the attention
+  kernel's reference point (rescaling o and l, and shifting the already-issued next half of the
+  same row); the result must still match the oracle."""
+  mod, z, seq = W.make_triangle(200, transpose=transpose, padded=True, seed=11, sharp=True)
+  hip = _prepared(mod)
+  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT", raising=False)
+  upd_default = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  monkeypatch.setenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT", "1")
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  # the moved reference points change the rounding, so the rescale path demonstrably ran
+  assert not torch.equal(upd, upd_default)
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert_close_bf16(upd, ref, f"triangle rescale N=200 transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
 def test_triangle_c2_n384_padded(transpose):
   mod, z, seq = W.make_triangle(384, transpose=transpose, padded=True, seed=2)
   hip = _prepared(mod)
