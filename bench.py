@@ -41,8 +41,8 @@ def core_flop(n=N, h=H, d=D) -> float:
 def parse():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
-  ap.add_argument("--steps", type=int, default=20)
-  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--steps", type=int, default=200)
+  ap.add_argument("--warmup", type=int, default=50, help="untimed calls first (the GPU clock ramps up)")
   ap.add_argument("--cpu-baseline", type=int, default=1, help="time the host-CPU math path (rank 0)")
   ap.add_argument("--cpu-rows", type=int, default=128, help="rows in the CPU-baseline sample")
   ap.add_argument("--other-configs", type=int, default=1, help="also time the other four configurations")
@@ -109,7 +109,7 @@ def traffic_from_profile() -> float | None:
 
 
 def _time_call(fn, iters: int) -> float:
-  for _ in range(3):
+  for _ in range(20):
     fn()
   torch.cuda.synchronize()
   return _events_time(fn, iters, torch.cuda.current_stream())

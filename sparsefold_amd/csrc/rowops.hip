@@ -7,6 +7,8 @@
 //   pair_logits_kernel  LN(z) . W -> [H, P] in one pass over z (blocks.py:745-749,
 //                       transformer.py:430-447); HBM-bound on z
 //   window_gather_kernel key-window gather of atom_layout.convert (atom_layout.py:61-83)
+#include <algorithm>
+
 #include "sf_common.h"
 
 namespace {
@@ -408,6 +410,90 @@ __global__ __launch_bounds__(256) void window_gather_kernel(const sf_window_gath
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// ------------------------------------------------------------------------------------
+// Pair logits, C = 128: 32 positions per wave step.  Lane (li, half) loads 8 x 16 bytes of
+// position li (the 32 rows of a step are 8 KB of contiguous memory), normalises them straight
+// into MFMA operands, and D = X . Wf^T against the gamma-folded weight held in LDS gives lane
+// li = head, registers = 4 consecutive positions: 8-byte stores into each bias plane.  Waves
+// stride over the steps, loading step n+1 while step n computes.
+// ------------------------------------------------------------------------------------
+constexpr int kPLWP = 128 + 8;        // LDS pitch (elements) of folded weight rows
+
+template <int HB>  // 32-head blocks (H <= 32 * HB)
+__global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[32 * HB * kPLWP];
+  __shared__ float sOff[32 * HB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, li = lane & 31;
+  const int H = a.H;
+  const uint16_t* wt = (const uint16_t*)a.w_t;
+  // fold: one wave per weight row, lane = 2 channels
+  for (int n = wave; n < 32 * HB; n += 4) {
+    float w0 = 0.f, w1 = 0.f;
+    if (n < H) {
+      const uint32_t raw = *reinterpret_cast<const uint32_t*>(wt + n * 128 + 2 * lane);
+      w0 = bflo(raw); w1 = bfhi(raw);
+    }
+    const float g0 = a.ln_w ? a.ln_w[2 * lane] : 1.f, g1 = a.ln_w ? a.ln_w[2 * lane + 1] : 1.f;
+    *reinterpret_cast<uint32_t*>(&sW[n * kPLWP + 2 * lane]) = pack_bf2(w0 * g0, w1 * g1);
+    const float part = a.ln_b ? a.ln_b[2 * lane] * w0 + a.ln_b[2 * lane + 1] * w1 : 0.f;
+    const float tot = wave_sum(part);
+    if (lane == 0) sOff[n] = tot;
+  }
+  __syncthreads();
+
+  const uint16_t* z = (const uint16_t*)a.z;
+  uint16_t* out = (uint16_t*)a.out;
+  const int64_t P = a.P;
+  const bool vec_out = (P % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+  auto load = [&](int64_t step, u32x4 (&x)[8], bool& valid) {
+    const int64_t p = step * 32 + li;
+    valid = p < P;
+    const uint16_t* zp = z + (valid ? p : 0) * 128 + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+  };
+  int64_t step = (int64_t)blockIdx.x * 4 + wave;
+  u32x4 xn[8];
+  bool vn = false;
+  if (step < steps) load(step, xn, vn);
+  for (; step < steps; step += wstride) {
+    bf16x8 xo[8];
+    ln128_operands(xn, vn, xo);
+    if (step + wstride < steps) load(step + wstride, xn, vn);
+    const int64_t p0 = step * 32;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * hb + li) * kPLWP + 16 * kk + 8 * half])), acc);
+      const int hh = 32 * hb + li;
+      if (hh < H) {
+        const float off = sOff[hh];
+        uint16_t* op = out + (int64_t)hh * P;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t pb = p0 + 8 * c + 4 * half;          // positions pb .. pb+3
+          const float v0 = acc[4 * c] + off, v1 = acc[4 * c + 1] + off;
+          const float v2 = acc[4 * c + 2] + off, v3 = acc[4 * c + 3] + off;
+          if (vec_out && pb + 4 <= P) {
+            *reinterpret_cast<u32x2*>(op + pb) = u32x2{pack_bf2(v0, v1), pack_bf2(v2, v3)};
+          } else {
+            if (pb < P) op[pb] = f2bf(v0);
+            if (pb + 1 < P) op[pb + 1] = f2bf(v1);
+            if (pb + 2 < P) op[pb + 2] = f2bf(v2);
+            if (pb + 3 < P) op[pb + 3] = f2bf(v3);
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream) {
@@ -472,6 +558,13 @@ extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream
   }
   if (!al16(a->z)) { sf_set_error("pair_logits: z must be 16-byte aligned"); return 1; }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->C == 128) {
+    const int64_t steps = (a->P + 31) / 32;
+    const int64_t groups = std::min<int64_t>((steps + 3) / 4, 256 * 8);
+    if (a->H <= 32) hipLaunchKernelGGL(pair_logits128_kernel<1>, dim3((unsigned)groups), dim3(256), 0, st, *a, steps);
+    else hipLaunchKernelGGL(pair_logits128_kernel<2>, dim3((unsigned)groups), dim3(256), 0, st, *a, steps);
+    return sf_check_launch("pair_logits128_kernel");
+  }
   const dim3 grid((unsigned)((a->P + 255) / 256));
   if (a->H <= 4) hipLaunchKernelGGL(pair_logits_kernel<4>, grid, dim3(256), 0, st, *a);
   else if (a->H <= 8) hipLaunchKernelGGL(pair_logits_kernel<8>, grid, dim3(256), 0, st, *a);

@@ -81,6 +81,38 @@ __device__ __forceinline__ u32x4 load8_guard(const uint16_t* row, int d0, int n,
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
+// LayerNorm (eps 1e-5, no affine: gamma / beta are folded into the consuming weight) of 32
+// positions x 128 channels, straight into MFMA operand registers: lane (li, half)
+// holds channels 16*kk + 8*half .. +7 of position li for kk = 0..7 -- the same registers serve
+// as A operand (rows = positions) and as B operand (columns = positions).
+__device__ __forceinline__ void ln128_operands(const u32x4 (&x)[8], bool valid, bf16x8 (&xo)[8]) {
+  float sum = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
+  sum += __shfl_xor(sum, 32);
+  const float mean = sum * (1.0f / 128);
+  float sq = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
+      sq += d0 * d0 + d1 * d1;
+    }
+  sq += __shfl_xor(sq, 32);
+  const float rstd = valid ? rsqrtf(sq * (1.0f / 128) + 1e-5f) : 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd, (bfhi(x[kk][e]) - mean) * rstd);
+      xo[kk][2 * e] = v[0];
+      xo[kk][2 * e + 1] = v[1];
+    }
+}
+
 // Thread-local last-error plumbing shared by all C entry points.
 void sf_set_error(const char* fmt, ...);
 int sf_check_launch(const char* what);

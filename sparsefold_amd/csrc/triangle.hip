@@ -129,37 +129,6 @@ struct TriProjArgs {
   int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
 
-// LN of the 32 positions of a block, straight into MFMA operand registers: lane (li, half)
-// holds channels 16*kk + 8*half .. +7 of position li for kk = 0..7 -- the same registers serve
-// as A operand (rows = positions) and as B operand (columns = positions).
-__device__ __forceinline__ void ln_operands(const u32x4 (&x)[8], bool valid, bf16x8 (&xo)[8]) {
-  float sum = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
-  sum += __shfl_xor(sum, 32);
-  const float mean = sum * (1.0f / kPC);
-  float sq = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
-      sq += d0 * d0 + d1 * d1;
-    }
-  sq += __shfl_xor(sq, 32);
-  const float rstd = valid ? rsqrtf(sq * (1.0f / kPC) + 1e-5f) : 0.f;
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd, (bfhi(x[kk][e]) - mean) * rstd);
-      xo[kk][2 * e] = v[0];
-      xo[kk][2 * e + 1] = v[1];
-    }
-}
-
 // Persistent: each workgroup keeps the folded weight in LDS and walks 32-position blocks;
 // positions of attention row r are z[r, p] (starting node) or z[p, r] (ending node).
 __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArgs a) {
@@ -198,7 +167,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
     bf16x8 xo[8];
     const bool valid = vn;
     const int r = rn, p = pn;                            // this lane's position p (= p0 + li)
-    ln_operands(xn, valid, xo);
+    ln128_operands(xn, valid, xo);
     if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
     const int p0 = p - li;
 

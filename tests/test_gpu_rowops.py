@@ -68,10 +68,14 @@ def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns(K):
   assert_close_bf16(y2, x.float() @ w.float()[:64].t(), "linear ycols")
 
 
-@pytest.mark.parametrize("H,C,with_b", [(4, 128, True), (16, 128, True), (12, 16, False), (64, 128, False)])
-def test_pair_logits(H, C, with_b):
+# C = 128 runs the MFMA kernel (P = 1320: a ragged last 32-position step; P = 1517: P % 4 != 0,
+# scalar stores); other C the per-position kernel.
+@pytest.mark.parametrize("H,C,with_b,shape", [(4, 128, True, (33, 40)), (16, 128, True, (33, 40)),
+                                              (16, 128, True, (37, 41)), (12, 16, False, (33, 40)),
+                                              (64, 128, False, (33, 40)), (40, 128, True, (37, 41))])
+def test_pair_logits(H, C, with_b, shape):
   g = torch.Generator().manual_seed(H * C)
-  z = torch.randn(33, 40, C, generator=g).to(torch.bfloat16)
+  z = torch.randn(*shape, C, generator=g).to(torch.bfloat16)
   lw, lb = 1 + 0.1 * torch.randn(C, generator=g), 0.1 * torch.randn(C, generator=g)
   w = (torch.randn(H, C, generator=g) / C ** 0.5).to(torch.bfloat16)
   out = ops.pair_logits(z.to(DEV), lw.to(DEV), lb.to(DEV) if with_b else None, w.to(DEV))
