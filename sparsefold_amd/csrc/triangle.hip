@@ -65,10 +65,13 @@ __host__ __device__ __forceinline__ int64_t vl_off(int r, int h, int H, int NP, 
 constexpr int kPC = 128;              // channels (C) handled by the fast path
 constexpr int kWP = kPC + 8;          // LDS pitch (elements) of weight rows
 constexpr int kPWaves = 8;            // waves per projection / output workgroup
-constexpr int kPCols = 17 * 32;       // q k v g (4 x 128) + bias block (32, 4 used)
+constexpr int kPCols = 17 * 32;       // folded rows: q k v g (4 x 128) + bias block (32, 4 used)
+// Blocks of 32 folded rows the projection keeps in LDS: q (0-3), k (4-7), v (8-11) and the bias
+// block (16, stored as LDS block 12); the gate rows (12-15) are used by the output kernel.
+constexpr int kProjBlocks = 13;
 
 struct FastWs {
-  uint16_t *q, *k, *vt, *g, *bias, *o, *wf;
+  uint16_t *q, *k, *vt, *bias, *o, *wf;
   float* off;
   size_t bytes;
 };
@@ -81,7 +84,6 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.q = (uint16_t*)(p + off); off += round_up(E * 2);
   w.k = (uint16_t*)(p + off); off += round_up(E * 2);
   w.vt = (uint16_t*)(p + off); off += round_up(E * 2);
-  w.g = (uint16_t*)(p + off); off += round_up(E * 2);
   w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
   w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
   w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
@@ -125,24 +127,25 @@ struct TriProjArgs {
   float qscale;                       // softmax scale * log2(e)
   const uint16_t* z; const uint8_t* seq;
   const uint16_t* wf; const float* off;   // folded weight [544, 128] and column offsets
-  uint16_t *q, *k, *vt, *g, *bias;
+  uint16_t *q, *k, *vt, *bias;
   int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
 
 // Persistent: each workgroup keeps the folded weight in LDS and walks 32-position blocks;
 // positions of attention row r are z[r, p] (starting node) or z[p, r] (ending node).
 __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[kPCols * kWP];
-  __shared__ __attribute__((aligned(16))) float sOff[kPCols];
+  __shared__ __attribute__((aligned(16))) uint16_t sW[kProjBlocks * 32 * kWP];
+  __shared__ __attribute__((aligned(16))) float sOff[kProjBlocks * 32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
 
-  for (int t = tid; t < kPCols * (kPC / 8); t += 64 * kPWaves) {
+  for (int t = tid; t < kProjBlocks * 32 * (kPC / 8); t += 64 * kPWaves) {
     const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    st16(&sW[n * kWP + c8], ld16(a.wf + (int64_t)n * kPC + c8));
+    const int src = n < 12 * 32 ? n : n + 4 * 32;      // LDS block 12 <- folded block 16
+    st16(&sW[n * kWP + c8], ld16(a.wf + (int64_t)src * kPC + c8));
   }
-  for (int n = tid; n < kPCols; n += 64 * kPWaves) sOff[n] = a.off[n];
+  for (int n = tid; n < kProjBlocks * 32; n += 64 * kPWaves) sOff[n] = a.off[n < 12 * 32 ? n : n + 4 * 32];
   __syncthreads();
 
   const int bpr = NP / 32;                              // position blocks per attention row
@@ -164,6 +167,9 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
   int rn = 0, pn = 0;
   if (first < last) block_load(first, xn, vn, rn, pn);
   for (int item = first; item < last; ++item) {
+    // the LDS weights are re-read every item: hoisted out of the loop they would not fit in
+    // registers
+    asm volatile("" ::: "memory");
     bf16x8 xo[8];
     const bool valid = vn;
     const int r = rn, p = pn;                            // this lane's position p (= p0 + li)
@@ -171,12 +177,11 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
     if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
     const int p0 = p - li;
 
-    // q, k, g: D^T = W . X^T -> lane = position; registers 8*kk .. 8*kk+7 are the 16 bytes
-    // of k-chunk kk in the Q/K/G layout
+    // q, k: D^T = W . X^T -> lane = position; registers 8*kk .. 8*kk+7 are the 16 bytes of
+    // k-chunk kk in the Q/K layout
 #pragma unroll
-    for (int which = 0; which < 4; ++which) {
-      if (which == 2) continue;
-      uint16_t* dst = which == 0 ? a.q : (which == 1 ? a.k : a.g);
+    for (int which = 0; which < 2; ++which) {
+      uint16_t* dst = which == 0 ? a.q : a.k;
       const float sc = which == 0 ? a.qscale : 1.0f;
 #pragma unroll
       for (int hh = 0; hh < 4; ++hh) {
@@ -232,7 +237,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
     }
     // bias planes: D = X . Wb^T, lane = head li (< H), 4 consecutive positions
     {
-      const int nb = 16;
+      const int nb = 12;                                // LDS block of the folded bias rows
       f32x16 acc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
@@ -240,7 +245,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
       if (li < H) {
-        const float off = sOff[4 * H * 32 + li];
+        const float off = sOff[32 * nb + li];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int pb = p0 + 8 * c + 4 * half;
@@ -270,23 +275,31 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 }
 
 // ---------------------------------------------------------------------------------------
-// 3. output projection + residual: out[p] = z[p] + o[p] . W_o^T over the N*N pair positions,
-//    W_o resident in LDS; lane = position, 4 consecutive output channels per register group.
-//    Within each head, o holds its 32 dims in the order the attention epilogue produces them
-//    (lane half hf, register group c, element e -> dim 8c + 4hf + e); W_o's columns are
-//    permuted to match when they are staged in LDS.
+// 3. gate + output projection + residual over the N*N pair positions (blocks.py:286-291):
+//      g = LN(z[p]) . W_g^T   (gamma folded into W_g, beta into its offset)
+//      out[p] = z[p] + (o[p] * sigmoid(g)) . W_o^T
+//    The gate of pair position (za, zb) is the gate the attention row used there for both the
+//    starting and the ending node, so it is recomputed here from z instead of being stored.
+//    W_g and W_o are resident in LDS; lane = position.  Within each head, o holds its 32 dims
+//    in the order the attention epilogue produces them (lane half hf, register group c,
+//    element e -> dim 8c + 4hf + e); W_o's columns are permuted to match when staged.
 // ---------------------------------------------------------------------------------------
 struct TriOutArgs {
   int64_t P;                          // N * N
   const uint16_t* o;                  // [P, 128]
   const uint16_t* wo;                 // [128 out, 128 in]
-  const uint16_t* z;                  // residual or nullptr
+  const uint16_t* wg;                 // folded gate rows [128, 128]
+  const float* goff;                  // [128]
+  const uint16_t* z;                  // [P, 128]
+  int add_residual;
   uint16_t* out;
   int items, items_per_wave;          // 32-position blocks
 };
 
 __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
+  __shared__ __attribute__((aligned(16))) uint16_t sG[kPC * kWP];
+  __shared__ __attribute__((aligned(16))) float sGoff[kPC];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   for (int t = tid; t < kPC * (kPC / 8); t += 64 * kPWaves) {
@@ -298,27 +311,37 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
     const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
     const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
     st16(&sW[n * kWP + c8], u32x4{lo[0], lo[1], hi[0], hi[1]});
+    st16(&sG[n * kWP + c8], ld16(a.wg + (int64_t)n * kPC + c8));
   }
+  for (int n = tid; n < kPC; n += 64 * kPWaves) sGoff[n] = a.goff[n];
   __syncthreads();
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
-  auto load = [&](int item, bf16x8 (&x)[8], int64_t& p) {
+  auto load = [&](int item, u32x4 (&xo)[8], u32x4 (&xz)[8], int64_t& p) {
     p = (int64_t)item * 32 + li;
     const bool ok = p < a.P;
     const uint16_t* op = a.o + (ok ? p : 0) * kPC + 8 * half;
+    const uint16_t* zp = a.z + (ok ? p : 0) * kPC + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) x[kk] = as_bf16x8(ok ? ld16(op + 16 * kk) : u32x4{0, 0, 0, 0});
+    for (int kk = 0; kk < 8; ++kk) {
+      xo[kk] = ok ? ld16(op + 16 * kk) : u32x4{0, 0, 0, 0};
+      xz[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    }
   };
-  bf16x8 xn[8];
+  u32x4 on[8], zn[8];
   int64_t pn = 0;
-  if (first < last) load(first, xn, pn);
+  if (first < last) load(first, on, zn, pn);
   for (int item = first; item < last; ++item) {
-    bf16x8 x[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) x[kk] = xn[kk];
+    asm volatile("" ::: "memory");                      // LDS weights are re-read every item
     const int64_t p = pn;
     const bool ok = p < a.P;                             // only the last block has idle lanes
-    if (item + 1 < last) load(item + 1, xn, pn);
+    bf16x8 zo[8];
+    ln128_operands(zn, ok, zo);
+
+    // gate of head nb: D^T = W_g . X^T -> lane (position, half hf) holds natural dims
+    // 8c + 4hf + e in register 4c + e; o operand chunk kk = 2nb + j of lane half h needs the
+    // gate of half j, register 8h + t -- one permlane32 swap per register pair gets it
+    bf16x8 xg[8];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       f32x16 acc;
@@ -326,9 +349,39 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), x[kk], acc);
+        acc = mfma32(as_bf16x8(ld16(&sG[(32 * nb + li) * kWP + 16 * kk + 8 * half])), zo[kk], acc);
+      float sg[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sg[r] = sigmoidf_(acc[r] + sGoff[32 * nb + 8 * (r >> 2) + 4 * half + (r & 3)]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(sg[t]), __float_as_uint(sg[t + 8]), false, false);
+        // sw[0]: gate for chunk 2nb (j = 0), sw[1]: for chunk 2nb + 1 (j = 1), element t
+        sg[t] = __uint_as_float(sw[0]);
+        sg[t + 8] = __uint_as_float(sw[1]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32x4 w = on[2 * nb + j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2 v = cvt_bf2(bflo(w[e]) * sg[8 * j + 2 * e], bfhi(w[e]) * sg[8 * j + 2 * e + 1]);
+          xg[2 * nb + j][2 * e] = v[0];
+          xg[2 * nb + j][2 * e + 1] = v[1];
+        }
+      }
+    }
+    if (item + 1 < last) load(item + 1, on, zn, pn);    // lands during the output projection
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      f32x16 acc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
       if (ok) {
-        const uint16_t* zp = a.z != nullptr ? a.z + p * kPC + 32 * nb + 4 * half : nullptr;
+        const uint16_t* zp = a.add_residual ? a.z + p * kPC + 32 * nb + 4 * half : nullptr;
         uint16_t* outp = a.out + p * kPC + 32 * nb + 4 * half;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -349,7 +402,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 struct TriAttnArgs {
   int N, NP, H, transpose;
   float mass_limit;                   // probability mass of a 32-key half that moves the reference
-  const uint16_t *q, *k, *vt, *g, *bias;
+  const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
   uint16_t* o;                        // [N][N][H][32] at pair positions, dims in epilogue order
 };
@@ -612,9 +665,9 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     if (tt + 1 < ntiles) tile_step(tt + 1, std::integral_constant<int, 0>{});
   }
 
-  // ---- epilogue: normalise, gate, store at the pair position ----
+  // ---- epilogue: normalise and store at the pair position (the gate is applied by the
+  //      output kernel, which recomputes it from z) ----
   if (i >= N) return;
-  const uint16_t* gbase = a.g + ql_off(r0, h, H, NP, 0, 0, 0);
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
     const int r = r0 + rr;
@@ -625,12 +678,10 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * half;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 gw = ld16(gbase + rr * rstride + qlane + kk * 512);   // dims of registers 8kk..8kk+7
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv * sigmoidf_(bflo(gw[e])),
-                        o[rr][8 * kk + 2 * e + 1] * inv * sigmoidf_(bfhi(gw[e])));
+        w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
       st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
@@ -638,8 +689,9 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
 
 // ---------------------------------------------------------------------------------------
 // Rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
-// reference's softmax is uniform over the N keys: o = sigmoid(g) * mean_k V[r, k].
-// One workgroup per row; rows with seq[r] != 0 return at once.  Keys past N hold V = 0.
+// reference's softmax is uniform over the N keys: o = mean_k V[r, k] (gated later, like every
+// other row).  One workgroup per row; rows with seq[r] != 0 return at once.  Keys past N hold
+// V = 0.
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void tri_masked_kernel(const TriAttnArgs a) {
   const int r = blockIdx.x;
@@ -666,14 +718,13 @@ __global__ __launch_bounds__(256) void tri_masked_kernel(const TriAttnArgs a) {
     uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 gw = ld16(a.g + ql_off(r, h, H, NP, i, kk, hf));
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t0 = 2 * e, t1 = 2 * e + 1;          // register 8kk + t -> dim 16kk + 8(t/4) + 4hf + t%4
         const float m0 = mean[h * 32 + 16 * kk + 8 * (t0 >> 2) + 4 * hf + (t0 & 3)];
         const float m1 = mean[h * 32 + 16 * kk + 8 * (t1 >> 2) + 4 * hf + (t1 & 3)];
-        w[e] = pack_bf2(m0 * sigmoidf_(bflo(gw[e])), m1 * sigmoidf_(bfhi(gw[e])));
+        w[e] = pack_bf2(m0, m1);
       }
       st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
     }
@@ -756,7 +807,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     pa.qscale = (1.0f / sqrtf(32.0f)) * SF_LOG2E;
     pa.z = (const uint16_t*)a->z; pa.seq = a->seq_mask;
     pa.wf = ws.wf; pa.off = ws.off;
-    pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.g = ws.g; pa.bias = ws.bias;
+    pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.bias = ws.bias;
     pa.items = NP * (NP / 32);
     const int pgroups = persistent_groups(pa.items, &pa.items_per_wave);
     hipLaunchKernelGGL(tri_proj_kernel, dim3(pgroups), dim3(64 * kPWaves), 0, st, pa);
@@ -767,7 +818,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     TriAttnArgs aa{};
     aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
     aa.mass_limit = mass_limit();
-    aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.g = ws.g; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
+    aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;
     hipLaunchKernelGGL(tri_attn_kernel, dim3(total), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
@@ -779,7 +830,8 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   TriOutArgs oa{};
   oa.P = (int64_t)N * N;
   oa.o = ws.o; oa.wo = (const uint16_t*)a->w_o;
-  oa.z = a->add_residual ? (const uint16_t*)a->z : nullptr;
+  oa.wg = ws.wf + (size_t)12 * 32 * kPC; oa.goff = ws.off + 12 * 32;   // folded gate rows 384..511
+  oa.z = (const uint16_t*)a->z; oa.add_residual = a->add_residual;
   oa.out = (uint16_t*)a->out;
   oa.items = (int)((oa.P + 31) / 32);
   const int ogroups = persistent_groups(oa.items, &oa.items_per_wave);
