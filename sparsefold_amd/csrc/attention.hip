@@ -12,6 +12,8 @@
 //   other 32 in lane^32), masked keys -> SF_MASKED_LOGIT, keys past K -> -inf
 //   O^T(D x 32 queries) += V^T * P^T          P^T fed from registers as the B operand
 // Epilogue: O / l, optional sigmoid gate, bf16 store.
+#include <cstdlib>
+
 #include "sf_common.h"
 
 namespace {
@@ -195,6 +197,303 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(const sf_attention_a
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Direct-to-LDS form (16-byte aligned q/k/v rows, head dims multiple of 8, bias rows 8-byte
+// aligned).  A wave owns 32 queries of one (batch, head).  Keys stream in tiles of 64:
+//   K, V  copied row-major into LDS by global_load_lds_dwordx4 (1 KB per instruction; the
+//         16-byte pieces of a K row are XOR-swizzled by key so that the S^T operand reads of
+//         consecutive lanes hit distinct banks)
+//   S^T   = K Q^T (+ bias tile as the fp32 accumulator seed, + one MFMA k-step that adds the
+//         key-mask column: 0, SF_MASKED_LOGIT for masked keys, kPadKey for keys past K)
+//   P     = exp(scale (S^T - m)) with the running row maximum m of S^T = q.k + bias / scale
+//         (the scale is applied in fp32); lane half h holds keys 8c + 4h + e of each 32-key half
+//   O^T  += V^T P^T, the V^T operand read straight from the row-major V tile with
+//         ds_read_b64_tr_b16: lane (d, h) of 16-lane group G gets the 4 keys the matching P^T
+//         lane holds, for one dim -- no transposed copy of V is ever made.
+// SHARED: the 4 waves of a workgroup are consecutive query blocks of one (batch, head) and
+// share the K/V tiles (cooperative copy, one barrier per tile).  PRIVATE: every wave is an
+// independent (batch, head, query block) task with its own tiles -- for short query ranges
+// (atom windows) and for grids too small to fill the GPU with 128-query workgroups.
+// ---------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint32_t lds_u32a;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+constexpr float kPadKey = -8.507059173023462e37f;  // -2^126: keys past K, below any masked key
+
+struct Attn2Plan {
+  int QB;            // 32-query blocks per (batch, head)
+  int64_t tasks;     // B0 * B1 * H * QB (PRIVATE) or groups of 4 blocks (SHARED)
+  int vec_out;       // 8-byte stores of out / loads of gate
+};
+
+template <int DP>
+struct Attn2Tile {
+  static constexpr int kRowBytes = DP * 2;
+  static constexpr int kKBytes = 64 * kRowBytes;            // one K tile (= one V tile)
+  static constexpr int kBufBytes = 2 * kKBytes;             // K + V
+  static constexpr int kChunks = kBufBytes / 1024;          // 1 KB copies per tile
+  static constexpr int kPieces = DP / 8;                    // 16-byte pieces per row
+  static constexpr int kKeysPerChunk = 1024 / kRowBytes;
+  __device__ static int kswz(int key) { return DP == 32 ? (key >> 2) & 3 : (key >> 1) & 7; }
+  __device__ static int vswz(int key) { return DP == 32 ? 0 : (key >> 1) & 1; }
+};
+
+template <int DP, bool SHARED>
+__global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, const Attn2Plan pl) {
+  using T = Attn2Tile<DP>;
+  constexpr int kWaveBufs = SHARED ? 1 : 4;                 // tile sets in LDS (shared or per wave)
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kWaveBufs * 2 * T::kBufBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, li = lane & 31;
+
+  // ---- task of this wave ----
+  int64_t task;
+  int qblk;
+  if (SHARED) {
+    task = blockIdx.x;                                       // (b, h, group of 4 blocks)
+    const int groups = (pl.QB + 3) / 4;
+    qblk = (int)(task % groups) * 4 + wave;
+    task /= groups;
+  } else {
+    const int64_t t = (int64_t)blockIdx.x * 4 + wave;
+    if (t >= pl.tasks) return;                               // private waves never meet a barrier
+    qblk = (int)(t % pl.QB);
+    task = t / pl.QB;
+  }
+  const int h = (int)(task % a.H);
+  const int64_t b = task / a.H;
+  const int b0 = (int)(b / a.B1), b1 = (int)(b - (int64_t)b0 * a.B1);
+  const int Q = a.Q, K = a.K, D = a.D, Dv = a.Dv;
+  const int i = qblk * 32 + li;                              // this lane's query
+  const int iq = min(i, Q - 1);
+  const bool wactive = qblk * 32 < Q;                        // uniform
+
+  const uint16_t* qp = (const uint16_t*)a.q + b0 * a.q_s[0] + b1 * a.q_s[1] + (int64_t)h * a.q_s[3];
+  const char* kp = (const char*)((const uint16_t*)a.k + b0 * a.k_s[0] + b1 * a.k_s[1] + (int64_t)h * a.k_s[3]);
+  const char* vp = (const char*)((const uint16_t*)a.v + b0 * a.v_s[0] + b1 * a.v_s[1] + (int64_t)h * a.v_s[3]);
+  const uint16_t* bp = a.bias ? (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] +
+                                    (int64_t)h * a.bias_s[2] + (int64_t)iq * a.bias_s[3]
+                              : nullptr;
+  const uint8_t* mkp = a.mask_k ? a.mask_k + b0 * a.mk_s[0] + b1 * a.mk_s[1] : nullptr;
+  bool qvalid = i < Q;
+  if (a.mask_q && i < Q) qvalid = a.mask_q[b0 * a.mq_s[0] + b1 * a.mq_s[1] + (int64_t)i * a.mq_s[2]] != 0;
+  const bool any_qmasked = __any(!qvalid && i < Q);          // uniform
+
+  // ---- Q operand (unscaled: S^T holds q.k + bias / scale, scaled in fp32 at the exp) ----
+  bf16x8 qb[DP / 16];
+#pragma unroll
+  for (int kk = 0; kk < DP / 16; ++kk) {
+    const int d0 = 16 * kk + 8 * half;
+    qb[kk] = as_bf16x8(d0 < D ? ld16(qp + (int64_t)iq * a.q_s[2] + d0) : u32x4{0, 0, 0, 0});
+  }
+  const float cs = a.scale * SF_LOG2E, inv_scale = 1.0f / a.scale;
+
+  // ---- tile copy: chunk c of a tile, K chunks first ----
+  uint8_t* wsm = smem + (SHARED ? 0 : wave * 2 * T::kBufBytes);
+  auto copy_chunk = [&](int c, int j0, int buf) __attribute__((always_inline)) {
+    const bool isk = c < T::kChunks / 2;
+    const int cc = isk ? c : c - T::kChunks / 2;
+    const int key = cc * T::kKeysPerChunk + lane / T::kPieces;
+    const int slot = lane % T::kPieces;
+    int piece = slot ^ (isk ? T::kswz(key) : T::vswz(key));
+    if (8 * piece >= (isk ? D : Dv)) piece = 0;              // dims past D: any finite data
+    const int row = min(j0 + key, K - 1);
+    const char* src = (isk ? kp + (int64_t)row * a.k_s[2] * 2 : vp + (int64_t)row * a.v_s[2] * 2) + piece * 16;
+    __builtin_amdgcn_global_load_lds(src, (lds_u32a*)(wsm + buf * T::kBufBytes + c * 1024), 16, 0, 0);
+  };
+  auto copy_tile = [&](int j0, int buf) __attribute__((always_inline)) {
+    if (SHARED) {
+#pragma unroll
+      for (int u = 0; u < T::kChunks / 4; ++u) copy_chunk(wave * (T::kChunks / 4) + u, j0, buf);
+    } else {
+#pragma unroll
+      for (int u = 0; u < T::kChunks; ++u) copy_chunk(u, j0, buf);
+    }
+  };
+  // ---- bias tile (this lane's query, its 32 keys) and key-mask bits ----
+  u32x2 bnext[8];
+  uint64_t mnext = ~0ull;
+  auto load_side = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {                            // keys j0 + 32(q/4) + 8(q%4) + 4half .. +3
+      const int j = j0 + 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
+      bnext[q] = (bp != nullptr && j + 4 <= K) ? *reinterpret_cast<const u32x2*>(bp + j) : u32x2{0, 0};
+      if (bp != nullptr && j < K && j + 4 > K) {             // ragged end of the key range
+        uint16_t t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = j + e < K ? bp[j + e] : 0;
+        bnext[q] = u32x2{(uint32_t)t[0] | ((uint32_t)t[1] << 16), (uint32_t)t[2] | ((uint32_t)t[3] << 16)};
+      }
+    }
+    const int jl = j0 + lane;
+    const bool kv = jl < K && (mkp == nullptr || mkp[(int64_t)jl * a.mk_s[2]] != 0);
+    mnext = __ballot(kv);
+  };
+
+  f32x16 o[DP / 32];
+#pragma unroll
+  for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  bf16x8 ones_b;                                             // B operand: 1 at k = 0 (half 0)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones_b[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
+
+  const int ntiles = (K + 63) / 64;
+  // Waits: the copies into LDS are ordinary loads to the compiler, so every wait is followed
+  // by a compiler barrier (or __syncthreads) that keeps the LDS reads of the tile after it.
+  copy_tile(0, 0);
+  load_side(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (SHARED) __syncthreads();
+  else asm volatile("" ::: "memory");
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1, j0 = t * 64;
+    const uint8_t* kt = wsm + buf * T::kBufBytes;
+    const uint8_t* vt = kt + T::kKBytes;
+    u32x2 bcur[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
+    const uint64_t mbits = mnext;
+    if (t + 1 < ntiles) {
+      copy_tile(j0 + 64, buf ^ 1);
+      load_side(j0 + 64);
+    }
+    if (wactive) {
+      // ---- S^T = K Q^T + bias (+ mask column) ----
+      const bool need_mask = mbits != ~0ull;                 // uniform
+      f32x16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            s[kb][4 * c + 2 * e] = bflo(bcur[4 * kb + c][e]) * inv_scale;
+            s[kb][4 * c + 2 * e + 1] = bfhi(bcur[4 * kb + c][e]) * inv_scale;
+          }
+        const int key = 32 * kb + li;
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk) {
+          const int piece = (2 * kk + half) ^ T::kswz(key);
+          s[kb] = mfma32(as_bf16x8(ld16(kt + key * T::kRowBytes + piece * 16)), qb[kk], s[kb]);
+        }
+        if (need_mask) {
+          bf16x8 mc;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mc[e] = (__bf16)0.0f;
+          const float mv = ((mbits >> key) & 1ull) ? 0.0f : (j0 + key < K ? SF_MASKED_LOGIT : kPadKey);
+          mc[0] = (__bf16)(half == 0 ? mv : 0.0f);
+          s[kb] = mfma32(mc, ones_b, s[kb]);
+        }
+      }
+      if (any_qmasked && !qvalid) {                          // masked query: uniform over keys < K
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            s[kb][r] = j0 + 32 * kb + 8 * (r >> 2) + 4 * half + (r & 3) < K ? 0.0f : kPadKey;
+      }
+      // ---- online softmax ----
+      float tmax = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kb][r]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float mnew = fmaxf(m, tmax);
+      const float alpha = fast_exp2((m - mnew) * cs);
+      m = mnew;
+      const float mb = mnew * cs;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      bf16x2 pw[16];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(s[kb][2 * e], cs, -mb)),
+                                   fast_exp2(__builtin_fmaf(s[kb][2 * e + 1], cs, -mb)));
+          l = add_bf2(pw[8 * kb + e], l);
+        }
+      // ---- O^T += V^T P^T ----
+      const int grp = lane >> 4, gi = lane & 15;            // 16-lane group, index in group
+      const int ekey = gi >> 2, q4 = gi & 3;                 // source lane: key e, dims 4q .. 4q+3
+#pragma unroll
+      for (int c2 = 0; c2 < 4; ++c2) {
+        bf16x8 pb;
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          pb[2 * q2] = pw[4 * c2 + q2][0];
+          pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
+        }
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db) {
+          const int d = 32 * db + 16 * (grp & 1) + 4 * q4;
+          u32x2 part[2];                // moved as 32-bit words: no 16-bit element extraction
+#pragma unroll
+          for (int rd = 0; rd < 2; ++rd) {
+            const int key = 16 * c2 + 8 * rd + 4 * (grp >> 1) + ekey;
+            const int off = key * T::kRowBytes + (((d >> 3) ^ T::vswz(key)) << 4) + ((d >> 2) & 1) * 8;
+            part[rd] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vt + off)));
+          }
+          const bf16x8 va = as_bf16x8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]});
+          o[db] = mfma32(va, pb, o[db]);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);                           // next tile, bias and mask landed
+    if (SHARED) __syncthreads();
+    else asm volatile("" ::: "memory");
+  }
+
+  // ---- epilogue: O / l, optional sigmoid gate ----
+  if (!wactive || i >= Q) return;
+  const float lt = l + __shfl_xor(l, 32);
+  const float inv = 1.0f / lt;
+  uint16_t* op = (uint16_t*)a.out + b0 * a.o_s[0] + b1 * a.o_s[1] + (int64_t)i * a.o_s[2] + (int64_t)h * a.o_s[3];
+  const uint16_t* gp = a.gate ? (const uint16_t*)a.gate + b0 * a.g_s[0] + b1 * a.g_s[1] + (int64_t)i * a.g_s[2] +
+                                    (int64_t)h * a.g_s[3]
+                              : nullptr;
+#pragma unroll
+  for (int db = 0; db < DP / 32; ++db) {
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const int d0 = 32 * db + 8 * c4 + 4 * half;
+      if (d0 >= Dv) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = o[db][4 * c4 + e] * inv;
+      const bool full = d0 + 4 <= Dv && pl.vec_out;
+      if (gp != nullptr) {
+        if (full) {
+          const u32x2 gw = *reinterpret_cast<const u32x2*>(gp + d0);
+          v[0] *= sigmoidf_(bflo(gw[0])); v[1] *= sigmoidf_(bfhi(gw[0]));
+          v[2] *= sigmoidf_(bflo(gw[1])); v[3] *= sigmoidf_(bfhi(gw[1]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (d0 + e < Dv) v[e] *= sigmoidf_(bf2f(gp[d0 + e]));
+        }
+      }
+      if (full) {
+        *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (d0 + e < Dv) op[d0 + e] = f2bf(v[e]);
+      }
+    }
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 
@@ -222,8 +521,32 @@ extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
     vec = (a->q_s[s] % 8 == 0) && (a->k_s[s] % 8 == 0) && (a->v_s[s] % 8 == 0);
   bool vec_out = aligned8(a->out);
   for (int s = 0; s < 4 && vec_out; ++s) vec_out = (a->o_s[s] % 4 == 0);
-  dim3 grid((a->Q + kQB - 1) / kQB, a->H, a->B0 * a->B1);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  bool bias_vec = a->bias == nullptr || aligned8(a->bias);
+  for (int s = 0; s < 4 && bias_vec && a->bias != nullptr; ++s) bias_vec = a->bias_s[s] % 4 == 0;
+  if (vec && bias_vec) {
+    Attn2Plan pl{};
+    pl.QB = (a->Q + 31) / 32;
+    pl.vec_out = vec_out && (a->gate == nullptr || aligned8(a->gate));
+    for (int s = 0; s < 4 && pl.vec_out && a->gate != nullptr; ++s) pl.vec_out = a->g_s[s] % 4 == 0;
+    const int64_t bh = (int64_t)a->B0 * a->B1 * a->H;
+    const int64_t groups = bh * ((pl.QB + 3) / 4);
+    bool shared = a->Q >= 128 && groups >= 512;
+    if (const char* e = getenv("SPARSEFOLD_HIP_ATTN_MODE")) shared = e[0] == 's';   // test hook
+    pl.tasks = shared ? groups : bh * pl.QB;
+    const int64_t wgs = shared ? groups : (pl.tasks + 3) / 4;
+    if (wgs > 0x7fffffff) { sf_set_error("attention: problem too large for the grid"); return 1; }
+    const dim3 g2((unsigned)wgs);
+    if (dmax <= 32) {
+      if (shared) hipLaunchKernelGGL((attn2_kernel<32, true>), g2, dim3(256), 0, st, *a, pl);
+      else hipLaunchKernelGGL((attn2_kernel<32, false>), g2, dim3(256), 0, st, *a, pl);
+    } else {
+      if (shared) hipLaunchKernelGGL((attn2_kernel<64, true>), g2, dim3(256), 0, st, *a, pl);
+      else hipLaunchKernelGGL((attn2_kernel<64, false>), g2, dim3(256), 0, st, *a, pl);
+    }
+    return sf_check_launch("attn2_kernel");
+  }
+  dim3 grid((a->Q + kQB - 1) / kQB, a->H, a->B0 * a->B1);
   if (dmax <= 32)
     hipLaunchKernelGGL(attention_fwd_kernel<32>, grid, dim3(256), 0, st, *a, (int)vec, (int)vec_out);
   else

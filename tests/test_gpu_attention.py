@@ -70,6 +70,23 @@ def test_head_dims_tails_masks_bias_gate(D, QK):
   assert_close_bf16(out, ref, f"D={D} Q={Q} K={K}")
 
 
+@pytest.mark.parametrize("D", [32, 48])
+def test_shared_tile_workgroups(D):
+  """Enough (batch, head) pairs that the kernel runs 4-wave workgroups sharing K/V tiles
+  (at least 512 groups of 128 queries), with ragged query / key ranges, masks, bias, gate."""
+  Q, K, B, H = 260, 257, 4, 48
+  g = torch.Generator().manual_seed(2000 + D)
+  q, k = torch.randn(B, Q, H, D, generator=g), torch.randn(B, K, H, D, generator=g)
+  v = torch.randn(B, K, H, D, generator=g)
+  bias = torch.randn(H, Q, K, generator=g)
+  gate = torch.randn(B, Q, H, D, generator=g)
+  mq = torch.rand(B, Q, generator=g) > 0.1
+  mk = torch.rand(B, K, generator=g) > 0.3
+  mk[2, :] = False
+  out, ref = _run(q, k, v, mask_q=mq, mask_k=mk, bias=bias, gate=gate)
+  assert_close_bf16(out, ref, f"shared D={D}")
+
+
 def test_fully_masked_rows_are_exact_means():
   g = torch.Generator().manual_seed(5)
   q, k = torch.randn(1, 70, 2, 32, generator=g), torch.randn(1, 150, 2, 32, generator=g)
