@@ -8,6 +8,7 @@
 //                       transformer.py:430-447); HBM-bound on z
 //   window_gather_kernel key-window gather of atom_layout.convert (atom_layout.py:61-83)
 #include <algorithm>
+#include <type_traits>
 
 #include "sf_common.h"
 
@@ -16,26 +17,35 @@ namespace {
 // ------------------------------------------------------------------------------------
 // LayerNorm / AdaLN: one wave per row, 16-byte chunks, fp32 statistics.
 // ------------------------------------------------------------------------------------
+// LPR lanes per row (C <= 8 * LPR * 4): a wave normalises 64 / LPR rows at once, so narrow
+// rows (C = 128: 16 lanes of 16 bytes) keep every lane busy.
+template <int LPR>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_args a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.M) return;
+  constexpr int RPW = 64 / LPR;                  // rows per wave
+  const int lane = threadIdx.x & 63, sub = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const bool live = row < a.M;
   const int C = a.C, nch = C / 8;
-  const uint16_t* xp = (const uint16_t*)a.x + row * a.x_rs;
+  const uint16_t* xp = (const uint16_t*)a.x + (live ? row : 0) * a.x_rs;
+  auto group_sum = [](float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+  };
   u32x4 w[4];
   float sum = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const int ch = lane + 64 * t;
-    w[t] = (ch < nch) ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
+    const int ch = sub + LPR * t;
+    w[t] = (live && ch < nch) ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int e = 0; e < 4; ++e) sum += bflo(w[t][e]) + bfhi(w[t][e]);
   }
-  const float mean = wave_sum(sum) / (float)C;
+  const float mean = group_sum(sum) / (float)C;
   float sq = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    if (lane + 64 * t < nch) {
+    if (sub + LPR * t < nch) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float d0 = bflo(w[t][e]) - mean, d1 = bfhi(w[t][e]) - mean;
@@ -43,7 +53,8 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
       }
     }
   }
-  const float rstd = rsqrtf(wave_sum(sq) / (float)C + a.eps);
+  const float rstd = rsqrtf(group_sum(sq) / (float)C + a.eps);
+  if (!live) return;
   const uint16_t* scp = nullptr;
   const uint16_t* shp = nullptr;
   if (a.scale != nullptr) {
@@ -54,7 +65,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
   uint16_t* yp = (uint16_t*)a.y + row * a.y_rs;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const int ch = lane + 64 * t;
+    const int ch = sub + LPR * t;
     if (ch >= nch) continue;
     float v[8];
 #pragma unroll
@@ -510,7 +521,16 @@ extern "C" int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream) 
     sf_set_error("layer_norm: rows must be 16-byte aligned"); return 1;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)((a->M + 3) / 4)), dim3(256), 0, st, *a);
+  const int nch = a->C / 8;
+  auto launch = [&](auto lpr) {
+    constexpr int LPR = decltype(lpr)::value;
+    const int64_t rows_per_wg = 4 * (64 / LPR);
+    hipLaunchKernelGGL(layer_norm_kernel<LPR>, dim3((unsigned)((a->M + rows_per_wg - 1) / rows_per_wg)), dim3(256), 0, st, *a);
+  };
+  if (nch <= 8 * 4) launch(std::integral_constant<int, 8>{});
+  else if (nch <= 16 * 4) launch(std::integral_constant<int, 16>{});
+  else if (nch <= 32 * 4) launch(std::integral_constant<int, 32>{});
+  else launch(std::integral_constant<int, 64>{});
   return sf_check_launch("layer_norm_kernel");
 }
 
