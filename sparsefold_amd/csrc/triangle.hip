@@ -337,6 +337,22 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
     const bool ok = p < a.P;                             // only the last block has idle lanes
     bf16x8 zo[8];
     ln128_operands(zn, ok, zo);
+    // residual: output features 8c + 4h + e (c even / odd) of lane half h sit in z chunk
+    // 2nb + c/2 of lane half c%2, elements 4h + e -- two permlane32 swaps per chunk bring
+    // them over before the registers are reused by the next item's loads
+    uint32_t zr[8][2][2];
+    if (a.add_residual) {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const auto s02 = __builtin_amdgcn_permlane32_swap(zn[kk][0], zn[kk][2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(zn[kk][1], zn[kk][3], false, false);
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+          zr[kk][par][0] = s02[par];
+          zr[kk][par][1] = s13[par];
+        }
+      }
+    }
 
     // gate of head nb: D^T = W_g . X^T -> lane (position, half hf) holds natural dims
     // 8c + 4hf + e in register 4c + e; o operand chunk kk = 2nb + j of lane half h needs the
@@ -381,16 +397,15 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
       if (ok) {
-        const uint16_t* zp = a.add_residual ? a.z + p * kPC + 32 * nb + 4 * half : nullptr;
         uint16_t* outp = a.out + p * kPC + 32 * nb + 4 * half;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
-          if (zp != nullptr) {
-            const u32x2 zw = *reinterpret_cast<const u32x2*>(zp + 8 * c);
-            v[0] += bflo(zw[0]); v[1] += bfhi(zw[0]); v[2] += bflo(zw[1]); v[3] += bfhi(zw[1]);
+          if (a.add_residual) {
+            const uint32_t z0 = zr[2 * nb + (c >> 1)][c & 1][0], z1 = zr[2 * nb + (c >> 1)][c & 1][1];
+            v[0] += bflo(z0); v[1] += bfhi(z0); v[2] += bflo(z1); v[3] += bfhi(z1);
           }
           *reinterpret_cast<u32x2*>(outp + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
         }
