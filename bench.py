@@ -46,6 +46,8 @@ def parse():
   ap.add_argument("--cpu-baseline", type=int, default=1, help="time the host-CPU math path (rank 0)")
   ap.add_argument("--cpu-rows", type=int, default=128, help="rows in the CPU-baseline sample")
   ap.add_argument("--other-configs", type=int, default=1, help="also time the other four configurations")
+  ap.add_argument("--profile-config", default="",
+                  help="only run this configuration --steps times (e.g. single_n768) and exit")
   ap.add_argument("--copy-mib", type=int, default=0,
                   help="only run a plain device-to-device copy of this many MiB 5 times and exit "
                        "(the known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters)")
@@ -115,71 +117,91 @@ def _time_call(fn, iters: int) -> float:
   return _events_time(fn, iters, torch.cuda.current_stream())
 
 
-def other_configs(iters: int) -> dict:
-  """The remaining parity configurations, each timed as one module call with inputs resident
-  in HBM.  Algorithmic work: FLOP for the MFMA-bound forms, bytes for the HBM-bound ones."""
+def _config_builders() -> dict:
+  """name -> builder() returning (call, metrics(t_ms) -> dict) for the remaining parity
+  configurations, each one module call with inputs resident in HBM.  Algorithmic work: FLOP
+  for the MFMA-bound forms, bytes for the HBM-bound ones."""
   from sparsefold_amd import backends
   from sparsefold_amd import workloads as W
   dev = torch.device("cuda:0")
-  res = {}
 
-  # C1: triangle attention, starting node, N=20, fp32 activations (launch-latency bound)
-  mod, z, seq = W.make_triangle(20, dtype=torch.float32, seed=1)
-  mod = mod.to(dev); backends.prepare(mod)
-  z, seq = z.to(dev), seq.to(dev)
-  t = _time_call(lambda: mod(z, seq), iters)
-  res["triangle_n20_fp32"] = {"us_per_call": round(t * 1e3, 2), "bound": "latency"}
-
-  # C2: triangle attention N=384, starting + ending node, last N//10 tokens padded
-  for tr in (False, True):
-    mod, z, seq = W.make_triangle(384, padded=True, transpose=tr, seed=2)
+  def c1():    # triangle attention, starting node, N=20, fp32 activations (launch-latency bound)
+    mod, z, seq = W.make_triangle(20, dtype=torch.float32, seed=1)
     mod = mod.to(dev); backends.prepare(mod)
     z, seq = z.to(dev), seq.to(dev)
-    t = _time_call(lambda: mod(z, seq), iters)
-    f = module_flop(384)
-    res["triangle_n384_" + ("end" if tr else "start")] = {
-        "ms_per_call": round(t, 4), "tflops": round(f / t / 1e9, 1),
-        "frac_bf16_peak": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"}
+    return (lambda: mod(z, seq)), (lambda t: {"us_per_call": round(t * 1e3, 2), "bound": "latency"})
 
-  # C3b: single attention with pair bias, N=768 (pair-logit prologue reads z: HBM-bound)
-  n, cs, cz, h, d = 768, 384, 128, 16, 24
-  mod, z, s_act, seq = W.make_single(n, seed=3)
-  mod = mod.to(dev); backends.prepare(mod)
-  z, s_act, seq = z.to(dev), s_act.to(dev), seq.to(dev)
-  t = _time_call(lambda: mod(z, s_act, seq), iters)
-  bytes_ = n * n * cz * 2 + h * n * n * 2 + 2 * n * cs * 2            # z, bias planes once, s in/out
-  flop = (2 * n * n * cz * h) + 2 * n * cs * 4 * cs + 4 * h * n * n * d + 2 * n * cs * cs
-  res["single_n768"] = {"ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
-                        "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4),
-                        "tflops": round(flop / t / 1e9, 2), "bound": "hbm"}
+  def c2(tr):  # triangle attention N=384, starting / ending node, last N//10 tokens padded
+    def build():
+      mod, z, seq = W.make_triangle(384, padded=True, transpose=tr, seed=2)
+      mod = mod.to(dev); backends.prepare(mod)
+      z, seq = z.to(dev), seq.to(dev)
+      f = module_flop(384)
+      return (lambda: mod(z, seq)), (lambda t: {"ms_per_call": round(t, 4), "tflops": round(f / t / 1e9, 1),
+                                                "frac_bf16_peak": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                                "bound": "mfma"})
+    return build
 
-  # C4: diffusion-transformer token attention, 5 samples x N=1024, one block
-  S, n, c, sc, h, d = 5, 1024, 768, 384, 16, 48
-  mod, act, cond, bias, mask = W.make_diffusion(n, S=S, seed=4)
-  mod = mod.to(dev); backends.prepare(mod)
-  act, cond, bias, mask = act.to(dev), cond.to(dev), bias.to(dev), mask.to(dev)
-  t = _time_call(lambda: mod(act, mask, pair_logits=bias, single_cond=cond), iters)
-  flop = (2 * n * sc * 2 * c + 2 * S * n * c * 4 * c + 4 * h * n * n * d * S + 2 * S * n * c * c
-          + 2 * n * sc * c)
-  res["diffusion_5x1024_block"] = {"ms_per_call": round(t, 4), "ms_24_blocks": round(24 * t, 3),
-                                   "tflops": round(flop / t / 1e9, 1),
-                                   "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4),
-                                   "bound": "mfma"}
+  def c3b():   # single attention with pair bias, N=768 (pair-logit prologue reads z: HBM-bound)
+    n, cs, cz, h, d = 768, 384, 128, 16, 24
+    mod, z, s_act, seq = W.make_single(n, seed=3)
+    mod = mod.to(dev); backends.prepare(mod)
+    z, s_act, seq = z.to(dev), s_act.to(dev), seq.to(dev)
+    bytes_ = n * n * cz * 2 + h * n * n * 2 + 2 * n * cs * 2            # z, bias planes once, s in/out
+    flop = (2 * n * n * cz * h) + 2 * n * cs * 4 * cs + 4 * h * n * n * d + 2 * n * cs * cs
+    return (lambda: mod(z, s_act, seq)), (lambda t: {
+        "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
+        "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "tflops": round(flop / t / 1e9, 2),
+        "bound": "hbm"})
 
-  # C5: windowed atom attention, 5 samples x 8192 atoms, 32-query / 128-key windows
-  S, atoms, c, h, d = 5, 8192, 128, 4, 32
-  mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5)
-  mod = mod.to(dev); backends.prepare(mod)
-  args = [x.to(dev) for x in (act, lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc, kc, bias)]
-  t = _time_call(lambda: mod.forward_indexed(*args), iters)
-  U = atoms // 32
-  flop = 4 * h * 32 * 128 * d * U * S + 2 * S * atoms * c * 2 * c * 2 + 2 * S * atoms * c * c
-  bytes_ = 2 * S * atoms * c * 2 + U * h * 32 * 128 * 2 + (atoms + U * 128) * c * 2
-  res["window_5x8192"] = {"ms_per_call": round(t, 4), "tflops": round(flop / t / 1e9, 2),
-                          "gbs": round(bytes_ / t / 1e6, 1),
-                          "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4),
-                          "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "balanced"}
+  def c4():    # diffusion-transformer token attention, 5 samples x N=1024, one block
+    S, n, c, sc, h, d = 5, 1024, 768, 384, 16, 48
+    mod, act, cond, bias, mask = W.make_diffusion(n, S=S, seed=4)
+    mod = mod.to(dev); backends.prepare(mod)
+    act, cond, bias, mask = act.to(dev), cond.to(dev), bias.to(dev), mask.to(dev)
+    flop = (2 * n * sc * 2 * c + 2 * S * n * c * 4 * c + 4 * h * n * n * d * S + 2 * S * n * c * c
+            + 2 * n * sc * c)
+    return (lambda: mod(act, mask, pair_logits=bias, single_cond=cond)), (lambda t: {
+        "ms_per_call": round(t, 4), "ms_24_blocks": round(24 * t, 3), "tflops": round(flop / t / 1e9, 1),
+        "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+
+  def c5():    # windowed atom attention, 5 samples x 8192 atoms, 32-query / 128-key windows
+    S, atoms, c, h, d = 5, 8192, 128, 4, 32
+    mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5)
+    mod = mod.to(dev); backends.prepare(mod)
+    args = [x.to(dev) for x in (act, lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc, kc, bias)]
+    U = atoms // 32
+    flop = 4 * h * 32 * 128 * d * U * S + 2 * S * atoms * c * 2 * c * 2 + 2 * S * atoms * c * c
+    bytes_ = 2 * S * atoms * c * 2 + U * h * 32 * 128 * 2 + (atoms + U * 128) * c * 2
+    return (lambda: mod.forward_indexed(*args)), (lambda t: {
+        "ms_per_call": round(t, 4), "tflops": round(flop / t / 1e9, 2), "gbs": round(bytes_ / t / 1e6, 1),
+        "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "balanced"})
+
+  return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
+          "single_n768": c3b, "diffusion_5x1024_block": c4, "window_5x8192": c5}
+
+
+def other_configs(iters: int) -> dict:
+  """Times every configuration of _config_builders (median-free: HIP events over `iters`
+  calls after a warm-up)."""
+  res = {}
+  for name, build in _config_builders().items():
+    call, metrics = build()
+    res[name] = metrics(_time_call(call, iters))
   return res
+
+
+def profile_config(name: str, calls: int) -> None:
+  """Runs one configuration `calls` times (for rocprofv3 kernel statistics)."""
+  builders = _config_builders()
+  if name not in builders:
+    raise SystemExit(f"unknown configuration {name!r}; one of {sorted(builders)}")
+  call, _ = builders[name]()
+  for _ in range(calls):
+    call()
+  torch.cuda.synchronize()
+  print(f"[bench] profiled {name}: {calls} calls", flush=True)
 
 
 def cpu_baseline(rows: int) -> dict:
@@ -219,6 +241,13 @@ def main():
     sys.exit(2)
   if args.copy_mib:
     copy_calibration(args.copy_mib)
+    return
+  if args.profile_config:
+    from sparsefold_amd import backends
+    from sparsefold_amd.runtime import config
+    config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda")
+    backends.init()
+    profile_config(args.profile_config, args.steps)
     return
   from sparsefold_amd import backends
   from sparsefold_amd import workloads as W
