@@ -142,10 +142,12 @@ int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t 
  * reference's projection / attention split of the row-sharded triangle attention
  * (backends/vecops/kernels/registry.py:1236-1309, grid_distributed_projection and
  * grid_distributed_attention):
- *   SF_TRI_STAGE_PROJECT  LN + q/k/v/g/bias projections into the workspace
- *   SF_TRI_STAGE_ATTEND   attention core + sigmoid gate (reads the projected operands)
- *   SF_TRI_STAGE_OUTPUT   output projection (+ residual) into out
- * Stages run in that order when several bits are set; sf_hip_triangle_attn_fwd == all three. */
+ *   SF_TRI_STAGE_PROJECT  LN + q/k/v/bias projections into the workspace (also folds the LN
+ *                         affine into the packed weight, which the output stage reuses)
+ *   SF_TRI_STAGE_ATTEND   attention core (reads the projected operands)
+ *   SF_TRI_STAGE_OUTPUT   sigmoid gate (recomputed from LN(z)), output projection (+ residual)
+ * Stages run in that order when several bits are set; sf_hip_triangle_attn_fwd == all three.
+ * A stage reads what the earlier stages left in the same workspace. */
 #define SF_TRI_STAGE_PROJECT 1
 #define SF_TRI_STAGE_ATTEND 2
 #define SF_TRI_STAGE_OUTPUT 4
