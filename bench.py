@@ -178,8 +178,29 @@ def _config_builders() -> dict:
         "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4),
         "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "balanced"})
 
+  def pack_tr():  # diffusion Transformer pair-logit pack, N=1024: [1024,1024,128] -> [6,4,16,1024,1024]
+    n, pc, planes = 1024, 128, 384
+    mod, pair_cond = W.make_transformer_pack(n, seed=6)
+    mod = mod.to(dev); backends.prepare(mod)
+    pair_cond = pair_cond.to(dev)
+    bytes_ = n * n * pc * 2 + planes * n * n * 2
+    return (lambda: mod.pair_logits_pack(pair_cond)), (lambda t: {
+        "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
+        "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
+
+  def pack_x():  # atom CrossAttTransformer pack, 8192 atoms: [256,32,128,16] -> [3,256,4,32,128]
+    U, pc, planes = 256, 16, 12
+    mod, pair_cond = W.make_cross_pack(U, seed=8)
+    mod = mod.to(dev); backends.prepare(mod)
+    pair_cond = pair_cond.to(dev)
+    bytes_ = U * 32 * 128 * (pc + planes) * 2
+    return (lambda: mod.pair_logits_pack(pair_cond)), (lambda t: {
+        "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
+        "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
+
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
-          "single_n768": c3b, "diffusion_5x1024_block": c4, "window_5x8192": c5}
+          "single_n768": c3b, "diffusion_5x1024_block": c4, "window_5x8192": c5,
+          "transformer_pack_n1024": pack_tr, "cross_pack_8192": pack_x}
 
 
 def other_configs(iters: int) -> dict:

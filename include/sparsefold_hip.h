@@ -21,6 +21,7 @@
  *                                backends/vecops/kernels/registry.py:1188-1233, dense form)
  *   sf_hip_pair_logits_fwd      model/trunk/blocks.py:745-749             SingleActUpdate pair logits
  *                               model/diffusion/transformer.py:430-447    Transformer pair-logit pack
+ *                               model/diffusion/transformer.py:655-666    CrossAttTransformer pack
  *   sf_hip_window_gather_fwd    schema/atom_layout.py:61-83               convert (queries_to_keys,
  *                               CrossAttTransformer block key gather, transformer.py:671-673)
  */
@@ -34,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 1
+#define SF_HIP_ABI_VERSION 2
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -156,16 +157,26 @@ int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* w
                               size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * Pair logits: out[h, p] = (LN(z[p,:]) W)[h] for H <= 64 planes; z bf16 [P, C] contiguous
- * (C <= 128, C % 8 == 0), ln_w/ln_b f32 [C] (either may be NULL), w_t bf16 [H, C],
- * out bf16 [H, P].
+ * Pair logits: plane hp, position p holds (LN(z[p,:]) W)[hp]; z bf16 [P, C] contiguous
+ * (C % 8 == 0, C <= 128), ln_w/ln_b f32 [C] (either may be NULL), w_t bf16 [H, C].
+ * H <= 64 planes for any C; up to 1024 planes when C == 128 (one pass over z).
+ *
+ * Output layout (bf16):
+ *   seg == 0: out[H, P]                       (plane-major, SingleActUpdate / Transformer pack:
+ *                                              planes ordered (super-block, block, head))
+ *   seg  > 0: out[H/group, P/seg, group, seg]  plane hp = blk*group + h, position p = u*seg + r
+ *              -> element ((blk*(P/seg) + u)*group + h)*seg + r   (CrossAttTransformer pack
+ *              "s q k b h -> b s h q k" with seg = Q*K, group = heads per block)
+ *   seg > 0 needs P % seg == 0 and H % group == 0.
  * ------------------------------------------------------------------------------------- */
 typedef struct sf_pair_logits_args {
   int64_t P; int32_t C, H;                      /* P = number of pair positions */
   const void* z;
   const float* ln_w; const float* ln_b;
   const void* w_t;
-  void* out;                                    /* [H, P] */
+  void* out;
+  int64_t seg;                                  /* 0 = plane-major output */
+  int32_t group, reserved;                      /* heads per block when seg > 0; reserved = 0 */
 } sf_pair_logits_args;
 
 int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream);

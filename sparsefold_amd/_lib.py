@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -74,6 +74,7 @@ class PairLogitsArgs(C.Structure):
   _fields_ = [
       ("P", _i64), ("C", _i32), ("H", _i32),
       ("z", _vp), ("ln_w", _vp), ("ln_b", _vp), ("w_t", _vp), ("out", _vp),
+      ("seg", _i64), ("group", _i32), ("reserved", _i32),
   ]
 
 

@@ -22,12 +22,14 @@ from sparsefold_amd.runtime import config
 
 _PATCHED_FACTORIES: list[tuple[object, str, object]] = []
 
-# native.ops name -> (factory attribute, HIP class attribute in backends.hip.modules)
+# native.ops name -> [(factory attribute, HIP class attribute in backends.hip.modules)]
 _REPLACE_MAP = {
-    "grid_self_attn": ("GridSelfAttention", "GridSelfAttentionHip"),
-    "evoformer_single_act_update": ("SingleActUpdate", "SingleActUpdateHip"),
-    "diffusion_self_attention": ("SelfAttention", "SelfAttentionHip"),
-    "diffusion_cross_attention": ("CrossAttention", "CrossAttentionHip"),
+    "grid_self_attn": [("GridSelfAttention", "GridSelfAttentionHip")],
+    "evoformer_single_act_update": [("SingleActUpdate", "SingleActUpdateHip")],
+    "diffusion_self_attention": [("SelfAttention", "SelfAttentionHip"),
+                                 ("TransformerPairLogits", "TransformerPairLogitsHip")],
+    "diffusion_cross_attention": [("CrossAttention", "CrossAttentionHip"),
+                                  ("CrossAttTransformerPairLogits", "CrossAttTransformerPairLogitsHip")],
 }
 
 
@@ -49,9 +51,10 @@ def apply() -> None:
   selected = list(config.native_ops)
   if "*" in selected or "all" in selected:
     selected = list(_REPLACE_MAP)
-  for key, (factory, impl) in _REPLACE_MAP.items():
+  for key, pairs in _REPLACE_MAP.items():
     if key in selected:
-      _replace_factory(_modules, factory, getattr(hip_modules, impl))
+      for factory, impl in pairs:
+        _replace_factory(_modules, factory, getattr(hip_modules, impl))
 
 
 def manual_seed(seed: int) -> None:

@@ -14,6 +14,13 @@ Replaced reference forwards:
 * ``CrossAttentionHip.forward``      transformer.py:549-585; ``forward_indexed`` additionally
                                      gathers the key windows (transformer.py:671-673)
 * ``SingleActUpdateHip.forward``     blocks.py:739-763 (attention half)
+* ``TransformerHipMixin``            transformer.py:430-447 -- the cached pair-logit pack
+                                     ``[n_super, super_block, H, N, N]`` in one pass over pair_cond
+* ``CrossAttTransformerHipMixin``    transformer.py:655-666 -- the cached pack
+                                     ``[num_blocks, U, H, Q, K]``, written in that layout directly
+The two Transformer mixins keep the reference ``forward`` (block loop, transitions) and only
+replace the factory of its ``ValueCache`` entry ``"pair_logits"``, so cache keys and
+``enable_cache`` behave as in the reference.
 """
 from __future__ import annotations
 
@@ -260,6 +267,105 @@ class SingleActUpdateHipMixin:
     return out
 
 
+# ---------------------------------------------------------------------------------------
+# Transformer / CrossAttTransformer: the cached pair-logit packs
+# ---------------------------------------------------------------------------------------
+
+class _PackFactory:
+  """Stands in for a ``ValueCache`` during one ``forward``: ``get`` of the entry ``name``
+  uses ``factory`` in place of the caller's; everything else goes to the wrapped cache."""
+
+  def __init__(self, cache, name: str, factory):
+    self._cache, self._name, self._factory = cache, name, factory
+
+  def get(self, *args, name=None, factory=None):
+    if name == self._name:
+      factory = self._factory
+    return self._cache.get(*args, name=name, factory=factory)
+
+  def __getattr__(self, attr):
+    return getattr(self._cache, attr)
+
+
+def _with_pack_factory(module, factory, call):
+  cache = module._cache
+  module._cache = _PackFactory(cache, "pair_logits", factory)
+  try:
+    return call()
+  finally:
+    module._cache = cache
+
+
+def _prepare_hip_children(module: torch.nn.Module) -> None:
+  """A container's ``prepare_native`` also prepares the HIP modules inside it (``prepare``
+  stops at the first HIP module it meets on each branch)."""
+  for child in module.modules():
+    if child is not module and isinstance(child, HIP_TYPES) and not getattr(child, "_native_prepared", False):
+      child.prepare_native()
+
+
+class TransformerHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    projections = list(self.pair_logits_projection)
+    Pc = self.pair_input_layer_norm.weight.shape[0]
+    w = [proj.weight.reshape(Pc, -1).t() for proj in projections]      # [P, S, H] -> [S*H, P]
+    _buf(self, "_hip_pack_w", _bf(torch.cat(w, 0)))                    # planes (super-block, s, h)
+    _buf(self, "_hip_pack_ln_w", _f32(self.pair_input_layer_norm.weight))
+    _buf(self, "_hip_pack_ln_b", _f32(getattr(self.pair_input_layer_norm, "bias", None)))
+    self._hip_pack_shape = (len(projections),) + tuple(projections[0].weight.shape[1:])
+    _prepare_hip_children(self)
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def pair_logits_pack(self, pair_cond: torch.Tensor) -> torch.Tensor:
+    """``pair_cond [N, N, P]`` -> ``[n_super, super_block, H, N, N]`` (transformer.py:431-438)."""
+    assert pair_cond.ndim == 3, "pair_cond must be [N, N, P]"
+    N0, N1 = pair_cond.shape[:2]
+    planes = ops.pair_logits(pair_cond, self._hip_pack_ln_w, self._hip_pack_ln_b, self._hip_pack_w)
+    pack = planes.view(*self._hip_pack_shape, N0, N1)
+    return pack.to(self.dtype or pair_cond.dtype)
+
+  def forward(self, act, mask, single_cond, pair_cond=None):
+    if pair_cond is None:
+      return super().forward(act, mask, single_cond, pair_cond)
+    return _with_pack_factory(self, lambda: self.pair_logits_pack(pair_cond),
+                              lambda: super(TransformerHipMixin, self).forward(act, mask, single_cond, pair_cond))
+
+
+class CrossAttTransformerHipMixin:
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    w = self.pair_logits_projection.weight                              # [P, num_blocks, H]
+    _buf(self, "_hip_pack_w", _bf(w.reshape(w.shape[0], -1).t()))        # planes (block, h)
+    _buf(self, "_hip_pack_ln_w", _f32(self.pair_input_layer_norm.weight))
+    _buf(self, "_hip_pack_ln_b", _f32(getattr(self.pair_input_layer_norm, "bias", None)))
+    self._hip_pack_shape = tuple(w.shape[1:])
+    _prepare_hip_children(self)
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def pair_logits_pack(self, pair_cond: torch.Tensor) -> torch.Tensor:
+    """``pair_cond [U, Q, K, P]`` -> ``[num_blocks, U, H, Q, K]`` (transformer.py:655-662),
+    stored by the kernel in that order (no permute pass)."""
+    assert pair_cond.ndim == 4, "pair_cond must be [num_subsets, num_queries, num_keys, P]"
+    U, Qn, Kn = pair_cond.shape[:3]
+    nb, H = self._hip_pack_shape
+    pack = ops.pair_logits(pair_cond, self._hip_pack_ln_w, self._hip_pack_ln_b, self._hip_pack_w,
+                           seg=Qn * Kn, group=H)                        # [nb, U, H, Q*K]
+    return pack.view(nb, U, H, Qn, Kn).to(pair_cond.dtype)
+
+  def forward(self, queries_act, queries_mask, queries_to_keys, keys_mask, queries_single_cond,
+              keys_single_cond, pair_cond):
+    return _with_pack_factory(
+        self, lambda: self.pair_logits_pack(pair_cond),
+        lambda: super(CrossAttTransformerHipMixin, self).forward(
+            queries_act, queries_mask, queries_to_keys, keys_mask, queries_single_cond, keys_single_cond,
+            pair_cond))
+
+
 class GridSelfAttentionHip(GridSelfAttentionHipMixin, base.GridSelfAttention):
   pass
 
@@ -276,4 +382,13 @@ class SingleActUpdateHip(SingleActUpdateHipMixin, base.SingleActUpdate):
   pass
 
 
-HIP_TYPES = (GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin)
+class TransformerPairLogitsHip(TransformerHipMixin, base.TransformerPairLogits):
+  pass
+
+
+class CrossAttTransformerPairLogitsHip(CrossAttTransformerHipMixin, base.CrossAttTransformerPairLogits):
+  pass
+
+
+HIP_TYPES = (GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin,
+             TransformerHipMixin, CrossAttTransformerHipMixin)

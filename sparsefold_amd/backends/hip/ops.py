@@ -181,19 +181,27 @@ def linear(x: torch.Tensor, wt: torch.Tensor, bias=None, *, residual=None, mul=N
   return None if y is None else y.view(*x.shape[:-1], ycols)
 
 
-def pair_logits(z: torch.Tensor, ln_w, ln_b, w_t: torch.Tensor) -> torch.Tensor:
-  """``[..., C]`` pair activations -> ``[H, P]`` logits planes (LN + projection)."""
+def pair_logits(z: torch.Tensor, ln_w, ln_b, w_t: torch.Tensor, *, seg: int = 0, group: int = 0) -> torch.Tensor:
+  """``[..., C]`` pair activations -> LN + projection logits planes.
+
+  ``seg == 0``: ``[H, P]``.  ``seg > 0``: ``[H // group, P // seg, group, seg]`` (plane
+  ``blk * group + h``, position ``u * seg + r``), the CrossAttTransformer pack layout."""
   _require_cuda(z, ln_w, ln_b, w_t)
   H, Cn = w_t.shape
   z2 = _rows(_bf16(z), Cn)
   P = z2.shape[0]
   _require(z2.stride(0) == Cn, "pair_logits: z rows must be contiguous")
-  out = torch.empty((H, P), dtype=BF16, device=z.device)
+  if seg:
+    _require(P % seg == 0 and group > 0 and H % group == 0, "pair_logits: P % seg and H % group must be 0")
+    out = torch.empty((H // group, P // seg, group, seg), dtype=BF16, device=z.device)
+  else:
+    out = torch.empty((H, P), dtype=BF16, device=z.device)
   lw, lb = _f32(ln_w), _f32(ln_b)
   wt = _bf16(w_t).contiguous()
   a = _lib.PairLogitsArgs()
   a.P, a.C, a.H = P, Cn, H
   a.z, a.ln_w, a.ln_b, a.w_t, a.out = _vp(z2), _vp(lw), _vp(lb), _vp(wt), _vp(out)
+  a.seg, a.group = int(seg), int(group) if seg else 0
   _lib.check(_lib.load().sf_hip_pair_logits_fwd(C.byref(a), _stream(z)), "sf_hip_pair_logits_fwd")
   return out
 

@@ -4,8 +4,8 @@
 //                       residual epilogue and an optional transposed second output
 //                       (primitives.py:328-372 Linear.forward; the transposed output emits
 //                       pair-bias planes [H, rows] as blocks.py:329 rearranges them)
-//   pair_logits_kernel  LN(z) . W -> [H, P] in one pass over z (blocks.py:745-749,
-//                       transformer.py:430-447); HBM-bound on z
+//   pair_logits_kernel  LN(z) . W -> bias planes in one pass over z (blocks.py:745-749,
+//                       transformer.py:430-447 and :655-666); HBM-bound on z and the planes
 //   window_gather_kernel key-window gather of atom_layout.convert (atom_layout.py:61-83)
 #include <algorithm>
 #include <type_traits>
@@ -395,9 +395,16 @@ __global__ __launch_bounds__(256) void pair_logits_kernel(const sf_pair_logits_a
     }
   }
   uint16_t* op = (uint16_t*)a.out;
+  // a.seg / a.group are normalised by the host (plane-major: seg = P, group = H)
+  const int64_t u = p / a.seg;
+  const int64_t pos = u * a.group * a.seg + (p - u * a.seg);
 #pragma unroll
-  for (int h = 0; h < H; ++h)
-    if (h < Hr) op[(int64_t)h * a.P + p] = f2bf(acc[h] * rstd + sS2[h]);
+  for (int h = 0; h < H; ++h) {
+    if (h < Hr) {
+      const int blk = h / a.group;
+      op[(int64_t)blk * a.group * a.P + (int64_t)(h - blk * a.group) * a.seg + pos] = f2bf(acc[h] * rstd + sS2[h]);
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------
@@ -427,22 +434,34 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // into MFMA operands, and D = X . Wf^T against the gamma-folded weight held in LDS gives lane
 // li = head, registers = 4 consecutive positions: 8-byte stores into each bias plane.  Waves
 // stride over the steps, loading step n+1 while step n computes.
+//
+// More than 64 planes (the Transformer pack has 384) are split over `hgroups` workgroups per
+// position worker, each folding its own 64 weight rows.  The hgroups workgroups of one worker
+// are dispatched back to back onto one XCD (workgroup ids b, b+8, b+16, ...), walk the same
+// steps in lock-step and so read each z row from HBM once: the repeats hit that XCD's L2.
 // ------------------------------------------------------------------------------------
 constexpr int kPLWP = 128 + 8;        // LDS pitch (elements) of folded weight rows
+constexpr int kPL128MaxH = 1024;
 
-template <int HB>  // 32-head blocks (H <= 32 * HB)
-__global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps) {
+template <int HB, bool SEG>  // 32-head blocks per workgroup (H <= 32 * HB * hgroups); SEG: segmented output
+__global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps, int hgroups) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[32 * HB * kPLWP];
   __shared__ float sOff[32 * HB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
+  // grid = hgroups * workers, workers % 8 == 0
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int hg = slot % hgroups;
+  const int64_t worker = (int64_t)(slot / hgroups) * 8 + xcd;
+  const int64_t workers = gridDim.x / hgroups;
+  const int h0 = hg * 32 * HB;
   const int H = a.H;
   const uint16_t* wt = (const uint16_t*)a.w_t;
   // fold: one wave per weight row, lane = 2 channels
   for (int n = wave; n < 32 * HB; n += 4) {
     float w0 = 0.f, w1 = 0.f;
-    if (n < H) {
-      const uint32_t raw = *reinterpret_cast<const uint32_t*>(wt + n * 128 + 2 * lane);
+    if (h0 + n < H) {
+      const uint32_t raw = *reinterpret_cast<const uint32_t*>(wt + (int64_t)(h0 + n) * 128 + 2 * lane);
       w0 = bflo(raw); w1 = bfhi(raw);
     }
     const float g0 = a.ln_w ? a.ln_w[2 * lane] : 1.f, g1 = a.ln_w ? a.ln_w[2 * lane + 1] : 1.f;
@@ -455,9 +474,15 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
 
   const uint16_t* z = (const uint16_t*)a.z;
   uint16_t* out = (uint16_t*)a.out;
-  const int64_t P = a.P;
-  const bool vec_out = (P % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
-  const int64_t wstride = (int64_t)gridDim.x * 4;
+  const int64_t P = a.P, seg = a.seg, grp = a.group;
+  const bool vec_out = (P % 4 == 0) && (seg % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  // element offset of position p inside its plane (plane hp adds blk*grp*P + h*seg)
+  auto pos_off = [&](int64_t p) -> int64_t {
+    if (!SEG) return p;
+    const int64_t u = p / seg;
+    return u * grp * seg + (p - u * seg);
+  };
+  const int64_t wstride = workers * 4;
   auto load = [&](int64_t step, u32x4 (&x)[8], bool& valid) {
     const int64_t p = step * 32 + li;
     valid = p < P;
@@ -465,7 +490,7 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
   };
-  int64_t step = (int64_t)blockIdx.x * 4 + wave;
+  int64_t step = worker * 4 + wave;
   u32x4 xn[8];
   bool vn = false;
   if (step < steps) load(step, xn, vn);
@@ -482,22 +507,21 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * hb + li) * kPLWP + 16 * kk + 8 * half])), acc);
-      const int hh = 32 * hb + li;
+      const int hh = h0 + 32 * hb + li;
       if (hh < H) {
-        const float off = sOff[hh];
-        uint16_t* op = out + (int64_t)hh * P;
+        const float off = sOff[32 * hb + li];
+        const int64_t blk = hh / grp;
+        uint16_t* op = out + blk * grp * P + (hh - blk * grp) * seg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int64_t pb = p0 + 8 * c + 4 * half;          // positions pb .. pb+3
-          const float v0 = acc[4 * c] + off, v1 = acc[4 * c + 1] + off;
-          const float v2 = acc[4 * c + 2] + off, v3 = acc[4 * c + 3] + off;
+          const float v[4] = {acc[4 * c] + off, acc[4 * c + 1] + off, acc[4 * c + 2] + off, acc[4 * c + 3] + off};
           if (vec_out && pb + 4 <= P) {
-            *reinterpret_cast<u32x2*>(op + pb) = u32x2{pack_bf2(v0, v1), pack_bf2(v2, v3)};
+            *reinterpret_cast<u32x2*>(op + pos_off(pb)) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
           } else {
-            if (pb < P) op[pb] = f2bf(v0);
-            if (pb + 1 < P) op[pb + 1] = f2bf(v1);
-            if (pb + 2 < P) op[pb + 2] = f2bf(v2);
-            if (pb + 3 < P) op[pb + 3] = f2bf(v3);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (pb + e < P) op[pos_off(pb + e)] = f2bf(v[e]);
           }
         }
       }
@@ -572,25 +596,42 @@ extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream
   if (a == nullptr || a->z == nullptr || a->w_t == nullptr || a->out == nullptr) {
     sf_set_error("pair_logits: null pointers"); return 1;
   }
-  if (a->P <= 0 || a->C <= 0 || a->C % 8 != 0 || a->C > kPLMaxC || a->H <= 0 || a->H > kPLMaxH) {
-    sf_set_error("pair_logits: need C a multiple of 8 <= %d and 0 < H <= %d (C=%d H=%d)", kPLMaxC, kPLMaxH, a->C, a->H);
+  const int max_h = a->C == 128 ? kPL128MaxH : kPLMaxH;
+  if (a->P <= 0 || a->C <= 0 || a->C % 8 != 0 || a->C > kPLMaxC || a->H <= 0 || a->H > max_h) {
+    sf_set_error("pair_logits: need C a multiple of 8 <= %d and 0 < H <= %d (1024 when C = 128) (C=%d H=%d)",
+                 kPLMaxC, kPLMaxH, a->C, a->H);
+    return 1;
+  }
+  if (a->seg < 0 || (a->seg > 0 && (a->P % a->seg != 0 || a->group <= 0 || a->H % a->group != 0))) {
+    sf_set_error("pair_logits: segmented output needs P %% seg == 0 and H %% group == 0 (P=%lld seg=%lld H=%d group=%d)",
+                 (long long)a->P, (long long)a->seg, a->H, a->group);
     return 1;
   }
   if (!al16(a->z)) { sf_set_error("pair_logits: z must be 16-byte aligned"); return 1; }
+  sf_pair_logits_args b = *a;
+  if (b.seg == 0) { b.seg = b.P; b.group = b.H; }       // plane-major == one segment, one block
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a->C == 128) {
-    const int64_t steps = (a->P + 31) / 32;
-    const int64_t groups = std::min<int64_t>((steps + 3) / 4, 256 * 8);
-    if (a->H <= 32) hipLaunchKernelGGL(pair_logits128_kernel<1>, dim3((unsigned)groups), dim3(256), 0, st, *a, steps);
-    else hipLaunchKernelGGL(pair_logits128_kernel<2>, dim3((unsigned)groups), dim3(256), 0, st, *a, steps);
+  if (b.C == 128) {
+    const int64_t steps = (b.P + 31) / 32;
+    const int hb = b.H <= 32 ? 1 : 2;
+    const int hgroups = (b.H + 32 * hb - 1) / (32 * hb);
+    const int64_t want = ((steps + 3) / 4 + 7) / 8 * 8;           // position workers, multiple of 8
+    const int64_t cap = std::max<int64_t>(8, (256 * 8 / hgroups) / 8 * 8);
+    const int64_t workers = std::min(want, cap);
+    const dim3 grid((unsigned)(workers * hgroups));
+    const bool seg = b.seg != b.P;
+    if (hb == 1 && !seg) hipLaunchKernelGGL((pair_logits128_kernel<1, false>), grid, dim3(256), 0, st, b, steps, hgroups);
+    else if (hb == 1) hipLaunchKernelGGL((pair_logits128_kernel<1, true>), grid, dim3(256), 0, st, b, steps, hgroups);
+    else if (!seg) hipLaunchKernelGGL((pair_logits128_kernel<2, false>), grid, dim3(256), 0, st, b, steps, hgroups);
+    else hipLaunchKernelGGL((pair_logits128_kernel<2, true>), grid, dim3(256), 0, st, b, steps, hgroups);
     return sf_check_launch("pair_logits128_kernel");
   }
-  const dim3 grid((unsigned)((a->P + 255) / 256));
-  if (a->H <= 4) hipLaunchKernelGGL(pair_logits_kernel<4>, grid, dim3(256), 0, st, *a);
-  else if (a->H <= 8) hipLaunchKernelGGL(pair_logits_kernel<8>, grid, dim3(256), 0, st, *a);
-  else if (a->H <= 16) hipLaunchKernelGGL(pair_logits_kernel<16>, grid, dim3(256), 0, st, *a);
-  else if (a->H <= 32) hipLaunchKernelGGL(pair_logits_kernel<32>, grid, dim3(256), 0, st, *a);
-  else hipLaunchKernelGGL(pair_logits_kernel<64>, grid, dim3(256), 0, st, *a);
+  const dim3 grid((unsigned)((b.P + 255) / 256));
+  if (b.H <= 4) hipLaunchKernelGGL(pair_logits_kernel<4>, grid, dim3(256), 0, st, b);
+  else if (b.H <= 8) hipLaunchKernelGGL(pair_logits_kernel<8>, grid, dim3(256), 0, st, b);
+  else if (b.H <= 16) hipLaunchKernelGGL(pair_logits_kernel<16>, grid, dim3(256), 0, st, b);
+  else if (b.H <= 32) hipLaunchKernelGGL(pair_logits_kernel<32>, grid, dim3(256), 0, st, b);
+  else hipLaunchKernelGGL(pair_logits_kernel<64>, grid, dim3(256), 0, st, b);
   return sf_check_launch("pair_logits_kernel");
 }
 

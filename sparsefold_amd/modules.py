@@ -16,6 +16,11 @@ Mirrored layouts (reference file:line):
 * ``CrossAttention``    transformer.py:480-547
 * ``SingleActUpdate``   blocks.py:692-737 (attention half; the transition is outside the
                         attention path)
+* ``TransformerPairLogits``         transformer.py:398-419 -- the pair-conditioning sub-modules
+                        of ``Transformer`` (``pair_input_layer_norm``, ``pair_logits_projection``)
+* ``CrossAttTransformerPairLogits`` transformer.py:611-620 -- the same for ``CrossAttTransformer``
+  (the self-attention / transition stacks of both are outside the attention path; parameter
+  names match, so those keys of a reference ``state_dict`` load into these mirrors)
 """
 from __future__ import annotations
 
@@ -226,3 +231,36 @@ class SingleActUpdate(_NoTorchPath, torch.nn.Module):
                                                 name="single_pair_logits_projection")
     self.single_attention = SelfAttention(attn_config, global_config, num_channels=seq_channels,
                                           name="single_attention_")
+
+
+class TransformerPairLogits(_NoTorchPath, torch.nn.Module):
+  """transformer.py:398-419: ``pair_input_layer_norm`` (no bias) and one
+  ``Linear(pair_cond_size, (super_block_size, num_head))`` per super-block."""
+
+  def __init__(self, *, num_blocks: int = 24, super_block_size: int = 4, num_head: int = 16,
+               pair_cond_size: int = 128, dtype: torch.dtype | None = None, name: str = "transformer"):
+    super().__init__()
+    assert num_blocks % super_block_size == 0
+    self.name = name
+    self.dtype = dtype
+    self.super_block_size = super_block_size
+    self.num_head = num_head
+    self.pair_logits_projection = torch.nn.ModuleList(
+        [Linear(pair_cond_size, (super_block_size, num_head), bias=False, name="pair_logits_projection")
+         for _ in range(num_blocks // super_block_size)])
+    self.pair_input_layer_norm = LayerNorm(pair_cond_size, bias=False, name="pair_input_layer_norm")
+
+
+class CrossAttTransformerPairLogits(_NoTorchPath, torch.nn.Module):
+  """transformer.py:611-620: ``pair_input_layer_norm`` (no bias) and
+  ``Linear(pair_cond_size, (num_blocks, num_head))``."""
+
+  def __init__(self, *, num_blocks: int = 3, num_head: int = 4, pair_cond_size: int = 16,
+               dtype: torch.dtype | None = None, name: str = "transformer"):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    self.num_head = num_head
+    self.pair_input_layer_norm = LayerNorm(pair_cond_size, bias=False, name="pair_input_layer_norm")
+    self.pair_logits_projection = Linear(pair_cond_size, (num_blocks, num_head), bias=False,
+                                         name="pair_logits_projection")

@@ -13,6 +13,8 @@ Configurations (sizes as used by the benchmark):
   window     act [S, U, 32, 128] (U = atoms/32 windows), keys = 128 atoms starting at 32u-48,
              indices outside [0, atoms) masked, last `pad` atoms padded; bias [U, 4, 32, 128];
              H=4, D=32
+  packs      Transformer pair-logit pack: pair_cond [N, N, 128] -> [6, 4, 16, N, N];
+             CrossAttTransformer pack: pair_cond [U, 32, 128, 16] -> [3, U, 4, 32, 128]
 """
 from __future__ import annotations
 
@@ -133,3 +135,22 @@ def make_window(atoms: int, *, S: int = 5, C: int = 128, H: int = 4, pad: int = 
                          num_channels=C, name="atom_transformer")
   fill_parameters(mod, seed + 1000, sharp=sharp)
   return mod, act, lay, qcond, kcond, bias
+
+
+def make_transformer_pack(N: int, *, P: int = 128, num_blocks: int = 24, super_block_size: int = 4, H: int = 16,
+                          seed: int = 6, dtype=torch.bfloat16):
+  """Pair-conditioning half of the diffusion Transformer and its pair_cond [N, N, P]."""
+  pair_cond = torch.randn(N, N, P, generator=_gen(seed)).to(dtype)
+  mod = M.TransformerPairLogits(num_blocks=num_blocks, super_block_size=super_block_size, num_head=H,
+                                pair_cond_size=P, dtype=dtype)
+  fill_parameters(mod, seed + 1000, sharp=True)
+  return mod, pair_cond
+
+
+def make_cross_pack(U: int, *, Qw: int = 32, Kw: int = 128, P: int = 16, num_blocks: int = 3, H: int = 4,
+                    seed: int = 8, dtype=torch.bfloat16):
+  """Pair-conditioning half of the atom CrossAttTransformer and its pair_cond [U, Qw, Kw, P]."""
+  pair_cond = torch.randn(U, Qw, Kw, P, generator=_gen(seed)).to(dtype)
+  mod = M.CrossAttTransformerPairLogits(num_blocks=num_blocks, num_head=H, pair_cond_size=P)
+  fill_parameters(mod, seed + 1000, sharp=True)
+  return mod, pair_cond

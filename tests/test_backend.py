@@ -50,6 +50,14 @@ def test_apply_replaces_and_restores_factories(reset_runtime):
   backends.init()
   assert M.GridSelfAttention is not original and issubclass(M.GridSelfAttention, original)
   assert M.SelfAttention.__name__ == "SelfAttention"          # not selected
+  assert M.TransformerPairLogits.__name__ == "TransformerPairLogits"
+  config.configure_runtime(backend="torch")
+  backends.init()
+  config.configure_runtime(backend="hip", device="cuda", native_ops=["diffusion_self_attention"])
+  backends.init()
+  assert M.SelfAttention.__name__ == "SelfAttentionHip"
+  assert M.TransformerPairLogits.__name__ == "TransformerPairLogitsHip"
+  assert M.CrossAttTransformerPairLogits.__name__ == "CrossAttTransformerPairLogits"
   config.configure_runtime(backend="torch")
   backends.init()
   assert M.GridSelfAttention is original
@@ -87,6 +95,13 @@ def test_reference_parameter_layouts():
   u = M.SingleActUpdate(M.GlobalConfig(), 128, 384, M.SelfAttention.Config(num_head=16))
   assert u.single_attention.key_dim == 24
   assert tuple(u.state_dict()["single_pair_logits_projection.weight"].shape) == (128, 16)
+  t = M.TransformerPairLogits(num_blocks=24, super_block_size=4, num_head=16, pair_cond_size=128)
+  shapes = {k: tuple(v.shape) for k, v in t.state_dict().items()}
+  assert shapes == {**{f"pair_logits_projection.{i}.weight": (128, 4, 16) for i in range(6)},
+                    "pair_input_layer_norm.weight": (128,)}
+  x = M.CrossAttTransformerPairLogits(num_blocks=3, num_head=4, pair_cond_size=16)
+  shapes = {k: tuple(v.shape) for k, v in x.state_dict().items()}
+  assert shapes == {"pair_logits_projection.weight": (16, 3, 4), "pair_input_layer_norm.weight": (16,)}
 
 
 def test_prepare_rejects_host_parameters_and_forward_requires_prepare(reset_runtime):
@@ -97,3 +112,57 @@ def test_prepare_rejects_host_parameters_and_forward_requires_prepare(reset_runt
     mod(torch.zeros(4, 4, 32), torch.ones(4, dtype=torch.bool))
   with pytest.raises(RuntimeError, match="on the GPU"):
     backends.prepare(mod)
+
+
+class _ValueCache:
+  """Behaviour of the reference ValueCache.get (runtime/cache.py:21-39): keyed by the
+  positional arguments' identities and the entry name; with caching off it calls the factory."""
+
+  def __init__(self, enabled: bool = True):
+    self.enabled, self.store = enabled, {}
+
+  def get(self, *args, name=None, factory=None):
+    if not self.enabled:
+      return factory()
+    key = (tuple(id(a) for a in args), name)
+    if self.store.get(key) is None and factory is not None:
+      self.store[key] = factory()
+    return self.store.get(key)
+
+  def reset(self):
+    self.store.clear()
+
+
+class _TransformerForward(torch.nn.Module):
+  """The cache use of Transformer.forward (transformer.py:430-447) plus one unrelated entry."""
+
+  def __init__(self, enabled: bool = True):
+    super().__init__()
+    self._cache = _ValueCache(enabled)
+
+  def forward(self, act, mask, single_cond, pair_cond=None):
+    pack = None if pair_cond is None else self._cache.get(name="pair_logits", factory=lambda: "reference pack")
+    return pack, self._cache.get(name="other", factory=lambda: "other")
+
+
+@pytest.mark.parametrize("enabled", [True, False])
+def test_transformer_pack_replaces_only_the_pair_logit_factory(enabled):
+  from sparsefold_amd.backends.hip.modules import TransformerHipMixin
+  calls = []
+
+  class Hip(TransformerHipMixin, _TransformerForward):
+    def pair_logits_pack(self, pair_cond):
+      calls.append(pair_cond)
+      return "hip pack"
+
+  mod = Hip(enabled)
+  cache = mod._cache
+  pc = torch.zeros(2, 2, 4)
+  assert mod(None, None, None, pc) == ("hip pack", "other")
+  assert mod(None, None, None, pc) == ("hip pack", "other")
+  assert len(calls) == (1 if enabled else 2)              # cached once per example when enabled
+  assert mod._cache is cache                              # the reference cache object is restored
+  assert mod(None, None, None, None) == (None, "other")
+  cache.reset()
+  mod(None, None, None, pc)
+  assert len(calls) == (2 if enabled else 3)

@@ -8,7 +8,7 @@ from oracle import modules as OM
 from sparsefold_amd import backends
 from sparsefold_amd import workloads as W
 from sparsefold_amd.runtime import config
-from tests._metrics import assert_close_bf16, bf16_round
+from tests._metrics import BF16_ULP, assert_close_bf16, bf16_round
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -172,3 +172,28 @@ def test_triangle_against_committed_fixture(transpose):
   upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
   ref = torch.from_numpy(f[f"tri20_{tag}_update"])
   assert_close_bf16(upd, ref, f"fixture triangle N=20 {tag}", max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("N", [96, 37])
+def test_transformer_pair_logit_pack(N):
+  """transformer.py:430-438: 6 super-blocks x (4 blocks x 16 heads) = 384 planes in one pass
+  (N=37: N*N is not a multiple of 4, the store tail)."""
+  mod, pair_cond = W.make_transformer_pack(N, seed=6 + N)
+  hip = _prepared(mod)
+  out = hip.pair_logits_pack(pair_cond.to(DEV))
+  assert out.shape == (6, 4, 16, N, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
+  ref = OM.transformer_pair_logits(pair_cond.float(), _params(hip), 4, None)
+  # logits of several units are stored in bf16 by the reference too (transformer.py:438)
+  assert_close_bf16(out.float().cpu(), ref, f"transformer pack N={N}", rtol=BF16_ULP)
+
+
+@pytest.mark.parametrize("U,Qw,Kw,P", [(8, 32, 128, 16), (6, 5, 7, 128), (4, 32, 128, 128)])
+def test_cross_att_pair_logit_pack(U, Qw, Kw, P):
+  """transformer.py:655-662: [U, Q, K, P] -> [num_blocks, U, H, Q, K] written in place
+  (P=16: one thread per position; P=128: the MFMA kernel, Q*K=35 takes the unaligned stores)."""
+  mod, pair_cond = W.make_cross_pack(U, Qw=Qw, Kw=Kw, P=P, seed=U + P)
+  hip = _prepared(mod)
+  out = hip.pair_logits_pack(pair_cond.to(DEV))
+  assert out.shape == (3, U, 4, Qw, Kw) and out.dtype == torch.bfloat16 and out.is_contiguous()
+  ref = OM.cross_att_pair_logits(pair_cond.float(), _params(hip))
+  assert_close_bf16(out.float().cpu(), ref, f"cross pack U={U} Q={Qw} K={Kw} P={P}", rtol=BF16_ULP)

@@ -7,7 +7,7 @@ from oracle.modules import atom_layout_convert
 from oracle.primitives import layer_norm as oracle_ln
 from sparsefold_amd.backends.hip import ops
 from sparsefold_amd import workloads as W
-from tests._metrics import assert_close_bf16, bf16_round
+from tests._metrics import BF16_ULP, assert_close_bf16, bf16_round
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -72,7 +72,8 @@ def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns(K):
 # scalar stores); other C the per-position kernel.
 @pytest.mark.parametrize("H,C,with_b,shape", [(4, 128, True, (33, 40)), (16, 128, True, (33, 40)),
                                               (16, 128, True, (37, 41)), (12, 16, False, (33, 40)),
-                                              (64, 128, False, (33, 40)), (40, 128, True, (37, 41))])
+                                              (64, 128, False, (33, 40)), (40, 128, True, (37, 41)),
+                                              (100, 128, True, (37, 41)), (384, 128, False, (64, 64))])
 def test_pair_logits(H, C, with_b, shape):
   g = torch.Generator().manual_seed(H * C)
   z = torch.randn(*shape, C, generator=g).to(torch.bfloat16)
@@ -80,7 +81,21 @@ def test_pair_logits(H, C, with_b, shape):
   w = (torch.randn(H, C, generator=g) / C ** 0.5).to(torch.bfloat16)
   out = ops.pair_logits(z.to(DEV), lw.to(DEV), lb.to(DEV) if with_b else None, w.to(DEV))
   ref = torch.einsum("abc,hc->hab", oracle_ln(z.float(), lw, lb if with_b else None), w.float()).reshape(H, -1)
-  assert_close_bf16(out, ref, f"pair_logits H={H} C={C}")
+  assert_close_bf16(out, ref, f"pair_logits H={H} C={C}", rtol=BF16_ULP)   # bf16 logits planes of O(1-5)
+
+
+@pytest.mark.parametrize("C,U,QK,blocks,H", [(16, 8, 4096, 3, 4), (128, 6, 35, 3, 4), (128, 3, 64, 12, 8)])
+def test_pair_logits_segmented_layout_is_a_permutation(C, U, QK, blocks, H):
+  """The segmented store writes exactly the plane-major values, permuted
+  [blocks, H, U, QK] -> [blocks, U, H, QK] (same arithmetic, different addresses)."""
+  g = torch.Generator().manual_seed(C + QK)
+  z = torch.randn(U * QK, C, generator=g).to(torch.bfloat16).to(DEV)
+  lw = (1 + 0.1 * torch.randn(C, generator=g)).to(DEV)
+  w = (torch.randn(blocks * H, C, generator=g) / C ** 0.5).to(torch.bfloat16).to(DEV)
+  flat = ops.pair_logits(z, lw, None, w)
+  seg = ops.pair_logits(z, lw, None, w, seg=QK, group=H)
+  assert seg.shape == (blocks, U, H, QK)
+  assert torch.equal(seg, flat.view(blocks, H, U, QK).permute(0, 2, 1, 3))
 
 
 def test_window_gather_exact():
