@@ -1,7 +1,10 @@
-// C-ABI plumbing: version, thread-local error messages, launch checks.
+// C-ABI plumbing: version, thread-local error messages, launch checks, occupancy queries.
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "sf_common.h"
 
@@ -23,6 +26,26 @@ int sf_check_launch(const char* what) {
     return 2;
   }
   return 0;
+}
+
+int sf_resident_workgroups(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  const auto key = std::make_tuple(dev, kernel, threads);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) per_cu = 1;
+  const int n = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = n;
+  return n;
 }
 
 extern "C" int sf_hip_abi_version(void) { return SF_HIP_ABI_VERSION; }

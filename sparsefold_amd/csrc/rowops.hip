@@ -340,70 +340,84 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
 // ------------------------------------------------------------------------------------
 constexpr int kPLMaxC = 128, kPLMaxH = 64;
 
-template <int H>  // H = compile-time capacity; a.H <= H planes are produced
+template <int H, int CM>  // capacities: a.H <= H planes, a.C <= CM channels (C % 8 == 0)
 __global__ __launch_bounds__(256) void pair_logits_kernel(const sf_pair_logits_args a) {
-  __shared__ float sG[kPLMaxC * H];   // gamma[c] * w[h][c]   (zero for h >= a.H)
+  __shared__ float sG[CM * H];        // gamma[c] * w[h][c]   (zero for h >= a.H)
   __shared__ float sS2[H];            // sum_c beta[c] * w[h][c]
+  __shared__ int64_t sPl[H];          // element offset of plane h (a.seg / a.group normalised by the host)
   const int C = a.C, Hr = a.H;
+  const int64_t P = a.P, seg = a.seg, grp = a.group;
   const uint16_t* wt = (const uint16_t*)a.w_t;
   for (int t = threadIdx.x; t < C * H; t += 256) {
     const int c = t / H, h = t % H;
     sG[t] = h < Hr ? bf2f(wt[h * C + c]) * (a.ln_w ? a.ln_w[c] : 1.f) : 0.f;
   }
   if (threadIdx.x < H) {
+    const int h = threadIdx.x;
     float s = 0.f;
-    if (a.ln_b && (int)threadIdx.x < Hr)
-      for (int c = 0; c < C; ++c) s += a.ln_b[c] * bf2f(wt[threadIdx.x * C + c]);
-    sS2[threadIdx.x] = s;
+    if (a.ln_b && h < Hr)
+      for (int c = 0; c < C; ++c) s += a.ln_b[c] * bf2f(wt[h * C + c]);
+    sS2[h] = s;
+    const int64_t blk = h / grp;
+    sPl[h] = blk * grp * P + (h - blk * grp) * seg;
   }
   __syncthreads();
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p >= a.P) return;
-  const uint16_t* zp = (const uint16_t*)a.z + p * C;
-  uint32_t xw[kPLMaxC / 2];
-  float sum = 0.f;
+  const uint16_t* z = (const uint16_t*)a.z;
+  uint16_t* op = (uint16_t*)a.out;
+  const bool narrow = seg <= 0xffffffffll;
+  auto load = [&](int64_t p, u32x4 (&x)[CM / 8]) {
+    const uint16_t* zp = z + (p < P ? p : 0) * C;
 #pragma unroll
-  for (int ch = 0; ch < kPLMaxC / 8; ++ch) {
-    if (8 * ch < C) {
-      const u32x4 w = ld16(zp + 8 * ch);
+    for (int ch = 0; ch < CM / 8; ++ch) x[ch] = (p < P && 8 * ch < C) ? ld16(zp + 8 * ch) : u32x4{0, 0, 0, 0};
+  };
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 xn[CM / 8];
+  load(p, xn);
+  for (; p < P; p += stride) {
+    asm volatile("" ::: "memory");            // keep the LDS weight reads inside the loop (no hoisting into VGPRs)
+    uint32_t xw[CM / 2];
+    float sum = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < CM / 8; ++ch)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        xw[4 * ch + e] = w[e];
-        sum += bflo(w[e]) + bfhi(w[e]);
+        xw[4 * ch + e] = xn[ch][e];
+        sum += bflo(xn[ch][e]) + bfhi(xn[ch][e]);          // channels >= C were loaded as zeros
+      }
+    load(p + stride, xn);
+    const float mean = sum / (float)C;
+    float sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < CM / 2; ++e) {
+      if (2 * e < C) {
+        const float d0 = bflo(xw[e]) - mean, d1 = bfhi(xw[e]) - mean;
+        sq += d0 * d0 + d1 * d1;
       }
     }
-  }
-  const float mean = sum / (float)C;
-  float sq = 0.f;
+    const float rstd = rsqrtf(sq / (float)C + 1e-5f);
+    float acc[H];
 #pragma unroll
-  for (int e = 0; e < kPLMaxC / 2; ++e) {
-    if (2 * e < C) {
-      const float d0 = bflo(xw[e]) - mean, d1 = bfhi(xw[e]) - mean;
-      sq += d0 * d0 + d1 * d1;
+    for (int h = 0; h < H; ++h) acc[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < CM / 2; ++e) {
+      if (2 * e < C) {
+        const float x0 = bflo(xw[e]) - mean, x1 = bfhi(xw[e]) - mean;
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[h] += x0 * sG[(2 * e) * H + h] + x1 * sG[(2 * e + 1) * H + h];
+      }
     }
-  }
-  const float rstd = rsqrtf(sq / (float)C + 1e-5f);
-  float acc[H];
-#pragma unroll
-  for (int h = 0; h < H; ++h) acc[h] = 0.f;
-#pragma unroll
-  for (int e = 0; e < kPLMaxC / 2; ++e) {
-    if (2 * e < C) {
-      const float x0 = bflo(xw[e]) - mean, x1 = bfhi(xw[e]) - mean;
-#pragma unroll
-      for (int h = 0; h < H; ++h) acc[h] += x0 * sG[(2 * e) * H + h] + x1 * sG[(2 * e + 1) * H + h];
+    int64_t pos;
+    if (narrow) {
+      const uint32_t u = (uint32_t)((uint64_t)p / (uint32_t)seg);
+      pos = (int64_t)u * grp * seg + (p - (int64_t)u * seg);
+    } else {
+      const int64_t u = p / seg;
+      pos = u * grp * seg + (p - u * seg);
     }
-  }
-  uint16_t* op = (uint16_t*)a.out;
-  // a.seg / a.group are normalised by the host (plane-major: seg = P, group = H)
-  const int64_t u = p / a.seg;
-  const int64_t pos = u * a.group * a.seg + (p - u * a.seg);
 #pragma unroll
-  for (int h = 0; h < H; ++h) {
-    if (h < Hr) {
-      const int blk = h / a.group;
-      op[(int64_t)blk * a.group * a.P + (int64_t)(h - blk * a.group) * a.seg + pos] = f2bf(acc[h] * rstd + sS2[h]);
-    }
+    for (int h = 0; h < H; ++h)
+      if (h < Hr) __builtin_nontemporal_store(f2bf(acc[h] * rstd + sS2[h]), op + sPl[h] + pos);
   }
 }
 
@@ -429,24 +443,50 @@ __global__ __launch_bounds__(256) void window_gather_kernel(const sf_window_gath
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // ------------------------------------------------------------------------------------
-// Pair logits, C = 128: 32 positions per wave step.  Lane (li, half) loads 8 x 16 bytes of
-// position li (the 32 rows of a step are 8 KB of contiguous memory), normalises them straight
-// into MFMA operands, and D = X . Wf^T against the gamma-folded weight held in LDS gives lane
-// li = head, registers = 4 consecutive positions: 8-byte stores into each bias plane.  Waves
-// stride over the steps, loading step n+1 while step n computes.
+// Pair logits, C = 128.  A workgroup of W waves takes 32 W consecutive positions per
+// iteration, one 32-row step per wave: lane (li, half) loads 8 x 16 bytes of position li,
+// normalises them straight into MFMA operands, and D = X . Wf^T against the gamma-folded weight
+// held in LDS gives lane li = head, registers = 4 consecutive positions.  The D tiles go to an
+// LDS tile [64 planes][32 W positions]; after one barrier each wave stores whole 64 W-byte plane
+// runs with 16-byte non-temporal stores (the planes are consumed by a later kernel, so they
+// bypass L2 and leave it to the z rows).  The next iteration's z rows are loaded before the
+// barrier; the tile is double-buffered, so one barrier per tile suffices.  A workgroup reuses
+// its normalised operands for G2 tiles of 64 planes (128 planes per z read).
 //
-// More than 64 planes (the Transformer pack has 384) are split over `hgroups` workgroups per
-// position worker, each folding its own 64 weight rows.  The hgroups workgroups of one worker
-// are dispatched back to back onto one XCD (workgroup ids b, b+8, b+16, ...), walk the same
-// steps in lock-step and so read each z row from HBM once: the repeats hit that XCD's L2.
+// More planes (the Transformer pack has 384) are split over `hgroups` workgroups per position
+// worker, each folding its own G2 x 64 weight rows.  The hgroups workgroups of one worker are
+// dispatched back to back onto one XCD (workgroup ids b, b+8, b+16, ...), walk the same
+// positions in lock-step and so read each z row from HBM once: the repeats hit that XCD's L2.
+// The grid holds only as many workgroups as are resident at once, so all of them sweep one
+// contiguous window of every plane together.
 // ------------------------------------------------------------------------------------
 constexpr int kPLWP = 128 + 8;        // LDS pitch (elements) of folded weight rows
 constexpr int kPL128MaxH = 1024;
+constexpr int kPLWaves = 4;           // waves per workgroup (4 and 8 measure the same)
 
-template <int HB, bool SEG>  // 32-head blocks per workgroup (H <= 32 * HB * hgroups); SEG: segmented output
-__global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps, int hgroups) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[32 * HB * kPLWP];
-  __shared__ float sOff[32 * HB];
+// LDS barrier that leaves global loads in flight: this wave's LDS accesses complete
+// (lgkmcnt 0; vmcnt / expcnt left at their maxima), then the workgroup barrier.
+__device__ __forceinline__ void lds_only_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// HB: 32-plane blocks per tile (NP = 32 HB planes); G2: tiles per workgroup (the normalised z
+// operands are reused for G2 * NP planes; H <= G2 * NP * hgroups); SEG: segmented output.
+template <int HB, int G2, bool SEG, int W>
+__global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps, int hgroups) {
+  constexpr int NP = 32 * HB;                 // planes per tile
+  constexpr int TPOS = 32 * W;                // positions per tile (one 32-row step per wave)
+  constexpr int TP = TPOS + 8;                // LDS pitch of tile rows
+  constexpr int LPP = TPOS / 8;               // lanes per plane run (16 bytes each)
+  constexpr int PPI = 64 / LPP;               // planes per store instruction
+  constexpr int PPW = NP / W;                 // planes stored per wave per tile
+  static_assert(PPW % PPI == 0, "tile planes must split evenly over the waves");
+  __shared__ __attribute__((aligned(16))) uint16_t sW[G2 * NP * kPLWP];
+  __shared__ __attribute__((aligned(16))) uint16_t sT[2][NP * TP];
+  __shared__ float sOff[G2 * NP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   // grid = hgroups * workers, workers % 8 == 0
@@ -454,11 +494,11 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
   const int hg = slot % hgroups;
   const int64_t worker = (int64_t)(slot / hgroups) * 8 + xcd;
   const int64_t workers = gridDim.x / hgroups;
-  const int h0 = hg * 32 * HB;
+  const int h0 = hg * G2 * NP;
   const int H = a.H;
   const uint16_t* wt = (const uint16_t*)a.w_t;
   // fold: one wave per weight row, lane = 2 channels
-  for (int n = wave; n < 32 * HB; n += 4) {
+  for (int n = wave; n < G2 * NP; n += W) {
     float w0 = 0.f, w1 = 0.f;
     if (h0 + n < H) {
       const uint32_t raw = *reinterpret_cast<const uint32_t*>(wt + (int64_t)(h0 + n) * 128 + 2 * lane);
@@ -475,30 +515,35 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
   const uint16_t* z = (const uint16_t*)a.z;
   uint16_t* out = (uint16_t*)a.out;
   const int64_t P = a.P, seg = a.seg, grp = a.group;
-  const bool vec_out = (P % 4 == 0) && (seg % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  const bool vec_out = (P % 8 == 0) && (seg % 8 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
   // element offset of position p inside its plane (plane hp adds blk*grp*P + h*seg)
   auto pos_off = [&](int64_t p) -> int64_t {
     if (!SEG) return p;
     const int64_t u = p / seg;
     return u * grp * seg + (p - u * seg);
   };
-  const int64_t wstride = workers * 4;
   auto load = [&](int64_t step, u32x4 (&x)[8], bool& valid) {
     const int64_t p = step * 32 + li;
-    valid = p < P;
+    valid = step < steps && p < P;
     const uint16_t* zp = z + (valid ? p : 0) * 128 + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
   };
-  int64_t step = worker * 4 + wave;
+  // the planes this wave stores: plane row pl = wave * PPW + PPI * i + lane / LPP, chunk lane % LPP
+  const int ch = lane % LPP;
+  const int64_t wstride = workers * W;
+  int64_t base = worker * W;                  // first step of this workgroup's tile
   u32x4 xn[8];
   bool vn = false;
-  if (step < steps) load(step, xn, vn);
-  for (; step < steps; step += wstride) {
+  if (base < steps) load(base + wave, xn, vn);
+  int buf = 0;
+  for (; base < steps; base += wstride) {
     bf16x8 xo[8];
     ln128_operands(xn, vn, xo);
-    if (step + wstride < steps) load(step + wstride, xn, vn);
-    const int64_t p0 = step * 32;
+    load(base + wstride + wave, xn, vn);
+#pragma unroll
+    for (int g = 0; g < G2; ++g, buf ^= 1) {
+    uint16_t* T = sT[buf];
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
       f32x16 acc;
@@ -506,25 +551,33 @@ __global__ __launch_bounds__(256) void pair_logits128_kernel(const sf_pair_logit
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * hb + li) * kPLWP + 16 * kk + 8 * half])), acc);
-      const int hh = h0 + 32 * hb + li;
-      if (hh < H) {
-        const float off = sOff[32 * hb + li];
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(g * NP + 32 * hb + li) * kPLWP + 16 * kk + 8 * half])), acc);
+      const float off = sOff[g * NP + 32 * hb + li];
+      uint16_t* trow = T + (32 * hb + li) * TP + 32 * wave + 4 * half;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<u32x2*>(trow + 8 * c) =
+            u32x2{pack_bf2(acc[4 * c] + off, acc[4 * c + 1] + off), pack_bf2(acc[4 * c + 2] + off, acc[4 * c + 3] + off)};
+    }
+    lds_only_barrier();
+    const int64_t p = base * 32 + 8 * ch;     // first of this lane's 8 positions
+#pragma unroll
+    for (int i = 0; i < PPW / PPI; ++i) {
+      const int pl = wave * PPW + PPI * i + lane / LPP;
+      const u32x4 v = ld16(T + pl * TP + 8 * ch);
+      const int hh = h0 + g * NP + pl;
+      if (hh < H && p < P) {
         const int64_t blk = hh / grp;
         uint16_t* op = out + blk * grp * P + (hh - blk * grp) * seg;
+        if (vec_out && p + 8 <= P) {
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(op + pos_off(p)));   // streamed past L2
+        } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int64_t pb = p0 + 8 * c + 4 * half;          // positions pb .. pb+3
-          const float v[4] = {acc[4 * c] + off, acc[4 * c + 1] + off, acc[4 * c + 2] + off, acc[4 * c + 3] + off};
-          if (vec_out && pb + 4 <= P) {
-            *reinterpret_cast<u32x2*>(op + pos_off(pb)) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (pb + e < P) op[pos_off(pb + e)] = f2bf(v[e]);
-          }
+          for (int e = 0; e < 8; ++e)
+            if (p + e < P) op[pos_off(p + e)] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
         }
       }
+    }
     }
   }
 }
@@ -614,24 +667,43 @@ extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream
   if (b.C == 128) {
     const int64_t steps = (b.P + 31) / 32;
     const int hb = b.H <= 32 ? 1 : 2;
-    const int hgroups = (b.H + 32 * hb - 1) / (32 * hb);
-    const int64_t want = ((steps + 3) / 4 + 7) / 8 * 8;           // position workers, multiple of 8
-    const int64_t cap = std::max<int64_t>(8, (256 * 8 / hgroups) / 8 * 8);
-    const int64_t workers = std::min(want, cap);
-    const dim3 grid((unsigned)(workers * hgroups));
+    const int g2 = b.H <= 64 ? 1 : 2;
+    const int hgroups = (b.H + 32 * hb * g2 - 1) / (32 * hb * g2);
     const bool seg = b.seg != b.P;
-    if (hb == 1 && !seg) hipLaunchKernelGGL((pair_logits128_kernel<1, false>), grid, dim3(256), 0, st, b, steps, hgroups);
-    else if (hb == 1) hipLaunchKernelGGL((pair_logits128_kernel<1, true>), grid, dim3(256), 0, st, b, steps, hgroups);
-    else if (!seg) hipLaunchKernelGGL((pair_logits128_kernel<2, false>), grid, dim3(256), 0, st, b, steps, hgroups);
-    else hipLaunchKernelGGL((pair_logits128_kernel<2, true>), grid, dim3(256), 0, st, b, steps, hgroups);
+    auto launch = [&](auto kernel) {
+      // position workers (a multiple of 8): enough for every tile, and no more workgroups than are
+      // resident at once
+      const int64_t want = ((steps + kPLWaves - 1) / kPLWaves + 7) / 8 * 8;
+      const int64_t cap = std::max<int64_t>(
+          8, (sf_resident_workgroups(reinterpret_cast<const void*>(kernel), 64 * kPLWaves) / hgroups) / 8 * 8);
+      const int64_t workers = std::min(want, cap);
+      hipLaunchKernelGGL(kernel, dim3((unsigned)(workers * hgroups)), dim3(64 * kPLWaves), 0, st, b, steps, hgroups);
+    };
+    if (hb == 1 && !seg) launch(pair_logits128_kernel<1, 1, false, kPLWaves>);
+    else if (hb == 1) launch(pair_logits128_kernel<1, 1, true, kPLWaves>);
+    else if (g2 == 1 && !seg) launch(pair_logits128_kernel<2, 1, false, kPLWaves>);
+    else if (g2 == 1) launch(pair_logits128_kernel<2, 1, true, kPLWaves>);
+    else if (!seg) launch(pair_logits128_kernel<2, 2, false, kPLWaves>);
+    else launch(pair_logits128_kernel<2, 2, true, kPLWaves>);
     return sf_check_launch("pair_logits128_kernel");
   }
-  const dim3 grid((unsigned)((b.P + 255) / 256));
-  if (b.H <= 4) hipLaunchKernelGGL(pair_logits_kernel<4>, grid, dim3(256), 0, st, b);
-  else if (b.H <= 8) hipLaunchKernelGGL(pair_logits_kernel<8>, grid, dim3(256), 0, st, b);
-  else if (b.H <= 16) hipLaunchKernelGGL(pair_logits_kernel<16>, grid, dim3(256), 0, st, b);
-  else if (b.H <= 32) hipLaunchKernelGGL(pair_logits_kernel<32>, grid, dim3(256), 0, st, b);
-  else hipLaunchKernelGGL(pair_logits_kernel<64>, grid, dim3(256), 0, st, b);
+  auto launch = [&](auto kernel) {
+    const int64_t want = (b.P + 255) / 256;
+    const int64_t cap = sf_resident_workgroups(reinterpret_cast<const void*>(kernel), 256);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)std::min(want, cap)), dim3(256), 0, st, b);
+  };
+  auto by_h = [&](auto cm) {
+    constexpr int CM = decltype(cm)::value;
+    if (b.H <= 4) launch(pair_logits_kernel<4, CM>);
+    else if (b.H <= 8) launch(pair_logits_kernel<8, CM>);
+    else if (b.H <= 16) launch(pair_logits_kernel<16, CM>);
+    else if (b.H <= 32) launch(pair_logits_kernel<32, CM>);
+    else launch(pair_logits_kernel<64, CM>);
+  };
+  if (b.C <= 16) by_h(std::integral_constant<int, 16>{});
+  else if (b.C <= 32) by_h(std::integral_constant<int, 32>{});
+  else if (b.C <= 64) by_h(std::integral_constant<int, 64>{});
+  else by_h(std::integral_constant<int, 128>{});
   return sf_check_launch("pair_logits_kernel");
 }
 

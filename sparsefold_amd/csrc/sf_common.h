@@ -116,3 +116,7 @@ __device__ __forceinline__ void ln128_operands(const u32x4 (&x)[8], bool valid, 
 // Thread-local last-error plumbing shared by all C entry points.
 void sf_set_error(const char* fmt, ...);
 int sf_check_launch(const char* what);
+
+// Workgroups of `kernel` (launched with `threads` threads, no dynamic LDS) that the current
+// device holds at once: CUs x occupancy; cached per (device, kernel).  At least 1.
+int sf_resident_workgroups(const void* kernel, int threads);
