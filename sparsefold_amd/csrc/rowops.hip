@@ -570,7 +570,7 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
         const int64_t blk = hh / grp;
         uint16_t* op = out + blk * grp * P + (hh - blk * grp) * seg;
         if (vec_out && p + 8 <= P) {
-          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(op + pos_off(p)));   // streamed past L2
+          st16_stream(op + pos_off(p), v);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e)

@@ -44,6 +44,12 @@ __device__ __forceinline__ float add_bf2(bf16x2 v, float acc) {
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// Non-temporal (streaming) 16-byte store: for outputs that a later kernel reads, written in runs
+// of whole 128-byte lines by each instruction.  Scattered partial-line streams are slower than
+// plain stores (measured 3x on 8-byte scattered stores), so use it only for full-line runs.
+__device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -205,7 +205,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
             w[2 + e] = pack_bf2(valid ? (acc[8 * kk + 4 + 2 * e] + o1[2 * e]) * sc : 0.f,
                                 valid ? (acc[8 * kk + 4 + 2 * e + 1] + o1[2 * e + 1]) * sc : 0.f);
           }
-          st16(op + kk * 512, u32x4{w[0], w[1], w[2], w[3]});
+          st16_stream(op + kk * 512, u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
           w[e] = pack_bf2(pos_valid(r, k0) ? acc[8 * cc + t0] + off : 0.f,
                           pos_valid(r, k1) ? acc[8 * cc + t1] + off : 0.f);
         }
-        st16(a.vt + vl_off(r, hh, H, NP, (p0 >> 4) + cc, half, li), u32x4{w[0], w[1], w[2], w[3]});
+        st16_stream(a.vt + vl_off(r, hh, H, NP, (p0 >> 4) + cc, half, li), u32x4{w[0], w[1], w[2], w[3]});
       }
     }
     // bias planes: D = X . Wb^T, lane = head li (< H), 4 consecutive positions
