@@ -300,8 +300,10 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
   __shared__ __attribute__((aligned(16))) uint16_t sG[kPC * kWP];
   __shared__ __attribute__((aligned(16))) float sGoff[kPC];
+  __shared__ __attribute__((aligned(16))) uint16_t sOut[kPWaves][32 * kWP];   // per-wave output rows
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
+  uint16_t* const so = sOut[wave];
   for (int t = tid; t < kPC * (kPC / 8); t += 64 * kPWaves) {
     const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
     // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
@@ -396,20 +398,30 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
         acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
-      if (ok) {
-        uint16_t* outp = a.out + p * kPC + 32 * nb + 4 * half;
+      uint16_t* orow = so + li * kWP + 32 * nb + 4 * half;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float v[4];
+      for (int c = 0; c < 4; ++c) {
+        float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
-          if (a.add_residual) {
-            const uint32_t z0 = zr[2 * nb + (c >> 1)][c & 1][0], z1 = zr[2 * nb + (c >> 1)][c & 1][1];
-            v[0] += bflo(z0); v[1] += bfhi(z0); v[2] += bflo(z1); v[3] += bfhi(z1);
-          }
-          *reinterpret_cast<u32x2*>(outp + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
+        if (a.add_residual) {
+          const uint32_t z0 = zr[2 * nb + (c >> 1)][c & 1][0], z1 = zr[2 * nb + (c >> 1)][c & 1][1];
+          v[0] += bflo(z0); v[1] += bfhi(z0); v[2] += bflo(z1); v[3] += bfhi(z1);
         }
+        *reinterpret_cast<u32x2*>(orow + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
       }
+    }
+    // the wave's 32 output rows are 8 KB of contiguous memory: lane (row 4i + lane/16, chunk
+    // lane%16) stores 16 bytes, four whole 256-byte rows per streaming store (the LDS rows were
+    // written by other lanes of this wave; LDS executes a wave's accesses in order).  Against
+    // 8-byte stores straight from the MFMA layout: 0.128 -> 0.106 ms at N=768.
+    asm volatile("" ::: "memory");
+    const int64_t p0 = p - li;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 4 * i + (lane >> 4), ch = lane & 15;
+      const u32x4 v = ld16(so + row * kWP + 8 * ch);
+      if (p0 + row < a.P) st16_stream(a.out + (p0 + row) * kPC + 8 * ch, v);
     }
   }
 }
