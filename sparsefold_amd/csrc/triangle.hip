@@ -592,13 +592,13 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   };
   // weights 2^(s - shift) as packed bf16 pairs in PV slot order; returns their sum
   auto weights_half = [&](const f32x16& s, float shift, bf16x2 (&pw)[8]) __attribute__((always_inline)) {
-    float ts = 0.f;
+    float ts0 = 0.f, ts1 = 0.f;                          // two chains of dependent sums
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       pw[e] = cvt_bf2(fast_exp2(s[2 * e] - shift), fast_exp2(s[2 * e + 1] - shift));
-      ts = add_bf2(pw[e], ts);
+      if (e & 1) ts1 = add_bf2(pw[e], ts1); else ts0 = add_bf2(pw[e], ts0);
     }
-    return ts;
+    return ts0 + ts1;
   };
   auto max_half = [&](const f32x16& s) __attribute__((always_inline)) {
     float v = s[0];
@@ -616,6 +616,36 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
         pb[2 * q2 + 1] = pw[4 * j + q2][1];
       }
       o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, 2 * kb + j))), pb, o[rr]);
+    }
+  };
+  // the same with operands read from LDS one unit earlier (the per-unit mass check is a branch,
+  // so reads issued in the unit that uses them would wait out the LDS latency every unit)
+  auto load_k = [&](int rr, int kb, int buf, bf16x8 (&kr)[2]) __attribute__((always_inline)) {
+    kr[0] = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
+    kr[1] = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
+  };
+  auto load_v = [&](int rr, int kb, int buf, bf16x8 (&vr)[2]) __attribute__((always_inline)) {
+    vr[0] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb)));
+    vr[1] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb + 1)));
+  };
+  auto qk_reg = [&](int rr, int kb, const bf16x8 (&kr)[2], f32x16& s) __attribute__((always_inline)) {
+    s = mfma32(kr[1], qb8[rr][1], mfma32(kr[0], qb8[rr][0], bseed[kb]));
+    bf16x8 mq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
+    mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
+    s = mfma32(ones_k, mq, s);
+  };
+  auto pv_reg = [&](int rr, const bf16x8 (&vr)[2], const bf16x2 (&pw)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 pb;
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        pb[2 * q2] = pw[4 * j + q2][0];
+        pb[2 * q2 + 1] = pw[4 * j + q2][1];
+      }
+      o[rr] = mfma32(vr[j], pb, o[rr]);
     }
   };
 
@@ -655,11 +685,16 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     if (active) {
       load_bias(buf);
       f32x16 sc, sn;
-      qk_half(0, 0, buf, true, sc);
+      bf16x8 kr[2], vr[2];
+      load_k(0, 0, buf, kr);
+      qk_reg(0, 0, kr, sc);
+      load_k(0, 1, buf, kr);
+      load_v(0, 0, buf, vr);
 #pragma unroll
       for (int u = 0; u < 2 * kTR; ++u) {
         const int rr = u >> 1, kb = u & 1;
-        if (u + 1 < 2 * kTR) qk_half((u + 1) >> 1, (u + 1) & 1, buf, true, sn);
+        if (u + 1 < 2 * kTR) qk_reg((u + 1) >> 1, (u + 1) & 1, kr, sn);
+        if (u + 2 < 2 * kTR) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
         bf16x2 pw[8];
         float ts = weights_half(sc, 0.0f, pw);
         if (__any(!(ts <= a.mass_limit))) {
@@ -680,7 +715,8 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
           }
         }
         l[rr] += ts;
-        pv_half(rr, kb, buf, pw);
+        pv_reg(rr, vr, pw);
+        if (u + 1 < 2 * kTR) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
         sc = sn;
       }
     }
