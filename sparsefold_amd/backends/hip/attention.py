@@ -65,10 +65,10 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     bias5 = _as5(bias.to(bf), batch, b0, b1)
   mq5 = mk5 = None
   if mask_q is not None:
-    mq = mask_q.to(torch.uint8).expand(*batch, Q)
+    mq = ops._u8(mask_q).expand(*batch, Q)
     mq5 = mq.reshape(b0, b1, Q)
   if mask_k is not None:
-    mk = mask_k.to(torch.uint8).expand(*batch, K)
+    mk = ops._u8(mask_k).expand(*batch, K)
     mk5 = mk.reshape(b0, b1, K)
   g5 = None
   if gate is not None:

@@ -55,7 +55,12 @@ def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
-  return t if t.dtype == torch.uint8 else t.to(torch.uint8)
+  """Byte mask: a bool tensor is reinterpreted in place (torch stores bool as 0/1 bytes)."""
+  if t.dtype == torch.uint8:
+    return t
+  if t.dtype == torch.bool:
+    return t.view(torch.uint8)
+  return (t != 0).view(torch.uint8)
 
 
 def _rows(t: torch.Tensor, last: int) -> torch.Tensor:

@@ -554,6 +554,7 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     m[rr] = 0.f;
     l[rr] = 0.f;
   }
+  int mflag = 0;                                         // bit rr: some lane of row rr has m != 0 (uniform)
   bf16x8 ones_k;                                         // A operand: 1 at k = 0 (lanes of half 0)
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones_k[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
@@ -630,11 +631,13 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   };
   auto qk_reg = [&](int rr, int kb, const bf16x8 (&kr)[2], f32x16& s) __attribute__((always_inline)) {
     s = mfma32(kr[1], qb8[rr][1], mfma32(kr[0], qb8[rr][0], bseed[kb]));
-    bf16x8 mq;
+    if (__builtin_amdgcn_readfirstlane(mflag) & (1 << rr)) {   // some lane of the row has m != 0
+      bf16x8 mq;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
-    mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
-    s = mfma32(ones_k, mq, s);
+      for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
+      mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
+      s = mfma32(ones_k, mq, s);
+    }
   };
   auto pv_reg = [&](int rr, const bf16x8 (&vr)[2], const bf16x2 (&pw)[8]) __attribute__((always_inline)) {
 #pragma unroll
@@ -665,8 +668,12 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       qk_half(rr, 1, 0, false, s1);
       const float smax = fmaxf(max_half(s0), max_half(s1));
       // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
-      const float m0 = smax > 0.5f * SF_MASKED_LOGIT ? (float)(__bf16)smax : 0.0f;
+      // rows whose tile-0 maximum is moderate keep the reference point at 0, which lets their
+      // later tiles skip the m step (exp2 of logits up to +-32 is far inside fp32 range; the mass
+      // check still moves m if a later tile climbs past the limit)
+      const float m0 = (smax > 0.5f * SF_MASKED_LOGIT && fabsf(smax) > 32.0f) ? (float)(__bf16)smax : 0.0f;
       m[rr] = m0;
+      if (__any(m0 != 0.0f)) mflag |= 1 << rr;
       bf16x2 pw[8];
       l[rr] = weights_half(s0, m0, pw);
       pv_half(rr, 0, 0, pw);
@@ -705,6 +712,7 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
           const float shift = mnew - m[rr];
           const float alpha = fast_exp2(-shift);
           m[rr] = mnew;
+          if (__any(mnew != 0.0f)) mflag |= 1 << rr;
           l[rr] *= alpha;
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
