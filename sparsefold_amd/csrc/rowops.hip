@@ -201,7 +201,9 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
   constexpr int CHUNKS = BUF / 1024, CPW = CHUNKS / 4;        // 1 KB chunks per wave per step
   constexpr int WR = BM / 2, WC = BN / 2;                     // wave tile
   constexpr int MB = WR / 32, NB = WC / 32;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * BUF];
+  constexpr int CP = BN + 4;                                  // fp32 pitch of the staged output tile
+  constexpr int SMEM = 2 * BUF > BM * CP * 4 ? 2 * BUF : BM * CP * 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
@@ -274,61 +276,110 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
     __syncthreads();
   }
 
-  // ---- epilogue: lane = output row m, register group c = 4 consecutive columns ----
+  // ---- epilogue.  The fp32 tile goes through LDS (the operand buffers are free after the
+  //      k-loop's last barrier); then each thread finishes 8 consecutive columns of one row, so
+  //      residual / multiplier rows are read and y rows written as 16-byte pieces, 16 threads
+  //      per 256-byte row (8-byte stores straight from the MFMA layout hit 32 rows at once).
+  //      The same fp32 operations run in the same order per element as before staging. ----
+  float* ct = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<f32x4*>(&ct[(wm * WR + 32 * mb + li) * CP + wn * WC + 32 * nb + 8 * c + 4 * half]) =
+            f32x4{acc[mb][nb][4 * c], acc[mb][nb][4 * c + 1], acc[mb][nb][4 * c + 2], acc[mb][nb][4 * c + 3]};
+  __syncthreads();
   uint16_t* yp = (uint16_t*)a.y;
   uint16_t* ytp = (uint16_t*)a.yt;
   const uint16_t* rp = (const uint16_t*)a.residual;
   const uint16_t* mp = (const uint16_t*)a.mul;
   const int ycols = a.ycols > 0 ? a.ycols : a.N;
+  const bool rvec = rp && (a.r_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0);
+  const bool mvec = mp && (a.mul_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(mp) & 15) == 0);
+  const bool yvec = yp && (a.y_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(yp) & 15) == 0);
+  constexpr int CPR = BN / 8;                                 // 8-column pieces per tile row
+  static_assert(256 % CPR == 0, "a thread keeps one column piece for all its rows");
+  const int cc = tid % CPR;
+  const int n = n0 + 8 * cc;                                  // this thread's columns n .. n+7
+  const bool full = n + 8 <= a.N;
+  float bv[8];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int64_t m = m0 + wm * WR + 32 * mb + li;
-    if (m >= a.M) continue;
+  for (int e = 0; e < 8; ++e) bv[e] = 0.f;
+  if (a.bias && n < a.N) {
+    if (full && ((reinterpret_cast<uintptr_t>(a.bias + n) & 15) == 0)) {
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.bias + n), b1 = *reinterpret_cast<const f32x4*>(a.bias + n + 4);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+      for (int e = 0; e < 4; ++e) { bv[e] = b0[e]; bv[4 + e] = b1[e]; }
+    } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int n = n0 + wn * WC + 32 * nb + 8 * c + 4 * half;   // columns n .. n+3
-        if (n >= a.N) continue;
-        const bool full = n + 4 <= a.N;
-        float v[4];
+      for (int e = 0; e < 8; ++e) bv[e] = n + e < a.N ? a.bias[n + e] : 0.f;
+    }
+  }
+  for (int rl = tid / CPR; rl < BM; rl += 256 / CPR) {
+    const int64_t m = m0 + rl;
+    if (m >= a.M || n >= a.N) continue;
+    float* cv = &ct[rl * CP + 8 * cc];
+    float v[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[mb][nb][4 * c + e] + ((a.bias && n + e < a.N) ? a.bias[n + e] : 0.f);
-        if (a.post_sigmoid) {
+    for (int e = 0; e < 8; ++e) v[e] = cv[e] + bv[e];
+    if (a.post_sigmoid) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = sigmoidf_(v[e]);
-        }
-        if (mp) {
-          const uint16_t* mrow = mp + (m % a.mul_rows) * a.mul_rs + n;
+      for (int e = 0; e < 8; ++e) v[e] = sigmoidf_(v[e]);
+    }
+    if (mp) {
+      const uint16_t* mrow = mp + (m % a.mul_rows) * a.mul_rs + n;
+      if (mvec && full) {
+        const u32x4 w = ld16(mrow);
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) v[e] *= bf2f(mrow[e]);
-        }
-        if (rp) {
-          const uint16_t* rrow = rp + m * a.r_rs + n;
+        for (int e = 0; e < 4; ++e) { v[2 * e] *= bflo(w[e]); v[2 * e + 1] *= bfhi(w[e]); }
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) v[e] += bf2f(rrow[e]);
-        }
-        if (yp && n < ycols) {
-          uint16_t* yrow = yp + m * a.y_rs + n;
-          if (full && n + 4 <= ycols && ((reinterpret_cast<uintptr_t>(yrow) & 7) == 0)) {
-            *reinterpret_cast<u32x2*>(yrow) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < a.N && n + e < ycols) yrow[e] = f2bf(v[e]);
-          }
-        }
-        if (ytp) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int ne = n + e;
-            if (ne < a.N && ne >= a.tcol0 && ne < a.tcol0 + a.tcols)
-              ytp[(int64_t)(ne - a.tcol0) * a.yt_rs + m] = f2bf(v[e]);
-          }
-        }
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N) v[e] *= bf2f(mrow[e]);
       }
+    }
+    if (rp) {
+      const uint16_t* rrow = rp + m * a.r_rs + n;
+      if (rvec && full) {
+        const u32x4 w = ld16(rrow);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[2 * e] += bflo(w[e]); v[2 * e + 1] += bfhi(w[e]); }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N) v[e] += bf2f(rrow[e]);
+      }
+    }
+    if (yp && n < ycols) {
+      uint16_t* yrow = yp + m * a.y_rs + n;
+      if (yvec && full && n + 8 <= ycols) {
+        st16(yrow, u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])});
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N && n + e < ycols) yrow[e] = f2bf(v[e]);
+      }
+    }
+    if (ytp) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cv[e] = v[e];              // final values for the transposed pass
+    }
+  }
+  if (ytp) {
+    // transposed columns [tcol0, tcol0 + tcols): each thread stores 8 consecutive rows of one column
+    __syncthreads();
+    constexpr int RPC = BM / 8;                               // 8-row pieces per tile column
+    for (int t = tid; t < BN * RPC; t += 256) {
+      const int nl = t / RPC, rc = t % RPC;
+      const int n = n0 + nl;
+      if (n >= a.N || n < a.tcol0 || n >= a.tcol0 + a.tcols) continue;
+      const int64_t mb0 = m0 + 8 * rc;
+      uint16_t* col = ytp + (int64_t)(n - a.tcol0) * a.yt_rs + mb0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (mb0 + e < a.M) col[e] = f2bf(ct[(8 * rc + e) * CP + nl]);
     }
   }
 }
