@@ -205,11 +205,20 @@ def _config_builders() -> dict:
 
 def other_configs(iters: int) -> dict:
   """Times every configuration of _config_builders (median-free: HIP events over `iters`
-  calls after a warm-up)."""
+  calls after a warm-up).  The module configurations are timed twice: eagerly (the line's
+  numbers) and with HIP-graph replay of the repeated call (`ms_per_call_hip_graphs`; the same
+  kernels, one graph launch instead of one launch per kernel)."""
+  from sparsefold_amd.runtime import config
   res = {}
   for name, build in _config_builders().items():
     call, metrics = build()
     res[name] = metrics(_time_call(call, iters))
+    if "pack" not in name:
+      config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda", hip_graphs=True)
+      try:
+        res[name]["ms_per_call_hip_graphs"] = round(_time_call(call, iters), 4)
+      finally:
+        config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda")
   return res
 
 

@@ -29,7 +29,7 @@ import functools
 import torch
 
 from sparsefold_amd import modules as base
-from sparsefold_amd.backends.hip import ops
+from sparsefold_amd.backends.hip import graphs, ops
 from sparsefold_amd.backends.hip.attention import dot_product_attention
 
 BF16 = torch.bfloat16
@@ -37,6 +37,7 @@ BF16 = torch.bfloat16
 
 def _begin_preparation(module: torch.nn.Module) -> None:
   module._native_prepared = False
+  graphs.clear(module)                                  # captured graphs hold the old weight buffers
   devices = {p.device.type for p in module.parameters()}
   if devices - {"cuda"}:
     raise RuntimeError("HIP kernels need the module's parameters on the GPU; move the model to 'cuda' first")
@@ -85,6 +86,7 @@ class GridSelfAttentionHipMixin:
     return True
 
   @_require_native_preparation
+  @graphs.graphed
   def forward(self, act: torch.Tensor, seq_mask: torch.Tensor, *, add_residual: bool = True) -> torch.Tensor:
     assert act.ndim >= 3
     N = act.shape[-2]
@@ -164,6 +166,7 @@ class SelfAttentionHipMixin:
     return True
 
   @_require_native_preparation
+  @graphs.graphed
   def forward(self, x: torch.Tensor, mask: torch.Tensor, *, pair_logits: torch.Tensor | None = None,
               single_cond: torch.Tensor | None = None, add_residual: bool = True) -> torch.Tensor:
     H, D = self.num_head, self.key_dim
@@ -203,6 +206,7 @@ class CrossAttentionHipMixin:
     return True
 
   @_require_native_preparation
+  @graphs.graphed
   def forward(self, x_q: torch.Tensor, x_k: torch.Tensor, mask_q: torch.Tensor, mask_k: torch.Tensor,
               pair_logits: torch.Tensor | None = None, single_cond_q: torch.Tensor | None = None,
               single_cond_k: torch.Tensor | None = None, *, add_residual: bool = True) -> torch.Tensor:
@@ -219,6 +223,7 @@ class CrossAttentionHipMixin:
     return _zero_init_residual(self, o, single_cond_q, x_q if add_residual else None).to(x_q.dtype)
 
   @_require_native_preparation
+  @graphs.graphed
   def forward_indexed(self, queries_act: torch.Tensor, queries_mask: torch.Tensor, gather_idxs: torch.Tensor,
                       gather_mask: torch.Tensor, keys_mask: torch.Tensor, queries_single_cond: torch.Tensor,
                       keys_single_cond: torch.Tensor, pair_logits: torch.Tensor | None = None, *,
@@ -254,6 +259,7 @@ class SingleActUpdateHipMixin:
     return True
 
   @_require_native_preparation
+  @graphs.graphed
   def forward(self, pair_act: torch.Tensor, single_act: torch.Tensor, seq_mask: torch.Tensor, *,
               add_residual: bool = True) -> torch.Tensor:
     N = pair_act.shape[-2]

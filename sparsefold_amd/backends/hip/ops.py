@@ -21,7 +21,14 @@ def _vp(t: torch.Tensor | None):
   return None if t is None else C.c_void_p(t.data_ptr())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor):
+  """torch's current stream on t's device (the raw handle; the public accessor builds a Stream
+  object per call, which costs more than some of the kernels it launches)."""
+  if _raw_stream is not None:
+    return C.c_void_p(_raw_stream(t.device.index))
   return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 

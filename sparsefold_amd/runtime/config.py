@@ -25,8 +25,10 @@ _LEGACY: dict[str, tuple[str, Any]] = {
     "native_ops": ("AF3_NATIVE_OPS", "*"),
     "sdpa_implementation": ("AF3_SDPA_IMPLEMENTATION", "math"),
     "diffusion_precision": ("AF3_DIFFUSION_PRECISION", "fp32"),
+    # HIP backend only, no reference counterpart: replay repeated module calls as HIP graphs
+    "hip_graphs": ("AF3_HIP_GRAPHS", "0"),
 }
-_BOOL_FIELDS = {"enable_sharding"}
+_BOOL_FIELDS = {"enable_sharding", "hip_graphs"}
 _state: dict[str, Any] | None = None
 
 

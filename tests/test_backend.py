@@ -166,3 +166,30 @@ def test_transformer_pack_replaces_only_the_pair_logit_factory(enabled):
   cache.reset()
   mod(None, None, None, pc)
   assert len(calls) == (2 if enabled else 3)
+
+
+def test_graph_replay_flag_and_signature(monkeypatch, reset_runtime):
+  from sparsefold_amd.backends.hip import graphs
+  monkeypatch.setenv("SPARSEFOLD_HIP_GRAPHS", "1")
+  config.reset()
+  assert config.hip_graphs is True
+  monkeypatch.delenv("SPARSEFOLD_HIP_GRAPHS")
+  config.reset()
+  assert config.hip_graphs is False
+  assert graphs._signature((torch.zeros(2),), {}) is None            # host tensors run eagerly
+  assert graphs._signature((object(),), {}) is None                  # unsupported argument
+  assert graphs._signature((1, None, True), {"b": 2.0, "a": "x"}) == (("a", "b"), (1, None, True, "x", 2.0))
+
+  calls = []
+
+  class Module:
+    @graphs.graphed
+    def forward(self, x, *, flag=False):
+      calls.append(flag)
+      return x
+
+  config.configure_runtime(hip_graphs=True)
+  m = Module()
+  for _ in range(3):
+    m.forward(torch.zeros(2), flag=True)
+  assert calls == [True] * 3 and "_hip_graph_cache" not in m.__dict__
