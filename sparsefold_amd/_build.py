@@ -2,7 +2,7 @@
 
 Objects are compiled in parallel into ``sparsefold_amd/_build/`` and linked in-tree, so the
 library travels with the source tree.  Every HIP translation unit is compiled with the
-packed-fp32 feature disabled.
+packed-fp32 feature disabled and with MFMA accumulators in VGPRs.
 """
 from __future__ import annotations
 
@@ -23,6 +23,9 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast",
+    # MFMA accumulators in VGPRs: left to its heuristics the compiler put the attention
+    # kernels' accumulators in AGPRs and copied them to VGPRs and back around every tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

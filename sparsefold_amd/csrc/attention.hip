@@ -14,6 +14,8 @@
 // Epilogue: O / l, optional sigmoid gate, bf16 store.
 #include <cstdlib>
 
+#include <type_traits>
+
 #include "sf_common.h"
 
 namespace {
@@ -220,6 +222,7 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 constexpr float kPadKey = -8.507059173023462e37f;  // -2^126: keys past K, below any masked key
+constexpr float kMassLimit = 1.152921504606846976e18f;   // 2^60: weight mass of a tile that moves m
 
 struct Attn2Plan {
   int QB;            // 32-query blocks per (batch, head)
@@ -239,11 +242,18 @@ struct Attn2Tile {
   __device__ static int vswz(int key) { return DP == 32 ? 0 : (key >> 1) & 1; }
 };
 
-template <int DP, bool SHARED>
+// KC: 16-dim chunks of q.k that hold data (ceil(D / 16)).  BL: the bias tile goes through LDS
+// (rows 16-byte aligned, K % 8 == 0): each wave copies its 32 query rows x 64 keys with four
+// direct-to-LDS loads of 8 rows x 128 bytes, slot-major [row/8][piece][row%8], and every lane
+// then reads its keys with conflict-free 8-byte LDS reads.  Loaded lane by lane from global
+// memory instead, every bias instruction touched 32 rows: 40% of the kernel's time.
+template <int DP, bool SHARED, int KC, bool BL>
 __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, const Attn2Plan pl) {
   using T = Attn2Tile<DP>;
   constexpr int kWaveBufs = SHARED ? 1 : 4;                 // tile sets in LDS (shared or per wave)
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kWaveBufs * 2 * T::kBufBytes];
+  constexpr int kKVRegion = kWaveBufs * 2 * T::kBufBytes;
+  constexpr int kBiasRegion = BL ? 4 * 2 * 4096 : 0;        // per wave: 2 buffers x 32 rows x 128 B
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kKVRegion + kBiasRegion];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
@@ -315,12 +325,41 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // ---- bias tile (this lane's query, its 32 keys) and key-mask bits ----
   u32x2 bnext[8];
   uint64_t mnext = ~0ull;
-  auto load_side = [&](int j0) __attribute__((always_inline)) {
+  uint8_t* bsm = smem + kKVRegion + wave * 2 * 4096;        // BL: this wave's two bias buffers
+  // BL source rows: lane L copies row 8u + L%8 of the wave's 32 queries, piece L/8 (keys 8p .. 8p+7)
+  const uint16_t* brow0 = nullptr;
+  int64_t brs8 = 0;                                          // elements between rows 8 apart
+  if (BL) {
+    const uint16_t* bh = (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] + (int64_t)h * a.bias_s[2];
+    brow0 = bh + (int64_t)min(qblk * 32 + (lane & 7), Q - 1) * a.bias_s[3] + 8 * (lane >> 3);
+    brs8 = 8 * a.bias_s[3];
+  }
+  const bool brows_clamped = qblk * 32 + 32 > Q;            // uniform: the last query block
+  auto load_bias_lds = [&](int j0, int buf) __attribute__((always_inline)) {
+    const int jc = min(j0, K - 8 - 8 * (lane >> 3)) - j0;   // pieces past K re-read the last one
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {                            // keys j0 + 32(q/4) + 8(q%4) + 4half .. +3
-      const int j = j0 + 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
-      bnext[q] = (bp != nullptr && j + 4 <= K) ? *reinterpret_cast<const u32x2*>(bp + j) : u32x2{0, 0};
-      if (bp != nullptr && j < K && j + 4 > K) {             // ragged end of the key range
+    for (int u = 0; u < 4; ++u) {
+      const uint16_t* src = brow0 + u * brs8;
+      if (brows_clamped) {
+        const uint16_t* bh = (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] + (int64_t)h * a.bias_s[2];
+        src = bh + (int64_t)min(qblk * 32 + 8 * u + (lane & 7), Q - 1) * a.bias_s[3] + 8 * (lane >> 3);
+      }
+      __builtin_amdgcn_global_load_lds(src + j0 + jc, (lds_u32a*)(bsm + buf * 4096 + u * 1024), 16, 0, 0);
+    }
+  };
+  auto load_side = [&](int j0) __attribute__((always_inline)) {
+    if (BL) {
+    } else if (bp == nullptr) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) bnext[q] = u32x2{0, 0};
+    } else if (j0 + 64 <= K) {                               // uniform: the whole tile is in range
+#pragma unroll
+      for (int q = 0; q < 8; ++q)                            // keys j0 + 32(q/4) + 8(q%4) + 4half .. +3
+        bnext[q] = *reinterpret_cast<const u32x2*>(bp + j0 + 32 * (q >> 2) + 8 * (q & 3) + 4 * half);
+    } else {                                                 // last tile: ragged end of the keys
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int j = j0 + 32 * (q >> 2) + 8 * (q & 3) + 4 * half;
         uint16_t t[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) t[e] = j + e < K ? bp[j + e] : 0;
@@ -346,6 +385,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // Waits: the copies into LDS are ordinary loads to the compiler, so every wait is followed
   // by a compiler barrier (or __syncthreads) that keeps the LDS reads of the tile after it.
   copy_tile(0, 0);
+  if (BL) load_bias_lds(0, 0);
   load_side(0);
   __builtin_amdgcn_s_waitcnt(0);
   if (SHARED) __syncthreads();
@@ -356,11 +396,18 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     const uint8_t* kt = wsm + buf * T::kBufBytes;
     const uint8_t* vt = kt + T::kKBytes;
     u32x2 bcur[8];
+    if (BL) {                                                // keys 32(q/4) + 8(q%4) + 4half .. +3 = piece q
 #pragma unroll
-    for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
+      for (int q = 0; q < 8; ++q)
+        bcur[q] = *reinterpret_cast<const u32x2*>(bsm + buf * 4096 + (li >> 3) * 1024 + q * 128 + (li & 7) * 16 + half * 8);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
+    }
     const uint64_t mbits = mnext;
     if (t + 1 < ntiles) {
       copy_tile(j0 + 64, buf ^ 1);
+      if (BL) load_bias_lds(j0 + 64, buf ^ 1);
       load_side(j0 + 64);
     }
     if (wactive) {
@@ -378,7 +425,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
           }
         const int key = 32 * kb + li;
 #pragma unroll
-        for (int kk = 0; kk < DP / 16; ++kk) {
+        for (int kk = 0; kk < KC; ++kk) {                    // chunks past D are zeros in q
           const int piece = (2 * kk + half) ^ T::kswz(key);
           s[kb] = mfma32(as_bf16x8(ld16(kt + key * T::kRowBytes + piece * 16)), qb[kk], s[kb]);
         }
@@ -398,31 +445,48 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
           for (int r = 0; r < 16; ++r)
             s[kb][r] = j0 + 32 * kb + 8 * (r >> 2) + 4 * half + (r & 3) < K ? 0.0f : kPadKey;
       }
-      // ---- online softmax ----
-      float tmax = s[0][0];
+      // ---- softmax against a reference point m (in units of S^T) ----
+      // Tile 0 sets m to the row maximum of its 64 keys.  Later tiles keep it unless the
+      // probability mass of the tile exceeds kMassLimit (all weights are >= 0, so the sum bounds
+      // every weight and an overflow cannot pass unnoticed); then m moves to the tile's maximum
+      // and what is accumulated is rescaled.  This replaces a running maximum (a max over the
+      // tile, one exp and a rescale of O every tile) by one compare.
+      auto row_max = [&]() __attribute__((always_inline)) {
+        float v = s[0][0];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kb][r]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float mnew = fmaxf(m, tmax);
-      const float alpha = fast_exp2((m - mnew) * cs);
-      m = mnew;
-      const float mb = mnew * cs;
-      l *= alpha;
+          for (int r = 0; r < 16; ++r) v = fmaxf(v, s[kb][r]);
+        return fmaxf(v, __shfl_xor(v, 32));
+      };
+      auto weights = [&](float mref, bf16x2 (&pw)[16]) __attribute__((always_inline)) {
+        const float mb = mref * cs;
+        float t0 = 0.f, t1 = 0.f;
 #pragma unroll
-      for (int db = 0; db < DP / 32; ++db)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+          for (int e = 0; e < 8; ++e) {
+            pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(s[kb][2 * e], cs, -mb)),
+                                     fast_exp2(__builtin_fmaf(s[kb][2 * e + 1], cs, -mb)));
+            if (e & 1) t1 = add_bf2(pw[8 * kb + e], t1); else t0 = add_bf2(pw[8 * kb + e], t0);
+          }
+        return t0 + t1;
+      };
+      if (t == 0) m = row_max();
       bf16x2 pw[16];
+      float ts = weights(m, pw);
+      if (__any(!(ts <= kMassLimit))) {                      // rare: move m up and rescale
+        const float mnew = fmaxf(m, row_max());
+        const float alpha = fast_exp2((m - mnew) * cs);
+        m = mnew;
+        l *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(s[kb][2 * e], cs, -mb)),
-                                   fast_exp2(__builtin_fmaf(s[kb][2 * e + 1], cs, -mb)));
-          l = add_bf2(pw[8 * kb + e], l);
-        }
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        ts = weights(m, pw);
+      }
+      l += ts;
       // ---- O^T += V^T P^T ----
       const int grp = lane >> 4, gi = lane & 15;            // 16-lane group, index in group
       const int ekey = gi >> 2, q4 = gi & 3;                 // source lane: key e, dims 4q .. 4q+3
@@ -537,12 +601,35 @@ extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
     const int64_t wgs = shared ? groups : (pl.tasks + 3) / 4;
     if (wgs > 0x7fffffff) { sf_set_error("attention: problem too large for the grid"); return 1; }
     const dim3 g2((unsigned)wgs);
+    const int kc = (a->D + 15) / 16;                        // q.k chunks holding data
+    // LDS bias tiles: always with shared tiles; per-wave tiles only for long key ranges, where the
+    // saved load time outweighs the lower occupancy of the larger LDS footprint (atom windows,
+    // K = 128: 31 us without, 41 us with; single attention, K = 768: 30 us without, 25 us with)
+    bool bl = a->bias != nullptr && aligned16(a->bias) && a->K % 8 == 0 && (shared || a->K >= 256);
+    for (int s2 = 0; s2 < 4 && bl; ++s2) bl = a->bias_s[s2] % 8 == 0;
+    auto launch = [&](auto dp, auto sh, auto kcc, auto blc) {
+      hipLaunchKernelGGL((attn2_kernel<decltype(dp)::value, decltype(sh)::value, decltype(kcc)::value,
+                                       decltype(blc)::value>), g2, dim3(256), 0, st, *a, pl);
+    };
+    using I32 = std::integral_constant<int, 32>;
+    using I64 = std::integral_constant<int, 64>;
+    using Tt = std::true_type;
+    using Ff = std::false_type;
+    auto by_bl = [&](auto dp, auto sh, auto kcc) {
+      if (bl) launch(dp, sh, kcc, Tt{});
+      else launch(dp, sh, kcc, Ff{});
+    };
+    auto by_sh = [&](auto dp, auto kcc) {
+      if (shared) by_bl(dp, Tt{}, kcc);
+      else by_bl(dp, Ff{}, kcc);
+    };
     if (dmax <= 32) {
-      if (shared) hipLaunchKernelGGL((attn2_kernel<32, true>), g2, dim3(256), 0, st, *a, pl);
-      else hipLaunchKernelGGL((attn2_kernel<32, false>), g2, dim3(256), 0, st, *a, pl);
+      if (kc <= 1) by_sh(I32{}, std::integral_constant<int, 1>{});
+      else by_sh(I32{}, std::integral_constant<int, 2>{});
+    } else if (kc <= 3) {
+      by_sh(I64{}, std::integral_constant<int, 3>{});
     } else {
-      if (shared) hipLaunchKernelGGL((attn2_kernel<64, true>), g2, dim3(256), 0, st, *a, pl);
-      else hipLaunchKernelGGL((attn2_kernel<64, false>), g2, dim3(256), 0, st, *a, pl);
+      by_sh(I64{}, std::integral_constant<int, 4>{});
     }
     return sf_check_launch("attn2_kernel");
   }
