@@ -118,3 +118,25 @@ def test_fp32_inputs_round_trip_dtype():
   assert out.dtype == torch.float32
   ref = oracle_dpa(bf16_round(q.cpu()), bf16_round(k.cpu()), bf16_round(v.cpu()))
   assert_close_bf16(out, ref, "fp32 in/out")
+
+
+@pytest.mark.parametrize("mode", ["s", "p"])
+def test_reference_point_moves_after_the_first_tile(mode, monkeypatch):
+  """The softmax keeps the first 64-key tile's maximum as its reference point and moves it only
+  when a later tile's weight mass passes 2^60.  Three ways to get there, checked against the
+  oracle: the first tile fully masked, logits 90 (log2 units) higher in a later tile, and both
+  in one batch (shared-tile and per-wave task modes)."""
+  monkeypatch.setenv("SPARSEFOLD_HIP_ATTN_MODE", mode)
+  gen = torch.Generator().manual_seed(99)
+  B, Q, K, H, D = 3, 160, 320, 2, 32
+  q = torch.randn(B, Q, H, D, generator=gen)
+  k = torch.randn(B, K, H, D, generator=gen)
+  v = torch.randn(B, K, H, D, generator=gen)
+  bias = torch.randn(B, H, Q, K, generator=gen)
+  mk = torch.ones(B, K, dtype=torch.bool)
+  mk[0, :64] = False                                     # batch 0: the first tile is all masked
+  bias[1, :, :, 200:] += 90.0 / 1.4426950408889634       # batch 1: +90 in log2 units after tile 3
+  mk[2, :70] = False                                     # batch 2: both
+  bias[2, :, :, 250:] += 70.0 / 1.4426950408889634
+  out, ref = _run(q, k, v, mask_k=mk, bias=bias)
+  assert_close_bf16(out, ref, f"reference point moves ({mode})")
