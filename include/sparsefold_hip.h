@@ -24,6 +24,12 @@
  *                               model/diffusion/transformer.py:655-666    CrossAttTransformer pack
  *   sf_hip_window_gather_fwd    schema/atom_layout.py:61-83               convert (queries_to_keys,
  *                               CrossAttTransformer block key gather, transformer.py:671-673)
+ *   sf_hip_self_attention_fwd   model/diffusion/transformer.py:306-345    SelfAttention.forward (+ AdaLN
+ *                               :80-96, AdaLN-zero :138-154); SingleActUpdate attention,
+ *                               model/trunk/blocks.py:750-763 (vecops ops evoformer_single_act_update,
+ *                               diffusion_self_attention)
+ *   sf_hip_cross_attention_fwd  model/diffusion/transformer.py:549-585    CrossAttention.forward, with the
+ *                               key gather of :671-673 (vecops op diffusion_cross_attention, indexed form)
  */
 #ifndef SPARSEFOLD_HIP_H_
 #define SPARSEFOLD_HIP_H_
@@ -35,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 2
+#define SF_HIP_ABI_VERSION 3
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -194,6 +200,75 @@ typedef struct sf_window_gather_args {
 } sf_window_gather_args;
 
 int sf_hip_window_gather_fwd(const sf_window_gather_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Whole attention modules, one call each (every stage is one of the op entry points above, so
+ * the numerics are those of the op-level path).  The caller provides the workspace; its size
+ * comes from the *_workspace_bytes query for the same arguments.  Weights are the packed forms
+ * the Python modules keep: f32 LayerNorm parameters, bf16 weights with K contiguous ([N, K]).
+ *
+ * Self attention, transformer.py:306-345 (single attention with pair bias, blocks.py:750-763;
+ * diffusion token attention), with AdaLN (:80-96) and AdaLN-zero (:138-154):
+ *   h = cond ? sigmoid(LN(c) W_scale^T + b_scale) * LN(x) + LN(c) W_shift^T : LN(x) * ln_w + ln_b
+ *   [q|k|v|g] = h W_qkvg^T + b_qkvg;  o = attention(q, k, v; mask, bias) * sigmoid(g)
+ *   out = (o W_t2^T) * (cond ? sigmoid(c W_zc^T + b_zc) : 1) + (add_residual ? x : 0)
+ * x bf16 [S, N, C] contiguous; mask u8 [N] or NULL (key mask); bias bf16 pair logits or NULL,
+ * strides [sample, head, query] (keys contiguous; sample stride 0 = shared); cond bf16 [N, Cs]
+ * shared by the S samples, or NULL (Cs ignored).  H*D heads, D <= 64.
+ * ------------------------------------------------------------------------------------- */
+typedef struct sf_self_attention_args {
+  int32_t S, N, C, H, D, Cs;
+  float scale;                                  /* logits scale; 0 = 1/sqrt(D) */
+  int32_t add_residual;
+  const void* x;                                /* bf16 [S, N, C] */
+  const uint8_t* mask;                          /* u8 [N] or NULL */
+  const void* bias; int64_t bias_s[3];          /* bf16 or NULL, strides [sample, head, query] */
+  const void* cond;                             /* bf16 [N, Cs] or NULL */
+  const float* ln_w; const float* ln_b;         /* no condition: f32 [C] or NULL */
+  const float* lnc_w; const float* lnc_b;       /* condition: LN of cond, f32 [Cs] or NULL */
+  const void* w_scale; const float* b_scale;    /* bf16 [C, Cs], f32 [C] */
+  const void* w_shift;                          /* bf16 [C, Cs] */
+  const void* w_qkvg; const float* b_qkvg;      /* bf16 [4*H*D, C] rows q, k, v, g; f32 [4*H*D] or NULL */
+  const void* w_t2;                             /* bf16 [C, H*D] */
+  const void* w_zc; const float* b_zc;          /* bf16 [C, Cs], f32 [C] (condition only) */
+  void* out;                                    /* bf16 [S, N, C] */
+} sf_self_attention_args;
+
+size_t sf_hip_self_attention_workspace_bytes(const sf_self_attention_args* a);
+int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* Cross attention, transformer.py:549-585 (windowed atom attention), both sides conditioned:
+ *   hq = AdaLN(xq, cond_q), hk = AdaLN(xk, cond_k) (as above, per side);
+ *   [q|g] = hq W_qg^T + b_qg, [k|v] = hk W_kv^T;  o = attention(q, k, v; mask_q, mask_k, bias) * sigmoid(g)
+ *   out = (o W_t2^T) * sigmoid(cond_q W_zc^T + b_zc) + (add_residual ? xq : 0)
+ * Keys: xk bf16 [S, U, Kw, C], or (CrossAttTransformer, transformer.py:671-673) gathered from
+ * the query rows: key row u*Kw + k of sample s = xq[s, gather_idx[u*Kw + k]] (flat index into the
+ * U*Qw rows), zero where gather_mask is 0 or the index is out of range (atom_layout.py:78-82).
+ * xq bf16 [S, U, Qw, C]; mask_q u8 [U, Qw], mask_k u8 [U, Kw] (NULL = all valid); bias bf16
+ * [U, H, Qw, Kw] shared by the S samples or NULL; cond_q [U, Qw, C], cond_k [U, Kw, C]. */
+typedef struct sf_cross_attention_args {
+  int32_t S, U, Qw, Kw, C, H, D;
+  float scale;                                  /* logits scale; 0 = 1/sqrt(D) */
+  int32_t add_residual;
+  const void* xq;                               /* bf16 [S, U, Qw, C] */
+  const void* xk;                               /* bf16 [S, U, Kw, C] or NULL with gather_idx */
+  const int32_t* gather_idx; const uint8_t* gather_mask;   /* [U*Kw] or NULL */
+  const uint8_t* mask_q; const uint8_t* mask_k;
+  const void* bias;                             /* bf16 [U, H, Qw, Kw] or NULL */
+  const void* cond_q; const void* cond_k;       /* bf16 [U, Qw, C], [U, Kw, C] */
+  const float* lnc_w_q; const float* lnc_b_q; const void* w_scale_q; const float* b_scale_q; const void* w_shift_q;
+  const float* lnc_w_k; const float* lnc_b_k; const void* w_scale_k; const float* b_scale_k; const void* w_shift_k;
+  const void* w_qg; const float* b_qg;          /* bf16 [2*H*D, C] rows q, g; f32 [2*H*D] or NULL */
+  const void* w_kv;                             /* bf16 [2*H*D, C] rows k, v */
+  const void* w_t2;                             /* bf16 [C, H*D] */
+  const void* w_zc; const float* b_zc;          /* bf16 [C, C], f32 [C] */
+  void* out;                                    /* bf16 [S, U, Qw, C] */
+} sf_cross_attention_args;
+
+size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a);
+int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 #ifdef __cplusplus
 }

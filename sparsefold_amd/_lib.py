@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -85,6 +85,31 @@ class WindowGatherArgs(C.Structure):
   ]
 
 
+class SelfAttentionArgs(C.Structure):
+  _fields_ = [
+      ("S", _i32), ("N", _i32), ("C", _i32), ("H", _i32), ("D", _i32), ("Cs", _i32),
+      ("scale", _f32), ("add_residual", _i32),
+      ("x", _vp), ("mask", _vp), ("bias", _vp), ("bias_s", _i64 * 3), ("cond", _vp),
+      ("ln_w", _vp), ("ln_b", _vp), ("lnc_w", _vp), ("lnc_b", _vp),
+      ("w_scale", _vp), ("b_scale", _vp), ("w_shift", _vp),
+      ("w_qkvg", _vp), ("b_qkvg", _vp), ("w_t2", _vp), ("w_zc", _vp), ("b_zc", _vp),
+      ("out", _vp),
+  ]
+
+
+class CrossAttentionArgs(C.Structure):
+  _fields_ = [
+      ("S", _i32), ("U", _i32), ("Qw", _i32), ("Kw", _i32), ("C", _i32), ("H", _i32), ("D", _i32),
+      ("scale", _f32), ("add_residual", _i32),
+      ("xq", _vp), ("xk", _vp), ("gather_idx", _vp), ("gather_mask", _vp),
+      ("mask_q", _vp), ("mask_k", _vp), ("bias", _vp), ("cond_q", _vp), ("cond_k", _vp),
+      ("lnc_w_q", _vp), ("lnc_b_q", _vp), ("w_scale_q", _vp), ("b_scale_q", _vp), ("w_shift_q", _vp),
+      ("lnc_w_k", _vp), ("lnc_b_k", _vp), ("w_scale_k", _vp), ("b_scale_k", _vp), ("w_shift_k", _vp),
+      ("w_qg", _vp), ("b_qg", _vp), ("w_kv", _vp), ("w_t2", _vp), ("w_zc", _vp), ("b_zc", _vp),
+      ("out", _vp),
+  ]
+
+
 STRUCTS = {
     "sf_attention_args": AttentionArgs,
     "sf_layer_norm_args": LayerNormArgs,
@@ -92,6 +117,8 @@ STRUCTS = {
     "sf_triangle_args": TriangleArgs,
     "sf_pair_logits_args": PairLogitsArgs,
     "sf_window_gather_args": WindowGatherArgs,
+    "sf_self_attention_args": SelfAttentionArgs,
+    "sf_cross_attention_args": CrossAttentionArgs,
 }
 
 # (name, restype, argtypes) of every exported entry point.
@@ -106,6 +133,10 @@ SIGNATURES = [
     ("sf_hip_triangle_stage_fwd", C.c_int, [C.POINTER(TriangleArgs), _i32, _vp, C.c_size_t, _vp]),
     ("sf_hip_pair_logits_fwd", C.c_int, [C.POINTER(PairLogitsArgs), _vp]),
     ("sf_hip_window_gather_fwd", C.c_int, [C.POINTER(WindowGatherArgs), _vp]),
+    ("sf_hip_self_attention_workspace_bytes", C.c_size_t, [C.POINTER(SelfAttentionArgs)]),
+    ("sf_hip_self_attention_fwd", C.c_int, [C.POINTER(SelfAttentionArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_cross_attention_workspace_bytes", C.c_size_t, [C.POINTER(CrossAttentionArgs)]),
+    ("sf_hip_cross_attention_fwd", C.c_int, [C.POINTER(CrossAttentionArgs), _vp, C.c_size_t, _vp]),
 ]
 
 _lib: C.CDLL | None = None

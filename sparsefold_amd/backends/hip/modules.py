@@ -165,6 +165,13 @@ class SelfAttentionHipMixin:
     self._native_prepared = True
     return True
 
+  def _native_weights(self) -> dict:
+    w = {"w_qkvg": self._hip_w_qkvg, "b_qkvg": self._hip_b_qkvg, "w_t2": self._hip_w_t2}
+    for key in ("ln_w", "ln_b", "lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift"):
+      w[key] = getattr(self, "_hip_ada_" + key, None)
+    w["w_zc"], w["b_zc"] = getattr(self, "_hip_w_zc", None), getattr(self, "_hip_b_zc", None)
+    return w
+
   @_require_native_preparation
   @graphs.graphed
   def forward(self, x: torch.Tensor, mask: torch.Tensor, *, pair_logits: torch.Tensor | None = None,
@@ -172,6 +179,15 @@ class SelfAttentionHipMixin:
     H, D = self.num_head, self.key_dim
     HD = H * D
     lead, N = x.shape[:-2], x.shape[-2]
+    S = x.numel() // max(N * x.shape[-1], 1)
+    native = (mask is None or tuple(mask.shape) == (N,)) and \
+        (pair_logits is None or tuple(pair_logits.shape) in {(H, N, N), (S, H, N, N)}) and \
+        (single_cond is None or (single_cond.dim() == 2 and single_cond.shape[0] == N)) and \
+        (single_cond is not None or hasattr(self, "_hip_ada_ln_w"))
+    if native:                                        # the whole module in one library call
+      out = ops.self_attention_module(x, mask, pair_logits, single_cond, self._native_weights(), num_head=H,
+                                      head_dim=D, add_residual=add_residual)
+      return out.to(x.dtype)
     xh = _adaln(self, "_hip_ada_", x, single_cond)
     y = ops.linear(xh, self._hip_w_qkvg, self._hip_b_qkvg)              # [..., N, 4HD]
     q, k, v, g = (y[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D)) for i in range(4))
@@ -205,6 +221,22 @@ class CrossAttentionHipMixin:
     self._native_prepared = True
     return True
 
+  def _native_weights(self) -> dict:
+    w = {"w_qg": self._hip_w_qg, "b_qg": self._hip_b_qg, "w_kv": self._hip_w_kv, "w_t2": self._hip_w_t2,
+         "w_zc": getattr(self, "_hip_w_zc", None), "b_zc": getattr(self, "_hip_b_zc", None)}
+    for side in ("q", "k"):
+      for key in ("lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift"):
+        w[f"{key}_{side}"] = getattr(self, f"_hip_ad{side}_{key}", None)
+    return w
+
+  def _native_ok(self, U, Qw, Kw, mask_q, mask_k, pair_logits, cq, ck) -> bool:
+    return (cq is not None and ck is not None and hasattr(self, "_hip_adq_w_scale")
+            and hasattr(self, "_hip_adk_w_scale") and getattr(self, "_hip_w_zc", None) is not None
+            and tuple(cq.shape[-3:-1]) == (U, Qw) and cq.dim() == 3 and tuple(ck.shape[-3:-1]) == (U, Kw)
+            and ck.dim() == 3 and (mask_q is None or tuple(mask_q.shape) == (U, Qw))
+            and (mask_k is None or tuple(mask_k.shape) == (U, Kw))
+            and (pair_logits is None or tuple(pair_logits.shape) == (U, self.num_head, Qw, Kw)))
+
   @_require_native_preparation
   @graphs.graphed
   def forward(self, x_q: torch.Tensor, x_k: torch.Tensor, mask_q: torch.Tensor, mask_k: torch.Tensor,
@@ -212,6 +244,13 @@ class CrossAttentionHipMixin:
               single_cond_k: torch.Tensor | None = None, *, add_residual: bool = True) -> torch.Tensor:
     H, D = self.num_head, self.key_dim
     HD = H * D
+    if x_q.dim() >= 3 and x_k.dim() == x_q.dim() and x_k.shape[:-2] == x_q.shape[:-2] and \
+        self._native_ok(x_q.shape[-3], x_q.shape[-2], x_k.shape[-2], mask_q, mask_k, pair_logits,
+                        single_cond_q, single_cond_k):
+      out = ops.cross_attention_module(x_q, x_k, None, None, mask_q, mask_k, pair_logits, single_cond_q,
+                                       single_cond_k, self._native_weights(), num_head=H, head_dim=D,
+                                       add_residual=add_residual)
+      return out.to(x_q.dtype)
     hq = _adaln(self, "_hip_adq_", x_q, single_cond_q)
     hk = _adaln(self, "_hip_adk_", x_k, single_cond_k)
     yq = ops.linear(hq, self._hip_w_qg, self._hip_b_qg)                 # [..., Q, 2HD]
@@ -232,6 +271,13 @@ class CrossAttentionHipMixin:
     the queries by ``queries_to_keys`` (flat index over ``[U, Qw]``, masked -> 0)."""
     lead = queries_act.shape[:-3]
     U, Qw, Cn = queries_act.shape[-3:]
+    Kw = gather_idxs.shape[-1]
+    if tuple(gather_idxs.shape) == (U, Kw) and self._native_ok(U, Qw, Kw, queries_mask, keys_mask, pair_logits,
+                                                               queries_single_cond, keys_single_cond):
+      out = ops.cross_attention_module(queries_act, None, gather_idxs, gather_mask, queries_mask, keys_mask,
+                                       pair_logits, queries_single_cond, keys_single_cond, self._native_weights(),
+                                       num_head=self.num_head, head_dim=self.key_dim, add_residual=add_residual)
+      return out.to(queries_act.dtype)
     S = 1
     for s in lead:
       S *= s

@@ -282,3 +282,92 @@ def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qk
 
 def default_scale(d: int) -> float:
   return 1.0 / math.sqrt(d)
+
+
+# ---------------------------------------------------------------------------------------
+# whole attention modules (one C call each; see sf_hip_self_attention_fwd /
+# sf_hip_cross_attention_fwd)
+# ---------------------------------------------------------------------------------------
+
+def _u8_or_none(t):
+  return None if t is None else _u8(t).contiguous()
+
+
+def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_head: int, head_dim: int,
+                          add_residual: bool = True) -> torch.Tensor:
+  """SelfAttention.forward as one call.  ``x`` ``[..., N, C]`` (leading dims = samples),
+  ``mask`` ``[N]`` or None, ``bias`` ``[H, N, N]`` (shared) or ``[S, H, N, N]`` or None,
+  ``cond`` ``[N, Cs]`` or None; ``w`` holds the packed weights (keys as in the C struct)."""
+  _require_cuda(x, mask, bias, cond)
+  N, Cn = x.shape[-2], x.shape[-1]
+  S = x.numel() // max(N * Cn, 1)
+  H, D = num_head, head_dim
+  x3 = _bf16(x).reshape(S, N, Cn).contiguous()
+  out = torch.empty_like(x3)
+  a = _lib.SelfAttentionArgs()
+  a.S, a.N, a.C, a.H, a.D = S, N, Cn, H, D
+  a.scale, a.add_residual = 0.0, int(bool(add_residual))
+  a.x, a.out = _vp(x3), _vp(out)
+  m8 = _u8_or_none(mask)
+  a.mask = _vp(m8)
+  if bias is not None:
+    b = _bf16(bias)
+    _require(b.stride(-1) == 1, "self_attention: bias keys must be contiguous")
+    if b.dim() == 3:
+      a.bias_s[0], a.bias_s[1], a.bias_s[2] = 0, b.stride(0), b.stride(1)
+    else:
+      a.bias_s[0], a.bias_s[1], a.bias_s[2] = b.stride(0), b.stride(1), b.stride(2)
+    a.bias = _vp(b)
+  c2 = None
+  if cond is not None:
+    c2 = _bf16(cond).contiguous()
+    a.cond, a.Cs = _vp(c2), c2.shape[-1]
+  for key in ("ln_w", "ln_b", "lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift", "w_qkvg", "b_qkvg",
+              "w_t2", "w_zc", "b_zc"):
+    setattr(a, key, _vp(w.get(key)))
+  lib = _lib.load()
+  ws = torch.empty(int(lib.sf_hip_self_attention_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=x.device)
+  _lib.check(lib.sf_hip_self_attention_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(x)), "sf_hip_self_attention_fwd")
+  return out.view(x.shape)
+
+
+def cross_attention_module(xq: torch.Tensor, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k,
+                           w: dict, *, num_head: int, head_dim: int, add_residual: bool = True) -> torch.Tensor:
+  """CrossAttention.forward as one call.  ``xq`` ``[..., U, Qw, C]``; keys either ``xk``
+  ``[..., U, Kw, C]`` or gathered from the query rows by ``gather_idx`` / ``gather_mask``
+  ``[U, Kw]``; masks ``[U, Qw]`` / ``[U, Kw]``; ``bias`` ``[U, H, Qw, Kw]``; conditions
+  ``[U, Qw, C]`` / ``[U, Kw, C]``."""
+  _require_cuda(xq, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k)
+  U, Qw, Cn = xq.shape[-3:]
+  S = xq.numel() // max(U * Qw * Cn, 1)
+  Kw = gather_idx.shape[-1] if gather_idx is not None else xk.shape[-2]
+  xq4 = _bf16(xq).reshape(S, U, Qw, Cn).contiguous()
+  out = torch.empty_like(xq4)
+  a = _lib.CrossAttentionArgs()
+  a.S, a.U, a.Qw, a.Kw, a.C, a.H, a.D = S, U, Qw, Kw, Cn, num_head, head_dim
+  a.scale, a.add_residual = 0.0, int(bool(add_residual))
+  a.xq, a.out = _vp(xq4), _vp(out)
+  keep = []
+  if gather_idx is not None:
+    idx32 = gather_idx.reshape(-1).to(torch.int32).contiguous()
+    gm8 = _u8(gather_mask.reshape(-1)).contiguous()
+    _require(idx32.numel() == U * Kw and gm8.numel() == U * Kw, "cross_attention: gather sizes")
+    a.gather_idx, a.gather_mask = _vp(idx32), _vp(gm8)
+    keep += [idx32, gm8]
+  else:
+    xk4 = _bf16(xk).reshape(S, U, Kw, Cn).contiguous()
+    a.xk = _vp(xk4)
+    keep.append(xk4)
+  mq8, mk8 = _u8_or_none(mask_q), _u8_or_none(mask_k)
+  a.mask_q, a.mask_k = _vp(mq8), _vp(mk8)
+  b = None if bias is None else _bf16(bias).contiguous()
+  a.bias = _vp(b)
+  cq, ck = _bf16(cond_q).contiguous(), _bf16(cond_k).contiguous()
+  a.cond_q, a.cond_k = _vp(cq), _vp(ck)
+  for key in ("lnc_w_q", "lnc_b_q", "w_scale_q", "b_scale_q", "w_shift_q", "lnc_w_k", "lnc_b_k", "w_scale_k",
+              "b_scale_k", "w_shift_k", "w_qg", "b_qg", "w_kv", "w_t2", "w_zc", "b_zc"):
+    setattr(a, key, _vp(w.get(key)))
+  lib = _lib.load()
+  ws = torch.empty(int(lib.sf_hip_cross_attention_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=xq.device)
+  _lib.check(lib.sf_hip_cross_attention_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(xq)), "sf_hip_cross_attention_fwd")
+  return out.view(xq.shape)

@@ -1,0 +1,257 @@
+// Module-level entry points: one C call runs a whole attention module's kernel chain against a
+// caller-provided workspace (no allocation, one host transition instead of one per kernel).
+//
+//   sf_hip_self_attention_fwd   SelfAttention.forward (transformer.py:306-345) with AdaLN
+//                               (:80-96) and AdaLN-zero (:138-154): single attention with pair
+//                               bias (SingleActUpdate's attention, blocks.py:750-763) and the
+//                               diffusion-transformer token attention
+//   sf_hip_cross_attention_fwd  CrossAttention.forward (transformer.py:549-585), optionally with
+//                               the key-window gather of CrossAttTransformer (:671-673)
+//
+// Each stage is one of the library's own op entry points (LayerNorm, linear, attention, window
+// gather), so the numerics are exactly those of the op-level path.
+#include <cmath>
+#include <cstdint>
+
+#include "sf_common.h"
+
+namespace {
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bump allocator over the caller's workspace; sizes are checked by the *_workspace_bytes query.
+struct Arena {
+  char* base;
+  size_t off = 0;
+  void* take(size_t bytes) {
+    void* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  }
+};
+
+// LN (gamma / beta) or AdaLN (LN of the condition, sigmoid scale, shift, modulated LN) of x.
+int adaln(int64_t rows, int C, const void* x, const void* cond, int64_t cond_rows, int Cs,
+          const float* ln_w, const float* ln_b, const float* lnc_w, const float* lnc_b,
+          const void* w_scale, const float* b_scale, const void* w_shift, Arena& ws, void* y,
+          hipStream_t st) {
+  sf_layer_norm_args ln{};
+  ln.M = rows; ln.C = C; ln.eps = 1e-5f;
+  ln.x = x; ln.x_rs = C; ln.y = y; ln.y_rs = C;
+  if (cond == nullptr) {
+    ln.gamma = ln_w; ln.beta = ln_b;
+    return sf_hip_layer_norm_fwd(&ln, st);
+  }
+  void* cln = ws.take((size_t)cond_rows * Cs * 2);
+  void* scale = ws.take((size_t)cond_rows * C * 2);
+  void* shift = ws.take((size_t)cond_rows * C * 2);
+  sf_layer_norm_args lc{};
+  lc.M = cond_rows; lc.C = Cs; lc.eps = 1e-5f;
+  lc.x = cond; lc.x_rs = Cs; lc.gamma = lnc_w; lc.beta = lnc_b; lc.y = cln; lc.y_rs = Cs;
+  int rc = sf_hip_layer_norm_fwd(&lc, st);
+  if (rc) return rc;
+  sf_linear_args l{};
+  l.M = cond_rows; l.N = C; l.K = Cs; l.x = cln; l.x_rs = Cs; l.mul_rows = 1;
+  l.wt = w_scale; l.bias = b_scale; l.post_sigmoid = 1; l.y = scale; l.y_rs = C;
+  if ((rc = sf_hip_linear_fwd(&l, st))) return rc;
+  l.wt = w_shift; l.bias = nullptr; l.post_sigmoid = 0; l.y = shift;
+  if ((rc = sf_hip_linear_fwd(&l, st))) return rc;
+  ln.scale = scale; ln.shift = shift; ln.cond_rows = cond_rows; ln.cond_rs = C;
+  return sf_hip_layer_norm_fwd(&ln, st);
+}
+
+// out = (o W_t2^T) * sigmoid(cond W_zc^T + b_zc) (when cond) + residual (when given)
+int zero_init_out(int64_t rows, int C, int HD, const void* o, const void* cond, int64_t cond_rows, int Cs,
+                  const void* w_zc, const float* b_zc, const void* w_t2, const void* residual, void* out,
+                  Arena& ws, hipStream_t st) {
+  int rc;
+  void* zmul = nullptr;
+  if (cond != nullptr) {
+    zmul = ws.take((size_t)cond_rows * C * 2);
+    sf_linear_args z{};
+    z.M = cond_rows; z.N = C; z.K = Cs; z.x = cond; z.x_rs = Cs; z.mul_rows = 1;
+    z.wt = w_zc; z.bias = b_zc; z.post_sigmoid = 1; z.y = zmul; z.y_rs = C;
+    if ((rc = sf_hip_linear_fwd(&z, st))) return rc;
+  }
+  sf_linear_args l{};
+  l.M = rows; l.N = C; l.K = HD; l.x = o; l.x_rs = HD; l.wt = w_t2;
+  l.mul = zmul; l.mul_rows = zmul ? cond_rows : 1; l.mul_rs = C;
+  l.residual = residual; l.r_rs = C;
+  l.y = out; l.y_rs = C;
+  return sf_hip_linear_fwd(&l, st);
+}
+
+// workspace of the self-attention chain (the arena walk below, run without a base)
+size_t self_ws(const sf_self_attention_args* a) {
+  Arena ws{nullptr};
+  const int64_t rows = (int64_t)a->S * a->N;
+  const int HD = a->H * a->D;
+  if (a->cond) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
+  ws.take((size_t)rows * a->C * 2);          // h
+  ws.take((size_t)rows * 4 * HD * 2);        // q k v g
+  ws.take((size_t)rows * HD * 2);            // o
+  if (a->cond) ws.take((size_t)a->N * a->C * 2);
+  return ws.off;
+}
+
+size_t cross_ws(const sf_cross_attention_args* a) {
+  Arena ws{nullptr};
+  const int64_t qrows = (int64_t)a->S * a->U * a->Qw, krows = (int64_t)a->S * a->U * a->Kw;
+  const int HD = a->H * a->D;
+  if (a->gather_idx) ws.take((size_t)krows * a->C * 2);
+  for (int side = 0; side < 2; ++side) {
+    const int64_t cr = (int64_t)a->U * (side ? a->Kw : a->Qw);
+    ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2);
+  }
+  ws.take((size_t)qrows * a->C * 2);
+  ws.take((size_t)krows * a->C * 2);
+  ws.take((size_t)qrows * 2 * HD * 2);
+  ws.take((size_t)krows * 2 * HD * 2);
+  ws.take((size_t)qrows * HD * 2);
+  ws.take((size_t)a->U * a->Qw * a->C * 2);
+  return ws.off;
+}
+
+}  // namespace
+
+extern "C" size_t sf_hip_self_attention_workspace_bytes(const sf_self_attention_args* a) {
+  return a == nullptr ? 0 : self_ws(a);
+}
+
+extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  if (a == nullptr || a->x == nullptr || a->out == nullptr || a->w_qkvg == nullptr || a->w_t2 == nullptr) {
+    sf_set_error("self_attention: x, out, w_qkvg and w_t2 must be non-null"); return 1;
+  }
+  if (a->S <= 0 || a->N <= 0 || a->C <= 0 || a->H <= 0 || a->D <= 0 || (a->cond && a->Cs <= 0)) {
+    sf_set_error("self_attention: sizes must be positive (S=%d N=%d C=%d H=%d D=%d Cs=%d)",
+                 a->S, a->N, a->C, a->H, a->D, a->Cs);
+    return 1;
+  }
+  if (a->cond && (a->w_scale == nullptr || a->w_shift == nullptr || a->w_zc == nullptr)) {
+    sf_set_error("self_attention: a condition needs w_scale, w_shift and w_zc"); return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < self_ws(a)) {
+    sf_set_error("self_attention: workspace of %zu bytes needed, %zu given", self_ws(a), workspace_bytes);
+    return 1;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Arena ws{static_cast<char*>(workspace)};
+  const int64_t rows = (int64_t)a->S * a->N;
+  const int HD = a->H * a->D;
+  void* h = nullptr;
+  int rc;
+  {
+    // the AdaLN workspace is taken first, as in self_ws
+    Arena probe = ws;
+    if (a->cond) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
+    h = probe.take((size_t)rows * a->C * 2);
+    if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b, a->w_scale,
+                    a->b_scale, a->w_shift, ws, h, st)))
+      return rc;
+    ws = probe;
+  }
+  void* y = ws.take((size_t)rows * 4 * HD * 2);
+  void* o = ws.take((size_t)rows * HD * 2);
+  sf_linear_args p{};
+  p.M = rows; p.N = 4 * HD; p.K = a->C; p.x = h; p.x_rs = a->C; p.wt = a->w_qkvg; p.bias = a->b_qkvg;
+  p.mul_rows = 1; p.y = y; p.y_rs = 4 * HD;
+  if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
+  sf_attention_args t{};
+  t.B0 = a->S; t.B1 = 1; t.Q = a->N; t.K = a->N; t.H = a->H; t.D = a->D; t.Dv = a->D;
+  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
+  const int64_t ys[4] = {(int64_t)a->N * 4 * HD, 0, 4 * HD, a->D};
+  const uint16_t* yb = static_cast<const uint16_t*>(y);
+  t.q = yb;          for (int i = 0; i < 4; ++i) t.q_s[i] = ys[i];
+  t.k = yb + HD;     for (int i = 0; i < 4; ++i) t.k_s[i] = ys[i];
+  t.v = yb + 2 * HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ys[i];
+  t.gate = yb + 3 * HD; for (int i = 0; i < 4; ++i) t.g_s[i] = ys[i];
+  if (a->bias) {
+    t.bias = a->bias; t.bias_s[0] = a->bias_s[0]; t.bias_s[1] = 0; t.bias_s[2] = a->bias_s[1]; t.bias_s[3] = a->bias_s[2];
+  }
+  if (a->mask) { t.mask_k = a->mask; t.mk_s[0] = 0; t.mk_s[1] = 0; t.mk_s[2] = 1; }
+  t.out = o; t.o_s[0] = (int64_t)a->N * HD; t.o_s[1] = 0; t.o_s[2] = HD; t.o_s[3] = a->D;
+  if ((rc = sf_hip_attention_fwd(&t, st))) return rc;
+  return zero_init_out(rows, a->C, HD, o, a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
+                       a->add_residual ? a->x : nullptr, a->out, ws, st);
+}
+
+extern "C" size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a) {
+  return a == nullptr ? 0 : cross_ws(a);
+}
+
+extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  if (a == nullptr || a->xq == nullptr || a->out == nullptr || a->w_qg == nullptr || a->w_kv == nullptr ||
+      a->w_t2 == nullptr || a->w_zc == nullptr || a->cond_q == nullptr || a->cond_k == nullptr) {
+    sf_set_error("cross_attention: xq, out, weights and both conditions must be non-null"); return 1;
+  }
+  if ((a->gather_idx == nullptr) == (a->xk == nullptr) || (a->gather_idx && a->gather_mask == nullptr)) {
+    sf_set_error("cross_attention: give either xk or gather_idx + gather_mask"); return 1;
+  }
+  if (a->S <= 0 || a->U <= 0 || a->Qw <= 0 || a->Kw <= 0 || a->C <= 0 || a->H <= 0 || a->D <= 0) {
+    sf_set_error("cross_attention: sizes must be positive"); return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < cross_ws(a)) {
+    sf_set_error("cross_attention: workspace of %zu bytes needed, %zu given", cross_ws(a), workspace_bytes);
+    return 1;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Arena ws{static_cast<char*>(workspace)};
+  const int C = a->C, HD = a->H * a->D;
+  const int64_t qrows = (int64_t)a->S * a->U * a->Qw, krows = (int64_t)a->S * a->U * a->Kw;
+  int rc;
+  const void* xk = a->xk;
+  if (a->gather_idx) {
+    void* keys = ws.take((size_t)krows * C * 2);
+    sf_window_gather_args gth{};
+    gth.S = a->S; gth.rows = a->U * a->Qw; gth.C = C; gth.UK = a->U * a->Kw;
+    gth.src = a->xq; gth.idx = a->gather_idx; gth.mask = a->gather_mask; gth.keys = keys;
+    if ((rc = sf_hip_window_gather_fwd(&gth, st))) return rc;
+    xk = keys;
+  }
+  // the two AdaLN chains take their scratch first, in the order cross_ws counts it
+  Arena side_q = ws;
+  Arena side_k = ws;
+  for (int i = 0; i < 3; ++i) side_k.take((size_t)a->U * a->Qw * C * 2);
+  Arena rest = side_k;
+  for (int i = 0; i < 3; ++i) rest.take((size_t)a->U * a->Kw * C * 2);
+  void* hq = rest.take((size_t)qrows * C * 2);
+  void* hk = rest.take((size_t)krows * C * 2);
+  if ((rc = adaln(qrows, C, a->xq, a->cond_q, (int64_t)a->U * a->Qw, C, nullptr, nullptr, a->lnc_w_q, a->lnc_b_q,
+                  a->w_scale_q, a->b_scale_q, a->w_shift_q, side_q, hq, st)))
+    return rc;
+  if ((rc = adaln(krows, C, xk, a->cond_k, (int64_t)a->U * a->Kw, C, nullptr, nullptr, a->lnc_w_k, a->lnc_b_k,
+                  a->w_scale_k, a->b_scale_k, a->w_shift_k, side_k, hk, st)))
+    return rc;
+  void* yq = rest.take((size_t)qrows * 2 * HD * 2);
+  void* yk = rest.take((size_t)krows * 2 * HD * 2);
+  void* o = rest.take((size_t)qrows * HD * 2);
+  sf_linear_args p{};
+  p.M = qrows; p.N = 2 * HD; p.K = C; p.x = hq; p.x_rs = C; p.wt = a->w_qg; p.bias = a->b_qg;
+  p.mul_rows = 1; p.y = yq; p.y_rs = 2 * HD;
+  if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
+  p.M = krows; p.x = hk; p.wt = a->w_kv; p.bias = nullptr; p.y = yk;
+  if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
+  sf_attention_args t{};
+  t.B0 = a->S; t.B1 = a->U; t.Q = a->Qw; t.K = a->Kw; t.H = a->H; t.D = a->D; t.Dv = a->D;
+  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
+  const uint16_t* qb = static_cast<const uint16_t*>(yq);
+  const uint16_t* kb = static_cast<const uint16_t*>(yk);
+  const int64_t qs[4] = {(int64_t)a->U * a->Qw * 2 * HD, (int64_t)a->Qw * 2 * HD, 2 * HD, a->D};
+  const int64_t ks[4] = {(int64_t)a->U * a->Kw * 2 * HD, (int64_t)a->Kw * 2 * HD, 2 * HD, a->D};
+  t.q = qb;      for (int i = 0; i < 4; ++i) t.q_s[i] = qs[i];
+  t.gate = qb + HD; for (int i = 0; i < 4; ++i) t.g_s[i] = qs[i];
+  t.k = kb;      for (int i = 0; i < 4; ++i) t.k_s[i] = ks[i];
+  t.v = kb + HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ks[i];
+  if (a->bias) {
+    t.bias = a->bias; t.bias_s[0] = 0; t.bias_s[1] = (int64_t)a->H * a->Qw * a->Kw;
+    t.bias_s[2] = (int64_t)a->Qw * a->Kw; t.bias_s[3] = a->Kw;
+  }
+  if (a->mask_q) { t.mask_q = a->mask_q; t.mq_s[0] = 0; t.mq_s[1] = a->Qw; t.mq_s[2] = 1; }
+  if (a->mask_k) { t.mask_k = a->mask_k; t.mk_s[0] = 0; t.mk_s[1] = a->Kw; t.mk_s[2] = 1; }
+  t.out = o; t.o_s[0] = (int64_t)a->U * a->Qw * HD; t.o_s[1] = (int64_t)a->Qw * HD; t.o_s[2] = HD; t.o_s[3] = a->D;
+  if ((rc = sf_hip_attention_fwd(&t, st))) return rc;
+  return zero_init_out(qrows, C, HD, o, a->cond_q, (int64_t)a->U * a->Qw, C, a->w_zc, a->b_zc, a->w_t2,
+                       a->add_residual ? a->xq : nullptr, a->out, rest, st);
+}
