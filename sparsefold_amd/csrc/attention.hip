@@ -226,8 +226,10 @@ constexpr float kMassLimit = 1.152921504606846976e18f;   // 2^60: weight mass of
 
 struct Attn2Plan {
   int QB;            // 32-query blocks per (batch, head)
-  int64_t tasks;     // B0 * B1 * H * QB (PRIVATE) or groups of 4 blocks (SHARED)
+  int64_t tasks;     // B0 * B1 * H * QB * ksplit (PRIVATE) or groups of 4 blocks (SHARED)
   int vec_out;       // 8-byte stores of out / loads of gate
+  int ksplit;        // PRIVATE: key-range slices per query block (1 = none)
+  float* part;       // ksplit > 1: per (block, slice) unnormalised O [32][DP] and (m, l) [32][2]
 };
 
 template <int DP>
@@ -269,9 +271,15 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   } else {
     const int64_t t = (int64_t)blockIdx.x * 4 + wave;
     if (t >= pl.tasks) return;                               // private waves never meet a barrier
-    qblk = (int)(t % pl.QB);
-    task = t / pl.QB;
+    const int64_t tb = t / pl.ksplit;                        // (batch, head, query block)
+    qblk = (int)(tb % pl.QB);
+    task = tb / pl.QB;
   }
+  // key-range slice of this wave: tiles [t_begin, t_end)
+  const int ntiles_all = (a.K + 63) / 64;
+  const int slice = SHARED ? 0 : (int)(((int64_t)blockIdx.x * 4 + wave) % pl.ksplit);
+  const int t_begin = (int)((int64_t)ntiles_all * slice / (SHARED ? 1 : pl.ksplit));
+  const int t_end = (int)((int64_t)ntiles_all * (slice + 1) / (SHARED ? 1 : pl.ksplit));
   const int h = (int)(task % a.H);
   const int64_t b = task / a.H;
   const int b0 = (int)(b / a.B1), b1 = (int)(b - (int64_t)b0 * a.B1);
@@ -381,18 +389,17 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
 #pragma unroll
   for (int e = 0; e < 8; ++e) ones_b[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
 
-  const int ntiles = (K + 63) / 64;
   // Waits: the copies into LDS are ordinary loads to the compiler, so every wait is followed
   // by a compiler barrier (or __syncthreads) that keeps the LDS reads of the tile after it.
-  copy_tile(0, 0);
-  if (BL) load_bias_lds(0, 0);
-  load_side(0);
+  copy_tile(t_begin * 64, 0);
+  if (BL) load_bias_lds(t_begin * 64, 0);
+  load_side(t_begin * 64);
   __builtin_amdgcn_s_waitcnt(0);
   if (SHARED) __syncthreads();
   else asm volatile("" ::: "memory");
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1, j0 = t * 64;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1, j0 = t * 64;
     const uint8_t* kt = wsm + buf * T::kBufBytes;
     const uint8_t* vt = kt + T::kKBytes;
     u32x2 bcur[8];
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
       for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
     }
     const uint64_t mbits = mnext;
-    if (t + 1 < ntiles) {
+    if (t + 1 < t_end) {
       copy_tile(j0 + 64, buf ^ 1);
       if (BL) load_bias_lds(j0 + 64, buf ^ 1);
       load_side(j0 + 64);
@@ -472,7 +479,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
           }
         return t0 + t1;
       };
-      if (t == 0) m = row_max();
+      if (t == t_begin) m = row_max();
       bf16x2 pw[16];
       float ts = weights(m, pw);
       if (__any(!(ts <= kMassLimit))) {                      // rare: move m up and rescale
@@ -521,6 +528,19 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // ---- epilogue: O / l, optional sigmoid gate ----
   if (!wactive || i >= Q) return;
   const float lt = l + __shfl_xor(l, 32);
+  if (!SHARED && pl.ksplit > 1) {
+    // one slice of the keys: unnormalised O, its reference point and weight sum, for the combine
+    const int64_t slot = ((int64_t)blockIdx.x * 4 + wave);  // (block, slice) in task order
+    float* po = pl.part + slot * 32 * (DP + 2);
+#pragma unroll
+    for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)
+        *reinterpret_cast<f32x4*>(po + li * DP + 32 * db + 8 * c4 + 4 * half) =
+            f32x4{o[db][4 * c4], o[db][4 * c4 + 1], o[db][4 * c4 + 2], o[db][4 * c4 + 3]};
+    if (half == 0) *reinterpret_cast<f32x2*>(po + 32 * DP + 2 * li) = f32x2{m, lt};
+    return;
+  }
   const float inv = 1.0f / lt;
   uint16_t* op = (uint16_t*)a.out + b0 * a.o_s[0] + b1 * a.o_s[1] + (int64_t)i * a.o_s[2] + (int64_t)h * a.o_s[3];
   const uint16_t* gp = a.gate ? (const uint16_t*)a.gate + b0 * a.g_s[0] + b1 * a.g_s[1] + (int64_t)i * a.g_s[2] +
@@ -558,13 +578,73 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   }
 }
 
+// Combine of the key-range slices: thread per (query block, query, 4 dims).  O and l of each
+// slice are relative to the slice's own reference point m_s; with M = max m_s the result is
+// sum_s O_s 2^(cs (m_s - M)) / sum_s l_s 2^(cs (m_s - M)), then the gate.  All loads of a thread
+// are independent and issued together: one memory round trip per thread.
+template <int DP, int KS>
+__global__ __launch_bounds__(256) void attn2_combine_kernel(const sf_attention_args a, const Attn2Plan pl) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nblk = pl.tasks / KS;
+  if (t >= nblk * 32 * (DP / 4)) return;
+  const int d0 = 4 * (int)(t % (DP / 4));
+  const int li = (int)((t / (DP / 4)) % 32);
+  const int64_t blk = t / (32 * (DP / 4));
+  const int qblk = (int)(blk % pl.QB);
+  const int64_t task = blk / pl.QB;
+  const int h = (int)(task % a.H);
+  const int64_t b = task / a.H;
+  const int b0 = (int)(b / a.B1), b1 = (int)(b - (int64_t)b0 * a.B1);
+  const int i = qblk * 32 + li;
+  if (i >= a.Q || d0 >= a.Dv) return;
+  const float cs = a.scale * SF_LOG2E;
+  const float* base = pl.part + blk * KS * 32 * (DP + 2);
+  f32x2 ml[KS];
+  f32x4 os[KS];
+#pragma unroll
+  for (int sl = 0; sl < KS; ++sl) {
+    ml[sl] = *reinterpret_cast<const f32x2*>(base + sl * 32 * (DP + 2) + 32 * DP + 2 * li);
+    os[sl] = *reinterpret_cast<const f32x4*>(base + sl * 32 * (DP + 2) + li * DP + d0);
+  }
+  float mx = ml[0][0];
+#pragma unroll
+  for (int sl = 1; sl < KS; ++sl) mx = fmaxf(mx, ml[sl][0]);
+  float lsum = 0.f, v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sl = 0; sl < KS; ++sl) {
+    const float w = fast_exp2((ml[sl][0] - mx) * cs);
+    lsum += w * ml[sl][1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += w * os[sl][e];
+  }
+  const float inv = 1.0f / lsum;
+  uint16_t* op = (uint16_t*)a.out + b0 * a.o_s[0] + b1 * a.o_s[1] + (int64_t)i * a.o_s[2] + (int64_t)h * a.o_s[3];
+  const uint16_t* gp = a.gate ? (const uint16_t*)a.gate + b0 * a.g_s[0] + b1 * a.g_s[1] + (int64_t)i * a.g_s[2] +
+                                    (int64_t)h * a.g_s[3]
+                              : nullptr;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (d0 + e >= a.Dv) continue;
+    float x = v[e] * inv;
+    if (gp != nullptr) x *= sigmoidf_(bf2f(gp[d0 + e]));
+    op[d0 + e] = f2bf(x);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
 
 }  // namespace
 
-extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
-  if (a == nullptr) { sf_set_error("attention: null args"); return 1; }
+namespace {
+
+struct AttnRoute {
+  bool vec, vec_out, attn2, shared, bl;
+  int dmax, kc, ksplit;
+  Attn2Plan pl;
+};
+
+int route(const sf_attention_args* a, bool allow_split, AttnRoute& r) {
   if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr) {
     sf_set_error("attention: q, k, v and out must be non-null"); return 1;
   }
@@ -573,40 +653,67 @@ extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
                  a->B0, a->B1, a->Q, a->K, a->H, a->D, a->Dv);
     return 1;
   }
-  const int dmax = a->D > a->Dv ? a->D : a->Dv;
-  if (dmax > 64) { sf_set_error("attention: head dims above 64 are not supported (D=%d Dv=%d)", a->D, a->Dv); return 1; }
+  r.dmax = a->D > a->Dv ? a->D : a->Dv;
+  if (r.dmax > 64) { sf_set_error("attention: head dims above 64 are not supported (D=%d Dv=%d)", a->D, a->Dv); return 1; }
   if ((int64_t)a->B0 * a->B1 > 65535 || a->H > 65535) {
     sf_set_error("attention: batch (%d) or heads (%d) exceed the grid limit", a->B0 * a->B1, a->H); return 1;
   }
   // 16-byte path for q/k/v rows: head dims multiple of 8, row/head strides multiple of 8,
   // 16-byte aligned bases.
-  bool vec = (a->D % 8 == 0) && (a->Dv % 8 == 0) && aligned16(a->q) && aligned16(a->k) && aligned16(a->v);
-  for (int s = 0; s < 4 && vec; ++s)
-    vec = (a->q_s[s] % 8 == 0) && (a->k_s[s] % 8 == 0) && (a->v_s[s] % 8 == 0);
-  bool vec_out = aligned8(a->out);
-  for (int s = 0; s < 4 && vec_out; ++s) vec_out = (a->o_s[s] % 4 == 0);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  r.vec = (a->D % 8 == 0) && (a->Dv % 8 == 0) && aligned16(a->q) && aligned16(a->k) && aligned16(a->v);
+  for (int s = 0; s < 4 && r.vec; ++s)
+    r.vec = (a->q_s[s] % 8 == 0) && (a->k_s[s] % 8 == 0) && (a->v_s[s] % 8 == 0);
+  r.vec_out = aligned8(a->out);
+  for (int s = 0; s < 4 && r.vec_out; ++s) r.vec_out = (a->o_s[s] % 4 == 0);
   bool bias_vec = a->bias == nullptr || aligned8(a->bias);
   for (int s = 0; s < 4 && bias_vec && a->bias != nullptr; ++s) bias_vec = a->bias_s[s] % 4 == 0;
-  if (vec && bias_vec) {
-    Attn2Plan pl{};
-    pl.QB = (a->Q + 31) / 32;
-    pl.vec_out = vec_out && (a->gate == nullptr || aligned8(a->gate));
-    for (int s = 0; s < 4 && pl.vec_out && a->gate != nullptr; ++s) pl.vec_out = a->g_s[s] % 4 == 0;
-    const int64_t bh = (int64_t)a->B0 * a->B1 * a->H;
-    const int64_t groups = bh * ((pl.QB + 3) / 4);
-    bool shared = a->Q >= 128 && groups >= 512;
-    if (const char* e = getenv("SPARSEFOLD_HIP_ATTN_MODE")) shared = e[0] == 's';   // test hook
-    pl.tasks = shared ? groups : bh * pl.QB;
-    const int64_t wgs = shared ? groups : (pl.tasks + 3) / 4;
+  r.attn2 = r.vec && bias_vec;
+  r.ksplit = 1;
+  r.pl = Attn2Plan{};
+  if (!r.attn2) return 0;
+  Attn2Plan& pl = r.pl;
+  pl.QB = (a->Q + 31) / 32;
+  pl.vec_out = r.vec_out && (a->gate == nullptr || aligned8(a->gate));
+  for (int s = 0; s < 4 && pl.vec_out && a->gate != nullptr; ++s) pl.vec_out = a->g_s[s] % 4 == 0;
+  const int64_t bh = (int64_t)a->B0 * a->B1 * a->H;
+  const int64_t groups = bh * ((pl.QB + 3) / 4);
+  r.shared = a->Q >= 128 && groups >= 512;
+  if (const char* e = getenv("SPARSEFOLD_HIP_ATTN_MODE")) r.shared = e[0] == 's';   // test hook
+  // Per-wave tasks on a grid too small for the GPU (single attention: 16 heads x 24 blocks =
+  // 384 waves for 1024 SIMDs) split their key range into slices of >= 2 tiles, up to ~2048 waves;
+  // a combine kernel merges the slices.  Needs a workspace (module-level entry points).
+  if (allow_split && !r.shared) {
+    const int ntiles = (a->K + 63) / 64;
+    const int64_t blocks = bh * pl.QB;
+    int ks = (int)((2048 + blocks - 1) / blocks);
+    ks = ks < 4 ? ks : 4;
+    ks = ks < ntiles / 2 ? ks : ntiles / 2;
+    r.ksplit = ks > 1 ? ks : 1;
+  }
+  pl.ksplit = r.ksplit;
+  pl.tasks = r.shared ? groups : bh * pl.QB * r.ksplit;
+  r.kc = (a->D + 15) / 16;                                  // q.k chunks holding data
+  // LDS bias tiles: always with shared tiles; per-wave tiles only for long key ranges, where the
+  // saved load time outweighs the lower occupancy of the larger LDS footprint (atom windows,
+  // K = 128: 31 us without, 41 us with; single attention, K = 768: 30 us without, 25 us with)
+  r.bl = a->bias != nullptr && aligned16(a->bias) && a->K % 8 == 0 && (r.shared || a->K >= 256);
+  for (int s2 = 0; s2 < 4 && r.bl; ++s2) r.bl = a->bias_s[s2] % 8 == 0;
+  return 0;
+}
+
+size_t split_bytes(const sf_attention_args* a, const AttnRoute& r) {
+  if (!r.attn2 || r.ksplit <= 1) return 0;
+  const int dp = r.dmax <= 32 ? 32 : 64;
+  return (size_t)r.pl.tasks * 32 * (dp + 2) * sizeof(float);
+}
+
+int launch_attention(const sf_attention_args* a, const AttnRoute& r, float* split_ws, hipStream_t st) {
+  if (r.attn2) {
+    Attn2Plan pl = r.pl;
+    pl.part = split_ws;
+    const int64_t wgs = r.shared ? pl.tasks : (pl.tasks + 3) / 4;
     if (wgs > 0x7fffffff) { sf_set_error("attention: problem too large for the grid"); return 1; }
     const dim3 g2((unsigned)wgs);
-    const int kc = (a->D + 15) / 16;                        // q.k chunks holding data
-    // LDS bias tiles: always with shared tiles; per-wave tiles only for long key ranges, where the
-    // saved load time outweighs the lower occupancy of the larger LDS footprint (atom windows,
-    // K = 128: 31 us without, 41 us with; single attention, K = 768: 30 us without, 25 us with)
-    bool bl = a->bias != nullptr && aligned16(a->bias) && a->K % 8 == 0 && (shared || a->K >= 256);
-    for (int s2 = 0; s2 < 4 && bl; ++s2) bl = a->bias_s[s2] % 8 == 0;
     auto launch = [&](auto dp, auto sh, auto kcc, auto blc) {
       hipLaunchKernelGGL((attn2_kernel<decltype(dp)::value, decltype(sh)::value, decltype(kcc)::value,
                                        decltype(blc)::value>), g2, dim3(256), 0, st, *a, pl);
@@ -616,27 +723,71 @@ extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
     using Tt = std::true_type;
     using Ff = std::false_type;
     auto by_bl = [&](auto dp, auto sh, auto kcc) {
-      if (bl) launch(dp, sh, kcc, Tt{});
+      if (r.bl) launch(dp, sh, kcc, Tt{});
       else launch(dp, sh, kcc, Ff{});
     };
     auto by_sh = [&](auto dp, auto kcc) {
-      if (shared) by_bl(dp, Tt{}, kcc);
+      if (r.shared) by_bl(dp, Tt{}, kcc);
       else by_bl(dp, Ff{}, kcc);
     };
-    if (dmax <= 32) {
-      if (kc <= 1) by_sh(I32{}, std::integral_constant<int, 1>{});
+    if (r.dmax <= 32) {
+      if (r.kc <= 1) by_sh(I32{}, std::integral_constant<int, 1>{});
       else by_sh(I32{}, std::integral_constant<int, 2>{});
-    } else if (kc <= 3) {
+    } else if (r.kc <= 3) {
       by_sh(I64{}, std::integral_constant<int, 3>{});
     } else {
       by_sh(I64{}, std::integral_constant<int, 4>{});
     }
-    return sf_check_launch("attn2_kernel");
+    int rc = sf_check_launch("attn2_kernel");
+    if (rc || pl.ksplit <= 1) return rc;
+    const int dp = r.dmax <= 32 ? 32 : 64;
+    const int64_t threads = pl.tasks / pl.ksplit * 32 * (dp / 4);
+    const dim3 gc((unsigned)((threads + 255) / 256));
+    auto combine = [&](auto ks) {
+      constexpr int KS = decltype(ks)::value;
+      if (dp == 32) hipLaunchKernelGGL((attn2_combine_kernel<32, KS>), gc, dim3(256), 0, st, *a, pl);
+      else hipLaunchKernelGGL((attn2_combine_kernel<64, KS>), gc, dim3(256), 0, st, *a, pl);
+    };
+    if (pl.ksplit > 8) { sf_set_error("attention: at most 8 key-range slices"); return 1; }
+    switch (pl.ksplit) {
+      case 2: combine(std::integral_constant<int, 2>{}); break;
+      case 3: combine(std::integral_constant<int, 3>{}); break;
+      case 4: combine(std::integral_constant<int, 4>{}); break;
+      case 5: combine(std::integral_constant<int, 5>{}); break;
+      case 6: combine(std::integral_constant<int, 6>{}); break;
+      case 7: combine(std::integral_constant<int, 7>{}); break;
+      default: combine(std::integral_constant<int, 8>{}); break;
+    }
+    return sf_check_launch("attn2_combine_kernel");
   }
   dim3 grid((a->Q + kQB - 1) / kQB, a->H, a->B0 * a->B1);
-  if (dmax <= 32)
-    hipLaunchKernelGGL(attention_fwd_kernel<32>, grid, dim3(256), 0, st, *a, (int)vec, (int)vec_out);
+  if (r.dmax <= 32)
+    hipLaunchKernelGGL(attention_fwd_kernel<32>, grid, dim3(256), 0, st, *a, (int)r.vec, (int)r.vec_out);
   else
-    hipLaunchKernelGGL(attention_fwd_kernel<64>, grid, dim3(256), 0, st, *a, (int)vec, (int)vec_out);
+    hipLaunchKernelGGL(attention_fwd_kernel<64>, grid, dim3(256), 0, st, *a, (int)r.vec, (int)r.vec_out);
   return sf_check_launch("attention_fwd_kernel");
+}
+
+}  // namespace
+
+size_t sf_attention_workspace_bytes(const sf_attention_args* a) {
+  AttnRoute r;
+  if (a == nullptr || route(a, true, r)) return 0;
+  return split_bytes(a, r);
+}
+
+int sf_attention_run(const sf_attention_args* a, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (a == nullptr) { sf_set_error("attention: null args"); return 1; }
+  AttnRoute r;
+  const bool can_split = workspace != nullptr;
+  if (route(a, can_split, r)) return 1;
+  if (can_split && split_bytes(a, r) > workspace_bytes) {
+    // the caller sized its workspace for a different route: run without slices
+    if (route(a, false, r)) return 1;
+  }
+  return launch_attention(a, r, static_cast<float*>(workspace), st);
+}
+
+extern "C" int sf_hip_attention_fwd(const sf_attention_args* a, void* stream) {
+  return sf_attention_run(a, nullptr, 0, reinterpret_cast<hipStream_t>(stream));
 }

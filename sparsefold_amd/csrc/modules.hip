@@ -81,6 +81,55 @@ int zero_init_out(int64_t rows, int C, int HD, const void* o, const void* cond, 
   return sf_hip_linear_fwd(&l, st);
 }
 
+// attention stage of the self-attention chain: q, k, v, g are column blocks of y [S*N, 4HD]
+sf_attention_args self_attn_args(const sf_self_attention_args* a, const void* y, void* o) {
+  const int HD = a->H * a->D;
+  sf_attention_args t{};
+  t.B0 = a->S; t.B1 = 1; t.Q = a->N; t.K = a->N; t.H = a->H; t.D = a->D; t.Dv = a->D;
+  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
+  const int64_t ys[4] = {(int64_t)a->N * 4 * HD, 0, 4 * HD, a->D};
+  const uint16_t* yb = static_cast<const uint16_t*>(y);
+  t.q = yb;          for (int i = 0; i < 4; ++i) t.q_s[i] = ys[i];
+  t.k = yb + HD;     for (int i = 0; i < 4; ++i) t.k_s[i] = ys[i];
+  t.v = yb + 2 * HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ys[i];
+  t.gate = yb + 3 * HD; for (int i = 0; i < 4; ++i) t.g_s[i] = ys[i];
+  if (a->bias) {
+    t.bias = a->bias; t.bias_s[0] = a->bias_s[0]; t.bias_s[1] = 0; t.bias_s[2] = a->bias_s[1]; t.bias_s[3] = a->bias_s[2];
+  }
+  if (a->mask) { t.mask_k = a->mask; t.mk_s[0] = 0; t.mk_s[1] = 0; t.mk_s[2] = 1; }
+  t.out = o; t.o_s[0] = (int64_t)a->N * HD; t.o_s[1] = 0; t.o_s[2] = HD; t.o_s[3] = a->D;
+  return t;
+}
+
+// attention stage of the cross-attention chain: q, g are column blocks of yq [rows_q, 2HD],
+// k, v of yk [rows_k, 2HD]
+sf_attention_args cross_attn_args(const sf_cross_attention_args* a, const void* yq, const void* yk, void* o) {
+  const int HD = a->H * a->D;
+  sf_attention_args t{};
+  t.B0 = a->S; t.B1 = a->U; t.Q = a->Qw; t.K = a->Kw; t.H = a->H; t.D = a->D; t.Dv = a->D;
+  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
+  const uint16_t* qb = static_cast<const uint16_t*>(yq);
+  const uint16_t* kb = static_cast<const uint16_t*>(yk);
+  const int64_t qs[4] = {(int64_t)a->U * a->Qw * 2 * HD, (int64_t)a->Qw * 2 * HD, 2 * HD, a->D};
+  const int64_t ks[4] = {(int64_t)a->U * a->Kw * 2 * HD, (int64_t)a->Kw * 2 * HD, 2 * HD, a->D};
+  t.q = qb;      for (int i = 0; i < 4; ++i) t.q_s[i] = qs[i];
+  t.gate = qb + HD; for (int i = 0; i < 4; ++i) t.g_s[i] = qs[i];
+  t.k = kb;      for (int i = 0; i < 4; ++i) t.k_s[i] = ks[i];
+  t.v = kb + HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ks[i];
+  if (a->bias) {
+    t.bias = a->bias; t.bias_s[0] = 0; t.bias_s[1] = (int64_t)a->H * a->Qw * a->Kw;
+    t.bias_s[2] = (int64_t)a->Qw * a->Kw; t.bias_s[3] = a->Kw;
+  }
+  if (a->mask_q) { t.mask_q = a->mask_q; t.mq_s[0] = 0; t.mq_s[1] = a->Qw; t.mq_s[2] = 1; }
+  if (a->mask_k) { t.mask_k = a->mask_k; t.mk_s[0] = 0; t.mk_s[1] = a->Kw; t.mk_s[2] = 1; }
+  t.out = o; t.o_s[0] = (int64_t)a->U * a->Qw * HD; t.o_s[1] = (int64_t)a->Qw * HD; t.o_s[2] = HD; t.o_s[3] = a->D;
+  return t;
+}
+
+// Stand-in buffer address for sizing queries: the attention route depends on pointer alignment
+// only, and every arena slice is 256-byte aligned.
+void* const kArenaAligned = reinterpret_cast<void*>(static_cast<uintptr_t>(1) << 20);
+
 // workspace of the self-attention chain (the arena walk below, run without a base)
 size_t self_ws(const sf_self_attention_args* a) {
   Arena ws{nullptr};
@@ -90,6 +139,8 @@ size_t self_ws(const sf_self_attention_args* a) {
   ws.take((size_t)rows * a->C * 2);          // h
   ws.take((size_t)rows * 4 * HD * 2);        // q k v g
   ws.take((size_t)rows * HD * 2);            // o
+  const sf_attention_args t = self_attn_args(a, kArenaAligned, kArenaAligned);
+  ws.take(sf_attention_workspace_bytes(&t));  // key-range slices of the attention
   if (a->cond) ws.take((size_t)a->N * a->C * 2);
   return ws.off;
 }
@@ -108,6 +159,8 @@ size_t cross_ws(const sf_cross_attention_args* a) {
   ws.take((size_t)qrows * 2 * HD * 2);
   ws.take((size_t)krows * 2 * HD * 2);
   ws.take((size_t)qrows * HD * 2);
+  const sf_attention_args t = cross_attn_args(a, kArenaAligned, kArenaAligned, kArenaAligned);
+  ws.take(sf_attention_workspace_bytes(&t));
   ws.take((size_t)a->U * a->Qw * a->C * 2);
   return ws.off;
 }
@@ -157,21 +210,10 @@ extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* 
   p.M = rows; p.N = 4 * HD; p.K = a->C; p.x = h; p.x_rs = a->C; p.wt = a->w_qkvg; p.bias = a->b_qkvg;
   p.mul_rows = 1; p.y = y; p.y_rs = 4 * HD;
   if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
-  sf_attention_args t{};
-  t.B0 = a->S; t.B1 = 1; t.Q = a->N; t.K = a->N; t.H = a->H; t.D = a->D; t.Dv = a->D;
-  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
-  const int64_t ys[4] = {(int64_t)a->N * 4 * HD, 0, 4 * HD, a->D};
-  const uint16_t* yb = static_cast<const uint16_t*>(y);
-  t.q = yb;          for (int i = 0; i < 4; ++i) t.q_s[i] = ys[i];
-  t.k = yb + HD;     for (int i = 0; i < 4; ++i) t.k_s[i] = ys[i];
-  t.v = yb + 2 * HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ys[i];
-  t.gate = yb + 3 * HD; for (int i = 0; i < 4; ++i) t.g_s[i] = ys[i];
-  if (a->bias) {
-    t.bias = a->bias; t.bias_s[0] = a->bias_s[0]; t.bias_s[1] = 0; t.bias_s[2] = a->bias_s[1]; t.bias_s[3] = a->bias_s[2];
-  }
-  if (a->mask) { t.mask_k = a->mask; t.mk_s[0] = 0; t.mk_s[1] = 0; t.mk_s[2] = 1; }
-  t.out = o; t.o_s[0] = (int64_t)a->N * HD; t.o_s[1] = 0; t.o_s[2] = HD; t.o_s[3] = a->D;
-  if ((rc = sf_hip_attention_fwd(&t, st))) return rc;
+  const sf_attention_args t = self_attn_args(a, y, o);
+  const size_t split = sf_attention_workspace_bytes(&t);
+  void* split_ws = ws.take(split);
+  if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
   return zero_init_out(rows, a->C, HD, o, a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
                        a->add_residual ? a->x : nullptr, a->out, ws, st);
 }
@@ -233,25 +275,10 @@ extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void
   if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
   p.M = krows; p.x = hk; p.wt = a->w_kv; p.bias = nullptr; p.y = yk;
   if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
-  sf_attention_args t{};
-  t.B0 = a->S; t.B1 = a->U; t.Q = a->Qw; t.K = a->Kw; t.H = a->H; t.D = a->D; t.Dv = a->D;
-  t.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
-  const uint16_t* qb = static_cast<const uint16_t*>(yq);
-  const uint16_t* kb = static_cast<const uint16_t*>(yk);
-  const int64_t qs[4] = {(int64_t)a->U * a->Qw * 2 * HD, (int64_t)a->Qw * 2 * HD, 2 * HD, a->D};
-  const int64_t ks[4] = {(int64_t)a->U * a->Kw * 2 * HD, (int64_t)a->Kw * 2 * HD, 2 * HD, a->D};
-  t.q = qb;      for (int i = 0; i < 4; ++i) t.q_s[i] = qs[i];
-  t.gate = qb + HD; for (int i = 0; i < 4; ++i) t.g_s[i] = qs[i];
-  t.k = kb;      for (int i = 0; i < 4; ++i) t.k_s[i] = ks[i];
-  t.v = kb + HD; for (int i = 0; i < 4; ++i) t.v_s[i] = ks[i];
-  if (a->bias) {
-    t.bias = a->bias; t.bias_s[0] = 0; t.bias_s[1] = (int64_t)a->H * a->Qw * a->Kw;
-    t.bias_s[2] = (int64_t)a->Qw * a->Kw; t.bias_s[3] = a->Kw;
-  }
-  if (a->mask_q) { t.mask_q = a->mask_q; t.mq_s[0] = 0; t.mq_s[1] = a->Qw; t.mq_s[2] = 1; }
-  if (a->mask_k) { t.mask_k = a->mask_k; t.mk_s[0] = 0; t.mk_s[1] = a->Kw; t.mk_s[2] = 1; }
-  t.out = o; t.o_s[0] = (int64_t)a->U * a->Qw * HD; t.o_s[1] = (int64_t)a->Qw * HD; t.o_s[2] = HD; t.o_s[3] = a->D;
-  if ((rc = sf_hip_attention_fwd(&t, st))) return rc;
+  const sf_attention_args t = cross_attn_args(a, yq, yk, o);
+  const size_t split = sf_attention_workspace_bytes(&t);
+  void* split_ws = rest.take(split);
+  if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
   return zero_init_out(qrows, C, HD, o, a->cond_q, (int64_t)a->U * a->Qw, C, a->w_zc, a->b_zc, a->w_t2,
                        a->add_residual ? a->xq : nullptr, a->out, rest, st);
 }

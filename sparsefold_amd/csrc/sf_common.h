@@ -126,3 +126,9 @@ int sf_check_launch(const char* what);
 // Workgroups of `kernel` (launched with `threads` threads, no dynamic LDS) that the current
 // device holds at once: CUs x occupancy; cached per (device, kernel).  At least 1.
 int sf_resident_workgroups(const void* kernel, int threads);
+
+// Attention with an optional workspace (library-internal; the C entry point has none): with a
+// workspace of sf_attention_workspace_bytes, per-wave tasks on a grid too small for the GPU
+// split their key range into slices merged by a combine kernel.
+size_t sf_attention_workspace_bytes(const sf_attention_args* a);
+int sf_attention_run(const sf_attention_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream);

@@ -120,7 +120,25 @@ def test_single_attention_with_pair_bias(N, padded, sharp):
   assert_close_bf16(upd, d_ref, f"single N={N} update", max_abs=2e-2 * d_ref.abs().max().item())
 
 
-@pytest.mark.parametrize("N,S,padded,sharp", [(100, 2, True, True), (1024, 5, False, False)])
+@pytest.mark.parametrize("N,keys", [(333, "padded"), (512, "second_half"), (512, "first_tile"), (512, "none")])
+def test_single_attention_key_slices(N, keys):
+  """Grids this small split each query block's key range over several waves and merge the
+  slices: slices whose keys are all masked, a reference point set by one slice only, ragged last
+  slices and rows with no valid key at all."""
+  mod, z, s, seq = W.make_single(N, seed=5, padded=keys == "padded", sharp=True)
+  if keys == "second_half":
+    seq[N // 2:] = False
+  elif keys == "first_tile":
+    seq[64:] = False
+  elif keys == "none":
+    seq[:] = False
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), s.to(DEV), seq.to(DEV), add_residual=False)
+  d_ref = OM.single_act_update_attention(z.float(), s.float(), seq, _params(hip), return_update=True)
+  assert_close_bf16(upd, d_ref, f"single N={N} keys={keys}", max_abs=2e-2 * d_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("N,S,padded,sharp", [(100, 2, True, True), (300, 1, True, True), (1024, 5, False, False)])
 def test_diffusion_token_attention(N, S, padded, sharp):
   mod, act, cond, bias, mask = W.make_diffusion(N, S=S, seed=4, padded=padded, sharp=sharp)
   hip = _prepared(mod)
