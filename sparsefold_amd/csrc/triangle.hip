@@ -22,13 +22,14 @@
 //                        For the ending node the workgroup walks z's column instead of its row,
 //                        so nothing is transposed in memory (blocks.py:345-346, :362-363).
 //   2. tri_attn_kernel   one workgroup per (4 rows, head, 256 queries); K / V^T tiles of 64
-//                        keys for the 4 rows double-buffered in LDS; each wave keeps the online
-//                        softmax state of its 32 queries for all 4 rows and feeds the bias tile
+//                        keys for the 4 rows double-buffered in LDS; each wave keeps the
+//                        softmax sums of its 32 queries for all 4 rows and feeds the bias tile
 //                        -- identical for every row -- as the accumulator input of the S^T MFMA;
-//                        sigmoid gate in the epilogue, output written at its pair position.
-//      tri_masked_kernel rows whose token is masked attend uniformly to every key (the
-//                        reference's finite -finfo.max mask): gate * mean of V, written over
-//                        what the attention kernel stored for them.
+//                        output written at its pair position, rows with an out-of-range
+//                        weight sum flagged.
+//      tri_fixup_kernel  rows whose token is masked attend uniformly to every key (the
+//                        reference's finite -finfo.max mask): mean of V; flagged rows are
+//                        recomputed with an exact two-pass softmax.
 //   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
@@ -73,6 +74,7 @@ constexpr int kProjBlocks = 13;
 struct FastWs {
   uint16_t *q, *k, *vt, *bias, *o, *wf;
   float* off;
+  uint8_t* flags;                     // [N][H] rows for the exact fix-up
   size_t bytes;
 };
 
@@ -88,23 +90,27 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
   w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
   w.off = (float*)(p + off); off += round_up((size_t)kPCols * 4);
+  w.flags = (uint8_t*)(p + off); off += round_up((size_t)N * H);
   w.bytes = off;
   return w;
 }
 
 // ---------------------------------------------------------------------------------------
 // 0. weight fold: wf[n][c] = bf16(w[n][c] * gamma[c]), off[n] = sum_c beta[c] w[n][c];
-//    rows 516..543 (padding of the bias block) are zero.  One wave per weight row.
+//    rows 516..543 (padding of the bias block) are zero.  One wave per weight row.  Also clears
+//    the attention kernel's fix-up flags.
 // ---------------------------------------------------------------------------------------
 struct TriFoldArgs {
   int nrows;                          // 4 * H * 32 + H
   const uint16_t* w;                  // [nrows, 128]
   const float* ln_w; const float* ln_b;
   uint16_t* wf; float* off;           // [544, 128], [544]
+  uint8_t* flags; int nflags;         // [N * H], cleared
 };
 
 __global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
   const int lane = threadIdx.x & 63;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nflags; f += gridDim.x * blockDim.x) a.flags[f] = 0;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= kPCols) return;
   const int c = 2 * lane;
@@ -428,10 +434,11 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
 
 struct TriAttnArgs {
   int N, NP, H, transpose;
-  float mass_limit;                   // probability mass of a 32-key half that moves the reference
+  float sum_limit;                    // weight sums outside [2^-100, sum_limit] flag the (row, head)
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
   uint16_t* o;                        // [N][N][H][32] at pair positions, dims in epilogue order
+  uint8_t* flags;                     // [N][H]: 1 = recomputed exactly by tri_fixup_kernel
 };
 
 constexpr int kTR = 4;                // rows per workgroup
@@ -539,25 +546,29 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   for (int rr = 0; rr < kTR; ++rr)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + qlane + kk * 512));
-  // Online softmax state.  m is the reference point of the exponentials (shared by the two
-  // lanes holding the same query), kept bf16-exact because it enters the S^T MFMA through an
-  // extra k-step: [K | 1] . [Q | -m]^T + bias = logit - m, so after tile 0 the weights are
-  // exp2 of the MFMA output directly.  Tile 0 sets m to its row maximum; later tiles move it
-  // only when the probability mass of a 32-key half exceeds mass_limit (2^60; all weights are
-  // >= 0, so the sum bounds every single weight and nothing can overflow unnoticed).
+  // Softmax against a fixed reference point of 0: the logits (log2 units, q carries
+  // scale * log2 e) are exponentiated as they come out of the S^T MFMA, with no running maximum
+  // and no rescaling of o.  Logits of realistic inputs lie far inside the range where that is
+  // exact in fp32/bf16 (2^+-100); a row whose weight sum leaves [2^-100, sum_limit] -- an
+  // overflow, an underflow of the whole row, or a forced test limit -- is flagged at the end
+  // and recomputed with an exact two-pass softmax by tri_fixup_kernel.  A weight w <= sum <=
+  // 2^100 cannot overflow, and o = sum_k w_k v_k stays finite for any bf16 v of moderate size.
   f32x16 o[kTR];
-  float m[kTR], l[kTR];
+  f32x4 lsum[kTR];
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[rr][e] = 0.f;
-    m[rr] = 0.f;
-    l[rr] = 0.f;
-  }
-  int mflag = 0;                                         // bit rr: some lane of row rr has m != 0 (uniform)
-  bf16x8 ones_k;                                         // A operand: 1 at k = 0 (lanes of half 0)
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ones_k[e] = (__bf16)((e == 0 && half == 0) ? 1.0f : 0.0f);
+    for (int e = 0; e < 4; ++e) lsum[rr][e] = 0.f;
+  }
+  // Row sums on the matrix core: a 16x16x32 MFMA whose B operand is the P^T chunk of the P.V
+  // MFMA (lane l: query l%32, keys of lane group l/16) and whose A operand selects lane groups
+  // {0, 2} into output rows 0..7 and {1, 3} into rows 8..15.  Output (m, n) is then the sum over
+  // the chunk's 16 keys of query n (m < 8) or query n + 16 (m >= 8).
+  bf16x8 sel;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sel[e] = (__bf16)((((lane & 15) < 8) == (((lane >> 4) & 1) == 0)) ? 1.0f : 0.0f);
 
   // bias tile of this wave's 32 queries -> fp32 accumulator seed in S^T register order
   f32x16 bseed[2];
@@ -576,51 +587,6 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       }
     }
   };
-  // The work of a tile is split into units (row rr, 32-key half kb): S^T half = 32 keys x 32
-  // queries (3 MFMAs), its 32 weights per lane pair, and their P.V (2 MFMAs).  Units are
-  // software-pipelined: the S^T MFMAs of unit u+1 are issued before the exponentials of unit u.
-  auto qk_half = [&](int rr, int kb, int buf, bool with_m, f32x16& s) __attribute__((always_inline)) {
-    const bf16x8 k0 = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
-    const bf16x8 k1 = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
-    s = mfma32(k1, qb8[rr][1], mfma32(k0, qb8[rr][0], bseed[kb]));
-    if (with_m) {
-      bf16x8 mq;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
-      mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
-      s = mfma32(ones_k, mq, s);
-    }
-  };
-  // weights 2^(s - shift) as packed bf16 pairs in PV slot order; returns their sum
-  auto weights_half = [&](const f32x16& s, float shift, bf16x2 (&pw)[8]) __attribute__((always_inline)) {
-    float ts0 = 0.f, ts1 = 0.f;                          // two chains of dependent sums
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pw[e] = cvt_bf2(fast_exp2(s[2 * e] - shift), fast_exp2(s[2 * e + 1] - shift));
-      if (e & 1) ts1 = add_bf2(pw[e], ts1); else ts0 = add_bf2(pw[e], ts0);
-    }
-    return ts0 + ts1;
-  };
-  auto max_half = [&](const f32x16& s) __attribute__((always_inline)) {
-    float v = s[0];
-#pragma unroll
-    for (int e = 1; e < 16; ++e) v = fmaxf(v, s[e]);
-    return fmaxf(v, __shfl_xor(v, 32));
-  };
-  auto pv_half = [&](int rr, int kb, int buf, const bf16x2 (&pw)[8]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf16x8 pb;                     // P^T chunk 2kb+j: pairs 4j .. 4j+3 of the half
-#pragma unroll
-      for (int q2 = 0; q2 < 4; ++q2) {
-        pb[2 * q2] = pw[4 * j + q2][0];
-        pb[2 * q2 + 1] = pw[4 * j + q2][1];
-      }
-      o[rr] = mfma32(as_bf16x8(ld16(vslot(buf, rr, 2 * kb + j))), pb, o[rr]);
-    }
-  };
-  // the same with operands read from LDS one unit earlier (the per-unit mass check is a branch,
-  // so reads issued in the unit that uses them would wait out the LDS latency every unit)
   auto load_k = [&](int rr, int kb, int buf, bf16x8 (&kr)[2]) __attribute__((always_inline)) {
     kr[0] = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
     kr[1] = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
@@ -629,121 +595,80 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     vr[0] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb)));
     vr[1] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb + 1)));
   };
-  auto qk_reg = [&](int rr, int kb, const bf16x8 (&kr)[2], f32x16& s) __attribute__((always_inline)) {
+  // S^T half of unit (row rr, 32-key half kb) = K Q^T + bias, logits in log2 units
+  auto qk = [&](int rr, int kb, const bf16x8 (&kr)[2], f32x16& s) __attribute__((always_inline)) {
     s = mfma32(kr[1], qb8[rr][1], mfma32(kr[0], qb8[rr][0], bseed[kb]));
-    if (__builtin_amdgcn_readfirstlane(mflag) & (1 << rr)) {   // some lane of the row has m != 0
-      bf16x8 mq;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mq[e] = (__bf16)0.0f;
-      mq[0] = (__bf16)(half == 0 ? -m[rr] : 0.0f);
-      s = mfma32(ones_k, mq, s);
-    }
   };
-  auto pv_reg = [&](int rr, const bf16x8 (&vr)[2], const bf16x2 (&pw)[8]) __attribute__((always_inline)) {
+
+  // The work of a tile is split into units (row rr, 32-key half kb): S^T half = 32 keys x 32
+  // queries (2 MFMAs), its 16 weights per lane, their P.V (2 MFMAs) and row sums (2 small
+  // MFMAs).  Units are software-pipelined: the S^T MFMAs of unit u+1 are issued before the
+  // exponentials of unit u, K operands are read two units ahead and V operands one unit ahead.
+  // The scheduling fences keep the compiler from sinking those reads to their uses (which
+  // exposed the LDS latency every unit) and from hoisting unit u+1's S^T MFMAs away from the
+  // exponentials they overlap.
+  auto units = [&](int buf) __attribute__((always_inline)) {
+    f32x16 sc, sn;
+    bf16x8 kr[2], vr[2];
+    load_k(0, 0, buf, kr);
+    qk(0, 0, kr, sc);
+    load_k(0, 1, buf, kr);
+    load_v(0, 0, buf, vr);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bf16x8 pb;
+    for (int u = 0; u < 2 * kTR; ++u) {
+      const int rr = u >> 1;
+      if (u + 1 < 2 * kTR) qk((u + 1) >> 1, (u + 1) & 1, kr, sn);
+      if (u + 2 < 2 * kTR) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int q2 = 0; q2 < 4; ++q2) {
-        pb[2 * q2] = pw[4 * j + q2][0];
-        pb[2 * q2 + 1] = pw[4 * j + q2][1];
+      for (int j = 0; j < 2; ++j) {
+        bf16x8 pb;                     // P^T chunk 2kb+j: weights 2^s as bf16 pairs
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const bf16x2 w = cvt_bf2(fast_exp2(sc[8 * j + 2 * q2]), fast_exp2(sc[8 * j + 2 * q2 + 1]));
+          pb[2 * q2] = w[0];
+          pb[2 * q2 + 1] = w[1];
+        }
+        o[rr] = mfma32(vr[j], pb, o[rr]);
+        lsum[rr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sel, pb, lsum[rr], 0, 0, 0);
       }
-      o[rr] = mfma32(vr[j], pb, o[rr]);
+      if (u + 1 < 2 * kTR) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
+      __builtin_amdgcn_sched_barrier(0);
+      sc = sn;
     }
   };
 
   const int ntiles = NP / kKT;
-
   load_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
-  // ---- tile 0: the reference point starts at the row maximum over the tile ----
-  if (ntiles > 1) load_tile(kKT, 1);
-  if (active) {
-    load_bias(0);
-#pragma unroll
-    for (int rr = 0; rr < kTR; ++rr) {
-      f32x16 s0, s1;
-      qk_half(rr, 0, 0, false, s0);
-      qk_half(rr, 1, 0, false, s1);
-      const float smax = fmaxf(max_half(s0), max_half(s1));
-      // a tile of masked keys only (max ~ SF_MASKED_LOGIT) leaves the reference at 0
-      // rows whose tile-0 maximum is moderate keep the reference point at 0, which lets their
-      // later tiles skip the m step (exp2 of logits up to +-32 is far inside fp32 range; the mass
-      // check still moves m if a later tile climbs past the limit)
-      const float m0 = (smax > 0.5f * SF_MASKED_LOGIT && fabsf(smax) > 32.0f) ? (float)(__bf16)smax : 0.0f;
-      m[rr] = m0;
-      if (__any(m0 != 0.0f)) mflag |= 1 << rr;
-      bf16x2 pw[8];
-      l[rr] = weights_half(s0, m0, pw);
-      pv_half(rr, 0, 0, pw);
-      l[rr] += weights_half(s1, m0, pw);
-      pv_half(rr, 1, 0, pw);
-    }
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  // tiles 1.. : buffer index is a compile-time constant inside each half of the pair
+  // buffer index is a compile-time constant inside each half of the pair
   auto tile_step = [&](int tt, auto bufc) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
-    const int j0 = tt * kKT;
-    if (tt + 1 < ntiles) load_tile(j0 + kKT, buf ^ 1);     // lands while this tile computes
+    if (tt + 1 < ntiles) load_tile((tt + 1) * kKT, buf ^ 1);   // lands while this tile computes
     if (active) {
       load_bias(buf);
-      f32x16 sc, sn;
-      bf16x8 kr[2], vr[2];
-      load_k(0, 0, buf, kr);
-      qk_reg(0, 0, kr, sc);
-      load_k(0, 1, buf, kr);
-      load_v(0, 0, buf, vr);
-#pragma unroll
-      for (int u = 0; u < 2 * kTR; ++u) {
-        const int rr = u >> 1, kb = u & 1;
-        if (u + 1 < 2 * kTR) qk_reg((u + 1) >> 1, (u + 1) & 1, kr, sn);
-        if (u + 2 < 2 * kTR) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
-        bf16x2 pw[8];
-        float ts = weights_half(sc, 0.0f, pw);
-        if (__any(!(ts <= a.mass_limit))) {
-          // rare: this half's mass passed the limit; sc holds logit - m exactly (|m| stays
-          // moderate), so move m up to the half's maximum and rescale what is accumulated.
-          // The next unit of the same row was issued against the old m: shift it too.
-          const float mnew = (float)(__bf16)(m[rr] + fmaxf(max_half(sc), 0.f));
-          const float shift = mnew - m[rr];
-          const float alpha = fast_exp2(-shift);
-          m[rr] = mnew;
-          if (__any(mnew != 0.0f)) mflag |= 1 << rr;
-          l[rr] *= alpha;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[rr][e] *= alpha;
-          ts = weights_half(sc, shift, pw);
-          if (kb == 0) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) sn[e] -= shift;
-          }
-        }
-        l[rr] += ts;
-        pv_reg(rr, vr, pw);
-        if (u + 1 < 2 * kTR) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
-        sc = sn;
-      }
+      units(buf);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
-  for (int tt = 1; tt < ntiles; tt += 2) {
-    tile_step(tt, std::integral_constant<int, 1>{});
-    if (tt + 1 < ntiles) tile_step(tt + 1, std::integral_constant<int, 0>{});
+  for (int tt = 0; tt < ntiles; tt += 2) {
+    tile_step(tt, std::integral_constant<int, 0>{});
+    if (tt + 1 < ntiles) tile_step(tt + 1, std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: normalise and store at the pair position (the gate is applied by the
   //      output kernel, which recomputes it from z) ----
   if (i >= N) return;
+  const int q32 = lane & 31;
+  const int src = q32 < 16 ? q32 : q32 + 16;         // a lane whose row-sum output holds query q32
 #pragma unroll
   for (int rr = 0; rr < kTR; ++rr) {
     const int r = r0 + rr;
+    const float lt = __shfl(lsum[rr][0], src);
     if (r >= N) continue;
-    const float lt = l[rr] + __shfl_xor(l[rr], 32);
+    if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
     const float inv = fast_rcp(lt);
     const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
     uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * half;
@@ -759,46 +684,104 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
 }
 
 // ---------------------------------------------------------------------------------------
-// Rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
-// reference's softmax is uniform over the N keys: o = mean_k V[r, k] (gated later, like every
-// other row).  One workgroup per row; rows with seq[r] != 0 return at once.  Keys past N hold
-// V = 0.
+// Rows the attention kernel cannot finish on its fast path, one workgroup per attention row:
+//  * rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
+//    reference's softmax is uniform over the N keys: o = mean_k V[r, k] (gated later, like
+//    every other row).  Keys past N hold V = 0.
+//  * (row, head) pairs flagged by tri_attn_kernel (a weight sum out of range): recomputed with
+//    an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from the same
+//    Q, K, V^T and bias operands, one query per thread; the flag is cleared afterwards.
+// Rows with nothing to do return at once.
 // ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void tri_masked_kernel(const TriAttnArgs a) {
+__global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
   const int r = blockIdx.x;
-  if (r >= a.N || a.seq[r] != 0) return;
-  __shared__ float mean[4 * 32];
+  if (r >= a.N) return;
   const int tid = threadIdx.x, N = a.N, NP = a.NP, H = a.H;
-  if (tid < H * 32) {
-    const int h = tid >> 5, d = tid & 31;
-    float s = 0.f;
-    for (int c16 = 0; c16 < NP / 16; ++c16)
+  // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
+  auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
+  if (a.seq[r] == 0) {
+    __shared__ float mean[4 * 32];
+    if (tid < H * 32) {
+      const int h = tid >> 5, d = tid & 31;
+      float s = 0.f;
+      for (int c16 = 0; c16 < NP / 16; ++c16)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const u32x4 v = ld16(a.vt + vl_off(r, h, H, NP, c16, hf, d));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += bflo(v[e]) + bfhi(v[e]);
+        }
+      mean[tid] = s / (float)N;
+    }
+    __syncthreads();
+    // one (query, head, lane half) per thread: 16 dims in epilogue order
+    for (int t = tid; t < N * H * 2; t += 256) {
+      const int hf = t & 1, h = (t >> 1) % H, i = (t >> 1) / H;
+      const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
+      uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack_bf2(mean[h * 32 + slot_dim(hf, kk, 2 * e)], mean[h * 32 + slot_dim(hf, kk, 2 * e + 1)]);
+        st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+      }
+    }
+    return;
+  }
+  for (int h = 0; h < H; ++h) {
+    if (a.flags[r * H + h] == 0) continue;               // same address for every thread: uniform
+    for (int i = tid; i < N; i += 256) {
+      // q.k is invariant under the common dim permutation of the Q / K layouts: dot in storage order
+      float q[32];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 v = ld16(a.q + ql_off(r, h, H, NP, i, c >> 1, c & 1));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { q[8 * c + 2 * e] = bflo(v[e]); q[8 * c + 2 * e + 1] = bfhi(v[e]); }
+      }
+      const uint16_t* brow = a.bias + ((int64_t)h * NP + i) * NP;
+      auto logit = [&](int j) {
+        float s = bf2f(brow[(j & ~63) + bias_pos64(j & 63)]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32x4 v = ld16(a.k + ql_off(r, h, H, NP, j, c >> 1, c & 1));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += q[8 * c + 2 * e] * bflo(v[e]) + q[8 * c + 2 * e + 1] * bfhi(v[e]);
+        }
+        return s;
+      };
+      float m = -INFINITY;
+      for (int j = 0; j < N; ++j) m = fmaxf(m, logit(j));
+      float l = 0.f, acc[32];
+#pragma unroll
+      for (int d = 0; d < 32; ++d) acc[d] = 0.f;
+      for (int j = 0; j < N; ++j) {
+        const float w = exp2f(logit(j) - m);
+        l += w;
+        // V^T piece of key j: chunk j/16, lane half (j/4)%2, element 4((j%16)/8) + j%4
+        const int c16 = j >> 4, hf = (j >> 2) & 1, t = 4 * ((j & 15) >> 3) + (j & 3);
+#pragma unroll
+        for (int d = 0; d < 32; ++d) acc[d] += w * bf2f(a.vt[vl_off(r, h, H, NP, c16, hf, d) + t]);
+      }
+      const float inv = 1.0f / l;
+      const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        const u32x4 v = ld16(a.vt + vl_off(r, h, H, NP, c16, hf, d));
+        uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s += bflo(v[e]) + bfhi(v[e]);
+        for (int kk = 0; kk < 2; ++kk) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = pack_bf2(acc[slot_dim(hf, kk, 2 * e)] * inv, acc[slot_dim(hf, kk, 2 * e + 1)] * inv);
+          st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+        }
       }
-    mean[tid] = s / (float)N;
-  }
-  __syncthreads();
-  // one (query, head, lane half) per thread: 16 dims in epilogue order
-  for (int t = tid; t < N * H * 2; t += 256) {
-    const int hf = t & 1, h = (t >> 1) % H, i = (t >> 1) / H;
-    const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-    uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t0 = 2 * e, t1 = 2 * e + 1;          // register 8kk + t -> dim 16kk + 8(t/4) + 4hf + t%4
-        const float m0 = mean[h * 32 + 16 * kk + 8 * (t0 >> 2) + 4 * hf + (t0 & 3)];
-        const float m1 = mean[h * 32 + 16 * kk + 8 * (t1 >> 2) + 4 * hf + (t1 & 3)];
-        w[e] = pack_bf2(m0, m1);
-      }
-      st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
     }
+    __syncthreads();                                     // every thread has read the flag
+    if (tid == 0) a.flags[r * H + h] = 0;
   }
 }
 
@@ -845,12 +828,12 @@ int persistent_groups(int items, int* items_per_wave) {
   return (waves + kPWaves - 1) / kPWaves;
 }
 
-// Mass of a 32-key half above which the attention kernel moves its reference point: 2^60, or
-// SPARSEFOLD_HIP_TRI_MASS_LIMIT (a positive finite float) so that tests can drive the rescale
+// Weight sum above which the attention kernel flags a (row, head) for the exact fix-up: 2^100,
+// or SPARSEFOLD_HIP_TRI_SUM_LIMIT (a positive finite float) so that tests can drive the fix-up
 // path with ordinary logits.  The result does not depend on it beyond rounding.
-float mass_limit() {
-  float v = 1.152921504606847e18f;
-  if (const char* e = getenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT")) {
+float sum_limit() {
+  float v = 0x1p100f;
+  if (const char* e = getenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT")) {
     const float f = strtof(e, nullptr);
     if (f > 0.f && f <= v) v = f;
   }
@@ -870,6 +853,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     fa.nrows = 4 * H * 32 + H;
     fa.w = (const uint16_t*)a->w_qkvgb; fa.ln_w = a->ln_w; fa.ln_b = a->ln_b;
     fa.wf = ws.wf; fa.off = ws.off;
+    fa.flags = ws.flags; fa.nflags = N * H;
     hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4), dim3(256), 0, st, fa);
     if (int rc = sf_check_launch("tri_fold_kernel")) return rc;
 
@@ -888,13 +872,14 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   if (stages & SF_TRI_STAGE_ATTEND) {
     TriAttnArgs aa{};
     aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
-    aa.mass_limit = mass_limit();
+    aa.sum_limit = sum_limit();
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
+    aa.flags = ws.flags;
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;
     hipLaunchKernelGGL(tri_attn_kernel, dim3(total), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
-    hipLaunchKernelGGL(tri_masked_kernel, dim3(N), dim3(256), 0, st, aa);
-    if (int rc = sf_check_launch("tri_masked_kernel")) return rc;
+    hipLaunchKernelGGL(tri_fixup_kernel, dim3(N), dim3(256), 0, st, aa);
+    if (int rc = sf_check_launch("tri_fixup_kernel")) return rc;
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
 

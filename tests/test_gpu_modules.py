@@ -64,22 +64,36 @@ def test_triangle_sharp_update_padded(transpose, N):
                     max_abs=2e-2 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("limit", ["1", "1500"])
 @pytest.mark.parametrize("transpose", [False, True])
-def test_triangle_reference_point_moves(transpose, monkeypatch):
-  """With the mass limit at 1, nearly every 32-key half after the first tile moves the attention
-  kernel's reference point (rescaling o and l, and shifting the already-issued next half of the
-  same row); the result must still match the oracle."""
+def test_triangle_exact_fixup(transpose, limit, monkeypatch):
+  """The attention kernel exponentiates logits against a fixed reference point and flags a
+  (row, head) whose weight sum leaves [2^-100, limit]; the fix-up kernel recomputes those with
+  an exact two-pass softmax.  A limit of 1 flags every row; 1500 lies near the 90th percentile
+  of the per-(row, head) maximum weight sums of this input (N=200, sharp weights), so flagged
+  and fast-path rows meet in one call.  Padded rows stay on the masked-row path.  The result
+  must match the oracle either way."""
   mod, z, seq = W.make_triangle(200, transpose=transpose, padded=True, seed=11, sharp=True)
   hip = _prepared(mod)
-  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT", raising=False)
+  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", raising=False)
   upd_default = hip(z.to(DEV), seq.to(DEV), add_residual=False)
-  monkeypatch.setenv("SPARSEFOLD_HIP_TRI_MASS_LIMIT", "1")
+  monkeypatch.setenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", limit)
   upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
-  # the moved reference points change the rounding, so the rescale path demonstrably ran
-  assert not torch.equal(upd, upd_default)
+  # the exact path keeps fp32 weights (the fast path rounds them to bf16), so the attention rows
+  # it recomputed differ from the default call: every unmasked row at limit 1, some at 1500
+  rows = (upd != upd_default).transpose(0, 1) if transpose else (upd != upd_default)
+  changed = rows.flatten(1).any(1).cpu()
+  assert not changed[~seq].any()
+  if limit == "1":
+    assert changed[seq].all()
+  else:
+    assert 0 < int(changed[seq].sum()) < int(seq.sum())
   ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
-  assert_close_bf16(upd, ref, f"triangle rescale N=200 transpose={transpose}",
+  assert_close_bf16(upd, ref, f"triangle exact fix-up N=200 limit={limit} transpose={transpose}",
                     max_abs=2e-2 * ref.abs().max().item())
+  # the flags were cleared: the next default call is the fast path again, bit for bit
+  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", raising=False)
+  assert torch.equal(hip(z.to(DEV), seq.to(DEV), add_residual=False), upd_default)
 
 
 @pytest.mark.parametrize("transpose", [False, True])
