@@ -64,6 +64,20 @@ def test_triangle_sharp_update_padded(transpose, N):
                     max_abs=2e-2 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("N,padded", [(1, False), (3, False), (11, True), (65, True), (257, False)])
+def test_triangle_edge_sizes(transpose, N, padded):
+  """Sizes at the edges of the fast path's tiling: a single token, fewer tokens than one
+  32-query block, one key past a 64-key tile (65: NP=128 with 63 padding keys), and one query
+  past a 256-query workgroup block (257)."""
+  mod, z, seq = W.make_triangle(N, transpose=transpose, padded=padded, seed=13, sharp=True)
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert torch.isfinite(upd).all()
+  assert_close_bf16(upd, ref, f"triangle N={N} transpose={transpose}", max_abs=2e-2 * ref.abs().max().item())
+
+
 @pytest.mark.parametrize("limit", ["1", "1500"])
 @pytest.mark.parametrize("transpose", [False, True])
 def test_triangle_exact_fixup(transpose, limit, monkeypatch):
