@@ -40,7 +40,9 @@
 
 namespace {
 size_t round_up(size_t x) { return (x + 255) & ~(size_t)255; }
-int round64(int n) { return (n + 63) & ~63; }
+// Padded token count of the fast path's operand layouts: a whole number of pairs of 64-key tiles,
+// so that the attention kernel's double-buffered tile pipeline starts every task in buffer 0.
+int round_np(int n) { return (n + 127) & ~127; }
 
 // ---------------------------------------------------------------------------------------
 // Operand layouts.
@@ -79,7 +81,7 @@ struct FastWs {
 };
 
 FastWs carve_fast(void* base, int32_t N, int32_t H) {
-  const size_t NP = (size_t)round64(N), E = NP * NP * H * 32;
+  const size_t NP = (size_t)round_np(N), E = NP * NP * H * 32;
   FastWs w{};
   char* p = (char*)base;
   size_t off = 0;
@@ -292,7 +294,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 // ---------------------------------------------------------------------------------------
 struct TriOutArgs {
   int64_t P;                          // N * N
-  const uint16_t* o;                  // [P, 128]
+  const uint16_t* o;                  // [4 heads][P][32]
   const uint16_t* wo;                 // [128 out, 128 in]
   const uint16_t* wg;                 // folded gate rows [128, 128]
   const float* goff;                  // [128]
@@ -328,11 +330,13 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   auto load = [&](int item, u32x4 (&xo)[8], u32x4 (&xz)[8], int64_t& p) {
     p = (int64_t)item * 32 + li;
     const bool ok = p < a.P;
-    const uint16_t* op = a.o + (ok ? p : 0) * kPC + 8 * half;
+    // o is head-major [head][P][32]: feature 16kk + 8half + 0..7 is head kk/2, dims
+    // 16(kk%2) + 8half + 0..7
+    const uint16_t* op = a.o + (ok ? p : 0) * 32 + 8 * half;
     const uint16_t* zp = a.z + (ok ? p : 0) * kPC + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      xo[kk] = ok ? ld16(op + 16 * kk) : u32x4{0, 0, 0, 0};
+      xo[kk] = ok ? ld16(op + (kk >> 1) * a.P * 32 + 16 * (kk & 1)) : u32x4{0, 0, 0, 0};
       xz[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
     }
   };
@@ -437,7 +441,7 @@ struct TriAttnArgs {
   float sum_limit;                    // weight sums outside [2^-100, sum_limit] flag the (row, head)
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
-  uint16_t* o;                        // [N][N][H][32] at pair positions, dims in epilogue order
+  uint16_t* o;                        // [H][N][N][32] head-major, dims in epilogue order
   uint8_t* flags;                     // [N][H]: 1 = recomputed exactly by tri_fixup_kernel
 };
 
@@ -471,6 +475,15 @@ struct TileLayout {
   static_assert(kChunks % kAW == 0, "tile chunks must split evenly over the waves");
 };
 
+// Task = (head, row group of 4 rows, block of 256 queries).  The grid is persistent: at most
+// one workgroup per CU (the double-buffered LDS tiles leave room for no second one), each walking
+// its tasks with the tile pipeline running straight through task boundaries -- the last tile of a
+// task loads the first tile of the next one, and the next task's Q operands are loaded while the
+// last tile computes.  With one short-lived workgroup per task the prologue (Q and first-tile
+// loads, nothing to overlap them with) and the epilogue cost 23% of the kernel.
+// Workgroup b is assumed to run on XCD b % 8 (round-robin dispatch) and takes the tasks
+// x * T/8 + b/8 + (G/8) j of XCD x's contiguous range, so the workgroups an XCD runs together
+// share one head's bias plane and neighbouring row groups' K/V tiles in its L2.
 __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) {
   using TL = TileLayout;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes];
@@ -479,46 +492,42 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
 
-  // ---- workgroup -> (head, row group, query block); XCD-major so that the workgroups an XCD
-  //      runs together share the head's bias plane and the row group's K/V tiles in its L2 ----
   const int QB = (NP + 32 * kAW - 1) / (32 * kAW), RG = NP / kTR;
-  const int total = QB * RG * H;
-  int t = blockIdx.x;
-  if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
-  const int qb = t % QB;
-  const int rg = (t / QB) % RG;
-  const int h = t / (QB * RG);
-  const int r0 = rg * kTR;
-  const int i = qb * 32 * kAW + 32 * wave + li;     // this lane's query
-  const int iq = min(i, NP - 1);                    // operand row for loads (results of i >= N unused)
-  const bool active = qb * 32 * kAW + 32 * wave < NP;   // uniform: the wave has queries below NP
+  const int per = QB * RG * H / 8;                  // tasks per XCD (RG is a multiple of 16)
+  const int xcd = blockIdx.x & 7, G8 = gridDim.x >> 3;
+  int task = blockIdx.x >> 3;                       // index within the XCD's range
+  if (task >= per) return;                          // uniform over the workgroup
+  auto decode = [&](int tl, int& r0, int& h, int& qb) __attribute__((always_inline)) {
+    const int t = xcd * per + tl;
+    qb = t % QB;
+    r0 = ((t / QB) % RG) * kTR;
+    h = t / (QB * RG);
+  };
 
-  // ---- tile loader: this wave's 1 KB chunks of the next tile, straight into LDS.  K and V^T
-  //      chunks are 1 KB of contiguous memory; bias chunks are 8 query rows of 128 bytes.
-  //      Every chunk address is a wave-uniform base plus one of two per-lane offsets. ----
+  // ---- tile loader: this wave's 1 KB chunks of a tile, straight into LDS.  K and V^T chunks
+  //      are 1 KB of contiguous memory; bias chunks are 8 query rows of 128 bytes.  Every chunk
+  //      address is a wave-uniform base plus one of two per-lane offsets. ----
   const int64_t rstride = (int64_t)H * NP * 32;             // row stride of the Q/K/G and V^T layouts
-  const uint16_t* kbase = a.k + ql_off(r0, h, H, NP, 0, 0, 0);
-  const uint16_t* vbase = a.vt + vl_off(r0, h, H, NP, 0, 0, 0);
-  const uint16_t* bbase = a.bias + (int64_t)h * NP * NP;
   const uint32_t lane16 = (uint32_t)lane * 16u;             // byte offsets: K / V^T chunks ...
   const uint32_t roffb = (uint32_t)((lane & 7) * NP + 8 * (lane >> 3)) * 2u;   // ... bias: row L%8, piece L/8
   // Waves 0-1 fetch K (rows 2w, 2w+1), waves 2-3 V^T (rows 2(w-2), 2(w-2)+1), waves 4-7 the bias
   // rows of queries 64(w-4) .. +63 of the block; chunk u of a wave is then a uniform base plus
   // a compile-time multiple of the wave's two strides.
-  const char* wsrc;
-  int64_t wrow;                          // bytes between the wave's chunks 4 apart (K / V^T rows)
-  int wq, wj, wlim;                      // bytes per quarter / per key; bias: last chunk row offset
-  uint32_t woff;
-  if (wave < 4) {
-    const uint16_t* b0 = wave < 2 ? kbase + 2 * wave * rstride : vbase + 2 * (wave - 2) * rstride;
-    wsrc = (const char*)b0; wrow = rstride * 2; wq = 1024; wj = 64; wlim = 0; woff = lane16;
-  } else {
+  const int64_t wrow = wave < 4 ? rstride * 2 : 0;          // bytes between chunks 4 apart (K / V^T rows)
+  const int wq = wave < 4 ? 1024 : 16 * NP;                 // bytes per quarter (K / V^T) or 8 bias rows
+  const int wj = wave < 4 ? 64 : 2;                         // bytes per key
+  const uint32_t woff = wave < 4 ? lane16 : roffb;
+  auto loader_src = [&](int r0, int h, int qb, int& wlim) __attribute__((always_inline)) -> const char* {
+    if (wave < 4) {
+      wlim = 0;
+      return wave < 2 ? (const char*)(a.k + ql_off(r0 + 2 * wave, h, H, NP, 0, 0, 0))
+                      : (const char*)(a.vt + vl_off(r0 + 2 * (wave - 2), h, H, NP, 0, 0, 0));
+    }
     const int q0 = qb * 32 * kAW + (wave - 4) * 64;
-    wsrc = (const char*)(bbase + (int64_t)q0 * NP); wrow = 0; wq = 16 * NP; wj = 2;
     wlim = NP - 8 - q0;                  // query rows past NP - 8 are clamped (idle waves only)
-    woff = roffb;
-  }
-  auto load_tile = [&](int j0, int buf) __attribute__((always_inline)) {
+    return (const char*)(a.bias + ((int64_t)h * NP + q0) * NP);
+  };
+  auto load_tile = [&](const char* wsrc, int wlim, int j0, int buf) __attribute__((always_inline)) {
     const char* src = wsrc + (int64_t)j0 * wj;
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerWave; ++u) {
@@ -538,14 +547,16 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     return smem + TL::kBiasBase + buf * TL::kBBytes + (row >> 3) * 1024 + pc * 128 + (row & 7) * 16;
   };
 
-  // Q operands (B of S^T = K Q^T) for the 4 rows.  Rows past N hold zeros and are never stored.
-  const int qlane = (int)(ql_off(0, 0, H, NP, iq, 0, half));   // lane offset within a (row, head)
-  const uint16_t* qbase = a.q + ql_off(r0, h, H, NP, 0, 0, 0);
+  // Q operands (B of S^T = K Q^T) of a task's 4 rows.  Rows past N hold zeros and are never stored.
   bf16x8 qb8[kTR][2];
+  auto load_q = [&](int r0, int h, int qb, bf16x8 (&qd)[kTR][2]) __attribute__((always_inline)) {
+    const int iq = min(qb * 32 * kAW + 32 * wave + li, NP - 1);   // operand row (results of i >= N unused)
+    const uint16_t* qbase = a.q + ql_off(r0, h, H, NP, iq, 0, half);
 #pragma unroll
-  for (int rr = 0; rr < kTR; ++rr)
+    for (int rr = 0; rr < kTR; ++rr)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + qlane + kk * 512));
+      for (int kk = 0; kk < 2; ++kk) qd[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + kk * 512));
+  };
   // Softmax against a fixed reference point of 0: the logits (log2 units, q carries
   // scale * log2 e) are exponentiated as they come out of the S^T MFMA, with no running maximum
   // and no rescaling of o.  Logits of realistic inputs lie far inside the range where that is
@@ -555,13 +566,6 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   // 2^100 cannot overflow, and o = sum_k w_k v_k stays finite for any bf16 v of moderate size.
   f32x16 o[kTR];
   f32x4 lsum[kTR];
-#pragma unroll
-  for (int rr = 0; rr < kTR; ++rr) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[rr][e] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) lsum[rr][e] = 0.f;
-  }
   // Row sums on the matrix core: a 16x16x32 MFMA whose B operand is the P^T chunk of the P.V
   // MFMA (lane l: query l%32, keys of lane group l/16) and whose A operand selects lane groups
   // {0, 2} into output rows 0..7 and {1, 3} into rows 8..15.  Output (m, n) is then the sum over
@@ -607,7 +611,11 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   // The scheduling fences keep the compiler from sinking those reads to their uses (which
   // exposed the LDS latency every unit) and from hoisting unit u+1's S^T MFMAs away from the
   // exponentials they overlap.
-  auto units = [&](int buf) __attribute__((always_inline)) {
+  // RELOAD (the last tile of a task): row rr's Q operands are replaced by the next task's (nq:
+  // this lane's Q of that task) as soon as the S^T MFMA of unit 2rr+1 -- their last use -- has
+  // been issued, so that those loads have most of a tile to land.
+  auto units = [&](int buf, auto reloadc, const uint16_t* nq) __attribute__((always_inline)) {
+    constexpr bool RELOAD = decltype(reloadc)::value;
     f32x16 sc, sn;
     bf16x8 kr[2], vr[2];
     load_k(0, 0, buf, kr);
@@ -619,6 +627,10 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       const int rr = u >> 1;
       if (u + 1 < 2 * kTR) qk((u + 1) >> 1, (u + 1) & 1, kr, sn);
       if (u + 2 < 2 * kTR) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
+      if (RELOAD && (u & 1) == 0) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(nq + rr * rstride + kk * 512));
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -639,48 +651,105 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   };
 
   const int ntiles = NP / kKT;
-  load_tile(0, 0);
+  const int q32 = lane & 31;
+  const int src_lane = q32 < 16 ? q32 : q32 + 16;   // a lane whose row-sum output holds query q32
+  int r0, h, qb, wlim;
+  decode(task, r0, h, qb);
+  const char* wsrc = loader_src(r0, h, qb, wlim);
+  load_tile(wsrc, wlim, 0, 0);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
-  // buffer index is a compile-time constant inside each half of the pair
-  auto tile_step = [&](int tt, auto bufc) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    if (tt + 1 < ntiles) load_tile((tt + 1) * kKT, buf ^ 1);   // lands while this tile computes
-    if (active) {
-      load_bias(buf);
-      units(buf);
+  load_q(r0, h, qb, qb8);
+  bool qready = true;                                      // qb8 holds this task's Q operands (uniform)
+  for (;;) {
+    const int next = task + G8;
+    const bool has_next = next < per;                      // uniform
+    int nr0 = 0, nh = 0, nqb = 0, nwlim = 0;
+    const char* nsrc = nullptr;
+    if (has_next) {
+      decode(next, nr0, nh, nqb);
+      nsrc = loader_src(nr0, nh, nqb, nwlim);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  };
-  for (int tt = 0; tt < ntiles; tt += 2) {
-    tile_step(tt, std::integral_constant<int, 0>{});
-    if (tt + 1 < ntiles) tile_step(tt + 1, std::integral_constant<int, 1>{});
-  }
+    const int i = qb * 32 * kAW + 32 * wave + li;          // this lane's query
+    const bool active = qb * 32 * kAW + 32 * wave < NP;    // uniform: the wave has queries below NP
+#pragma unroll
+    for (int rr = 0; rr < kTR; ++rr) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[rr][e] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lsum[rr][e] = 0.f;
+    }
+    // One tile: the loads of the tile after it (or of the next task's first tile) are issued
+    // first and land while it computes.  The first and last tiles of a task are separate code
+    // instances: the last one loads the next task's Q operands (into the registers of rows it has
+    // finished with), the first one waits for them -- with a wait the compiler sees, so that it
+    // puts no conservative wait of its own in front of the first S^T MFMA, where it would also
+    // wait for the tile loads just issued.  A plain __syncthreads would also wait for the Q loads
+    // at the end of the last tile.
+    // this lane's Q operands of the next task (of this task again on the last one: a harmless reload)
+    const uint16_t* nq = has_next ? a.q + ql_off(nr0, nh, H, NP, min(nqb * 32 * kAW + 32 * wave + li, NP - 1), 0, half)
+                                  : a.q + ql_off(r0, h, H, NP, min(qb * 32 * kAW + 32 * wave + li, NP - 1), 0, half);
+    auto tile = [&](int tt, auto firstc, auto lastc, auto bufc) __attribute__((always_inline)) {
+      constexpr bool FIRST = decltype(firstc)::value, LAST = decltype(lastc)::value;
+      constexpr int buf = decltype(bufc)::value;             // compile-time: the compiler then
+                                                             // sees that no LDS read of this tile
+                                                             // aliases the loads into the other
+      if (FIRST) {
+        if (!qready) load_q(r0, h, qb, qb8);
+        __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0): this task's Q operands
+      }
+      // the tile after this one; after the last tile, the next task's first tile (the last task
+      // loads its own first tile again: unused, but the code stays branch-free)
+      if (!LAST) load_tile(wsrc, wlim, (tt + 1) * kKT, buf ^ 1);
+      else load_tile(has_next ? nsrc : wsrc, has_next ? nwlim : wlim, 0, buf ^ 1);
+      if (active) {                                          // (idle waves need no Q operands)
+        load_bias(buf);
+        units(buf, lastc, nq);
+      }
+      // tile loads landed (the 8 Q loads of the last tile, the youngest, may stay in flight;
+      // idle waves issued none and wait for everything)
+      if (LAST && active) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    // ntiles is even: every task starts in buffer 0 and ends in buffer 1
+    using F = std::false_type; using T = std::true_type;
+    using B0 = std::integral_constant<int, 0>; using B1 = std::integral_constant<int, 1>;
+    tile(0, T{}, F{}, B0{});
+    for (int tt = 1; tt + 1 < ntiles; tt += 2) {
+      tile(tt, F{}, F{}, B1{});
+      tile(tt + 1, F{}, F{}, B0{});
+    }
+    tile(ntiles - 1, F{}, T{}, B1{});
+    qready = active;                 // an idle wave loaded no Q operands for the next task
 
-  // ---- epilogue: normalise and store at the pair position (the gate is applied by the
-  //      output kernel, which recomputes it from z) ----
-  if (i >= N) return;
-  const int q32 = lane & 31;
-  const int src = q32 < 16 ? q32 : q32 + 16;         // a lane whose row-sum output holds query q32
+    // ---- epilogue: normalise and store at the pair position (the gate is applied by the
+    //      output kernel, which recomputes it from z) ----
+    if (i < N) {
 #pragma unroll
-  for (int rr = 0; rr < kTR; ++rr) {
-    const int r = r0 + rr;
-    const float lt = __shfl(lsum[rr][0], src);
-    if (r >= N) continue;
-    if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
-    const float inv = fast_rcp(lt);
-    const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-    uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * half;
+      for (int rr = 0; rr < kTR; ++rr) {
+        const int r = r0 + rr;
+        const float lt = __shfl(lsum[rr][0], src_lane);
+        if (r >= N) continue;
+        if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
+        const float inv = fast_rcp(lt);
+        const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
+        uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * half;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      uint32_t w[4];
+        for (int kk = 0; kk < 2; ++kk) {
+          uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
-      st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+          for (int e = 0; e < 4; ++e)
+            w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
+          st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+        }
+      }
     }
+    if (!has_next) break;
+    task = next; r0 = nr0; h = nh; qb = nqb; wsrc = nsrc; wlim = nwlim;
   }
+  __builtin_amdgcn_s_waitcnt(0);                           // the last task's Q reloads
 }
 
 // ---------------------------------------------------------------------------------------
@@ -718,7 +787,7 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
     for (int t = tid; t < N * H * 2; t += 256) {
       const int hf = t & 1, h = (t >> 1) % H, i = (t >> 1) / H;
       const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-      uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
+      uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * hf;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         uint32_t w[4];
@@ -769,7 +838,7 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
       const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        uint16_t* op = a.o + ((int64_t)za * N + zb) * (H * 32) + h * 32 + 16 * hf;
+        uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * hf;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           uint32_t w[4];
@@ -847,7 +916,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     sf_set_error("triangle: workspace too small (%zu < %zu bytes)", workspace_bytes, ws.bytes);
     return 1;
   }
-  const int NP = round64(N);
+  const int NP = round_np(N);
   if (stages & SF_TRI_STAGE_PROJECT) {
     TriFoldArgs fa{};
     fa.nrows = 4 * H * 32 + H;
@@ -875,8 +944,8 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     aa.sum_limit = sum_limit();
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     aa.flags = ws.flags;
-    const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;
-    hipLaunchKernelGGL(tri_attn_kernel, dim3(total), dim3(64 * kAW), 0, st, aa);
+    const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;   // a multiple of 64
+    hipLaunchKernelGGL(tri_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
     hipLaunchKernelGGL(tri_fixup_kernel, dim3(N), dim3(256), 0, st, aa);
     if (int rc = sf_check_launch("tri_fixup_kernel")) return rc;
