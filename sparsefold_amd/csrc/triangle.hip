@@ -769,23 +769,40 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
   // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
   if (a.seq[r] == 0) {
+    // sum over the keys: thread (part, head, dim), part p of the 16-key chunks; four loads in
+    // flight per thread (H * 32 = 128 on this path)
+    __shared__ float part[2][4 * 32];
     __shared__ float mean[4 * 32];
-    if (tid < H * 32) {
-      const int h = tid >> 5, d = tid & 31;
-      float s = 0.f;
-      for (int c16 = 0; c16 < NP / 16; ++c16)
+    {
+      const int hd = tid & 127, h = hd >> 5, d = hd & 31, pp = tid >> 7;
+      const int nc = NP / 16, c0 = pp * (nc / 2), c1 = pp ? nc : nc / 2;
+      float s0 = 0.f, s1 = 0.f;
+      int c16 = c0;
+      for (; c16 + 2 <= c1; c16 += 2) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ld16(a.vt + vl_off(r, h, H, NP, c16 + (u >> 1), u & 1, d));
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
+      }
+      for (; c16 < c1; ++c16)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const u32x4 v = ld16(a.vt + vl_off(r, h, H, NP, c16, hf, d));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s += bflo(v[e]) + bfhi(v[e]);
+          for (int e = 0; e < 4; ++e) { s0 += bflo(v[e]); s1 += bfhi(v[e]); }
         }
-      mean[tid] = s / (float)N;
+      part[pp][hd] = s0 + s1;
     }
     __syncthreads();
-    // one (query, head, lane half) per thread: 16 dims in epilogue order
+    if (tid < 128) mean[tid] = (part[0][tid] + part[1][tid]) / (float)N;
+    __syncthreads();
+    // one (query, head, lane half) per thread: 16 dims in epilogue order; consecutive threads
+    // write consecutive positions of one head's plane
     for (int t = tid; t < N * H * 2; t += 256) {
-      const int hf = t & 1, h = (t >> 1) % H, i = (t >> 1) / H;
+      const int hf = t & 1, i = (t >> 1) % N, h = (t >> 1) / N;
       const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
       uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * hf;
 #pragma unroll
