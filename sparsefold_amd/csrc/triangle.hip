@@ -148,10 +148,21 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
 
-  for (int t = tid; t < kProjBlocks * 32 * (kPC / 8); t += 64 * kPWaves) {
-    const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+  // every load is issued before the first LDS store: one memory latency for the whole staging
+  // (a loop of load, wait, store paid it 13 times per workgroup)
+  constexpr int kStage = kProjBlocks * 32 * (kPC / 8) / (64 * kPWaves);
+  static_assert(kProjBlocks * 32 * (kPC / 8) % (64 * kPWaves) == 0, "whole staging rounds");
+  u32x4 wst[kStage];
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int t = tid + j * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
     const int src = n < 12 * 32 ? n : n + 4 * 32;      // LDS block 12 <- folded block 16
-    st16(&sW[n * kWP + c8], ld16(a.wf + (int64_t)src * kPC + c8));
+    wst[j] = ld16(a.wf + (int64_t)src * kPC + c8);
+  }
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int t = tid + j * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    st16(&sW[n * kWP + c8], wst[j]);
   }
   for (int n = tid; n < kProjBlocks * 32; n += 64 * kPWaves) sOff[n] = a.off[n < 12 * 32 ? n : n + 4 * 32];
   __syncthreads();
@@ -312,16 +323,27 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   uint16_t* const so = sOut[wave];
-  for (int t = tid; t < kPC * (kPC / 8); t += 64 * kPWaves) {
-    const int n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+  // all loads first, then the LDS stores: one memory latency for the staging
+  constexpr int kStage = kPC * (kPC / 8) / (64 * kPWaves);
+  static_assert(kPC * (kPC / 8) % (64 * kPWaves) == 0, "whole staging rounds");
+  u32x2 wlo[kStage], whi[kStage];
+  u32x4 gst[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
     // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
     // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head
     const int hd = c8 & ~31, hf = (c8 >> 4) & 1, j = (c8 >> 3) & 1;
     const uint16_t* src = a.wo + (int64_t)n * kPC + hd + 16 * j + 4 * hf;
-    const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
-    const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
-    st16(&sW[n * kWP + c8], u32x4{lo[0], lo[1], hi[0], hi[1]});
-    st16(&sG[n * kWP + c8], ld16(a.wg + (int64_t)n * kPC + c8));
+    wlo[u] = *reinterpret_cast<const u32x2*>(src);
+    whi[u] = *reinterpret_cast<const u32x2*>(src + 8);
+    gst[u] = ld16(a.wg + (int64_t)n * kPC + c8);
+  }
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    st16(&sW[n * kWP + c8], u32x4{wlo[u][0], wlo[u][1], whi[u][0], whi[u][1]});
+    st16(&sG[n * kWP + c8], gst[u]);
   }
   for (int n = tid; n < kPC; n += 64 * kPWaves) sGoff[n] = a.goff[n];
   __syncthreads();
@@ -702,6 +724,9 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       // loads its own first tile again: unused, but the code stays branch-free)
       if (!LAST) load_tile(wsrc, wlim, (tt + 1) * kKT, buf ^ 1);
       else load_tile(has_next ? nsrc : wsrc, has_next ? nwlim : wlim, 0, buf ^ 1);
+      // the Q reloads below must stay younger than these tile loads (the vmcnt(8) wait at the
+      // end of the last tile counts on it): no memory operation crosses this point
+      if (LAST) asm volatile("" ::: "memory");
       if (active) {                                          // (idle waves need no Q operands)
         load_bias(buf);
         units(buf, lastc, nq);
