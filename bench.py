@@ -165,6 +165,30 @@ def _config_builders() -> dict:
         "ms_per_call": round(t, 4), "ms_24_blocks": round(24 * t, 3), "tflops": round(flop / t / 1e9, 1),
         "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
 
+  def c4_stack():  # the 24 attention blocks of the diffusion Transformer, 5 samples x N=1024: every
+    # block's AdaLN conditioning in one call, then the 24 blocks on their precomputed layers
+    # (transition blocks are not part of this library).  One block's weights serve all 24 layers.
+    from sparsefold_amd.backends.hip import ops as HO
+    S, n, c, sc, h, d, L = 5, 1024, 768, 384, 16, 48, 24
+    mod, act, cond, bias, mask = W.make_diffusion(n, S=S, seed=4)
+    mod = mod.to(dev); backends.prepare(mod)
+    act, cond, bias, mask = act.to(dev), cond.to(dev), bias.to(dev), mask.to(dev)
+    stacked = (mod._hip_ada_lnc_w.repeat(L, 1), mod._hip_ada_w_scale.repeat(L, 1), mod._hip_ada_b_scale.repeat(L),
+               mod._hip_ada_w_shift.repeat(L, 1), mod._hip_w_zc.repeat(L, 1), mod._hip_b_zc.repeat(L))
+    flop = L * (2 * n * sc * 2 * c + 2 * S * n * c * 4 * c + 4 * h * n * n * d * S + 2 * S * n * c * c
+                + 2 * n * sc * c)
+
+    def call():
+      scale, shift, zgate = HO.diffusion_conditioning(cond, *stacked)
+      x = act
+      for layer in range(L):
+        x = mod(x, mask, pair_logits=bias, adaptive_scale=scale[layer], adaptive_bias=shift[layer],
+                zero_gate=zgate[layer])
+      return x
+    return call, (lambda t: {
+        "ms_per_block": round(t / L, 4), "ms_24_blocks": round(t, 3), "tflops": round(flop / t / 1e9, 1),
+        "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+
   def c5():    # windowed atom attention, 5 samples x 8192 atoms, 32-query / 128-key windows
     S, atoms, c, h, d = 5, 8192, 128, 4, 32
     mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5)
@@ -199,7 +223,8 @@ def _config_builders() -> dict:
         "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
 
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
-          "single_n768": c3b, "diffusion_5x1024_block": c4, "window_5x8192": c5,
+          "single_n768": c3b, "diffusion_5x1024_block": c4,
+          "diffusion_5x1024_24_blocks": c4_stack, "window_5x8192": c5,
           "transformer_pack_n1024": pack_tr, "cross_pack_8192": pack_x}
 
 
@@ -212,8 +237,8 @@ def other_configs(iters: int) -> dict:
   res = {}
   for name, build in _config_builders().items():
     call, metrics = build()
-    res[name] = metrics(_time_call(call, iters))
-    if "pack" not in name:
+    res[name] = metrics(_time_call(call, iters if "24_blocks" not in name else max(iters // 8, 5)))
+    if "pack" not in name and "24_blocks" not in name:
       config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda", hip_graphs=True)
       try:
         res[name]["ms_per_call_hip_graphs"] = round(_time_call(call, iters), 4)

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 3
+#define SF_HIP_ABI_VERSION 4
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -232,6 +232,11 @@ typedef struct sf_self_attention_args {
   const void* w_t2;                             /* bf16 [C, H*D] */
   const void* w_zc; const float* b_zc;          /* bf16 [C, Cs], f32 [C] (condition only) */
   void* out;                                    /* bf16 [S, N, C] */
+  /* Precomputed conditioning of this layer (one layer's columns of the
+   * sf_hip_diffusion_conditioning_fwd outputs), or NULL: bf16 [N, C] each, row stride pre_rs.
+   * When pre_scale is given, h = pre_scale * LN(x) + pre_shift and the output multiplier is
+   * pre_zgate; cond, lnc_*, w_scale, b_scale, w_shift, w_zc and b_zc are not read. */
+  const void* pre_scale; const void* pre_shift; const void* pre_zgate; int64_t pre_rs;
 } sf_self_attention_args;
 
 size_t sf_hip_self_attention_workspace_bytes(const sf_self_attention_args* a);
@@ -269,6 +274,38 @@ typedef struct sf_cross_attention_args {
 size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a);
 int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* AdaLN conditioning of L conditioned layers in one call -- the diffusion Transformer's
+ * per-layer scale, shift and zero-gate from one shared condition, computed once per Transformer
+ * call instead of once per block.  Replaces diffusion_conditioning_packed
+ * (backends/vecops/kernels/registry.py:720-760, DiffusionConditioning.cpp:78-222), which the
+ * native Transformer calls once per super-block (backends/vecops/modules.py:1083-1092,1151);
+ * Transformer.forward hands the same single_cond to every block (transformer.py:452-463).
+ * For layer l (transformer.py:80-96 AdaLN, :138-154 AdaLN-zero):
+ *   scale_l = sigmoid(LN(c) * lnc_w[l] W_scale,l^T + b_scale,l)
+ *   shift_l = LN(c) * lnc_w[l] W_shift,l^T
+ *   zgate_l = sigmoid(c W_zc,l^T + b_zc,l)
+ * cond bf16 [rows, Cs]; lnc_w f32 [L, Cs] (the condition LayerNorm has no bias,
+ * transformer.py:56-59); weights bf16 [L*C, Cs] (layer l = rows [l*C, (l+1)*C), each the
+ * layer's [C, Cs] K-contiguous form); b_scale, b_zc f32 [L*C].  Outputs bf16 [rows, L*C] with
+ * row stride out_rs >= L*C: layer l in columns [l*C, (l+1)*C).  scale and zgate hold values
+ * after the sigmoid (the reference stores them before it and applies it in the block).
+ * LN(c) is computed once and lnc_w is folded into the weights, (LN(c) * g) W^T = LN(c) (W * g)^T,
+ * so each output is one GEMM of M = rows, N = L*C, K = Cs.  Cs % 8 == 0, Cs <= 2048. */
+typedef struct sf_diffusion_conditioning_args {
+  int64_t rows; int32_t L, C, Cs;
+  const void* cond;                             /* bf16 [rows, Cs] */
+  const float* lnc_w;                           /* f32 [L, Cs] */
+  const void* w_scale; const float* b_scale;    /* bf16 [L*C, Cs], f32 [L*C] or NULL */
+  const void* w_shift;                          /* bf16 [L*C, Cs] */
+  const void* w_zc; const float* b_zc;          /* bf16 [L*C, Cs], f32 [L*C] or NULL */
+  void* scale; void* shift; void* zgate;        /* bf16 [rows, L*C], row stride out_rs */
+  int64_t out_rs;
+} sf_diffusion_conditioning_args;
+
+size_t sf_hip_diffusion_conditioning_workspace_bytes(const sf_diffusion_conditioning_args* a);
+int sf_hip_diffusion_conditioning_fwd(const sf_diffusion_conditioning_args* a, void* workspace,
+                                      size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -94,6 +94,7 @@ class SelfAttentionArgs(C.Structure):
       ("w_scale", _vp), ("b_scale", _vp), ("w_shift", _vp),
       ("w_qkvg", _vp), ("b_qkvg", _vp), ("w_t2", _vp), ("w_zc", _vp), ("b_zc", _vp),
       ("out", _vp),
+      ("pre_scale", _vp), ("pre_shift", _vp), ("pre_zgate", _vp), ("pre_rs", _i64),
   ]
 
 
@@ -110,6 +111,14 @@ class CrossAttentionArgs(C.Structure):
   ]
 
 
+class DiffusionConditioningArgs(C.Structure):
+  _fields_ = [
+      ("rows", _i64), ("L", _i32), ("C", _i32), ("Cs", _i32),
+      ("cond", _vp), ("lnc_w", _vp), ("w_scale", _vp), ("b_scale", _vp), ("w_shift", _vp),
+      ("w_zc", _vp), ("b_zc", _vp), ("scale", _vp), ("shift", _vp), ("zgate", _vp), ("out_rs", _i64),
+  ]
+
+
 STRUCTS = {
     "sf_attention_args": AttentionArgs,
     "sf_layer_norm_args": LayerNormArgs,
@@ -119,6 +128,7 @@ STRUCTS = {
     "sf_window_gather_args": WindowGatherArgs,
     "sf_self_attention_args": SelfAttentionArgs,
     "sf_cross_attention_args": CrossAttentionArgs,
+    "sf_diffusion_conditioning_args": DiffusionConditioningArgs,
 }
 
 # (name, restype, argtypes) of every exported entry point.
@@ -137,6 +147,8 @@ SIGNATURES = [
     ("sf_hip_self_attention_fwd", C.c_int, [C.POINTER(SelfAttentionArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_cross_attention_workspace_bytes", C.c_size_t, [C.POINTER(CrossAttentionArgs)]),
     ("sf_hip_cross_attention_fwd", C.c_int, [C.POINTER(CrossAttentionArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_diffusion_conditioning_workspace_bytes", C.c_size_t, [C.POINTER(DiffusionConditioningArgs)]),
+    ("sf_hip_diffusion_conditioning_fwd", C.c_int, [C.POINTER(DiffusionConditioningArgs), _vp, C.c_size_t, _vp]),
 ]
 
 _lib: C.CDLL | None = None

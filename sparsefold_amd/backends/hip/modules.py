@@ -15,12 +15,15 @@ Replaced reference forwards:
                                      gathers the key windows (transformer.py:671-673)
 * ``SingleActUpdateHip.forward``     blocks.py:739-763 (attention half)
 * ``TransformerHipMixin``            transformer.py:430-447 -- the cached pair-logit pack
-                                     ``[n_super, super_block, H, N, N]`` in one pass over pair_cond
+                                     ``[n_super, super_block, H, N, N]`` in one pass over pair_cond;
+                                     with condition-only HIP attention blocks, also every block's
+                                     AdaLN conditioning in one call before the block loop (the
+                                     native Transformer's, backends/vecops/modules.py:1093-1183)
 * ``CrossAttTransformerHipMixin``    transformer.py:655-666 -- the cached pack
                                      ``[num_blocks, U, H, Q, K]``, written in that layout directly
-The two Transformer mixins keep the reference ``forward`` (block loop, transitions) and only
-replace the factory of its ``ValueCache`` entry ``"pair_logits"``, so cache keys and
-``enable_cache`` behave as in the reference.
+The pair-logit pack replaces only the factory of the ``ValueCache`` entry ``"pair_logits"``, so
+cache keys and ``enable_cache`` behave as in the reference; the transition blocks always run as
+they are.
 """
 from __future__ import annotations
 
@@ -175,24 +178,42 @@ class SelfAttentionHipMixin:
   @_require_native_preparation
   @graphs.graphed
   def forward(self, x: torch.Tensor, mask: torch.Tensor, *, pair_logits: torch.Tensor | None = None,
-              single_cond: torch.Tensor | None = None, add_residual: bool = True) -> torch.Tensor:
+              single_cond: torch.Tensor | None = None, add_residual: bool = True,
+              adaptive_scale: torch.Tensor | None = None, adaptive_bias: torch.Tensor | None = None,
+              zero_gate: torch.Tensor | None = None) -> torch.Tensor:
+    """``adaptive_scale`` / ``adaptive_bias`` / ``zero_gate`` ``[N, C]``: this layer's precomputed
+    conditioning (``TransformerHipMixin.diffusion_conditioning``; the reference's
+    ``forward_prepared``, backends/vecops/modules.py:1171-1176), used in place of ``single_cond``."""
     H, D = self.num_head, self.key_dim
     HD = H * D
     lead, N = x.shape[:-2], x.shape[-2]
     S = x.numel() // max(N * x.shape[-1], 1)
+    pre = None
+    if adaptive_scale is not None:
+      pre = (adaptive_scale, adaptive_bias, zero_gate)
+      assert all(t is not None for t in pre), "adaptive_scale, adaptive_bias and zero_gate go together"
     native = (mask is None or tuple(mask.shape) == (N,)) and \
         (pair_logits is None or tuple(pair_logits.shape) in {(H, N, N), (S, H, N, N)}) and \
         (single_cond is None or (single_cond.dim() == 2 and single_cond.shape[0] == N)) and \
-        (single_cond is not None or hasattr(self, "_hip_ada_ln_w"))
+        (single_cond is not None or pre is not None or hasattr(self, "_hip_ada_ln_w")) and \
+        (pre is None or all(tuple(t.shape) == (N, x.shape[-1]) and t.stride(-1) == 1 and
+                            t.stride(0) == adaptive_scale.stride(0) for t in pre))
     if native:                                        # the whole module in one library call
-      out = ops.self_attention_module(x, mask, pair_logits, single_cond, self._native_weights(), num_head=H,
-                                      head_dim=D, add_residual=add_residual)
+      out = ops.self_attention_module(x, mask, pair_logits, None if pre else single_cond, self._native_weights(),
+                                      num_head=H, head_dim=D, add_residual=add_residual, pre=pre)
       return out.to(x.dtype)
-    xh = _adaln(self, "_hip_ada_", x, single_cond)
+    if pre is not None:
+      xh = ops.layer_norm(x, scale=adaptive_scale.reshape(-1, adaptive_scale.shape[-1]),
+                          shift=adaptive_bias.reshape(-1, adaptive_bias.shape[-1]))
+    else:
+      xh = _adaln(self, "_hip_ada_", x, single_cond)
     y = ops.linear(xh, self._hip_w_qkvg, self._hip_b_qkvg)              # [..., N, 4HD]
     q, k, v, g = (y[..., i * HD:(i + 1) * HD].unflatten(-1, (H, D)) for i in range(4))
     o = dot_product_attention(q, k, v, mask_k=mask, bias=pair_logits, gate=g)
     o = o.reshape(*lead, N, HD)
+    if pre is not None:
+      return ops.linear(o, self._hip_w_t2, mul=zero_gate.reshape(-1, zero_gate.shape[-1]),
+                        residual=x if add_residual else None).to(x.dtype)
     return _zero_init_residual(self, o, single_cond, x if add_residual else None).to(x.dtype)
 
 
@@ -367,8 +388,51 @@ class TransformerHipMixin:
     _buf(self, "_hip_pack_ln_b", _f32(getattr(self.pair_input_layer_norm, "bias", None)))
     self._hip_pack_shape = (len(projections),) + tuple(projections[0].weight.shape[1:])
     _prepare_hip_children(self)
+    self._prepare_conditioning()
     self._native_prepared = True
     return True
+
+  def _attention_layers(self) -> list | None:
+    """The SelfAttention blocks in call order (super-block, block), or None when the stacks are
+    not [super-block][block] containers of prepared, condition-only HIP blocks."""
+    try:
+      layers = [[a for a in sb] for sb in self.self_attention]
+      trans = [[t for t in sb] for sb in self.transition_block]
+    except (AttributeError, TypeError):
+      return None
+    if [len(x) for x in layers] != [len(x) for x in trans]:
+      return None
+    flat = [a for sb in layers for a in sb]
+    ok = bool(flat) and all(isinstance(a, SelfAttentionHipMixin) and getattr(a, "_hip_ada_lnc_w", None) is not None
+                            and getattr(a, "_hip_ada_lnc_b", None) is None and getattr(a, "_hip_w_zc", None) is not None
+                            for a in flat)
+    return flat if ok else None
+
+  def _prepare_conditioning(self) -> None:
+    """Stacks every block's AdaLN / AdaLN-zero condition weights so one call conditions them all
+    (the reference packs them per super-block, backends/vecops/modules.py:1040-1081)."""
+    self._hip_dc = None
+    flat = self._attention_layers()
+    if flat is None:
+      return
+    zeros = lambda a: torch.zeros(a._hip_ada_w_scale.shape[0], dtype=torch.float32, device=a._hip_ada_w_scale.device)
+    self._hip_dc = {
+        "lnc_w": torch.stack([a._hip_ada_lnc_w for a in flat]).contiguous(),
+        "w_scale": torch.cat([a._hip_ada_w_scale for a in flat]).contiguous(),
+        "b_scale": torch.cat([a._hip_ada_b_scale if a._hip_ada_b_scale is not None else zeros(a) for a in flat]),
+        "w_shift": torch.cat([a._hip_ada_w_shift for a in flat]).contiguous(),
+        "w_zc": torch.cat([a._hip_w_zc for a in flat]).contiguous(),
+        "b_zc": torch.cat([a._hip_b_zc if a._hip_b_zc is not None else zeros(a) for a in flat]),
+    }
+
+  @_require_native_preparation
+  def diffusion_conditioning(self, single_cond: torch.Tensor):
+    """Every block's AdaLN scale, shift and AdaLN-zero gate from ``single_cond [N, Cs]`` in one
+    call: (scale, shift, zgate), each ``[L, N, C]`` (L = number of blocks; scale and zgate after
+    the sigmoid).  The reference computes them per super-block (DiffusionConditioning.cpp)."""
+    d = self._hip_dc
+    return ops.diffusion_conditioning(single_cond, d["lnc_w"], d["w_scale"], d["b_scale"], d["w_shift"],
+                                      d["w_zc"], d["b_zc"])
 
   @_require_native_preparation
   def pair_logits_pack(self, pair_cond: torch.Tensor) -> torch.Tensor:
@@ -380,10 +444,31 @@ class TransformerHipMixin:
     return pack.to(self.dtype or pair_cond.dtype)
 
   def forward(self, act, mask, single_cond, pair_cond=None):
+    if getattr(self, "_hip_dc", None) is not None and isinstance(single_cond, torch.Tensor) and \
+        single_cond.is_cuda and single_cond.dim() == 2 and single_cond.shape[0] == act.shape[-2]:
+      return self._forward_conditioned(act, mask, single_cond, pair_cond)
     if pair_cond is None:
       return super().forward(act, mask, single_cond, pair_cond)
     return _with_pack_factory(self, lambda: self.pair_logits_pack(pair_cond),
                               lambda: super(TransformerHipMixin, self).forward(act, mask, single_cond, pair_cond))
+
+  def _forward_conditioned(self, act, mask, single_cond, pair_cond):
+    """Transformer.forward (transformer.py:422-477) with every block's conditioning computed once
+    up front: the native Transformer's loop (backends/vecops/modules.py:1093-1183) -- the
+    attention blocks take their precomputed layer, the transition blocks run as they are."""
+    pack = None
+    if pair_cond is not None:
+      pack = self._cache.get(name="pair_logits", factory=lambda: self.pair_logits_pack(pair_cond))
+    scale, shift, zgate = self.diffusion_conditioning(single_cond)
+    x = act.to(self.dtype) if getattr(self, "dtype", None) is not None else act
+    layer = 0
+    for sb, (attentions, transitions) in enumerate(zip(self.self_attention, self.transition_block)):
+      for b, (attention, transition) in enumerate(zip(attentions, transitions)):
+        x = attention(x, mask, pair_logits=None if pack is None else pack[sb][b], single_cond=single_cond,
+                      adaptive_scale=scale[layer], adaptive_bias=shift[layer], zero_gate=zgate[layer])
+        x = transition(x, single_cond=single_cond)
+        layer += 1
+    return x.to(act.dtype)
 
 
 class CrossAttTransformerHipMixin:

@@ -294,11 +294,13 @@ def _u8_or_none(t):
 
 
 def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_head: int, head_dim: int,
-                          add_residual: bool = True) -> torch.Tensor:
+                          add_residual: bool = True, pre=None) -> torch.Tensor:
   """SelfAttention.forward as one call.  ``x`` ``[..., N, C]`` (leading dims = samples),
   ``mask`` ``[N]`` or None, ``bias`` ``[H, N, N]`` (shared) or ``[S, H, N, N]`` or None,
-  ``cond`` ``[N, Cs]`` or None; ``w`` holds the packed weights (keys as in the C struct)."""
-  _require_cuda(x, mask, bias, cond)
+  ``cond`` ``[N, Cs]`` or None; ``w`` holds the packed weights (keys as in the C struct).
+  ``pre`` = (scale, shift, zgate) ``[N, C]`` views with one row stride (one layer of
+  ``diffusion_conditioning``) replaces the AdaLN computation from ``cond``."""
+  _require_cuda(x, mask, bias, cond, *(pre or ()))
   N, Cn = x.shape[-2], x.shape[-1]
   S = x.numel() // max(N * Cn, 1)
   H, D = num_head, head_dim
@@ -325,6 +327,13 @@ def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_hea
   for key in ("ln_w", "ln_b", "lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift", "w_qkvg", "b_qkvg",
               "w_t2", "w_zc", "b_zc"):
     setattr(a, key, _vp(w.get(key)))
+  if pre is not None:
+    ps, pb, pz = pre
+    rs = ps.stride(0)
+    for t in pre:
+      _require(t.dtype == torch.bfloat16 and tuple(t.shape) == (N, Cn) and t.stride() == (rs, 1),
+               "self_attention: precomputed conditioning must be bf16 [N, C] views with one row stride")
+    a.pre_scale, a.pre_shift, a.pre_zgate, a.pre_rs = _vp(ps), _vp(pb), _vp(pz), rs
   lib = _lib.load()
   ws = torch.empty(int(lib.sf_hip_self_attention_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=x.device)
   _lib.check(lib.sf_hip_self_attention_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(x)), "sf_hip_self_attention_fwd")
@@ -371,3 +380,37 @@ def cross_attention_module(xq: torch.Tensor, xk, gather_idx, gather_mask, mask_q
   ws = torch.empty(int(lib.sf_hip_cross_attention_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=xq.device)
   _lib.check(lib.sf_hip_cross_attention_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(xq)), "sf_hip_cross_attention_fwd")
   return out.view(xq.shape)
+
+
+def diffusion_conditioning(cond: torch.Tensor, lnc_w: torch.Tensor, w_scale: torch.Tensor, b_scale, w_shift: torch.Tensor,
+                           w_zc: torch.Tensor, b_zc) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+  """AdaLN conditioning of L layers from one condition, one call (sf_hip_diffusion_conditioning_fwd;
+  the reference's diffusion_conditioning_packed, backends/vecops/kernels/registry.py:720-760).
+  ``cond`` ``[..., N, Cs]``; ``lnc_w`` f32 ``[L, Cs]``; weights bf16 ``[L*C, Cs]``; biases f32
+  ``[L*C]``.  Returns (scale, shift, zgate), each ``[L, rows, C]`` (rows = cond's leading dims x N)
+  as per-layer views of one ``[rows, L*C]`` buffer; scale and zgate after the sigmoid."""
+  _require_cuda(cond, lnc_w, w_scale, b_scale, w_shift, w_zc, b_zc)
+  L, Cs = lnc_w.shape
+  LC = w_scale.shape[0]
+  _require(LC % L == 0 and cond.shape[-1] == Cs, "diffusion_conditioning: shapes do not match")
+  Cn = LC // L
+  for t, n in ((w_scale, "w_scale"), (w_shift, "w_shift"), (w_zc, "w_zc")):
+    _require(tuple(t.shape) == (LC, Cs) and t.dtype == torch.bfloat16 and t.is_contiguous(),
+             f"diffusion_conditioning: {n} must be contiguous bf16 [L*C, Cs]")
+  c2 = _bf16(cond).reshape(-1, Cs).contiguous()
+  rows = c2.shape[0]
+  outs = [torch.empty(rows, LC, dtype=torch.bfloat16, device=cond.device) for _ in range(3)]
+  a = _lib.DiffusionConditioningArgs()
+  a.rows, a.L, a.C, a.Cs = rows, L, Cn, Cs
+  g = lnc_w.float().contiguous()
+  bs = None if b_scale is None else b_scale.float().contiguous()
+  bz = None if b_zc is None else b_zc.float().contiguous()
+  a.cond, a.lnc_w, a.w_scale, a.b_scale, a.w_shift = _vp(c2), _vp(g), _vp(w_scale), _vp(bs), _vp(w_shift)
+  a.w_zc, a.b_zc = _vp(w_zc), _vp(bz)
+  a.scale, a.shift, a.zgate, a.out_rs = _vp(outs[0]), _vp(outs[1]), _vp(outs[2]), LC
+  lib = _lib.load()
+  ws = torch.empty(int(lib.sf_hip_diffusion_conditioning_workspace_bytes(C.byref(a))), dtype=torch.uint8,
+                   device=cond.device)
+  _lib.check(lib.sf_hip_diffusion_conditioning_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(cond)),
+             "sf_hip_diffusion_conditioning_fwd")
+  return tuple(o.view(rows, L, Cn).transpose(0, 1) for o in outs)

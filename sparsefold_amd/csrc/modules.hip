@@ -7,6 +7,11 @@
 //                               diffusion-transformer token attention
 //   sf_hip_cross_attention_fwd  CrossAttention.forward (transformer.py:549-585), optionally with
 //                               the key-window gather of CrossAttTransformer (:671-673)
+//   sf_hip_diffusion_conditioning_fwd
+//                               the AdaLN scale / shift / zero-gate of every conditioned layer of a
+//                               diffusion Transformer from its one shared condition
+//                               (DiffusionConditioning.cpp:78-222), consumed through the self-attention
+//                               entry's pre_scale / pre_shift / pre_zgate
 //
 // Each stage is one of the library's own op entry points (LayerNorm, linear, attention, window
 // gather), so the numerics are exactly those of the op-level path.
@@ -61,21 +66,24 @@ int adaln(int64_t rows, int C, const void* x, const void* cond, int64_t cond_row
 }
 
 // out = (o W_t2^T) * sigmoid(cond W_zc^T + b_zc) (when cond) + residual (when given)
+// A precomputed multiplier pre_mul [cond_rows, C] (row stride pre_rs) replaces the cond GEMM.
 int zero_init_out(int64_t rows, int C, int HD, const void* o, const void* cond, int64_t cond_rows, int Cs,
                   const void* w_zc, const float* b_zc, const void* w_t2, const void* residual, void* out,
-                  Arena& ws, hipStream_t st) {
+                  Arena& ws, hipStream_t st, const void* pre_mul = nullptr, int64_t pre_rs = 0) {
   int rc;
-  void* zmul = nullptr;
-  if (cond != nullptr) {
-    zmul = ws.take((size_t)cond_rows * C * 2);
+  const void* zmul = pre_mul;
+  int64_t zrs = pre_mul ? pre_rs : C;
+  if (pre_mul == nullptr && cond != nullptr) {
+    void* zbuf = ws.take((size_t)cond_rows * C * 2);
     sf_linear_args z{};
     z.M = cond_rows; z.N = C; z.K = Cs; z.x = cond; z.x_rs = Cs; z.mul_rows = 1;
-    z.wt = w_zc; z.bias = b_zc; z.post_sigmoid = 1; z.y = zmul; z.y_rs = C;
+    z.wt = w_zc; z.bias = b_zc; z.post_sigmoid = 1; z.y = zbuf; z.y_rs = C;
     if ((rc = sf_hip_linear_fwd(&z, st))) return rc;
+    zmul = zbuf;
   }
   sf_linear_args l{};
   l.M = rows; l.N = C; l.K = HD; l.x = o; l.x_rs = HD; l.wt = w_t2;
-  l.mul = zmul; l.mul_rows = zmul ? cond_rows : 1; l.mul_rs = C;
+  l.mul = zmul; l.mul_rows = zmul ? cond_rows : 1; l.mul_rs = zrs;
   l.residual = residual; l.r_rs = C;
   l.y = out; l.y_rs = C;
   return sf_hip_linear_fwd(&l, st);
@@ -135,13 +143,14 @@ size_t self_ws(const sf_self_attention_args* a) {
   Arena ws{nullptr};
   const int64_t rows = (int64_t)a->S * a->N;
   const int HD = a->H * a->D;
-  if (a->cond) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
+  const bool cond_gemms = a->cond && !a->pre_scale;   // AdaLN from cond (not precomputed)
+  if (cond_gemms) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
   ws.take((size_t)rows * a->C * 2);          // h
   ws.take((size_t)rows * 4 * HD * 2);        // q k v g
   ws.take((size_t)rows * HD * 2);            // o
   const sf_attention_args t = self_attn_args(a, kArenaAligned, kArenaAligned);
   ws.take(sf_attention_workspace_bytes(&t));  // key-range slices of the attention
-  if (a->cond) ws.take((size_t)a->N * a->C * 2);
+  if (cond_gemms) ws.take((size_t)a->N * a->C * 2);
   return ws.off;
 }
 
@@ -176,12 +185,18 @@ extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* 
   if (a == nullptr || a->x == nullptr || a->out == nullptr || a->w_qkvg == nullptr || a->w_t2 == nullptr) {
     sf_set_error("self_attention: x, out, w_qkvg and w_t2 must be non-null"); return 1;
   }
-  if (a->S <= 0 || a->N <= 0 || a->C <= 0 || a->H <= 0 || a->D <= 0 || (a->cond && a->Cs <= 0)) {
+  if (a->S <= 0 || a->N <= 0 || a->C <= 0 || a->H <= 0 || a->D <= 0 || (a->cond && !a->pre_scale && a->Cs <= 0)) {
     sf_set_error("self_attention: sizes must be positive (S=%d N=%d C=%d H=%d D=%d Cs=%d)",
                  a->S, a->N, a->C, a->H, a->D, a->Cs);
     return 1;
   }
-  if (a->cond && (a->w_scale == nullptr || a->w_shift == nullptr || a->w_zc == nullptr)) {
+  const bool pre = a->pre_scale != nullptr;
+  if (pre && (a->pre_shift == nullptr || a->pre_zgate == nullptr || a->pre_rs < a->C)) {
+    sf_set_error("self_attention: pre_scale needs pre_shift, pre_zgate and pre_rs >= C (pre_rs=%lld)",
+                 (long long)a->pre_rs);
+    return 1;
+  }
+  if (!pre && a->cond && (a->w_scale == nullptr || a->w_shift == nullptr || a->w_zc == nullptr)) {
     sf_set_error("self_attention: a condition needs w_scale, w_shift and w_zc"); return 1;
   }
   if (workspace == nullptr || workspace_bytes < self_ws(a)) {
@@ -197,11 +212,18 @@ extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* 
   {
     // the AdaLN workspace is taken first, as in self_ws
     Arena probe = ws;
-    if (a->cond) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
+    if (a->cond && !pre) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
     h = probe.take((size_t)rows * a->C * 2);
-    if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b, a->w_scale,
-                    a->b_scale, a->w_shift, ws, h, st)))
+    if (pre) {
+      sf_layer_norm_args ln{};
+      ln.M = rows; ln.C = a->C; ln.eps = 1e-5f;
+      ln.x = a->x; ln.x_rs = a->C; ln.y = h; ln.y_rs = a->C;
+      ln.scale = a->pre_scale; ln.shift = a->pre_shift; ln.cond_rows = a->N; ln.cond_rs = a->pre_rs;
+      if ((rc = sf_hip_layer_norm_fwd(&ln, st))) return rc;
+    } else if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b,
+                           a->w_scale, a->b_scale, a->w_shift, ws, h, st))) {
       return rc;
+    }
     ws = probe;
   }
   void* y = ws.take((size_t)rows * 4 * HD * 2);
@@ -214,8 +236,8 @@ extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* 
   const size_t split = sf_attention_workspace_bytes(&t);
   void* split_ws = ws.take(split);
   if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
-  return zero_init_out(rows, a->C, HD, o, a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
-                       a->add_residual ? a->x : nullptr, a->out, ws, st);
+  return zero_init_out(rows, a->C, HD, o, pre ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
+                       a->add_residual ? a->x : nullptr, a->out, ws, st, a->pre_zgate, a->pre_rs);
 }
 
 extern "C" size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a) {
@@ -281,4 +303,98 @@ extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void
   if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
   return zero_init_out(qrows, C, HD, o, a->cond_q, (int64_t)a->U * a->Qw, C, a->w_zc, a->b_zc, a->w_t2,
                        a->add_residual ? a->xq : nullptr, a->out, rest, st);
+}
+
+namespace {
+
+// W'[j, k] = W[j, k] * g[j / C, k] for the scale and shift weights (blockIdx.y picks which),
+// eight bf16 per thread; Cs % 8 == 0 keeps each group of eight inside one row.
+__global__ void __launch_bounds__(256) fold_gamma_kernel(const uint16_t* __restrict__ w0,
+                                                         const uint16_t* __restrict__ w1,
+                                                         const float* __restrict__ g, uint16_t* o0,
+                                                         uint16_t* o1, int64_t groups, int C, int Cs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= groups) return;
+  const uint16_t* w = blockIdx.y ? w1 : w0;
+  uint16_t* o = blockIdx.y ? o1 : o0;
+  const int64_t e = i * 8;
+  const int64_t row = e / Cs;
+  const int k0 = (int)(e - row * Cs);
+  const float* gl = g + (row / C) * Cs + k0;
+  const u32x4 v = ld16(w + e);
+  u32x4 r;
+  r[0] = pack_bf2(bflo(v[0]) * gl[0], bfhi(v[0]) * gl[1]);
+  r[1] = pack_bf2(bflo(v[1]) * gl[2], bfhi(v[1]) * gl[3]);
+  r[2] = pack_bf2(bflo(v[2]) * gl[4], bfhi(v[2]) * gl[5]);
+  r[3] = pack_bf2(bflo(v[3]) * gl[6], bfhi(v[3]) * gl[7]);
+  st16(o + e, r);
+}
+
+size_t conditioning_ws(const sf_diffusion_conditioning_args* a) {
+  Arena ws{nullptr};
+  ws.take((size_t)a->rows * a->Cs * 2);                  // LN(c)
+  ws.take((size_t)a->L * a->C * a->Cs * 2);              // W_scale * g
+  ws.take((size_t)a->L * a->C * a->Cs * 2);              // W_shift * g
+  return ws.off;
+}
+
+}  // namespace
+
+extern "C" size_t sf_hip_diffusion_conditioning_workspace_bytes(const sf_diffusion_conditioning_args* a) {
+  return a == nullptr ? 0 : conditioning_ws(a);
+}
+
+extern "C" int sf_hip_diffusion_conditioning_fwd(const sf_diffusion_conditioning_args* a, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
+  if (a == nullptr || a->cond == nullptr || a->lnc_w == nullptr || a->w_scale == nullptr ||
+      a->w_shift == nullptr || a->w_zc == nullptr || a->scale == nullptr || a->shift == nullptr ||
+      a->zgate == nullptr) {
+    sf_set_error("diffusion_conditioning: cond, lnc_w, the three weights and the three outputs must be non-null");
+    return 1;
+  }
+  if (a->rows < 0 || a->L <= 0 || a->C <= 0 || a->Cs <= 0 || a->Cs % 8 != 0 || a->Cs > 2048) {
+    sf_set_error("diffusion_conditioning: need rows >= 0, L, C > 0 and 0 < Cs <= 2048 with Cs %% 8 == 0 "
+                 "(rows=%lld L=%d C=%d Cs=%d)", (long long)a->rows, a->L, a->C, a->Cs);
+    return 1;
+  }
+  const int64_t LC = (int64_t)a->L * a->C;
+  if (LC > 0x7fffffff || a->out_rs < LC) {
+    sf_set_error("diffusion_conditioning: need L*C < 2^31 and out_rs >= L*C (L*C=%lld out_rs=%lld)",
+                 (long long)LC, (long long)a->out_rs);
+    return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < conditioning_ws(a)) {
+    sf_set_error("diffusion_conditioning: workspace of %zu bytes needed, %zu given", conditioning_ws(a),
+                 workspace_bytes);
+    return 1;
+  }
+  if (((reinterpret_cast<uintptr_t>(a->w_scale) | reinterpret_cast<uintptr_t>(a->w_shift)) & 15) != 0) {
+    sf_set_error("diffusion_conditioning: w_scale and w_shift must be 16-byte aligned");
+    return 1;
+  }
+  if (a->rows == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Arena ws{static_cast<char*>(workspace)};
+  void* cn = ws.take((size_t)a->rows * a->Cs * 2);
+  void* ws_scale = ws.take((size_t)LC * a->Cs * 2);
+  void* ws_shift = ws.take((size_t)LC * a->Cs * 2);
+  sf_layer_norm_args ln{};
+  ln.M = a->rows; ln.C = a->Cs; ln.eps = 1e-5f;
+  ln.x = a->cond; ln.x_rs = a->Cs; ln.y = cn; ln.y_rs = a->Cs;
+  int rc = sf_hip_layer_norm_fwd(&ln, st);
+  if (rc) return rc;
+  const int64_t groups = LC * a->Cs / 8;
+  hipLaunchKernelGGL(fold_gamma_kernel, dim3((unsigned)((groups + 255) / 256), 2), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(a->w_scale), static_cast<const uint16_t*>(a->w_shift),
+                     a->lnc_w, static_cast<uint16_t*>(ws_scale), static_cast<uint16_t*>(ws_shift), groups,
+                     a->C, a->Cs);
+  if ((rc = sf_check_launch("fold_gamma_kernel"))) return rc;
+  sf_linear_args l{};
+  l.M = a->rows; l.N = (int32_t)LC; l.K = a->Cs; l.x = cn; l.x_rs = a->Cs; l.mul_rows = 1;
+  l.wt = ws_scale; l.bias = a->b_scale; l.post_sigmoid = 1; l.y = a->scale; l.y_rs = a->out_rs;
+  if ((rc = sf_hip_linear_fwd(&l, st))) return rc;
+  l.wt = ws_shift; l.bias = nullptr; l.post_sigmoid = 0; l.y = a->shift;
+  if ((rc = sf_hip_linear_fwd(&l, st))) return rc;
+  l.x = a->cond; l.wt = a->w_zc; l.bias = a->b_zc; l.post_sigmoid = 1; l.y = a->zgate;
+  return sf_hip_linear_fwd(&l, st);
 }

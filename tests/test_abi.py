@@ -37,6 +37,9 @@ def test_error_reporting_without_gpu_work():
   assert "non-null" in _lib.last_error()
   with pytest.raises(RuntimeError, match="sf_hip_attention_fwd failed"):
     _lib.check(rc, "sf_hip_attention_fwd")
+  d = _lib.DiffusionConditioningArgs()
+  assert lib.sf_hip_diffusion_conditioning_fwd(ctypes.byref(d), None, 0, None) != 0
+  assert "non-null" in _lib.last_error()
   assert lib.sf_hip_triangle_workspace_bytes(0, 128, 4, 32) == 0
   assert lib.sf_hip_triangle_workspace_bytes(768, 128, 4, 32) > 768 * 768 * 128 * 2
 

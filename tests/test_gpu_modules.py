@@ -243,3 +243,79 @@ def test_cross_att_pair_logit_pack(U, Qw, Kw, P):
   assert out.shape == (3, U, 4, Qw, Kw) and out.dtype == torch.bfloat16 and out.is_contiguous()
   ref = OM.cross_att_pair_logits(pair_cond.float(), _params(hip))
   assert_close_bf16(out.float().cpu(), ref, f"cross pack U={U} Q={Qw} K={Kw} P={P}", rtol=BF16_ULP)
+
+
+# --------------------------------------------------------------------------------------
+# Diffusion Transformer: every block's AdaLN conditioning in one call
+# --------------------------------------------------------------------------------------
+
+class _Transition(torch.nn.Module):
+  """Stand-in for TransitionBlock (outside this library): halves the activations, exactly in bf16."""
+
+  def forward(self, x, single_cond=None):
+    return x * 0.5
+
+
+class _NoCache:
+  def get(self, *args, name=None, factory=None):
+    return factory()
+
+
+def _diffusion_stack(N: int, n_super: int = 2, sb: int = 2, seed: int = 40):
+  """A diffusion Transformer of n_super x sb blocks: the package's pair-logit half plus the
+  [super-block][block] stacks transformer.py:375-403 builds."""
+  mod, pair_cond = W.make_transformer_pack(N, P=16, num_blocks=n_super * sb, super_block_size=sb, seed=seed)
+  mod.self_attention = torch.nn.ModuleList(
+      [torch.nn.ModuleList([W.make_diffusion(N, S=1, seed=seed + 10 * i + j, sharp=True)[0] for j in range(sb)])
+       for i in range(n_super)])
+  mod.transition_block = torch.nn.ModuleList(
+      [torch.nn.ModuleList([_Transition() for _ in range(sb)]) for _ in range(n_super)])
+  mod._cache = _NoCache()
+  return _prepared(mod), pair_cond
+
+
+@pytest.mark.parametrize("N", [100, 1])
+def test_diffusion_conditioning_matches_oracle(N):
+  """scale / shift / zero-gate of every block (transformer.py:80-96, :138-154) against the
+  oracle's LayerNorm and Linear, layer by layer."""
+  from oracle import primitives as OP
+  mod, _ = _diffusion_stack(N)
+  cond = torch.randn(N, 384, generator=torch.Generator().manual_seed(N)).to(torch.bfloat16)
+  scale, shift, zgate = mod.diffusion_conditioning(cond.to(DEV))
+  assert scale.shape == shift.shape == zgate.shape == (4, N, 768)
+  blocks = [b for sb in mod.self_attention for b in sb]
+  for layer, blk in enumerate(blocks):
+    p = _params(blk)
+    pre = "layer_norm."
+    cn = OP.layer_norm(cond.float(), p[pre + "single_cond_layer_norm.weight"], None, compute_dtype=torch.float32)
+    ref_scale = OP.linear(cn, p[pre + "single_cond_scale.weight"], p[pre + "single_cond_scale.bias"], post_op="sigmoid")
+    ref_shift = OP.linear(cn, p[pre + "single_cond_bias.weight"])
+    ref_zgate = OP.linear(cond.float(), p["zero_init.adaptive_zero_cond.weight"], p["zero_init.adaptive_zero_cond.bias"],
+                          post_op="sigmoid")
+    for got, ref, what in ((scale, ref_scale, "scale"), (shift, ref_shift, "shift"), (zgate, ref_zgate, "zgate")):
+      assert_close_bf16(got[layer].float().cpu(), ref, f"conditioning N={N} layer {layer} {what}",
+                        max_abs=2e-2 * max(ref.abs().max().item(), 1.0))
+
+
+def test_transformer_conditioned_block_loop():
+  """Transformer.forward (transformer.py:422-477) with the conditioning computed once: against the
+  oracle chain and against the per-block path that conditions each block from single_cond."""
+  N = 100
+  mod, pair_cond = _diffusion_stack(N)
+  _, act, cond, _, mask = W.make_diffusion(N, S=2, seed=99, padded=True)
+  calls = []
+  whole = mod.diffusion_conditioning
+  mod.diffusion_conditioning = lambda c: (calls.append(c), whole(c))[1]
+  out = mod(act.to(DEV), mask.to(DEV), cond.to(DEV), pair_cond.to(DEV))
+  assert len(calls) == 1 and out.dtype == act.dtype and out.shape == act.shape
+  blocks = [[b for b in sb] for sb in mod.self_attention]
+  pack = mod.pair_logits_pack(pair_cond.to(DEV))
+  x = act.to(DEV)
+  opack = OM.transformer_pair_logits(pair_cond.float(), _params(mod), 2, None)
+  ref = act.float()
+  for i, row in enumerate(blocks):
+    for j, blk in enumerate(row):
+      x = blk(x, mask.to(DEV), pair_logits=pack[i][j], single_cond=cond.to(DEV)) * 0.5
+      ref = OM.self_attention(ref, mask, _params(blk), pair_logits=opack[i][j], single_cond=cond.float()) * 0.5
+  assert_close_bf16(out, x, "conditioned loop vs per-block conditioning", max_abs=2e-2 * x.abs().max().item())
+  assert_close_bf16(out, ref, "conditioned loop vs oracle", max_abs=2e-2 * ref.abs().max().item())
