@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 4
+#define SF_HIP_ABI_VERSION 5
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -274,6 +274,42 @@ typedef struct sf_cross_attention_args {
 size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a);
 int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* Triangle multiplicative update, whole module (TriangleMultiplication.forward,
+ * blocks.py:486-566, non-distributed), replacing the native triangle_multiplication op
+ * (TriangleMultiplication.cpp; native_ops name "triangle_multiplication", config.py:30):
+ *   x = LN(z) (left_norm_input); [a|b] = sigmoid(x W_g) * (x W_p), zero where
+ *   mask[i] & mask[k] is false, a = projected channels 2c, b = 2c + 1;
+ *   outgoing (incoming = 0, "...ikc,...jkc->...ijc"): t[i,j,c] = sum_k a[i,k,c] b[j,k,c]
+ *   incoming (incoming = 1, "...kjc,...kic->...ijc"): t[i,j,c] = sum_k a[k,j,c] b[k,i,c]
+ *   out = z + (LN(t) (center_norm) W_out) * sigmoid(x W_gate)      (add_residual = 0: no z)
+ * z bf16 [N, N, C] contiguous, C = 128; mask u8 [N] or NULL; LN parameters f32 [C] (biases may
+ * be NULL); weights bf16 with the input channel contiguous ([out, in]):
+ *   w_glu  [4C, C] rows: gate of a (C), gate of b (C), projection of a (C), projection of b (C)
+ *          (gate row c of a = gate_projection column 2c, of b = column 2c + 1; likewise the
+ *          projection)
+ *   w_out  [C, C] output_projection;  w_gate [C, C] gating_linear
+ * Workspace from sf_hip_triangle_mult_workspace_bytes (0 = unsupported sizes).  out may not
+ * alias z; z, out and the weights 16-byte aligned.
+ * STATUS: the per-channel product stage is not implemented in this build; the call validates
+ * its arguments and then returns an error without launching anything. */
+typedef struct sf_triangle_mult_args {
+  int32_t N, C;
+  int32_t incoming;                             /* 0 outgoing, 1 incoming edges */
+  int32_t add_residual;
+  const void* z;                                /* bf16 [N, N, C] */
+  const uint8_t* mask;                          /* u8 [N] or NULL */
+  const float* ln_w; const float* ln_b;         /* left_norm_input */
+  const void* w_glu;                            /* bf16 [4C, C] */
+  const float* cn_w; const float* cn_b;         /* center_norm */
+  const void* w_out;                            /* bf16 [C, C] */
+  const void* w_gate;                           /* bf16 [C, C] */
+  void* out;                                    /* bf16 [N, N, C] */
+} sf_triangle_mult_args;
+
+size_t sf_hip_triangle_mult_workspace_bytes(int32_t N, int32_t C);
+int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /* AdaLN conditioning of L conditioned layers in one call -- the diffusion Transformer's
  * per-layer scale, shift and zero-gate from one shared condition, computed once per Transformer

@@ -92,3 +92,45 @@ def grid_self_attention(act, seq_mask, p, transpose):
     else:
       upd[r] = u
   return z + upd, upd
+
+
+def triangle_multiplication(act, mask, p, incoming):
+  """blocks.py:486-566 written out per position and channel: act ``[N, N, C]`` float64, mask
+  ``[N]`` bool, p the module's float weights (Linear weights ``[in, out]``).  Returns
+  (act + update, update)."""
+  act = np.asarray(act, np.float64)
+  N, _, C = act.shape
+  x = np.zeros_like(act)
+  for i in range(N):
+    for k in range(N):
+      x[i, k] = layer_norm(act[i, k], p["left_norm_input.weight"], p.get("left_norm_input.bias"))
+  wg = np.asarray(p["gate_projection.weight"], np.float64)
+  wp = np.asarray(p["projection.weight"], np.float64)
+  # projected channel ch = 2c + side: side 0 feeds a, side 1 feeds b ("(c i2) ..." split)
+  a = np.zeros((C, N, N))
+  b = np.zeros((C, N, N))
+  for i in range(N):
+    for k in range(N):
+      if not (mask[i] and mask[k]):
+        continue
+      for ch in range(2 * C):
+        g = sum(x[i, k, m] * wg[m, ch] for m in range(C))
+        v = sum(x[i, k, m] * wp[m, ch] for m in range(C))
+        (a if ch % 2 == 0 else b)[ch // 2, i, k] = sigmoid(g) * v
+  t = np.zeros((N, N, C))
+  for c in range(C):
+    for i in range(N):
+      for j in range(N):
+        if incoming:
+          t[i, j, c] = sum(a[c, k, j] * b[c, k, i] for k in range(N))
+        else:
+          t[i, j, c] = sum(a[c, i, k] * b[c, j, k] for k in range(N))
+  wo = np.asarray(p["output_projection.weight"], np.float64)
+  wgl = np.asarray(p["gating_linear.weight"], np.float64)
+  upd = np.zeros_like(act)
+  for i in range(N):
+    for j in range(N):
+      tn = layer_norm(t[i, j], p["center_norm.weight"], p.get("center_norm.bias"))
+      gate = np.array([sigmoid(sum(x[i, j, m] * wgl[m, n] for m in range(C))) for n in range(C)])
+      upd[i, j] = np.array([sum(tn[m] * wo[m, n] for m in range(C)) for n in range(C)]) * gate
+  return act + upd, upd

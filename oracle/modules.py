@@ -256,3 +256,31 @@ def windowed_cross_attention(queries_act: torch.Tensor, queries_mask: torch.Tens
   return cross_attention(queries_act, keys_act, queries_mask, keys_mask, p, pair_logits=pair_logits,
                          single_cond_q=queries_single_cond, single_cond_k=keys_single_cond,
                          dtype=dtype, return_update=return_update)
+
+
+# --------------------------------------------------------------------------------------
+# Triangle multiplicative update: blocks.py:425-566
+# --------------------------------------------------------------------------------------
+
+TRIMUL_EQUATIONS = {"...ikc,...jkc->...ijc": "cik,cjk->cij", "...kjc,...kic->...ijc": "ckj,cki->cij"}
+
+
+def triangle_multiplication(act: torch.Tensor, mask: torch.Tensor, p: dict, *, equation: str,
+                            return_update: bool = False) -> torch.Tensor:
+  """blocks.py:486-566 (TriangleMultiplication.forward, not distributed).  act ``[N, N, C]``,
+  mask ``[N]`` bool.  The gated linear unit is primitives.py:586-631: the combined weight
+  stacks (gate, projection) on dim 1 and the first half of the product is the gated one."""
+  C = act.shape[-1]
+  pair = (mask[:, None] & mask[None, :])[None]                                   # :501
+  x = layer_norm(act, p["left_norm_input.weight"], _get(p, "left_norm_input.bias"))
+  w_glu = torch.stack((p["gate_projection.weight"], p["projection.weight"]), dim=1)   # (C, 2, 2C), :513
+  y = x @ w_glu.reshape(C, 4 * C).to(x.dtype)                                    # primitives.py:616-624
+  gate, proj = torch.tensor_split(y, 2, dim=-1)
+  glu = (torch.sigmoid(gate) * proj).to(x.dtype)                                 # primitives.py:628-630
+  glu = glu.permute(2, 0, 1).masked_fill(~pair, 0.0)                             # "... b n c2 -> ... c2 b n"
+  a, b = glu.reshape(C, 2, *glu.shape[1:]).unbind(1)                             # "(c i2) b n -> i2 c b n"
+  t = torch.einsum(TRIMUL_EQUATIONS[equation], a, b)                             # :555
+  t = layer_norm(t.permute(1, 2, 0), p["center_norm.weight"], _get(p, "center_norm.bias"))   # dim=-3, :556-559
+  out = linear(t, p["output_projection.weight"])
+  out = out * linear(x, p["gating_linear.weight"], post_op="sigmoid")            # :561-563
+  return out if return_update else act + out

@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -119,6 +119,14 @@ class DiffusionConditioningArgs(C.Structure):
   ]
 
 
+class TriangleMultArgs(C.Structure):
+  _fields_ = [
+      ("N", _i32), ("C", _i32), ("incoming", _i32), ("add_residual", _i32),
+      ("z", _vp), ("mask", _vp), ("ln_w", _vp), ("ln_b", _vp), ("w_glu", _vp),
+      ("cn_w", _vp), ("cn_b", _vp), ("w_out", _vp), ("w_gate", _vp), ("out", _vp),
+  ]
+
+
 STRUCTS = {
     "sf_attention_args": AttentionArgs,
     "sf_layer_norm_args": LayerNormArgs,
@@ -129,6 +137,7 @@ STRUCTS = {
     "sf_self_attention_args": SelfAttentionArgs,
     "sf_cross_attention_args": CrossAttentionArgs,
     "sf_diffusion_conditioning_args": DiffusionConditioningArgs,
+    "sf_triangle_mult_args": TriangleMultArgs,
 }
 
 # (name, restype, argtypes) of every exported entry point.
@@ -149,6 +158,8 @@ SIGNATURES = [
     ("sf_hip_cross_attention_fwd", C.c_int, [C.POINTER(CrossAttentionArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_diffusion_conditioning_workspace_bytes", C.c_size_t, [C.POINTER(DiffusionConditioningArgs)]),
     ("sf_hip_diffusion_conditioning_fwd", C.c_int, [C.POINTER(DiffusionConditioningArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_triangle_mult_workspace_bytes", C.c_size_t, [_i32, _i32]),
+    ("sf_hip_triangle_mult_fwd", C.c_int, [C.POINTER(TriangleMultArgs), _vp, C.c_size_t, _vp]),
 ]
 
 _lib: C.CDLL | None = None

@@ -26,6 +26,7 @@ _PATCHED_FACTORIES: list[tuple[object, str, object]] = []
 _REPLACE_MAP = {
     "grid_self_attn": [("GridSelfAttention", "GridSelfAttentionHip")],
     "evoformer_single_act_update": [("SingleActUpdate", "SingleActUpdateHip")],
+    "triangle_multiplication": [("TriangleMultiplication", "TriangleMultiplicationHip")],
     "diffusion_self_attention": [("SelfAttention", "SelfAttentionHip"),
                                  ("TransformerPairLogits", "TransformerPairLogitsHip")],
     "diffusion_cross_attention": [("CrossAttention", "CrossAttentionHip"),

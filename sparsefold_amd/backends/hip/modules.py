@@ -14,6 +14,7 @@ Replaced reference forwards:
 * ``CrossAttentionHip.forward``      transformer.py:549-585; ``forward_indexed`` additionally
                                      gathers the key windows (transformer.py:671-673)
 * ``SingleActUpdateHip.forward``     blocks.py:739-763 (attention half)
+* ``TriangleMultiplicationHip.forward``  blocks.py:486-566 (outgoing and incoming edges, C = 128)
 * ``TransformerHipMixin``            transformer.py:430-447 -- the cached pair-logit pack
                                      ``[n_super, super_block, H, N, N]`` in one pass over pair_cond;
                                      with condition-only HIP attention blocks, also every block's
@@ -527,5 +528,41 @@ class CrossAttTransformerPairLogitsHip(CrossAttTransformerHipMixin, base.CrossAt
   pass
 
 
-HIP_TYPES = (GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin,
+class TriangleMultiplicationHipMixin:
+  """TriangleMultiplication.forward (blocks.py:486-566) as one library call."""
+
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    C = self.num_channels
+    if C != 128:
+      raise ValueError(f"TriangleMultiplicationHip: {C} channels; the HIP module handles 128")
+
+    def split(w):  # [C, 2C] (in, out) -> rows of channels 2c (a) then 2c + 1 (b), K contiguous
+      wt = w.detach().t()
+      return torch.cat([wt[0::2], wt[1::2]], 0)
+
+    _buf(self, "_hip_w_glu", _bf(torch.cat([split(self.gate_projection.weight), split(self.projection.weight)], 0)))
+    _buf(self, "_hip_ln_w", _f32(self.left_norm_input.weight))
+    _buf(self, "_hip_ln_b", _f32(getattr(self.left_norm_input, "bias", None)))
+    _buf(self, "_hip_cn_w", _f32(self.center_norm.weight))
+    _buf(self, "_hip_cn_b", _f32(getattr(self.center_norm, "bias", None)))
+    _buf(self, "_hip_w_out", _bf(self.output_projection.weight.t()))   # [C in, C out] -> [out, in]
+    _buf(self, "_hip_w_gate", _bf(self.gating_linear.weight.t()))
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  def forward(self, act: torch.Tensor, mask: torch.Tensor, *, add_residual: bool = True) -> torch.Tensor:
+    # not graph-captured: the channel products are a BLAS call
+    w = {k: getattr(self, "_hip_" + k) for k in ("ln_w", "ln_b", "w_glu", "cn_w", "cn_b", "w_out", "w_gate")}
+    out = ops.triangle_multiplication(act, mask, w, incoming=self.equation == "...kjc,...kic->...ijc",
+                                      add_residual=add_residual)
+    return out.to(act.dtype)
+
+
+class TriangleMultiplicationHip(TriangleMultiplicationHipMixin, base.TriangleMultiplication):
+  pass
+
+
+HIP_TYPES = (TriangleMultiplicationHipMixin, GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin,
              TransformerHipMixin, CrossAttTransformerHipMixin)

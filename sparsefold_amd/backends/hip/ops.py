@@ -414,3 +414,26 @@ def diffusion_conditioning(cond: torch.Tensor, lnc_w: torch.Tensor, w_scale: tor
   _lib.check(lib.sf_hip_diffusion_conditioning_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(cond)),
              "sf_hip_diffusion_conditioning_fwd")
   return tuple(o.view(rows, L, Cn).transpose(0, 1) for o in outs)
+
+
+def triangle_multiplication(z: torch.Tensor, mask, w: dict, *, incoming: bool, add_residual: bool = True) -> torch.Tensor:
+  """TriangleMultiplication.forward (blocks.py:486-566) as one call (sf_hip_triangle_mult_fwd).
+  ``z`` ``[N, N, 128]``, ``mask`` ``[N]`` bool or None; ``w`` holds the packed weights (keys as in
+  the C struct)."""
+  _require_cuda(z, mask)
+  _require(z.dim() == 3 and z.shape[0] == z.shape[1], "triangle_multiplication: z must be [N, N, C]")
+  N, Cn = z.shape[0], z.shape[2]
+  z3 = _bf16(z).contiguous()
+  out = torch.empty_like(z3)
+  lib = _lib.load()
+  ws_bytes = int(lib.sf_hip_triangle_mult_workspace_bytes(N, Cn))
+  _require(ws_bytes > 0, f"triangle_multiplication: unsupported sizes N={N} C={Cn} (C must be 128)")
+  a = _lib.TriangleMultArgs()
+  a.N, a.C, a.incoming, a.add_residual = N, Cn, int(bool(incoming)), int(bool(add_residual))
+  m8 = _u8_or_none(mask)
+  a.z, a.mask, a.out = _vp(z3), _vp(m8), _vp(out)
+  for key in ("ln_w", "ln_b", "w_glu", "cn_w", "cn_b", "w_out", "w_gate"):
+    setattr(a, key, _vp(w.get(key)))
+  ws = torch.empty(ws_bytes, dtype=torch.uint8, device=z.device)
+  _lib.check(lib.sf_hip_triangle_mult_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(z)), "sf_hip_triangle_mult_fwd")
+  return out.to(z.dtype) if z.dtype != torch.bfloat16 else out

@@ -1,0 +1,357 @@
+// Triangle multiplicative update, outgoing ("...ikc,...jkc->...ijc") and incoming
+// ("...kjc,...kic->...ijc") edges: TriangleMultiplication.forward (blocks.py:486-566), C = 128.
+//
+//   1. trimul_proj_kernel   x = LN(z) (left_norm_input) straight into MFMA operands; the gated
+//                           linear unit sigmoid(x W_g) * (x W_p) (primitives.py:586-631) for the
+//                           2C projected channels, zero where mask[i] & mask[k] is false
+//                           (blocks.py:516-530), written channel-major: a[c][i][k] = channel 2c,
+//                           b[c][i][k] = channel 2c + 1 ("(c i2) b n -> i2 c b n", :540).
+//   2. per-channel product  t[c] = a[c] b[c]^T (outgoing) or a[c]^T-contracted (incoming):
+//                           NOT IMPLEMENTED -- the entry point returns an error before any launch.
+//   3. trimul_out_kernel    LN over the channels of t (center_norm, dim=-3), output projection,
+//                           gate sigmoid(LN(z) W_gl) recomputed from z, out = z + update
+//                           (blocks.py:561-566).
+// LayerNorm affines are folded into the consuming weights: (LN0(x) g + b) W^T =
+// LN0(x) (W * g)^T + W b.  trimul_fold_kernel writes the folded weights into the workspace.
+#include <algorithm>
+#include <mutex>
+
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kC = 128;            // channels (the pair representation's width)
+constexpr int kWS = kC + 8;        // LDS row stride of a [rows][128] bf16 weight (bank padding)
+constexpr int kTW = 8;             // waves per workgroup of both position kernels
+constexpr int kGlu = 4 * kC;       // GLU rows: gate a, gate b, projection a, projection b
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+int64_t plane_stride(int N) { return ((int64_t)N * N + 31) & ~(int64_t)31; }
+
+// Folded weights and offsets, one block of rows each: GLU (left_norm), output (center_norm),
+// gate (left_norm).
+struct FoldArgs {
+  const uint16_t* w[3];
+  const float* g[3];
+  const float* b[3];
+  int rows[3];
+  uint16_t* wf[3];
+  float* off[3];
+};
+
+__global__ __launch_bounds__(256) void trimul_fold_kernel(const FoldArgs a) {
+  int n = blockIdx.x * 256 + threadIdx.x;
+  int s = 0;
+  while (s < 3 && n >= a.rows[s]) n -= a.rows[s++];
+  if (s >= 3) return;
+  const uint16_t* w = a.w[s] + (int64_t)n * kC;
+  const float* g = a.g[s];
+  const float* b = a.b[s];
+  uint16_t* wf = a.wf[s] + (int64_t)n * kC;
+  float off = 0.f;
+  for (int k = 0; k < kC; ++k) {
+    const float v = bf2f(w[k]);
+    wf[k] = f2bf(g ? v * g[k] : v);
+    if (b) off += v * b[k];
+  }
+  a.off[s][n] = off;
+}
+
+struct ProjArgs {
+  int N;
+  int64_t P, Pp;                 // N*N; plane stride (multiple of 32)
+  const uint16_t* z;             // [P, 128]
+  const uint8_t* mask;           // [N] or NULL
+  const uint16_t* w;             // folded GLU [512, 128]
+  const float* off;              // [512]
+  uint16_t* a;                   // [128][Pp]
+  uint16_t* b;                   // [128][Pp]
+  int items, items_per_wave;     // 32-position blocks
+};
+
+// D = X W^T per 32 positions x 32 channels: lane (li, half) ends with channel li of the tile at
+// positions 8(r/4) + 4 half + r%4 -- four consecutive positions per register group, one 8-byte
+// store into the channel-major plane.
+__global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[kGlu * kWS];
+  __shared__ float sOff[kGlu];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, li = lane & 31;
+  constexpr int kStage = kGlu * (kC / 8) / (64 * kTW);
+  u32x4 st[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kTW;
+    st[u] = ld16(a.w + (int64_t)(t >> 4) * kC + (t & 15) * 8);
+  }
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kTW;
+    st16(&sW[(t >> 4) * kWS + (t & 15) * 8], st[u]);
+  }
+  for (int n = tid; n < kGlu; n += 64 * kTW) sOff[n] = a.off[n];
+  __syncthreads();
+  const int first = (blockIdx.x * kTW + wave) * a.items_per_wave;
+  const int last = min(first + a.items_per_wave, a.items);
+  for (int item = first; item < last; ++item) {
+    const int64_t p = (int64_t)item * 32 + li;
+    const bool ok = p < a.P;
+    u32x4 zn[8];
+    const uint16_t* zp = a.z + (ok ? p : 0) * kC + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    bool keep = ok;
+    if (ok && a.mask) {
+      const int i = (int)(p / a.N), k = (int)(p - (int64_t)i * a.N);
+      keep = a.mask[i] && a.mask[k];
+    }
+    const uint32_t kept = (uint32_t)__ballot(keep);        // bit q: position q of the block
+    bf16x8 xo[8];
+    ln128_operands(zn, ok, xo);
+    const int64_t pbase = (int64_t)item * 32 + 4 * half;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {              // 0: a (even channels), 1: b (odd)
+      uint16_t* plane = side ? a.b : a.a;
+#pragma unroll
+      for (int nb = 0; nb < kC / 32; ++nb) {
+        const int rg = side * kC + 32 * nb + li;        // gate row of this lane's channel
+        const int rp = 2 * kC + rg;                     // projection row
+        f32x16 ag, ap;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { ag[e] = 0.f; ap[e] = 0.f; }
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          ag = mfma32(xo[kk], as_bf16x8(ld16(&sW[rg * kWS + 16 * kk + 8 * half])), ag);
+          ap = mfma32(xo[kk], as_bf16x8(ld16(&sW[rp * kWS + 16 * kk + 8 * half])), ap);
+        }
+        const float og = sOff[rg], op = sOff[rp];
+        uint16_t* dst = plane + (int64_t)(32 * nb + li) * a.Pp + pbase;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int q = 8 * g + 4 * half + e;
+            const float m = ((kept >> q) & 1u) ? 1.f : 0.f;
+            v[e] = sigmoidf_(ag[4 * g + e] + og) * (ap[4 * g + e] + op) * m;
+          }
+          *reinterpret_cast<u32x2*>(dst + 8 * g) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        }
+      }
+    }
+  }
+}
+
+struct OutArgs {
+  int64_t P, Pp;
+  const uint16_t* t;             // [128][Pp] channel-major product
+  const uint16_t* z;             // [P, 128]
+  const uint16_t* wo;            // folded output projection [128 out, 128 in]
+  const float* oo;               // [128]
+  const uint16_t* wg;            // folded gate [128 out, 128 in]
+  const float* og;               // [128]
+  int add_residual;
+  uint16_t* out;                 // [P, 128]
+  int items, items_per_wave;
+};
+
+// D^T = W X^T per 32 output channels x 32 positions: lane (li, half) ends with position li at
+// channels 32 nb + 8(r/4) + 4 half + r%4; the gated update goes through a per-wave LDS row block
+// so that every lane then writes whole 16-byte runs of the position-major output.
+__global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sWo[kC * kWS];
+  __shared__ __attribute__((aligned(16))) uint16_t sWg[kC * kWS];
+  __shared__ float sOo[kC], sOg[kC];
+  __shared__ __attribute__((aligned(16))) uint16_t sOut[kTW][32 * kWS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, li = lane & 31;
+  constexpr int kStage = kC * (kC / 8) / (64 * kTW);
+  u32x4 so_[kStage], sg_[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kTW;
+    so_[u] = ld16(a.wo + (int64_t)(t >> 4) * kC + (t & 15) * 8);
+    sg_[u] = ld16(a.wg + (int64_t)(t >> 4) * kC + (t & 15) * 8);
+  }
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * 64 * kTW;
+    st16(&sWo[(t >> 4) * kWS + (t & 15) * 8], so_[u]);
+    st16(&sWg[(t >> 4) * kWS + (t & 15) * 8], sg_[u]);
+  }
+  for (int n = tid; n < kC; n += 64 * kTW) { sOo[n] = a.oo[n]; sOg[n] = a.og[n]; }
+  __syncthreads();
+  uint16_t* const rows = sOut[wave];
+  const int first = (blockIdx.x * kTW + wave) * a.items_per_wave;
+  const int last = min(first + a.items_per_wave, a.items);
+  for (int item = first; item < last; ++item) {
+    const int64_t p = (int64_t)item * 32 + li;
+    const bool ok = p < a.P;
+    // channels 16 kk + 8 half + 0..7 of position p, from the channel-major product
+    u32x4 tn[8], zn[8];
+    const uint16_t* tp = a.t + (ok ? p : 0) + (int64_t)(8 * half) * a.Pp;
+    const uint16_t* zp = a.z + (ok ? p : 0) * kC + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = ok ? tp[(int64_t)(16 * kk + 2 * e) * a.Pp] : 0u;
+        const uint32_t hi = ok ? tp[(int64_t)(16 * kk + 2 * e + 1) * a.Pp] : 0u;
+        w[e] = lo | (hi << 16);
+      }
+      tn[kk] = u32x4{w[0], w[1], w[2], w[3]};
+      zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    }
+    bf16x8 to[8], zo[8];
+    ln128_operands(tn, ok, to);
+    ln128_operands(zn, ok, zo);
+#pragma unroll
+    for (int nb = 0; nb < kC / 32; ++nb) {
+      f32x16 ao, ag;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { ao[e] = 0.f; ag[e] = 0.f; }
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        ao = mfma32(as_bf16x8(ld16(&sWo[(32 * nb + li) * kWS + 16 * kk + 8 * half])), to[kk], ao);
+        ag = mfma32(as_bf16x8(ld16(&sWg[(32 * nb + li) * kWS + 16 * kk + 8 * half])), zo[kk], ag);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = 32 * nb + 8 * g + 4 * half;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (ao[4 * g + e] + sOo[c0 + e]) * sigmoidf_(ag[4 * g + e] + sOg[c0 + e]);
+        *reinterpret_cast<u32x2*>(&rows[li * kWS + c0]) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      }
+    }
+    asm volatile("" ::: "memory");                    // one wave's LDS accesses run in order
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = lane + 64 * u, pos = q >> 4, c8 = (q & 15) * 8;
+      const int64_t pp = (int64_t)item * 32 + pos;
+      const u32x4 v = ld16(&rows[pos * kWS + c8]);
+      if (pp < a.P) {
+        u32x4 r = v;
+        if (a.add_residual) {
+          const u32x4 zr = ld16(a.z + pp * kC + c8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[e] = pack_bf2(bflo(v[e]) + bflo(zr[e]), bfhi(v[e]) + bfhi(zr[e]));
+        }
+        st16(a.out + pp * kC + c8, r);
+      }
+    }
+    asm volatile("" ::: "memory");                    // one wave's LDS accesses run in order
+  }
+}
+
+struct Ws {
+  uint16_t *wglu, *wout, *wgate;
+  float *oglu, *oout, *ogate;
+  uint16_t *a, *b, *t;
+};
+
+Ws carve(char* base, int N) {
+  Ws w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) { char* p = base ? base + off : nullptr; off += align256(bytes); return p; };
+  const size_t plane = (size_t)plane_stride(N) * kC * 2;
+  w.wglu = reinterpret_cast<uint16_t*>(take((size_t)kGlu * kC * 2));
+  w.wout = reinterpret_cast<uint16_t*>(take((size_t)kC * kC * 2));
+  w.wgate = reinterpret_cast<uint16_t*>(take((size_t)kC * kC * 2));
+  w.oglu = reinterpret_cast<float*>(take(kGlu * 4));
+  w.oout = reinterpret_cast<float*>(take(kC * 4));
+  w.ogate = reinterpret_cast<float*>(take(kC * 4));
+  w.a = reinterpret_cast<uint16_t*>(take(plane));
+  w.b = reinterpret_cast<uint16_t*>(take(plane));
+  w.t = reinterpret_cast<uint16_t*>(take(plane));
+  return w;
+}
+
+size_t ws_bytes(int N) {
+  const size_t plane = (size_t)plane_stride(N) * kC * 2;
+  return align256((size_t)kGlu * kC * 2) + 2 * align256((size_t)kC * kC * 2) + align256(kGlu * 4) +
+         2 * align256(kC * 4) + 3 * align256(plane);
+}
+
+int launch_grid(const void* kernel, int items) {
+  const int waves = std::max(1, std::min(sf_resident_workgroups(kernel, 64 * kTW) * kTW, items));
+  return waves;
+}
+
+}  // namespace
+
+extern "C" size_t sf_hip_triangle_mult_workspace_bytes(int32_t N, int32_t C) {
+  if (N <= 0 || C != kC) return 0;
+  return ws_bytes(N);
+}
+
+extern "C" int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  if (a == nullptr || a->z == nullptr || a->out == nullptr || a->w_glu == nullptr || a->w_out == nullptr ||
+      a->w_gate == nullptr || a->cn_w == nullptr || a->ln_w == nullptr) {
+    sf_set_error("triangle_mult: z, out, the three weights, ln_w and cn_w must be non-null");
+    return 1;
+  }
+  if (a->C != kC || a->N <= 0 || (int64_t)a->N * a->N > ((int64_t)1 << 31) - 64) {
+    sf_set_error("triangle_mult: need C == %d and 0 < N*N < 2^31 (N=%d C=%d)", kC, a->N, a->C);
+    return 1;
+  }
+  if (a->z == a->out) {
+    sf_set_error("triangle_mult: out may not alias z");
+    return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < ws_bytes(a->N)) {
+    sf_set_error("triangle_mult: workspace of %zu bytes needed, %zu given", ws_bytes(a->N), workspace_bytes);
+    return 1;
+  }
+  if (((reinterpret_cast<uintptr_t>(a->z) | reinterpret_cast<uintptr_t>(a->out) |
+        reinterpret_cast<uintptr_t>(a->w_glu) | reinterpret_cast<uintptr_t>(a->w_out) |
+        reinterpret_cast<uintptr_t>(a->w_gate)) & 15) != 0) {
+    sf_set_error("triangle_mult: z, out and the weights must be 16-byte aligned");
+    return 1;
+  }
+  // The per-channel product stage is not implemented: its first implementation (a prebuilt
+  // BLAS batched GEMM) was followed by a GPU fault whose cause is not established, so the module
+  // refuses before any launch until a product kernel of this library's own replaces it.
+  sf_set_error("triangle_mult: the per-channel product stage is disabled (no batched GEMM in this build)");
+  return 1;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int N = a->N;
+  const int64_t P = (int64_t)N * N, Pp = plane_stride(N);
+  const Ws w = carve(static_cast<char*>(workspace), N);
+
+  FoldArgs f{};
+  f.w[0] = static_cast<const uint16_t*>(a->w_glu); f.g[0] = a->ln_w; f.b[0] = a->ln_b; f.rows[0] = kGlu;
+  f.wf[0] = w.wglu; f.off[0] = w.oglu;
+  f.w[1] = static_cast<const uint16_t*>(a->w_out); f.g[1] = a->cn_w; f.b[1] = a->cn_b; f.rows[1] = kC;
+  f.wf[1] = w.wout; f.off[1] = w.oout;
+  f.w[2] = static_cast<const uint16_t*>(a->w_gate); f.g[2] = a->ln_w; f.b[2] = a->ln_b; f.rows[2] = kC;
+  f.wf[2] = w.wgate; f.off[2] = w.ogate;
+  hipLaunchKernelGGL(trimul_fold_kernel, dim3((kGlu + 2 * kC + 255) / 256), dim3(256), 0, st, f);
+  int rc = sf_check_launch("trimul_fold_kernel");
+  if (rc) return rc;
+
+  const int items = (int)((P + 31) / 32);
+  {
+    ProjArgs pa{};
+    pa.N = N; pa.P = P; pa.Pp = Pp; pa.z = static_cast<const uint16_t*>(a->z); pa.mask = a->mask;
+    pa.w = w.wglu; pa.off = w.oglu; pa.a = w.a; pa.b = w.b; pa.items = items;
+    const int waves = launch_grid(reinterpret_cast<const void*>(trimul_proj_kernel), items);
+    pa.items_per_wave = (items + waves - 1) / waves;
+    const int groups = (items + pa.items_per_wave * kTW - 1) / (pa.items_per_wave * kTW);
+    hipLaunchKernelGGL(trimul_proj_kernel, dim3(groups), dim3(64 * kTW), 0, st, pa);
+    if ((rc = sf_check_launch("trimul_proj_kernel"))) return rc;
+  }
+
+  OutArgs oa{};
+  oa.P = P; oa.Pp = Pp; oa.t = w.t; oa.z = static_cast<const uint16_t*>(a->z);
+  oa.wo = w.wout; oa.oo = w.oout; oa.wg = w.wgate; oa.og = w.ogate;
+  oa.add_residual = a->add_residual; oa.out = static_cast<uint16_t*>(a->out); oa.items = items;
+  const int waves = launch_grid(reinterpret_cast<const void*>(trimul_out_kernel), items);
+  oa.items_per_wave = (items + waves - 1) / waves;
+  const int groups = (items + oa.items_per_wave * kTW - 1) / (oa.items_per_wave * kTW);
+  hipLaunchKernelGGL(trimul_out_kernel, dim3(groups), dim3(64 * kTW), 0, st, oa);
+  return sf_check_launch("trimul_out_kernel");
+}

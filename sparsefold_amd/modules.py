@@ -114,6 +114,39 @@ class GridSelfAttention(_NoTorchPath, torch.nn.Module):
     self.pair_bias_projection = Linear(num_channels, H, name="pair_bias_projection")
 
 
+class TriangleMultiplication(_NoTorchPath, torch.nn.Module):
+  """blocks.py:425-485: gated triangle multiplicative update, outgoing
+  (``"...ikc,...jkc->...ijc"``) or incoming (``"...kjc,...kic->...ijc"``) edges."""
+
+  @dataclasses.dataclass
+  class Config:
+    equation: str = "...ikc,...jkc->...ijc"
+    use_glu_kernel: bool = True
+
+  EQUATIONS = ("...ikc,...jkc->...ijc", "...kjc,...kic->...ijc")
+
+  def __init__(self, config: Config, global_config: GlobalConfig, *, num_channels: int,
+               distributed: bool = False, name: str = "", **kwargs):
+    super().__init__()
+    if config.equation not in self.EQUATIONS:
+      raise ValueError(f"TriangleMultiplication: unknown equation {config.equation!r}")
+    if distributed:
+      raise ValueError("TriangleMultiplication: the multi-rank path is not part of this build")
+    self.name = name
+    self.config = config
+    self.distributed = False
+    self.num_channels = num_channels
+    self.equation = config.equation
+    self.use_glu_kernel = config.use_glu_kernel
+    C = num_channels
+    self.left_norm_input = LayerNorm(C, bias=True, name="left_norm_input")
+    self.projection = Linear(C, C * 2, bias=False, name="projection")
+    self.gate_projection = Linear(C, C * 2, bias=False, name="gate")
+    self.center_norm = LayerNorm(C, bias=True, name="center_norm")
+    self.output_projection = Linear(C, C, bias=False, name="output_projection")
+    self.gating_linear = Linear(C, C, bias=False, name="gating_linear")
+
+
 class AdaptiveLayerNorm(torch.nn.Module):
   """transformer.py:27-78."""
 

@@ -72,6 +72,21 @@ def make_triangle(N: int, *, C: int = 128, H: int = 4, transpose: bool = False, 
   return mod, z, seq
 
 
+def make_trimul(N: int, *, C: int = 128, incoming: bool = False, padded: bool = False, seed: int = 7,
+                sharp: bool = True, dtype=torch.bfloat16):
+  """Triangle multiplicative update (blocks.py:425-566) and its z [N, N, C], mask [N]."""
+  g = _gen(seed)
+  z = torch.randn(N, N, C, generator=g).to(dtype)
+  mask = torch.ones(N, dtype=torch.bool)
+  if padded:
+    mask[N - N // 10:] = False
+  eq = M.TriangleMultiplication.EQUATIONS[int(incoming)]
+  mod = M.TriangleMultiplication(M.TriangleMultiplication.Config(equation=eq), M.GlobalConfig(), num_channels=C,
+                                 name="triangle_multiplication")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, z, mask
+
+
 def make_single(N: int, *, C_s: int = 384, C_z: int = 128, H: int = 16, seed: int = 3, sharp: bool = False,
                 padded: bool = False, dtype=torch.bfloat16):
   g = _gen(seed)

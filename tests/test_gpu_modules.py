@@ -319,3 +319,50 @@ def test_transformer_conditioned_block_loop():
       ref = OM.self_attention(ref, mask, _params(blk), pair_logits=opack[i][j], single_cond=cond.float()) * 0.5
   assert_close_bf16(out, x, "conditioned loop vs per-block conditioning", max_abs=2e-2 * x.abs().max().item())
   assert_close_bf16(out, ref, "conditioned loop vs oracle", max_abs=2e-2 * ref.abs().max().item())
+
+
+# --------------------------------------------------------------------------------------
+# Triangle multiplicative update (blocks.py:425-566)
+# --------------------------------------------------------------------------------------
+
+_TRIMUL_OFF = pytest.mark.skip(reason="triangle multiplication is disabled: its first full GPU test run, "
+                               "with a prebuilt BLAS product stage, faulted the GPU and the cause is not "
+                               "established; the product stage was removed and the entry point refuses")
+
+
+@_TRIMUL_OFF
+@pytest.mark.parametrize("N,incoming,padded", [(64, False, False), (64, True, True), (37, False, True),
+                                               (37, True, False), (1, False, False), (384, False, True),
+                                               (384, True, True)])
+def test_triangle_multiplication(N, incoming, padded):
+  mod, z, mask = W.make_trimul(N, incoming=incoming, padded=padded, seed=7 + N)
+  hip = _prepared(mod)
+  eq = mod.EQUATIONS[int(incoming)]
+  out = hip(z.to(DEV), mask.to(DEV))
+  assert out.dtype == z.dtype and out.shape == z.shape
+  p = _params(hip)
+  ref = OM.triangle_multiplication(z.float(), mask, p, equation=eq)
+  d_ref = OM.triangle_multiplication(z.float(), mask, p, equation=eq, return_update=True)
+  # the update (up to ~4 with sharp weights) passes through bf16 operands a, b and product t, as
+  # in the reference's bf16 module: the max-abs bound scales with the update, as for the other
+  # modules' update checks (a float emulation of exactly these roundings gives the same error)
+  scale = max(1.0, d_ref.abs().max().item())
+  assert_close_bf16(out, ref, f"trimul N={N} incoming={incoming} padded={padded}", max_abs=2e-2 * scale,
+                    rtol=BF16_ULP)
+  upd = hip(z.to(DEV), mask.to(DEV), add_residual=False)
+  assert_close_bf16(upd, d_ref, "trimul update", max_abs=2e-2 * scale)
+
+
+@_TRIMUL_OFF
+def test_triangle_multiplication_n768_transpose_identity():
+  """N=768 (the headline pair size): incoming edges of z equal the outgoing edges of z^T
+  transposed back, with the same weights -- a size-independent property of the module."""
+  out_mod, z, mask = W.make_trimul(768, padded=True, seed=70)
+  in_mod, _, _ = W.make_trimul(768, incoming=True, seed=70)
+  in_mod.load_state_dict(out_mod.state_dict())
+  hip_out, hip_in = _prepared(out_mod), _prepared(in_mod)
+  zd, md = z.to(DEV), mask.to(DEV)
+  inc = hip_in(zd, md, add_residual=False)
+  out_t = hip_out(zd.transpose(0, 1).contiguous(), md, add_residual=False).transpose(0, 1)
+  assert_close_bf16(inc, out_t, "trimul N=768 incoming vs outgoing of z^T",
+                    max_abs=2e-2 * out_t.float().abs().max().item())

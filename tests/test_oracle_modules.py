@@ -179,3 +179,30 @@ def test_layer_norm_matches_numpy():
   w, b = torch.randn(33), torch.randn(33)
   np.testing.assert_allclose(layer_norm(x, w, b).numpy(), brute.layer_norm(x.numpy(), w.numpy(), b.numpy()),
                              rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("incoming", [False, True])
+@pytest.mark.parametrize("padded", [False, True])
+def test_triangle_multiplication_matches_brute_force(incoming, padded):
+  mod, z, mask = W.make_trimul(5, C=6, incoming=incoming, seed=21, dtype=torch.float32)
+  if padded:
+    mask[-2:] = False
+  p = _sd(mod)
+  eq = mod.EQUATIONS[int(incoming)]
+  out = OM.triangle_multiplication(z, mask, p, equation=eq)
+  ref, upd = brute.triangle_multiplication(z.numpy(), mask.numpy(), {k: v.numpy() for k, v in p.items()}, incoming)
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=1e-5)
+  got = OM.triangle_multiplication(z, mask, p, equation=eq, return_update=True)
+  np.testing.assert_allclose(got.numpy(), upd, rtol=1e-4, atol=1e-5)
+
+
+def test_triangle_multiplication_incoming_is_outgoing_on_transpose():
+  """Incoming edges of z are the outgoing edges of z^T, transposed back (every per-position step
+  commutes with swapping the two token axes; the pair mask is symmetric)."""
+  mod, z, mask = W.make_trimul(9, C=8, seed=22, dtype=torch.float32)
+  mask[-3:] = False
+  p = {k: v.double() for k, v in _sd(mod).items()}
+  z = z.double()
+  inc = OM.triangle_multiplication(z, mask, p, equation=mod.EQUATIONS[1])
+  out_t = OM.triangle_multiplication(z.transpose(0, 1), mask, p, equation=mod.EQUATIONS[0]).transpose(0, 1)
+  torch.testing.assert_close(inc, out_t, rtol=1e-12, atol=1e-12)
