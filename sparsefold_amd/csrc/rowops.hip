@@ -32,15 +32,39 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
     for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
   };
-  u32x4 w[4];
-  float sum = 0.f;
+  // every operand of the row is requested before the statistics need the first one: the
+  // affine / modulation loads do not depend on them, so a row costs one memory round trip
+  const uint16_t* scp = nullptr;
+  const uint16_t* shp = nullptr;
+  if (a.scale != nullptr && live) {
+    const int64_t crow = row % a.cond_rows;
+    scp = (const uint16_t*)a.scale + crow * a.cond_rs;
+    shp = (const uint16_t*)a.shift + crow * a.cond_rs;
+  }
+  u32x4 w[4], sw[4], hw[4];
+  float gv[4][8], bv[4][8];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int ch = sub + LPR * t;
-    w[t] = (live && ch < nch) ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
+    const bool on = live && ch < nch;
+    w[t] = on ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
+    if (a.gamma != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gv[t][e] = on ? a.gamma[8 * ch + e] : 0.f;
+        bv[t][e] = (on && a.beta) ? a.beta[8 * ch + e] : 0.f;
+      }
+    }
+    if (scp != nullptr) {
+      sw[t] = on ? ld16(scp + 8 * ch) : u32x4{0, 0, 0, 0};
+      hw[t] = on ? ld16(shp + 8 * ch) : u32x4{0, 0, 0, 0};
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) sum += bflo(w[t][e]) + bfhi(w[t][e]);
-  }
   const float mean = group_sum(sum) / (float)C;
   float sq = 0.f;
 #pragma unroll
@@ -55,13 +79,6 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
   }
   const float rstd = rsqrtf(group_sum(sq) / (float)C + a.eps);
   if (!live) return;
-  const uint16_t* scp = nullptr;
-  const uint16_t* shp = nullptr;
-  if (a.scale != nullptr) {
-    const int64_t crow = row % a.cond_rows;
-    scp = (const uint16_t*)a.scale + crow * a.cond_rs;
-    shp = (const uint16_t*)a.shift + crow * a.cond_rs;
-  }
   uint16_t* yp = (uint16_t*)a.y + row * a.y_rs;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -76,14 +93,13 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
     const int c0 = 8 * ch;
     if (a.gamma != nullptr) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = v[e] * a.gamma[c0 + e] + (a.beta ? a.beta[c0 + e] : 0.f);
+      for (int e = 0; e < 8; ++e) v[e] = v[e] * gv[t][e] + bv[t][e];
     }
     if (scp != nullptr) {
-      const u32x4 sw = ld16(scp + c0), hw = ld16(shp + c0);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[2 * e] = v[2 * e] * bflo(sw[e]) + bflo(hw[e]);
-        v[2 * e + 1] = v[2 * e + 1] * bfhi(sw[e]) + bfhi(hw[e]);
+        v[2 * e] = v[2 * e] * bflo(sw[t][e]) + bflo(hw[t][e]);
+        v[2 * e + 1] = v[2 * e + 1] * bfhi(sw[t][e]) + bfhi(hw[t][e]);
       }
     }
     st16(yp + c0, u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]),
@@ -655,9 +671,13 @@ extern "C" int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream) 
     const int64_t rows_per_wg = 4 * (64 / LPR);
     hipLaunchKernelGGL(layer_norm_kernel<LPR>, dim3((unsigned)((a->M + rows_per_wg - 1) / rows_per_wg)), dim3(256), 0, st, *a);
   };
-  if (nch <= 8 * 4) launch(std::integral_constant<int, 8>{});
-  else if (nch <= 16 * 4) launch(std::integral_constant<int, 16>{});
-  else if (nch <= 32 * 4) launch(std::integral_constant<int, 32>{});
+  // fewest lanes per row that hold the row in four 16-byte chunks each, widened (up to a wave
+  // per row) while the grid would leave most of the 256 CUs idle
+  int lpr = nch <= 8 * 4 ? 8 : nch <= 16 * 4 ? 16 : nch <= 32 * 4 ? 32 : 64;
+  while (lpr < 64 && (a->M + 4 * (64 / lpr) - 1) / (4 * (64 / lpr)) < 512) lpr *= 2;
+  if (lpr == 8) launch(std::integral_constant<int, 8>{});
+  else if (lpr == 16) launch(std::integral_constant<int, 16>{});
+  else if (lpr == 32) launch(std::integral_constant<int, 32>{});
   else launch(std::integral_constant<int, 64>{});
   return sf_check_launch("layer_norm_kernel");
 }
