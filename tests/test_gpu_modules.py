@@ -366,3 +366,21 @@ def test_triangle_multiplication_n768_transpose_identity():
   out_t = hip_out(zd.transpose(0, 1).contiguous(), md, add_residual=False).transpose(0, 1)
   assert_close_bf16(inc, out_t, "trimul N=768 incoming vs outgoing of z^T",
                     max_abs=2e-2 * out_t.float().abs().max().item())
+
+
+def test_precomputed_conditioning_op_level_path():
+  """A per-sample key mask takes the op-level path (LayerNorm, linear, attention, linear); with a
+  block's precomputed conditioning it must agree with the one-call path on the same values."""
+  N, S = 100, 2
+  mod, _ = _diffusion_stack(N, n_super=1, sb=2)
+  _, act, cond, bias, mask = W.make_diffusion(N, S=S, seed=98, padded=True, sharp=True)
+  scale, shift, zgate = mod.diffusion_conditioning(cond.to(DEV))
+  blk = [b for b in mod.self_attention[0]][1]
+  x, m = act.to(DEV), mask.to(DEV)
+  pre = dict(adaptive_scale=scale[1], adaptive_bias=shift[1], zero_gate=zgate[1])
+  fused = blk(x, m, pair_logits=bias.to(DEV), **pre)
+  op_level = blk(x, m.expand(S, N).contiguous(), pair_logits=bias.to(DEV), **pre)
+  assert_close_bf16(op_level, fused, "op-level vs one-call path, precomputed conditioning",
+                    max_abs=2e-2 * fused.float().abs().max().item())
+  ref = OM.self_attention(act.float(), mask, _params(blk), pair_logits=bias.float(), single_cond=cond.float())
+  assert_close_bf16(op_level, ref, "op-level path vs oracle", rtol=BF16_ULP)
