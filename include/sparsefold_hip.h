@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 5
+#define SF_HIP_ABI_VERSION 6
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -83,6 +83,10 @@ int sf_hip_attention_fwd(const sf_attention_args* a, void* stream);
  *   y[m,:] = LN(x[m,:]) * gamma + beta                       (gamma/beta f32 or NULL)
  *   y[m,:] = LN(x[m,:]) * scale[m % cond_rows,:] + shift[m % cond_rows,:]   (AdaLN)
  * x, y bf16 row-major with row strides; eps as given (reference 1e-5).  C <= 2048.
+ * Optional row gather (the key windows of CrossAttTransformer, transformer.py:671-673): with
+ * gather_idx, row m = s * gather_rows + r normalises x row s * gather_src_rows + gather_idx[r],
+ * or a zero row where gather_mask[r] is 0 or the index is outside [0, gather_src_rows) -- the
+ * rows sf_hip_window_gather_fwd would produce, without materialising them.
  * ------------------------------------------------------------------------------------- */
 typedef struct sf_layer_norm_args {
   int64_t M; int32_t C; float eps;
@@ -91,6 +95,8 @@ typedef struct sf_layer_norm_args {
   const void* scale; const void* shift;         /* bf16 [cond_rows, C] or NULL (AdaLN) */
   int64_t cond_rows; int64_t cond_rs;
   void* y; int64_t y_rs;                        /* bf16 */
+  const int32_t* gather_idx; const uint8_t* gather_mask;   /* [gather_rows] or NULL */
+  int64_t gather_rows, gather_src_rows;
 } sf_layer_norm_args;
 
 int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream);

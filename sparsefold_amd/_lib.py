@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -42,6 +42,7 @@ class LayerNormArgs(C.Structure):
       ("scale", _vp), ("shift", _vp),
       ("cond_rows", _i64), ("cond_rs", _i64),
       ("y", _vp), ("y_rs", _i64),
+      ("gather_idx", _vp), ("gather_mask", _vp), ("gather_rows", _i64), ("gather_src_rows", _i64),
   ]
 
 

@@ -36,13 +36,17 @@ struct Arena {
 };
 
 // LN (gamma / beta) or AdaLN (LN of the condition, sigmoid scale, shift, modulated LN) of x.
+// With gidx, the rows of x are gathered as sf_hip_window_gather_fwd would (gmask, grows rows per
+// sample of the gathered space, gsrc rows per sample of x).
 int adaln(int64_t rows, int C, const void* x, const void* cond, int64_t cond_rows, int Cs,
           const float* ln_w, const float* ln_b, const float* lnc_w, const float* lnc_b,
           const void* w_scale, const float* b_scale, const void* w_shift, Arena& ws, void* y,
-          hipStream_t st) {
+          hipStream_t st, const int32_t* gidx = nullptr, const uint8_t* gmask = nullptr, int64_t grows = 0,
+          int64_t gsrc = 0) {
   sf_layer_norm_args ln{};
   ln.M = rows; ln.C = C; ln.eps = 1e-5f;
   ln.x = x; ln.x_rs = C; ln.y = y; ln.y_rs = C;
+  ln.gather_idx = gidx; ln.gather_mask = gmask; ln.gather_rows = grows; ln.gather_src_rows = gsrc;
   if (cond == nullptr) {
     ln.gamma = ln_w; ln.beta = ln_b;
     return sf_hip_layer_norm_fwd(&ln, st);
@@ -158,7 +162,6 @@ size_t cross_ws(const sf_cross_attention_args* a) {
   Arena ws{nullptr};
   const int64_t qrows = (int64_t)a->S * a->U * a->Qw, krows = (int64_t)a->S * a->U * a->Kw;
   const int HD = a->H * a->D;
-  if (a->gather_idx) ws.take((size_t)krows * a->C * 2);
   for (int side = 0; side < 2; ++side) {
     const int64_t cr = (int64_t)a->U * (side ? a->Kw : a->Qw);
     ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2);
@@ -265,15 +268,8 @@ extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void
   const int C = a->C, HD = a->H * a->D;
   const int64_t qrows = (int64_t)a->S * a->U * a->Qw, krows = (int64_t)a->S * a->U * a->Kw;
   int rc;
-  const void* xk = a->xk;
-  if (a->gather_idx) {
-    void* keys = ws.take((size_t)krows * C * 2);
-    sf_window_gather_args gth{};
-    gth.S = a->S; gth.rows = a->U * a->Qw; gth.C = C; gth.UK = a->U * a->Kw;
-    gth.src = a->xq; gth.idx = a->gather_idx; gth.mask = a->gather_mask; gth.keys = keys;
-    if ((rc = sf_hip_window_gather_fwd(&gth, st))) return rc;
-    xk = keys;
-  }
+  // gathered keys are never materialised: their LayerNorm reads the query rows through the gather
+  const void* xk = a->gather_idx ? a->xq : a->xk;
   // the two AdaLN chains take their scratch first, in the order cross_ws counts it
   Arena side_q = ws;
   Arena side_k = ws;
@@ -286,7 +282,8 @@ extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void
                   a->w_scale_q, a->b_scale_q, a->w_shift_q, side_q, hq, st)))
     return rc;
   if ((rc = adaln(krows, C, xk, a->cond_k, (int64_t)a->U * a->Kw, C, nullptr, nullptr, a->lnc_w_k, a->lnc_b_k,
-                  a->w_scale_k, a->b_scale_k, a->w_shift_k, side_k, hk, st)))
+                  a->w_scale_k, a->b_scale_k, a->w_shift_k, side_k, hk, st, a->gather_idx, a->gather_mask,
+                  (int64_t)a->U * a->Kw, (int64_t)a->U * a->Qw)))
     return rc;
   void* yq = rest.take((size_t)qrows * 2 * HD * 2);
   void* yk = rest.take((size_t)krows * 2 * HD * 2);

@@ -26,7 +26,16 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
   const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
   const bool live = row < a.M;
   const int C = a.C, nch = C / 8;
-  const uint16_t* xp = (const uint16_t*)a.x + (live ? row : 0) * a.x_rs;
+  int64_t src = row;                             // x row this row normalises
+  bool zero = false;                             // gathered row outside the window: all zeros
+  if (a.gather_idx != nullptr && live) {
+    const int64_t smp = row / a.gather_rows, r = row - smp * a.gather_rows;
+    const int gi = a.gather_idx[r];
+    const bool ok = a.gather_mask[r] != 0 && gi >= 0 && gi < a.gather_src_rows;
+    src = smp * a.gather_src_rows + (ok ? gi : 0);
+    zero = !ok;
+  }
+  const uint16_t* xp = (const uint16_t*)a.x + (live ? src : 0) * a.x_rs;
   auto group_sum = [](float v) {
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -47,7 +56,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const sf_layer_norm_arg
   for (int t = 0; t < 4; ++t) {
     const int ch = sub + LPR * t;
     const bool on = live && ch < nch;
-    w[t] = on ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
+    w[t] = (on && !zero) ? ld16(xp + 8 * ch) : u32x4{0, 0, 0, 0};
     if (a.gamma != nullptr) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -659,6 +668,11 @@ extern "C" int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream) 
   }
   if ((a->scale == nullptr) != (a->shift == nullptr) || (a->scale && a->cond_rows <= 0)) {
     sf_set_error("layer_norm: scale and shift must be given together with cond_rows > 0"); return 1;
+  }
+  if (a->gather_idx && (a->gather_mask == nullptr || a->gather_rows <= 0 || a->gather_src_rows <= 0 ||
+                        a->M % a->gather_rows != 0)) {
+    sf_set_error("layer_norm: a gather needs gather_mask, gather_rows > 0 dividing M and gather_src_rows > 0");
+    return 1;
   }
   if (!al16(a->x) || !al16(a->y) || a->x_rs % 8 || a->y_rs % 8 ||
       (a->scale && (!al16(a->scale) || !al16(a->shift) || a->cond_rs % 8))) {
