@@ -25,6 +25,7 @@ import torch
 N, C, H, D = 768, 128, 4, 32
 PEAK_BF16_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+CLOCK_WARMUP_S = 0.5               # minimum wall time of untimed calls before the timed steps
 
 
 def module_flop(n=N, c=C, h=H, d=D) -> float:
@@ -44,7 +45,6 @@ def parse():
   ap.add_argument("--steps", type=int, default=200)
   ap.add_argument("--warmup", type=int, default=50, help="untimed calls first (the GPU clock ramps up)")
   ap.add_argument("--cpu-baseline", type=int, default=1, help="time the host-CPU math path (rank 0)")
-  ap.add_argument("--cpu-rows", type=int, default=128, help="rows in the CPU-baseline sample")
   ap.add_argument("--other-configs", type=int, default=1, help="also time the other four configurations")
   ap.add_argument("--profile-config", default="",
                   help="only run this configuration --steps times (e.g. single_n768) and exit")
@@ -165,25 +165,28 @@ def _config_builders() -> dict:
         "ms_per_call": round(t, 4), "ms_24_blocks": round(24 * t, 3), "tflops": round(flop / t / 1e9, 1),
         "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
 
-  def c4_stack():  # the 24 attention blocks of the diffusion Transformer, 5 samples x N=1024: every
-    # block's AdaLN conditioning in one call, then the 24 blocks on their precomputed layers
-    # (transition blocks are not part of this library).  One block's weights serve all 24 layers.
+  def c4_stack():  # the 24 attention blocks of the diffusion Transformer, 5 samples x N=1024, each
+    # with its own seeded weights: every block's AdaLN conditioning in one call, then the 24 blocks
+    # on their precomputed layers (the transition blocks between them are timed separately)
     from sparsefold_amd.backends.hip import ops as HO
     S, n, c, sc, h, d, L = 5, 1024, 768, 384, 16, 48, 24
-    mod, act, cond, bias, mask = W.make_diffusion(n, S=S, seed=4)
-    mod = mod.to(dev); backends.prepare(mod)
+    mods, act, cond, bias, mask = W.make_diffusion_stack(n, S=S, L=L, seed=4)
+    mods = [m.to(dev) for m in mods]
+    for m in mods:
+      backends.prepare(m)
     act, cond, bias, mask = act.to(dev), cond.to(dev), bias.to(dev), mask.to(dev)
-    stacked = (mod._hip_ada_lnc_w.repeat(L, 1), mod._hip_ada_w_scale.repeat(L, 1), mod._hip_ada_b_scale.repeat(L),
-               mod._hip_ada_w_shift.repeat(L, 1), mod._hip_w_zc.repeat(L, 1), mod._hip_b_zc.repeat(L))
+    stacked = (torch.stack([m._hip_ada_lnc_w for m in mods]), torch.cat([m._hip_ada_w_scale for m in mods]),
+               torch.cat([m._hip_ada_b_scale for m in mods]), torch.cat([m._hip_ada_w_shift for m in mods]),
+               torch.cat([m._hip_w_zc for m in mods]), torch.cat([m._hip_b_zc for m in mods]))
     flop = L * (2 * n * sc * 2 * c + 2 * S * n * c * 4 * c + 4 * h * n * n * d * S + 2 * S * n * c * c
                 + 2 * n * sc * c)
 
     def call():
       scale, shift, zgate = HO.diffusion_conditioning(cond, *stacked)
       x = act
-      for layer in range(L):
-        x = mod(x, mask, pair_logits=bias, adaptive_scale=scale[layer], adaptive_bias=shift[layer],
-                zero_gate=zgate[layer])
+      for layer, m in enumerate(mods):
+        x = m(x, mask, pair_logits=bias, adaptive_scale=scale[layer], adaptive_bias=shift[layer],
+              zero_gate=zgate[layer])
       return x
     return call, (lambda t: {
         "ms_per_block": round(t / L, 4), "ms_24_blocks": round(t, 3), "tflops": round(flop / t / 1e9, 1),
@@ -259,33 +262,58 @@ def profile_config(name: str, calls: int) -> None:
   print(f"[bench] profiled {name}: {calls} calls", flush=True)
 
 
-def cpu_baseline(rows: int) -> dict:
-  """Host-CPU Torch math path (oracle restatement of blocks.py:293-366 in bf16, SDPA MATH,
-  128-row chunks as configs/cpu.toml's runtime.sharding): the shared prologue (LN + bias)
-  once, plus `rows` attention rows, scaled to the full N rows."""
+def _host_cpu() -> dict:
+  """The host CPU as the baseline protocol asks: model, physical cores of the affinity set,
+  affinity set size and AMX-BF16 presence (from /proc/cpuinfo and the sysfs topology)."""
+  aff = sorted(os.sched_getaffinity(0))
+  model, flags = "unknown", set()
+  try:
+    with open("/proc/cpuinfo") as f:
+      for line in f:
+        if line.startswith("model name") and model == "unknown":
+          model = line.split(":", 1)[1].strip()
+        elif line.startswith("flags") and not flags:
+          flags = set(line.split(":", 1)[1].split())
+  except OSError:
+    pass
+  cores = set()
+  for cpu in aff:
+    base = f"/sys/devices/system/cpu/cpu{cpu}/topology/"
+    try:
+      with open(base + "physical_package_id") as f1, open(base + "core_id") as f2:
+        cores.add((f1.read().strip(), f2.read().strip()))
+    except OSError:
+      cores.add(("?", str(cpu)))
+  return {"cpu_model": model, "physical_cores": len(cores), "affinity_cpus": len(aff),
+          "amx_bf16": "amx_bf16" in flags}
+
+
+def cpu_baseline() -> dict:
+  """Host-CPU Torch math path: the oracle restatement of GridSelfAttention.forward
+  (blocks.py:293-366) in bf16 with SDPA MATH and 128-row chunks (configs/cpu.toml: sdpa "math",
+  runtime.sharding), on the same seeded inputs as the GPU measurement, under
+  torch.inference_mode with one thread per physical core of the affinity set.  The whole call
+  (all 768 rows) is timed: median of 5 runs after 2 warm-ups."""
   from oracle import modules as OM
-  from oracle.primitives import layer_norm, linear
   from sparsefold_amd import workloads as W
-  cores = len(os.sched_getaffinity(0))
-  torch.set_num_threads(cores)
+  host = _host_cpu()
+  threads = max(1, host["physical_cores"])
+  torch.set_num_threads(threads)
   mod, z, seq = W.make_triangle(N, seed=3)
   p = {k: v.to(torch.bfloat16) for k, v in W.state_dict_f32(mod).items()}
+  times = []
   with torch.inference_mode():
-    t0 = time.perf_counter()
-    x = layer_norm(z, p["act_norm.weight"], p["act_norm.bias"])
-    bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
-    t1 = time.perf_counter()
-    OM.grid_self_attention_rows(z, seq, p, transpose=False, rows=range(rows), bias=bias)   # warm-up
-    reps = []
-    for _ in range(2):
-      t2 = time.perf_counter()
-      OM.grid_self_attention_rows(z, seq, p, transpose=False, rows=range(rows), bias=bias)
-      reps.append(time.perf_counter() - t2)
-  chunk = min(reps)
-  total_s = (t1 - t0) + chunk * (N / rows)
-  return {"value": total_s * 1e3, "unit": "ms/call", "cores": cores, "kind": "port",
-          "sample": f"bf16 Torch math (oracle restatement), prologue once + {rows} of {N} rows "
-                    f"(min of 2 after 1 warm-up), scaled x{N / rows:g}"}
+    for i in range(7):
+      t0 = time.perf_counter()
+      OM.grid_self_attention(z, seq, p, transpose=False, chunk_size=128)
+      times.append(time.perf_counter() - t0)
+      print(f"[bench]   cpu run {i} ({'warm-up' if i < 2 else 'timed'}): {times[-1]:.2f} s", flush=True)
+  timed = sorted(times[2:])
+  med = timed[len(timed) // 2]
+  return {"value": med * 1e3, "unit": "ms/call", "cores": threads, "kind": "port",
+          "sample": f"the whole N=768 call (prologue + all {N} rows in 128-row chunks), bf16 Torch math "
+                    "(oracle restatement of blocks.py:293-366, SDPA MATH); median of 5 after 2 warm-ups",
+          "runs_s": [round(t, 3) for t in times], **host}
 
 
 def main():
@@ -317,6 +345,15 @@ def main():
   z, seq = z.to(dev), seq.to(dev)
   stream = torch.cuda.current_stream()
   print(f"[bench] triangle start N={N} C={C} H={H} D={D} warmup={args.warmup} steps={args.steps}", flush=True)
+  # the GPU clock ramps up under load: besides the W warm-up calls, calls run until at least
+  # CLOCK_WARMUP_S of wall time has passed, whatever W is, so that short runs time a steady clock
+  t0 = time.perf_counter()
+  extra = 0
+  while time.perf_counter() - t0 < CLOCK_WARMUP_S:
+    for _ in range(10):
+      mod(z, seq)
+    torch.cuda.synchronize()
+    extra += 10
   for _ in range(args.warmup):
     mod(z, seq)
   torch.cuda.synchronize()
@@ -339,7 +376,7 @@ def main():
   cpu = None
   if args.cpu_baseline:
     print("[bench] timing host-CPU math path sample...", flush=True)
-    cpu = cpu_baseline(args.cpu_rows)
+    cpu = cpu_baseline()
     print(f"[bench] cpu baseline {cpu['value']:.1f} ms/call on {cpu['cores']} threads", flush=True)
   line = {
       "metric": "ms/call + % bf16 MFMA peak, triangle attention N=768; vs host-CPU math path",
@@ -348,6 +385,7 @@ def main():
       "n_gpus": 1,
       "steps": args.steps,
       "warmup": args.warmup,
+      "clock_warmup": {"calls": extra, "min_seconds": CLOCK_WARMUP_S},
       "ms_per_step": round(ms, 4),
       "higher_is_better": False,
       "scaling": "weak",

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 6
+#define SF_HIP_ABI_VERSION 7
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -74,6 +74,10 @@ typedef struct sf_attention_args {
   const uint8_t* mask_k; int64_t mk_s[3];       /* u8 or NULL, strides [b0, b1, k]         */
   const void* gate; int64_t g_s[4];             /* bf16 or NULL (sigmoid gate logits)      */
   void* out;        int64_t o_s[4];             /* bf16, strides [b0, b1, q, h]            */
+  /* Work decomposition: 0 = chosen from the sizes (normal use); 1 = query blocks of one
+   * (batch, head) share their K/V tiles; 2 = every 32-query block is an independent task.
+   * Both give the same result up to fp32 summation order; tests select each explicitly. */
+  int32_t schedule;
 } sf_attention_args;
 
 int sf_hip_attention_fwd(const sf_attention_args* a, void* stream);
@@ -145,6 +149,12 @@ typedef struct sf_triangle_args {
   const void* w_qkvgb;
   const void* w_o;
   void* out;
+  /* Weight-sum limit of the head-dim-32 path's fixed-reference-point softmax: a (row, head)
+   * whose sum of weights leaves [2^-100, limit] is recomputed by an exact two-pass softmax.
+   * 0 = 2^100 (normal use); a smaller positive value sends more rows through the exact path, so
+   * that tests can reach it with ordinary logits.  The result does not depend on it beyond
+   * rounding. */
+  float fixup_sum_limit;
 } sf_triangle_args;
 
 size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t D);

@@ -134,3 +134,117 @@ def triangle_multiplication(act, mask, p, incoming):
       gate = np.array([sigmoid(sum(x[i, j, m] * wgl[m, n] for m in range(C))) for n in range(C)])
       upd[i, j] = np.array([sum(tn[m] * wo[m, n] for m in range(C)) for n in range(C)]) * gate
   return act + upd, upd
+
+
+def _ln_gamma(x, w):
+  """LayerNorm with a scale and no offset (the pair_input_layer_norm of both packs)."""
+  return layer_norm(x, w, None)
+
+
+def transformer_pair_logits(pair_cond, p):
+  """transformer.py:430-438 written per element: pair_cond ``[N0, N1, P]`` float64 ->
+  ``[n_super, S, H, N0, N1]``.  Plane (sb, s, h) at (b, n) is the dot product of the normalised
+  pair_cond[b, n] with column (s, h) of super-block sb's projection ``[P, S, H]``."""
+  pc = np.asarray(pair_cond, np.float64)
+  N0, N1, P = pc.shape
+  gamma = np.asarray(p["pair_input_layer_norm.weight"], np.float64)
+  ws = []
+  while f"pair_logits_projection.{len(ws)}.weight" in p:
+    ws.append(np.asarray(p[f"pair_logits_projection.{len(ws)}.weight"], np.float64))
+  S, H = ws[0].shape[1:]
+  out = np.zeros((len(ws), S, H, N0, N1))
+  for b in range(N0):
+    for n in range(N1):
+      x = _ln_gamma(pc[b, n], gamma)
+      for sb, w in enumerate(ws):
+        for s in range(S):
+          for h in range(H):
+            out[sb, s, h, b, n] = sum(x[c] * w[c, s, h] for c in range(P))
+  return out
+
+
+def cross_att_pair_logits(pair_cond, p):
+  """transformer.py:655-662 written per element: pair_cond ``[U, Q, K, P]`` float64 ->
+  ``[blocks, U, H, Q, K]``.  Plane (blk, h) of window u at (q, k) is the dot product of the
+  normalised pair_cond[u, q, k] with column (blk, h) of the projection ``[P, blocks, H]``."""
+  pc = np.asarray(pair_cond, np.float64)
+  U, Q, K, P = pc.shape
+  gamma = np.asarray(p["pair_input_layer_norm.weight"], np.float64)
+  w = np.asarray(p["pair_logits_projection.weight"], np.float64)
+  nb, H = w.shape[1:]
+  out = np.zeros((nb, U, H, Q, K))
+  for u in range(U):
+    for q in range(Q):
+      for k in range(K):
+        x = _ln_gamma(pc[u, q, k], gamma)
+        for blk in range(nb):
+          for h in range(H):
+            out[blk, u, h, q, k] = sum(x[c] * w[c, blk, h] for c in range(P))
+  return out
+
+
+def _adaln_row(x, c, p, prefix):
+  """AdaLN of one row (transformer.py:80-96): LN(x) scaled by sigmoid(LN_g(c) Ws + bs), shifted
+  by LN_g(c) Wb.  Without a condition: LN(x) with the side's own scale and offset."""
+  if c is None:
+    return layer_norm(x, p[prefix + "layer_norm.weight"], p.get(prefix + "layer_norm.bias"))
+  cn = layer_norm(c, p[prefix + "single_cond_layer_norm.weight"], p.get(prefix + "single_cond_layer_norm.bias"))
+  ws = np.asarray(p[prefix + "single_cond_scale.weight"], np.float64)
+  bs = np.asarray(p[prefix + "single_cond_scale.bias"], np.float64)
+  wb = np.asarray(p[prefix + "single_cond_bias.weight"], np.float64)
+  C = ws.shape[1]
+  xn = layer_norm(x)
+  return np.array([sigmoid(sum(cn[m] * ws[m, n] for m in range(len(cn))) + bs[n]) * xn[n]
+                   + sum(cn[m] * wb[m, n] for m in range(len(cn))) for n in range(C)])
+
+
+def cross_attention(x_q, x_k, mask_q, mask_k, p, pair_logits=None, cond_q=None, cond_k=None):
+  """transformer.py:549-585 (CrossAttention.forward) written per window, query, key and head in
+  float64: x_q ``[U, Q, C]``, x_k ``[U, K, C]``, masks ``[U, Q]`` / ``[U, K]``, pair_logits
+  ``[U, H, Q, K]``, conditions ``[U, Q, C]`` / ``[U, K, C]``.  The query side is normalised with
+  the ``q_layernorm.`` parameters and its condition, the key side with ``k_layernorm.`` and
+  its own; the gate comes from the normalised queries, the AdaLN-zero multiplier from the
+  query condition.  Returns (x_q + update, update)."""
+  xq = np.asarray(x_q, np.float64)
+  xk = np.asarray(x_k, np.float64)
+  U, Q, C = xq.shape
+  K = xk.shape[1]
+  wq = np.asarray(p["q_projection.weight"], np.float64)        # [C, H, D]
+  bq = np.asarray(p["q_projection.bias"], np.float64)          # [H, D]
+  wk = np.asarray(p["k_projection.weight"], np.float64)
+  wv = np.asarray(p["v_projection.weight"], np.float64)
+  wg = np.asarray(p["gating_query.weight"], np.float64)        # [C, H*D]
+  wt = np.asarray(p["zero_init.transition2.weight"], np.float64)   # [H*D, C]
+  H, D = wq.shape[1:]
+  upd = np.zeros_like(xq)
+  for u in range(U):
+    hq = [_adaln_row(xq[u, i], None if cond_q is None else np.asarray(cond_q[u, i], np.float64), p, "q_layernorm.")
+          for i in range(Q)]
+    hk = [_adaln_row(xk[u, j], None if cond_k is None else np.asarray(cond_k[u, j], np.float64), p, "k_layernorm.")
+          for j in range(K)]
+    for i in range(Q):
+      o = np.zeros(H * D)
+      for h in range(H):
+        q = np.array([sum(hq[i][c] * wq[c, h, d] for c in range(C)) + bq[h, d] for d in range(D)])
+        ks = [np.array([sum(hk[j][c] * wk[c, h, d] for c in range(C)) for d in range(D)]) for j in range(K)]
+        vs = [np.array([sum(hk[j][c] * wv[c, h, d] for c in range(C)) for d in range(D)]) for j in range(K)]
+        valid = [bool(mask_q[u, i]) and bool(mask_k[u, j]) for j in range(K)]
+        logits = [sum(q[d] * ks[j][d] for d in range(D)) / np.sqrt(D)
+                  + (0.0 if pair_logits is None else float(pair_logits[u, h, i, j])) for j in range(K)]
+        if any(valid):
+          m = max(l for l, ok in zip(logits, valid) if ok)
+          e = [np.exp(l - m) if ok else 0.0 for l, ok in zip(logits, valid)]
+        else:
+          e = [1.0] * K                                        # every logit is the same -max
+        tot = sum(e)
+        for d in range(D):
+          o[h * D + d] = sum(e[j] * vs[j][d] for j in range(K)) / tot
+      g = np.array([sigmoid(sum(hq[i][c] * wg[c, n] for c in range(C))) for n in range(H * D)])
+      y = np.array([sum(o[n] * g[n] * wt[n, c] for n in range(H * D)) for c in range(C)])
+      if cond_q is not None:
+        cq = np.asarray(cond_q[u, i], np.float64)
+        wz = np.asarray(p["zero_init.adaptive_zero_cond.weight"], np.float64)
+        bz = np.asarray(p["zero_init.adaptive_zero_cond.bias"], np.float64)
+        y = y * np.array([sigmoid(sum(cq[m] * wz[m, c] for m in range(len(cq))) + bz[c]) for c in range(C)])
+      upd[u, i] = y
+  return xq + upd, upd

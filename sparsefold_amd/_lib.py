@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -31,6 +31,7 @@ class AttentionArgs(C.Structure):
       ("mask_k", _vp), ("mk_s", _i64 * 3),
       ("gate", _vp), ("g_s", _i64 * 4),
       ("out", _vp), ("o_s", _i64 * 4),
+      ("schedule", _i32),
   ]
 
 
@@ -68,6 +69,7 @@ class TriangleArgs(C.Structure):
       ("ln_w", _vp), ("ln_b", _vp),
       ("w_qkvgb", _vp), ("w_o", _vp),
       ("out", _vp),
+      ("fixup_sum_limit", _f32),
   ]
 
 

@@ -41,7 +41,7 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           mask_q: torch.Tensor | None = None,
                           mask_k: torch.Tensor | None = None,
                           bias: torch.Tensor | None = None,
-                          *, gate: torch.Tensor | None = None) -> torch.Tensor:
+                          *, gate: torch.Tensor | None = None, schedule: int = 0) -> torch.Tensor:
   if q.ndim < 3 or k.ndim < 3 or v.ndim < 3:
     raise ValueError("dot_product_attention: q, k, v need (..., L, H, D) layouts")
   dtype = q.dtype
@@ -75,5 +75,5 @@ def dot_product_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     g5 = _as5(gate.to(bf).reshape(*batch, Q, H, Dv), batch, b0, b1)
   out = torch.empty((*batch, Q, H, Dv), dtype=bf, device=q.device)
   ops.attention(q5, k5, v5, scale=scale, bias=bias5, mask_q=mq5, mask_k=mk5, gate=g5,
-                out=out.view(b0, b1, Q, H, Dv))
+                out=out.view(b0, b1, Q, H, Dv), schedule=schedule)
   return out if dtype == bf else out.to(dtype)

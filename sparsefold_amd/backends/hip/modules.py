@@ -551,11 +551,15 @@ class TriangleMultiplicationHipMixin:
     self._native_prepared = True
     return True
 
+  # incoming edges, in the config's form and in the per-channel form the reference module stores
+  # (blocks.py:447-451)
+  INCOMING_EQUATIONS = ("...kjc,...kic->...ijc", "...ckj,...cki->...cij")
+
   @_require_native_preparation
+  @graphs.graphed
   def forward(self, act: torch.Tensor, mask: torch.Tensor, *, add_residual: bool = True) -> torch.Tensor:
-    # not graph-captured: the channel products are a BLAS call
     w = {k: getattr(self, "_hip_" + k) for k in ("ln_w", "ln_b", "w_glu", "cn_w", "cn_b", "w_out", "w_gate")}
-    out = ops.triangle_multiplication(act, mask, w, incoming=self.equation == "...kjc,...kic->...ijc",
+    out = ops.triangle_multiplication(act, mask, w, incoming=self.equation in self.INCOMING_EQUATIONS,
                                       add_residual=add_residual)
     return out.to(act.dtype)
 

@@ -82,12 +82,14 @@ def _rows(t: torch.Tensor, last: int) -> torch.Tensor:
 # attention core
 # ---------------------------------------------------------------------------------------
 
-def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gate=None, out=None):
+def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gate=None, out=None,
+              schedule: int = 0):
   """Core launch on 2-level batched views.
 
   q ``[B0,B1,Q,H,D]``, k ``[B0,B1,K,H,D]``, v ``[B0,B1,K,H,Dv]``, gate like the output
   ``[B0,B1,Q,H,Dv]``; bias ``[B0,B1,H,Q,K]`` (zero strides allowed), masks ``[B0,B1,Q]`` /
-  ``[B0,B1,K]`` uint8.  All bf16 with unit last stride.  Returns ``out``.
+  ``[B0,B1,K]`` uint8.  All bf16 with unit last stride.  ``schedule``: 0 chooses the work
+  decomposition from the sizes, 1 / 2 force shared-tile / per-wave tasks.  Returns ``out``.
   """
   dev = _require_cuda(q, k, v, bias, mask_q, mask_k, gate, out)
   _require(q.ndim == 5 and k.ndim == 5 and v.ndim == 5, "attention: q/k/v must be [B0,B1,L,H,D]")
@@ -121,6 +123,8 @@ def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gat
     _require(tuple(gate.shape) == (B0, B1, Q, H, Dv), f"attention: gate shape {tuple(gate.shape)}")
     a.gate, a.g_s = _vp(gate), (C.c_int64 * 4)(*gate.stride()[:4])
   a.out, a.o_s = _vp(out), (C.c_int64 * 4)(*out.stride()[:4])
+  _require(schedule in (0, 1, 2), f"attention: schedule {schedule} is not 0, 1 or 2")
+  a.schedule = schedule
   lib = _lib.load()
   _lib.check(lib.sf_hip_attention_fwd(C.byref(a), _stream(q)), "sf_hip_attention_fwd")
   return out
@@ -246,10 +250,11 @@ def triangle_workspace_bytes(N: int, C_: int, H: int, D: int) -> int:
 def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qkvgb: torch.Tensor,
                        w_o: torch.Tensor, *, num_head: int, transpose: bool, add_residual: bool = True,
                        workspace: torch.Tensor | None = None, stages: int = _lib.TRI_STAGE_ALL,
-                       out: torch.Tensor | None = None) -> torch.Tensor:
+                       out: torch.Tensor | None = None, fixup_sum_limit: float = 0.0) -> torch.Tensor:
   """GridSelfAttention on ``z [N, N, C]`` (bf16).  Weights packed as the C ABI documents.
   ``stages`` selects a subset of the pipeline (projection / attention / output projection)
-  against a caller-held ``workspace``."""
+  against a caller-held ``workspace``.  ``fixup_sum_limit`` > 0 lowers the weight-sum limit
+  above which a (row, head) is recomputed by the exact two-pass softmax (0 = the default 2^100)."""
   _require_cuda(z, seq_mask, ln_w, ln_b, w_qkvgb, w_o, workspace)
   _require(z.ndim == 3 and z.shape[0] == z.shape[1], f"triangle: z must be [N, N, C], got {tuple(z.shape)}")
   N, _, Cn = z.shape
@@ -272,6 +277,8 @@ def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qk
   a.transpose, a.add_residual = int(bool(transpose)), int(bool(add_residual))
   a.z, a.seq_mask, a.ln_w, a.ln_b = _vp(zc), _vp(m8), _vp(lw), _vp(lb)
   a.w_qkvgb, a.w_o, a.out = _vp(w_qkvgb), _vp(w_o), _vp(out)
+  _require(fixup_sum_limit >= 0.0, "triangle: fixup_sum_limit must be >= 0")
+  a.fixup_sum_limit = float(fixup_sum_limit)
   if stages == _lib.TRI_STAGE_ALL:
     rc = _lib.load().sf_hip_triangle_attn_fwd(C.byref(a), _vp(workspace), workspace.numel(), _stream(z))
   else:

@@ -677,8 +677,7 @@ int route(const sf_attention_args* a, bool allow_split, AttnRoute& r) {
   for (int s = 0; s < 4 && pl.vec_out && a->gate != nullptr; ++s) pl.vec_out = a->g_s[s] % 4 == 0;
   const int64_t bh = (int64_t)a->B0 * a->B1 * a->H;
   const int64_t groups = bh * ((pl.QB + 3) / 4);
-  r.shared = a->Q >= 128 && groups >= 512;
-  if (const char* e = getenv("SPARSEFOLD_HIP_ATTN_MODE")) r.shared = e[0] == 's';   // test hook
+  r.shared = a->schedule == 0 ? (a->Q >= 128 && groups >= 512) : a->schedule == 1;
   // Per-wave tasks on a grid too small for the GPU (single attention: 16 heads x 24 blocks =
   // 384 waves for 1024 SIMDs) split their key range into slices of >= 2 tiles, up to ~2048 waves;
   // a combine kernel merges the slices.  Needs a workspace (module-level entry points).

@@ -33,7 +33,6 @@
 //   3. tri_out_kernel    out = z + o W_o (blocks.py:291, :366), W_o resident in LDS.
 // Other head dims use the generic kernels (layer_norm, linear, attention_fwd, linear).
 #include <cmath>
-#include <cstdlib>
 #include <type_traits>
 
 #include "sf_common.h"
@@ -940,15 +939,10 @@ int persistent_groups(int items, int* items_per_wave) {
 }
 
 // Weight sum above which the attention kernel flags a (row, head) for the exact fix-up: 2^100,
-// or SPARSEFOLD_HIP_TRI_SUM_LIMIT (a positive finite float) so that tests can drive the fix-up
-// path with ordinary logits.  The result does not depend on it beyond rounding.
-float sum_limit() {
-  float v = 0x1p100f;
-  if (const char* e = getenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT")) {
-    const float f = strtof(e, nullptr);
-    if (f > 0.f && f <= v) v = f;
-  }
-  return v;
+// or the caller's smaller positive limit (tests drive the fix-up path with ordinary logits).
+float sum_limit(float requested) {
+  const float v = 0x1p100f;
+  return requested > 0.f && requested <= v ? requested : v;
 }
 
 int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_bytes, hipStream_t st, int stages) {
@@ -983,7 +977,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   if (stages & SF_TRI_STAGE_ATTEND) {
     TriAttnArgs aa{};
     aa.N = N; aa.NP = NP; aa.H = H; aa.transpose = a->transpose;
-    aa.sum_limit = sum_limit();
+    aa.sum_limit = sum_limit(a->fixup_sum_limit);
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     aa.flags = ws.flags;
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;   // a multiple of 64

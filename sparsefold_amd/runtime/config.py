@@ -1,107 +1,126 @@
-"""Runtime settings for backend selection -- mirror of ``src/sparsefold/runtime/config.py``.
+"""Runtime settings that select the attention path.
 
-Same API (``configure_runtime(**overrides)``, ``backend=`` alias, ``normalize_backend``,
-``get_runtime_options``, ``reset``, module attribute access) and the same environment
-variables (``SPARSEFOLD_*``, legacy ``AF3_*``), restricted to the settings that select the
-attention path.  The value sets are those of the reference (config.py:271-285) extended with
-the HIP backend: ``acclib_implementation`` (``[native] impl``) and ``sdpa_implementation``
-(``[precision] sdpa``) both accept ``"hip"``.
+Interface kept from the reference (``src/sparsefold/runtime/config.py``), because callers and
+configuration files depend on it:
+
+* ``configure_runtime(**settings)`` resolves every setting once (explicit values win over the
+  environment); ``backend=`` is accepted in place of ``acclib_implementation``;
+* the environment names ``SPARSEFOLD_<SETTING>`` and their deprecated ``AF3_<SETTING>`` forms;
+* module attribute access (``config.device``, ``config.acclib_implementation`` ...),
+  ``get_runtime_options()`` (an independent copy) and ``reset()``;
+* backend names: ``none`` means ``torch``, ``cpp`` is the deprecated name of ``vecops``.
+
+Only the settings that matter to the attention path are modelled.  The allowed values are the
+reference's (``src/sparsefold/config.py:271-285``) plus ``"hip"`` for both the native backend
+(``[native] impl``) and the SDPA implementation (``[precision] sdpa``).
 """
 from __future__ import annotations
 
-import copy
+import dataclasses
 import os
 import warnings
-from typing import Any
+from typing import Any, Callable
 
 SDPA_IMPLEMENTATIONS = frozenset({"math", "flash", "efficient", "hip"})
 BACKENDS = frozenset({"torch", "vecops", "hip"})
 
-# name -> (legacy env var, default); runtime/config.py:13-28
-_LEGACY: dict[str, tuple[str, Any]] = {
-    "device": ("AF3_DEVICE", "cpu"),
-    "enable_sharding": ("AF3_ENABLE_SHARDING", "0"),
-    "acclib_implementation": ("AF3_ACCLIB_IMPLEMENTATION", "torch"),
-    "native_ops": ("AF3_NATIVE_OPS", "*"),
-    "sdpa_implementation": ("AF3_SDPA_IMPLEMENTATION", "math"),
-    "diffusion_precision": ("AF3_DIFFUSION_PRECISION", "fp32"),
-    # HIP backend only, no reference counterpart: replay repeated module calls as HIP graphs
-    "hip_graphs": ("AF3_HIP_GRAPHS", "0"),
-}
-_BOOL_FIELDS = {"enable_sharding", "hip_graphs"}
-_state: dict[str, Any] | None = None
-
 
 def normalize_backend(value: str) -> str:
-  """runtime/config.py:42-49: ``none`` -> ``torch``, deprecated ``cpp`` -> ``vecops``."""
-  value = value.lower()
-  if value == "none":
-    return "torch"
-  if value == "cpp":
-    warnings.warn("backend 'cpp' is deprecated; use 'vecops'", DeprecationWarning, stacklevel=2)
+  """Canonical backend name: lower case, ``none`` -> ``torch``, ``cpp`` -> ``vecops``."""
+  name = str(value).strip().lower()
+  aliases = {"none": "torch"}
+  if name == "cpp":
+    warnings.warn("the backend name 'cpp' is deprecated; select 'vecops'", DeprecationWarning, stacklevel=2)
     return "vecops"
-  return value
+  return aliases.get(name, name)
 
 
-def _environment_value(name: str) -> Any:
-  legacy, default = _LEGACY[name]
-  current = legacy.replace("AF3_", "SPARSEFOLD_", 1)
-  if current in os.environ:
-    raw = os.environ[current]
-  elif legacy in os.environ:
-    raw = os.environ[legacy]
-    warnings.warn(f"{legacy} is deprecated; use {current} or configure_runtime()",
-                  DeprecationWarning, stacklevel=3)
-  else:
-    raw = default
-  if name == "native_ops":
-    return [p.strip() for p in raw.split(",") if p.strip()]
-  if name in _BOOL_FIELDS:
-    return str(raw).lower() in {"1", "true", "yes", "on"}
-  if name == "acclib_implementation":
-    return normalize_backend(raw)
-  return raw
+def _flag(text: str) -> bool:
+  return str(text).strip().lower() in ("1", "true", "yes", "on")
 
 
-def _validate(state: dict[str, Any]) -> None:
-  if state["sdpa_implementation"] not in SDPA_IMPLEMENTATIONS:
-    raise ValueError(f"Unsupported SDPA implementation: {state['sdpa_implementation']!r}")
-  if state["acclib_implementation"] not in BACKENDS:
-    raise ValueError(f"Unsupported backend: {state['acclib_implementation']!r}")
+def _names(text: str) -> list[str]:
+  return [item.strip() for item in str(text).split(",") if item.strip()]
 
 
-def configure_runtime(**overrides: Any) -> None:
-  """runtime/config.py:93-111.  ``backend=`` is an alias for ``acclib_implementation``."""
-  global _state
-  if "backend" in overrides:
-    if "acclib_implementation" in overrides:
-      raise ValueError("Pass either backend or acclib_implementation")
-    overrides["acclib_implementation"] = overrides.pop("backend")
-  unknown = overrides.keys() - _LEGACY.keys()
-  if unknown:
-    raise TypeError(f"Unknown runtime settings: {sorted(unknown)}")
-  state = {name: _environment_value(name) for name in _LEGACY}
-  state.update(overrides)
-  state["acclib_implementation"] = normalize_backend(state["acclib_implementation"])
-  state["native_ops"] = list(state["native_ops"])
-  _validate(state)
-  _state = state
+@dataclasses.dataclass(frozen=True)
+class _Setting:
+  """One runtime setting: its environment suffix, default text and parser."""
+  env: str
+  default: str
+  parse: Callable[[str], Any] = str
+
+
+_SETTINGS: dict[str, _Setting] = {
+    "device": _Setting("DEVICE", "cpu"),
+    "enable_sharding": _Setting("ENABLE_SHARDING", "0", _flag),
+    "acclib_implementation": _Setting("ACCLIB_IMPLEMENTATION", "torch", normalize_backend),
+    "native_ops": _Setting("NATIVE_OPS", "*", _names),
+    "sdpa_implementation": _Setting("SDPA_IMPLEMENTATION", "math"),
+    "diffusion_precision": _Setting("DIFFUSION_PRECISION", "fp32"),
+    # no counterpart in the reference: replay repeated HIP module calls as captured graphs
+    "hip_graphs": _Setting("HIP_GRAPHS", "0", _flag),
+}
+
+_resolved: dict[str, Any] | None = None
+
+
+def _from_environment(name: str) -> Any:
+  spec = _SETTINGS[name]
+  current, legacy = "SPARSEFOLD_" + spec.env, "AF3_" + spec.env
+  text = os.environ.get(current)
+  if text is None and legacy in os.environ:
+    warnings.warn(f"{legacy} is deprecated; set {current} or call configure_runtime()",
+                  DeprecationWarning, stacklevel=4)
+    text = os.environ[legacy]
+  return spec.parse(spec.default if text is None else text)
+
+
+def _check(settings: dict[str, Any]) -> None:
+  if settings["sdpa_implementation"] not in SDPA_IMPLEMENTATIONS:
+    raise ValueError(f"Unsupported SDPA implementation {settings['sdpa_implementation']!r}; "
+                     f"choose one of {sorted(SDPA_IMPLEMENTATIONS)}")
+  if settings["acclib_implementation"] not in BACKENDS:
+    raise ValueError(f"Unsupported backend {settings['acclib_implementation']!r}; choose one of {sorted(BACKENDS)}")
+
+
+def configure_runtime(**settings: Any) -> None:
+  """Resolves all settings: the given ones, the environment for the rest."""
+  global _resolved
+  if "backend" in settings:
+    if "acclib_implementation" in settings:
+      raise ValueError("Pass either backend or acclib_implementation, not both")
+    settings["acclib_implementation"] = settings.pop("backend")
+  extra = sorted(set(settings) - set(_SETTINGS))
+  if extra:
+    raise TypeError(f"Unknown runtime settings: {extra}")
+  resolved = {name: settings[name] if name in settings else _from_environment(name) for name in _SETTINGS}
+  resolved["acclib_implementation"] = normalize_backend(resolved["acclib_implementation"])
+  resolved["native_ops"] = list(resolved["native_ops"])
+  _check(resolved)
+  _resolved = resolved
+
+
+def _value(name: str) -> Any:
+  return _resolved[name] if _resolved is not None else _from_environment(name)
 
 
 def get_runtime_options() -> dict[str, Any]:
-  return copy.deepcopy({name: __getattr__(name) for name in _LEGACY})
+  """A copy of the current settings that ``configure_runtime(**options)`` accepts back."""
+  return {name: (list(v) if isinstance(v, list) else v) for name, v in ((n, _value(n)) for n in _SETTINGS)}
 
 
 def uses_hip() -> bool:
-  return __getattr__("acclib_implementation") == "hip"
+  return _value("acclib_implementation") == "hip"
 
 
 def reset() -> None:
-  global _state
-  _state = None
+  """Forgets explicit settings: values come from the environment again."""
+  global _resolved
+  _resolved = None
 
 
 def __getattr__(name: str) -> Any:
-  if name in _LEGACY:
-    return _state[name] if _state is not None else _environment_value(name)
+  if name in _SETTINGS:
+    return _value(name)
   raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

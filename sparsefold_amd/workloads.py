@@ -115,6 +115,19 @@ def make_diffusion(N: int, *, S: int = 5, C: int = 768, C_cond: int = 384, H: in
   return mod, act, cond, bias, mask
 
 
+def make_diffusion_stack(N: int, *, S: int = 5, L: int = 24, C: int = 768, C_cond: int = 384, H: int = 16,
+                         seed: int = 4, dtype=torch.bfloat16):
+  """L diffusion-transformer attention blocks, each with its own seeded weights (block l from
+  seed + 1000 + l), and the inputs of make_diffusion(N, seed=seed)."""
+  mod0, act, cond, bias, mask = make_diffusion(N, S=S, C=C, C_cond=C_cond, H=H, seed=seed, dtype=dtype)
+  mods = [mod0]
+  for layer in range(1, L):
+    m = M.SelfAttention(M.SelfAttention.Config(num_head=H), M.GlobalConfig(), num_channels=C,
+                        single_cond_size=C_cond, name="diffusion_transformer")
+    mods.append(fill_parameters(m, seed + 1000 + layer))
+  return mods, act, cond, bias, mask
+
+
 @dataclasses.dataclass
 class WindowLayout:
   """Key windows for 32-atom query blocks: window u covers atoms [32u - 48, 32u + 80)."""

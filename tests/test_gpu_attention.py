@@ -16,8 +16,10 @@ def _run(q, k, v, **kw):
   mq, mk = kw.pop("mask_q", None), kw.pop("mask_k", None)
   bias = kw.pop("bias", None)
   gate = kw.pop("gate", None)
+  schedule = kw.pop("schedule", 0)
   out = hip_dpa(cast(q), cast(k), cast(v), mask_q=None if mq is None else mq.to(DEV),
-                mask_k=None if mk is None else mk.to(DEV), bias=cast(bias), gate=cast(gate), **kw)
+                mask_k=None if mk is None else mk.to(DEV), bias=cast(bias), gate=cast(gate),
+                schedule=schedule, **kw)
   torch.cuda.synchronize()
   ref = oracle_dpa(bf16_round(q), bf16_round(k), bf16_round(v), mask_q=mq, mask_k=mk,
                    bias=None if bias is None else bf16_round(bias), **kw)
@@ -121,12 +123,11 @@ def test_fp32_inputs_round_trip_dtype():
 
 
 @pytest.mark.parametrize("mode", ["s", "p"])
-def test_reference_point_moves_after_the_first_tile(mode, monkeypatch):
+def test_reference_point_moves_after_the_first_tile(mode):
   """The softmax keeps the first 64-key tile's maximum as its reference point and moves it only
   when a later tile's weight mass passes 2^60.  Three ways to get there, checked against the
   oracle: the first tile fully masked, logits 90 (log2 units) higher in a later tile, and both
   in one batch (shared-tile and per-wave task modes)."""
-  monkeypatch.setenv("SPARSEFOLD_HIP_ATTN_MODE", mode)
   gen = torch.Generator().manual_seed(99)
   B, Q, K, H, D = 3, 160, 320, 2, 32
   q = torch.randn(B, Q, H, D, generator=gen)
@@ -138,5 +139,5 @@ def test_reference_point_moves_after_the_first_tile(mode, monkeypatch):
   bias[1, :, :, 200:] += 90.0 / 1.4426950408889634       # batch 1: +90 in log2 units after tile 3
   mk[2, :70] = False                                     # batch 2: both
   bias[2, :, :, 250:] += 70.0 / 1.4426950408889634
-  out, ref = _run(q, k, v, mask_k=mk, bias=bias)
+  out, ref = _run(q, k, v, mask_k=mk, bias=bias, schedule=1 if mode == "s" else 2)
   assert_close_bf16(out, ref, f"reference point moves ({mode})")

@@ -78,9 +78,17 @@ def test_triangle_edge_sizes(transpose, N, padded):
   assert_close_bf16(upd, ref, f"triangle N={N} transpose={transpose}", max_abs=2e-2 * ref.abs().max().item())
 
 
-@pytest.mark.parametrize("limit", ["1", "1500"])
+def _triangle_update(hip, z, seq, **kw):
+  """The module's update through the C entry point with its packed weights (the module's own
+  forward, plus the explicit test controls of ops.triangle_attention)."""
+  from sparsefold_amd.backends.hip import ops
+  return ops.triangle_attention(z, seq, hip._hip_ln_w, hip._hip_ln_b, hip._hip_w_qkvgb, hip._hip_w_o,
+                                num_head=hip.config.num_head, transpose=hip.transpose, add_residual=False, **kw)
+
+
+@pytest.mark.parametrize("limit", [1.0, 1500.0])
 @pytest.mark.parametrize("transpose", [False, True])
-def test_triangle_exact_fixup(transpose, limit, monkeypatch):
+def test_triangle_exact_fixup(transpose, limit):
   """The attention kernel exponentiates logits against a fixed reference point and flags a
   (row, head) whose weight sum leaves [2^-100, limit]; the fix-up kernel recomputes those with
   an exact two-pass softmax.  A limit of 1 flags every row; 1500 lies near the 90th percentile
@@ -89,16 +97,16 @@ def test_triangle_exact_fixup(transpose, limit, monkeypatch):
   must match the oracle either way."""
   mod, z, seq = W.make_triangle(200, transpose=transpose, padded=True, seed=11, sharp=True)
   hip = _prepared(mod)
-  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", raising=False)
-  upd_default = hip(z.to(DEV), seq.to(DEV), add_residual=False)
-  monkeypatch.setenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", limit)
-  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  upd_default = hip(zd, sd, add_residual=False)
+  assert torch.equal(_triangle_update(hip, zd, sd), upd_default)
+  upd = _triangle_update(hip, zd, sd, fixup_sum_limit=limit)
   # the exact path keeps fp32 weights (the fast path rounds them to bf16), so the attention rows
   # it recomputed differ from the default call: every unmasked row at limit 1, some at 1500
   rows = (upd != upd_default).transpose(0, 1) if transpose else (upd != upd_default)
   changed = rows.flatten(1).any(1).cpu()
   assert not changed[~seq].any()
-  if limit == "1":
+  if limit == 1.0:
     assert changed[seq].all()
   else:
     assert 0 < int(changed[seq].sum()) < int(seq.sum())
@@ -106,8 +114,7 @@ def test_triangle_exact_fixup(transpose, limit, monkeypatch):
   assert_close_bf16(upd, ref, f"triangle exact fix-up N=200 limit={limit} transpose={transpose}",
                     max_abs=2e-2 * ref.abs().max().item())
   # the flags were cleared: the next default call is the fast path again, bit for bit
-  monkeypatch.delenv("SPARSEFOLD_HIP_TRI_SUM_LIMIT", raising=False)
-  assert torch.equal(hip(z.to(DEV), seq.to(DEV), add_residual=False), upd_default)
+  assert torch.equal(hip(zd, sd, add_residual=False), upd_default)
 
 
 @pytest.mark.parametrize("transpose", [False, True])
@@ -133,6 +140,70 @@ def test_triangle_c3_n768_sampled_rows(transpose):
   ref = OM.grid_self_attention_rows(z.float(), seq, _params(hip), transpose=transpose, rows=rows)
   got = upd[:, rows].transpose(0, 1) if transpose else upd[rows]
   assert_close_bf16(got, ref, f"C3 triangle N=768 rows transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+_N768_CACHE: dict = {}
+
+
+def _n768_sharp_padded(transpose: bool):
+  """HIP update, oracle inputs and the shared LN / bias prologue of the sharp, padded N=768
+  triangle case (computed once per node for the row-range tests below)."""
+  if transpose not in _N768_CACHE:
+    from oracle.primitives import layer_norm, linear
+    mod, z, seq = W.make_triangle(768, transpose=transpose, padded=True, seed=17, sharp=True)
+    hip = _prepared(mod)
+    print(f"[case] triangle N=768 sharp padded transpose={transpose}", flush=True)
+    upd = hip(z.to(DEV), seq.to(DEV), add_residual=False).float().cpu()
+    p = _params(hip)
+    zf = z.float()
+    x = layer_norm(zf, p["act_norm.weight"], p["act_norm.bias"])
+    bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
+    _N768_CACHE.clear()
+    _N768_CACHE[transpose] = (upd.transpose(0, 1) if transpose else upd, zf, seq, p, bias)
+  return _N768_CACHE[transpose]
+
+
+# rows of the first and the last task of every persistent attention workgroup at N=768 (256
+# workgroups x 9 tasks of 4 rows; task t of XCD x covers rows 4 ((t/3) mod 192)): the prologue
+# with nothing to overlap and the final drain
+_N768_FIRST_LAST = list(range(0, 44)) + list(range(340, 428)) + list(range(724, 768))
+
+
+@pytest.mark.parametrize("transpose,rows", [(False, (0, 256)), (False, (256, 512)), (False, (512, 768)),
+                                            (True, "first_last")])
+def test_triangle_c3_n768_sharp_padded_rows(transpose, rows):
+  """N=768 (the headline size) with sharp weights (a far-from-uniform softmax) and the last 76
+  tokens padded, against the oracle row by row: every row of the starting node -- so every task
+  boundary, where the next task's first tile and Q operands are loaded during the last tile --
+  and, for the ending node, the rows of every workgroup's first and last task.  Covers the
+  masked rows (fix-up kernel) and the padded keys of the last 64-key tile."""
+  got_all, zf, seq, p, bias = _n768_sharp_padded(transpose)
+  assert torch.isfinite(got_all).all()
+  sel = list(range(*rows)) if rows != "first_last" else _N768_FIRST_LAST
+  refs = [OM.grid_self_attention_rows(zf, seq, p, transpose=transpose, rows=sel[i:i + 32], bias=bias)
+          for i in range(0, len(sel), 32)]
+  ref = torch.cat(refs)
+  got = got_all[sel]
+  assert_close_bf16(got, ref, f"C3 triangle N=768 sharp padded rows {rows} transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+  masked = [i for i, r in enumerate(sel) if not bool(seq[r])]
+  if masked:                          # padded tokens attend uniformly: the mean of V, gated and projected
+    assert got[masked].abs().max() > 0
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_n768_exact_fixup_every_row(transpose):
+  """N=768 with a weight-sum limit of 1: every unmasked (row, head) is flagged by the attention
+  kernel and recomputed by the exact two-pass fix-up kernel."""
+  mod, z, seq = W.make_triangle(768, transpose=transpose, padded=True, seed=19, sharp=True)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  upd = _triangle_update(hip, zd, sd, fixup_sum_limit=1.0).float().cpu()
+  rows = list(range(0, 768, 37)) + [767]
+  ref = OM.grid_self_attention_rows(z.float(), seq, _params(hip), transpose=transpose, rows=rows)
+  got = upd[:, rows].transpose(0, 1) if transpose else upd[rows]
+  assert_close_bf16(got, ref, f"triangle N=768 exact path transpose={transpose}",
                     max_abs=2e-2 * ref.abs().max().item())
 
 
@@ -197,6 +268,60 @@ def test_windowed_atom_attention(atoms, S, sharp):
   upd = hip.forward_indexed(*args, add_residual=False)
   d_ref = OM.windowed_cross_attention(*oargs, return_update=True)
   assert_close_bf16(upd, d_ref, "window update", max_abs=2e-2 * d_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False)])
+def test_cross_attention_explicit_keys(atoms, S, sharp):
+  """The reference's own call into CrossAttention (transformer.py:671-683): keys gathered by
+  convert() first, then cross_attention(x_q, x_k, ...).  That is the module entry with explicit
+  key rows (no gather index); it must match forward_indexed on the same inputs and the oracle."""
+  from sparsefold_amd.backends.hip import ops
+  mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5, sharp=sharp)
+  hip = _prepared(mod)
+  U = atoms // 32
+  ad, qcd, kcd, bd = act.to(DEV), qc.to(DEV), kc.to(DEV), bias.to(DEV)
+  qm, km = lay.queries_mask.to(DEV), lay.keys_mask.to(DEV)
+  keys = ops.window_gather(ad.reshape(S, U * 32, 128), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV))
+  keys = keys.view(S, U, 128, 128)
+  # the gather is the reference's convert (its known answers pin the oracle's)
+  ref_keys = OM.atom_layout_convert(lay.gather_idxs, lay.gather_mask, (U, 32), act.float(), layout_axes=(-3, -2))
+  assert torch.equal(keys.float().cpu(), ref_keys)
+  out = hip(ad, keys, qm, km, bd, qcd, kcd)
+  idx = hip.forward_indexed(ad, qm, lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV), km, qcd, kcd, bd)
+  assert torch.equal(out, idx), "explicit keys and the indexed entry must run the same arithmetic"
+  p = _params(hip)
+  oargs = (act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc.float(), kc.float(),
+           bias.float(), p)
+  ref = OM.windowed_cross_attention(*oargs)
+  assert_close_bf16(out, ref, f"cross attention explicit keys atoms={atoms}")
+  upd = hip(ad, keys, qm, km, bd, qcd, kcd, add_residual=False)
+  d_ref = OM.windowed_cross_attention(*oargs, return_update=True)
+  assert_close_bf16(upd, d_ref, "cross attention explicit keys update", max_abs=2e-2 * d_ref.abs().max().item())
+
+
+def test_cross_attention_op_level_path():
+  """Arguments outside the module entry's contract (a per-sample key condition [S, U, Kw, C])
+  take the op-level composition (AdaLN, linear, attention, linear kernels); with the condition
+  identical across samples it must agree with the module entry and the oracle."""
+  from sparsefold_amd.backends.hip import ops
+  S, atoms = 2, 256
+  mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=29, sharp=True)
+  hip = _prepared(mod)
+  U = atoms // 32
+  ad, qcd, kcd, bd = act.to(DEV), qc.to(DEV), kc.to(DEV), bias.to(DEV)
+  qm, km = lay.queries_mask.to(DEV), lay.keys_mask.to(DEV)
+  keys = ops.window_gather(ad.reshape(S, U * 32, 128), lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV))
+  keys = keys.view(S, U, 128, 128)
+  kc4 = kcd.unsqueeze(0).expand(S, U, 128, 128).contiguous()
+  assert not hip._native_ok(U, 32, 128, qm, km, bd, qcd, kc4)
+  upd_op = hip(ad, keys, qm, km, bd, qcd, kc4, add_residual=False)
+  upd_mod = hip(ad, keys, qm, km, bd, qcd, kcd, add_residual=False)
+  p = _params(hip)
+  d_ref = OM.windowed_cross_attention(act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask,
+                                      lay.keys_mask, qc.float(), kc.float(), bias.float(), p, return_update=True)
+  tol = 2e-2 * d_ref.abs().max().item()
+  assert_close_bf16(upd_op, d_ref, "cross attention op-level path", max_abs=tol)
+  assert_close_bf16(upd_op, upd_mod.float().cpu(), "op-level vs module entry", max_abs=tol)
 
 
 @pytest.mark.parametrize("transpose", [False, True])

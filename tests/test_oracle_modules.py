@@ -206,3 +206,130 @@ def test_triangle_multiplication_incoming_is_outgoing_on_transpose():
   inc = OM.triangle_multiplication(z, mask, p, equation=mod.EQUATIONS[1])
   out_t = OM.triangle_multiplication(z.transpose(0, 1), mask, p, equation=mod.EQUATIONS[0]).transpose(0, 1)
   torch.testing.assert_close(inc, out_t, rtol=1e-12, atol=1e-12)
+
+
+# --------------------------------------------------------------------------------------
+# Pair-logit packs and CrossAttention against float64 per-element loops (oracle/brute.py)
+# --------------------------------------------------------------------------------------
+
+def _npd(p):
+  return {k: v.double().numpy() for k, v in p.items()}
+
+
+@pytest.mark.parametrize("shape", [(3, 4), (4, 4)])
+def test_transformer_pair_logits_matches_brute_force(shape):
+  """transformer.py:430-438: stack over super-blocks of rearrange(LN_g(pc) W, "b n s h -> s h b n").
+  S=2 and H=3 differ, so an "h s" order is a shape mismatch; on the square case the values of a
+  swapped "n b" order differ (pair_cond[b, n] != pair_cond[n, b])."""
+  from sparsefold_amd import modules as M
+  mod = M.TransformerPairLogits(num_blocks=4, super_block_size=2, num_head=3, pair_cond_size=8)
+  W.fill_parameters(mod, 31, sharp=True)
+  pc = torch.randn(*shape, 8, generator=torch.Generator().manual_seed(32))
+  p = _sd(mod)
+  out = OM.transformer_pair_logits(pc, p, 2, None)
+  ref = brute.transformer_pair_logits(pc.numpy(), _npd(p))
+  assert out.shape == ref.shape == (2, 2, 3) + shape
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)
+  if shape[0] == shape[1]:
+    assert not np.allclose(out.numpy(), ref.swapaxes(-1, -2), atol=1e-3)
+
+
+def test_cross_att_pair_logits_matches_brute_force():
+  """transformer.py:655-662: rearrange(LN_g(pc) W, "s q k b h -> b s h q k") with every axis a
+  different size, so any other order is a shape mismatch."""
+  from sparsefold_amd import modules as M
+  mod = M.CrossAttTransformerPairLogits(num_blocks=3, num_head=2, pair_cond_size=8)
+  W.fill_parameters(mod, 33, sharp=True)
+  pc = torch.randn(4, 5, 6, 8, generator=torch.Generator().manual_seed(34))
+  p = _sd(mod)
+  out = OM.cross_att_pair_logits(pc, p)
+  ref = brute.cross_att_pair_logits(pc.numpy(), _npd(p))
+  assert out.shape == ref.shape == (3, 4, 2, 5, 6)
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+def _small_cross(seed: int, Q: int = 4, K: int = 4, C: int = 8, H: int = 2):
+  from sparsefold_amd import modules as M
+  mod = M.CrossAttention(M.CrossAttention.Config(num_head=H, key_dim=C, value_dim=C), M.GlobalConfig(),
+                         num_channels=C, name="pin")
+  W.fill_parameters(mod, seed, sharp=True)
+  g = torch.Generator().manual_seed(seed + 1)
+  U = 2
+  xq, xk = torch.randn(U, Q, C, generator=g), torch.randn(U, K, C, generator=g)
+  cq, ck = torch.randn(U, Q, C, generator=g), torch.randn(U, K, C, generator=g)
+  bias = 2.0 * torch.randn(U, H, Q, K, generator=g)
+  mq = torch.ones(U, Q, dtype=torch.bool)
+  mk = torch.ones(U, K, dtype=torch.bool)
+  mq[1, -1] = False                  # a query with no valid key: uniform over all keys
+  mk[0, 1] = False
+  mk[1, 0] = False
+  return mod, xq, xk, mq, mk, bias, cq, ck
+
+
+@pytest.mark.parametrize("Q,K", [(4, 4), (3, 5)])
+def test_cross_attention_matches_brute_force(Q, K):
+  """transformer.py:549-585 against per-element float64 loops.  Q == K keeps a swapped
+  q_layernorm / k_layernorm prefix, or a swapped condition side, shape-compatible, so that only
+  the values can reveal it -- both plants below must fail the comparison."""
+  mod, xq, xk, mq, mk, bias, cq, ck = _small_cross(35, Q, K)
+  p = _sd(mod)
+  out = OM.cross_attention(xq, xk, mq, mk, p, pair_logits=bias, single_cond_q=cq, single_cond_k=ck)
+  ref, upd = brute.cross_attention(xq.numpy(), xk.numpy(), mq.numpy(), mk.numpy(), _npd(p), bias.numpy(),
+                                   cq.numpy(), ck.numpy())
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=1e-5)
+  got_u = OM.cross_attention(xq, xk, mq, mk, p, pair_logits=bias, single_cond_q=cq, single_cond_k=ck,
+                             return_update=True)
+  np.testing.assert_allclose(got_u.numpy(), upd, rtol=1e-4, atol=1e-5)
+  # the fully masked query attends uniformly: its update is the gated, projected mean of V
+  assert np.abs(upd[1, -1]).max() > 0
+  if Q != K:
+    return
+  # planted mistakes in the oracle's inputs: the brute force must tell them apart
+  swapped = {}
+  for k, v in p.items():
+    if k.startswith("q_layernorm."):
+      swapped["k_layernorm." + k[len("q_layernorm."):]] = v
+    elif k.startswith("k_layernorm."):
+      swapped["q_layernorm." + k[len("k_layernorm."):]] = v
+    else:
+      swapped[k] = v
+  bad = OM.cross_attention(xq, xk, mq, mk, swapped, pair_logits=bias, single_cond_q=cq, single_cond_k=ck,
+                           return_update=True)
+  assert not np.allclose(bad.numpy(), upd, rtol=1e-3, atol=1e-4)
+  bad = OM.cross_attention(xq, xk, mq, mk, p, pair_logits=bias, single_cond_q=ck, single_cond_k=cq,
+                           return_update=True)
+  assert not np.allclose(bad.numpy(), upd, rtol=1e-3, atol=1e-4)
+
+
+def test_windowed_cross_attention_matches_brute_force_over_converted_keys():
+  """One CrossAttTransformer block's attention (transformer.py:668-682): the keys are the
+  reference's convert() of the queries, then CrossAttention -- against the brute force applied
+  to the same gathered keys (the gather itself is pinned by the reference's convert known answers)."""
+  from sparsefold_amd import modules as M
+  C, H, Qw, Kw, U = 8, 2, 4, 6, 3
+  mod = M.CrossAttention(M.CrossAttention.Config(num_head=H, key_dim=C, value_dim=C), M.GlobalConfig(),
+                         num_channels=C, name="pin")
+  W.fill_parameters(mod, 36, sharp=True)
+  g = torch.Generator().manual_seed(37)
+  xq = torch.randn(U, Qw, C, generator=g)
+  start = torch.arange(U) * Qw + Qw // 2 - Kw // 2
+  idx = start[:, None] + torch.arange(Kw)[None]
+  gmask = (idx >= 0) & (idx < U * Qw)
+  idx = idx.clamp(0, U * Qw - 1).to(torch.int32)
+  qmask = torch.ones(U, Qw, dtype=torch.bool)
+  qmask[-1, -1] = False
+  kmask = gmask & qmask.reshape(-1)[idx.long()]
+  cq = torch.randn(U, Qw, C, generator=g)
+  ck = OM.atom_layout_convert(idx, gmask, (U, Qw), cq, layout_axes=(0, 1))
+  bias = torch.randn(U, H, Qw, Kw, generator=g)
+  p = _sd(mod)
+  out = OM.windowed_cross_attention(xq, qmask, idx, gmask, kmask, cq, ck, bias, p, return_update=True)
+  keys = np.zeros((U, Kw, C))
+  flat = xq.reshape(U * Qw, C).numpy()
+  for u in range(U):
+    for j in range(Kw):
+      if gmask[u, j]:
+        keys[u, j] = flat[int(idx[u, j])]
+  _, upd = brute.cross_attention(xq.numpy(), keys, qmask.numpy(), kmask.numpy(), _npd(p), bias.numpy(),
+                                 cq.numpy(), ck.numpy())
+  np.testing.assert_allclose(out.numpy(), upd, rtol=1e-4, atol=1e-5)
