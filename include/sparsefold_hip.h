@@ -259,6 +259,18 @@ size_t sf_hip_self_attention_workspace_bytes(const sf_self_attention_args* a);
 int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Allocation-free form of sf_hip_self_attention_fwd: no reference counterpart.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and result, with the module's scratch taken from a fixed
+ * per-GPU device array of SF_HIP_NOALLOC_SCRATCH_BYTES (held by each GPU the library runs on
+ * until the process ends) instead of a workspace.  Sizes whose
+ * sf_hip_self_attention_workspace_bytes exceeds it are refused with an error (64 MiB covers
+ * single attention up to N = 4096 at C = 384 and a 5 x 1024 x 768 diffusion block).  The call
+ * allocates nothing.  All calls on one GPU share the array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must be serialised by the caller. */
+#define SF_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+int sf_hip_self_attention_fwd_noalloc(const sf_self_attention_args* a, void* stream);
+
 /* Cross attention, transformer.py:549-585 (windowed atom attention), both sides conditioned:
  *   hq = AdaLN(xq, cond_q), hk = AdaLN(xk, cond_k) (as above, per side);
  *   [q|g] = hq W_qg^T + b_qg, [k|v] = hk W_kv^T;  o = attention(q, k, v; mask_q, mask_k, bias) * sigmoid(g)

@@ -12,6 +12,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
 ABI_VERSION = 7
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
+NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 _u8p = C.POINTER(C.c_uint8)
@@ -157,6 +158,7 @@ SIGNATURES = [
     ("sf_hip_window_gather_fwd", C.c_int, [C.POINTER(WindowGatherArgs), _vp]),
     ("sf_hip_self_attention_workspace_bytes", C.c_size_t, [C.POINTER(SelfAttentionArgs)]),
     ("sf_hip_self_attention_fwd", C.c_int, [C.POINTER(SelfAttentionArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_self_attention_fwd_noalloc", C.c_int, [C.POINTER(SelfAttentionArgs), _vp]),
     ("sf_hip_cross_attention_workspace_bytes", C.c_size_t, [C.POINTER(CrossAttentionArgs)]),
     ("sf_hip_cross_attention_fwd", C.c_int, [C.POINTER(CrossAttentionArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_diffusion_conditioning_workspace_bytes", C.c_size_t, [C.POINTER(DiffusionConditioningArgs)]),

@@ -301,12 +301,13 @@ def _u8_or_none(t):
 
 
 def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_head: int, head_dim: int,
-                          add_residual: bool = True, pre=None) -> torch.Tensor:
+                          add_residual: bool = True, pre=None, noalloc: bool = False) -> torch.Tensor:
   """SelfAttention.forward as one call.  ``x`` ``[..., N, C]`` (leading dims = samples),
   ``mask`` ``[N]`` or None, ``bias`` ``[H, N, N]`` (shared) or ``[S, H, N, N]`` or None,
   ``cond`` ``[N, Cs]`` or None; ``w`` holds the packed weights (keys as in the C struct).
   ``pre`` = (scale, shift, zgate) ``[N, C]`` views with one row stride (one layer of
-  ``diffusion_conditioning``) replaces the AdaLN computation from ``cond``."""
+  ``diffusion_conditioning``) replaces the AdaLN computation from ``cond``.  ``noalloc`` runs
+  the allocation-free entry point (the library's fixed per-GPU scratch; no workspace)."""
   _require_cuda(x, mask, bias, cond, *(pre or ()))
   N, Cn = x.shape[-2], x.shape[-1]
   S = x.numel() // max(N * Cn, 1)
@@ -342,6 +343,9 @@ def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_hea
                "self_attention: precomputed conditioning must be bf16 [N, C] views with one row stride")
     a.pre_scale, a.pre_shift, a.pre_zgate, a.pre_rs = _vp(ps), _vp(pb), _vp(pz), rs
   lib = _lib.load()
+  if noalloc:      # the library's fixed per-GPU scratch instead of a workspace
+    _lib.check(lib.sf_hip_self_attention_fwd_noalloc(C.byref(a), _stream(x)), "sf_hip_self_attention_fwd_noalloc")
+    return out.view(x.shape)
   ws = torch.empty(int(lib.sf_hip_self_attention_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=x.device)
   _lib.check(lib.sf_hip_self_attention_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(x)), "sf_hip_self_attention_fwd")
   return out.view(x.shape)

@@ -17,6 +17,7 @@
 // gather), so the numerics are exactly those of the op-level path.
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "sf_common.h"
 
@@ -183,8 +184,8 @@ extern "C" size_t sf_hip_self_attention_workspace_bytes(const sf_self_attention_
   return a == nullptr ? 0 : self_ws(a);
 }
 
-extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace,
-                                         size_t workspace_bytes, void* stream) {
+static int self_attention_run(const sf_self_attention_args* a, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   if (a == nullptr || a->x == nullptr || a->out == nullptr || a->w_qkvg == nullptr || a->w_t2 == nullptr) {
     sf_set_error("self_attention: x, out, w_qkvg and w_t2 must be non-null"); return 1;
   }
@@ -241,6 +242,62 @@ extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* 
   if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
   return zero_init_out(rows, a->C, HD, o, pre ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
                        a->add_residual ? a->x : nullptr, a->out, ws, st, a->pre_zgate, a->pre_rs);
+}
+
+extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  return self_attention_run(a, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free variant: the chain's scratch (normalised rows, q/k/v/g, o, key-slice
+// partials, AdaLN terms) lives in a fixed device array instead of a caller workspace.  Every
+// byte of it that a kernel reads was written earlier in the same call, so nothing needs
+// clearing between calls.  Each GPU holds its own copy of the array for the life of the process;
+// calls that overlap on one GPU share it and race.
+// ---------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[SF_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+hipError_t g_scratch_status[kMaxDevices];
+void* g_scratch_addr[kMaxDevices];
+
+// The device address of this GPU's scratch array, looked up once per device with that device
+// current (host code must never pass the array's own name to a kernel: it is a host-side stand-in).
+int scratch_address(void** addr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    sf_set_error("self_attention_noalloc: no usable current device (%d)", dev);
+    return 1;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_addr[dev] = g_scratch_status[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_status[dev] != hipSuccess || g_scratch_addr[dev] == nullptr) {
+    sf_set_error("self_attention_noalloc: scratch address lookup failed on device %d: %s", dev,
+                 hipGetErrorString(g_scratch_status[dev]));
+    return 1;
+  }
+  *addr = g_scratch_addr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int sf_hip_self_attention_fwd_noalloc(const sf_self_attention_args* a, void* stream) {
+  if (a == nullptr) { sf_set_error("self_attention_noalloc: null arguments"); return 1; }
+  const size_t need = self_ws(a);
+  if (need > (size_t)SF_HIP_NOALLOC_SCRATCH_BYTES) {
+    sf_set_error("self_attention_noalloc: these sizes need %zu bytes of scratch; the fixed scratch holds %zu "
+                 "(use sf_hip_self_attention_fwd with a workspace)", need, (size_t)SF_HIP_NOALLOC_SCRATCH_BYTES);
+    return 1;
+  }
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  return self_attention_run(a, ws, SF_HIP_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a) {
