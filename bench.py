@@ -192,6 +192,28 @@ def _config_builders() -> dict:
         "ms_per_block": round(t / L, 4), "ms_24_blocks": round(t, 3), "tflops": round(flop / t / 1e9, 1),
         "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
 
+  def c4_transition():  # diffusion-transformer transition block, 5 samples x N=1024, C=768, I=1536
+    S, n, c, sc, inter = 5, 1024, 768, 384, 1536
+    mod, act, cond = W.make_diffusion_transition(n, S=S, seed=11, sharp=False)
+    mod = mod.to(dev); backends.prepare(mod)
+    act, cond = act.to(dev), cond.to(dev)
+    flop = 2 * S * n * c * 2 * inter + 2 * S * n * inter * c + 2 * n * sc * 3 * c
+    return (lambda: mod(act, single_cond=cond)), (lambda t: {
+        "ms_per_call": round(t, 4), "tflops": round(flop / t / 1e9, 1),
+        "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+
+  def trunk_transition(n_rows, c, lead):  # trunk transition: single (C=384) or pair (C=128), I = 4C
+    def build():
+      mod, act = W.make_transition(n_rows, C=c, lead=lead, seed=12, sharp=False)
+      mod = mod.to(dev); backends.prepare(mod)
+      act = act.to(dev)
+      rows = act.numel() // c
+      flop = 2 * rows * c * 8 * c + 2 * rows * 4 * c * c
+      return (lambda: mod(act)), (lambda t: {
+          "ms_per_call": round(t, 4), "tflops": round(flop / t / 1e9, 1),
+          "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+    return build
+
   def c5():    # windowed atom attention, 5 samples x 8192 atoms, 32-query / 128-key windows
     S, atoms, c, h, d = 5, 8192, 128, 4, 32
     mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5)
@@ -227,7 +249,9 @@ def _config_builders() -> dict:
 
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
           "single_n768": c3b, "diffusion_5x1024_block": c4,
-          "diffusion_5x1024_24_blocks": c4_stack, "window_5x8192": c5,
+          "diffusion_5x1024_24_blocks": c4_stack, "diffusion_transition_5x1024": c4_transition,
+          "single_transition_n768": trunk_transition(768, 384, ()),
+          "pair_transition_n384": trunk_transition(384, 128, (384,)), "window_5x8192": c5,
           "transformer_pack_n1024": pack_tr, "cross_pack_8192": pack_x}
 
 

@@ -30,6 +30,8 @@
  *                               diffusion_self_attention)
  *   sf_hip_cross_attention_fwd  model/diffusion/transformer.py:549-585    CrossAttention.forward, with the
  *                               key gather of :671-673 (vecops op diffusion_cross_attention, indexed form)
+ *   sf_hip_transition_fwd       model/trunk/blocks.py:84-96                TransitionBlock.forward
+ *                               model/diffusion/transformer.py:209-231     TransitionBlock.forward (diffusion)
  */
 #ifndef SPARSEFOLD_HIP_H_
 #define SPARSEFOLD_HIP_H_
@@ -41,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 7
+#define SF_HIP_ABI_VERSION 8
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -113,6 +115,9 @@ int sf_hip_layer_norm_fwd(const sf_layer_norm_args* a, void* stream);
  * Only columns [0, ycols) go to y (ycols = 0 means all N).  Optional second output:
  * columns [tcol0, tcol0+tcols) are also written transposed, yt[n - tcol0, m] (bf16, row
  * stride yt_rs) -- used to emit [H, rows] bias planes.  K % 8 == 0.
+ * Gated form (glu = 1, the SwiGLU of the transition blocks, primitives.py:586-631): the weight
+ * rows are interleaved pairs, and y[m, j] = swish(v[2j]) * v[2j+1] with v = x wt^T (+ bias), so y
+ * has N/2 columns; needs K % 64 == 0, N % 8 == 0 and no mul / residual / post_sigmoid / yt.
  * ------------------------------------------------------------------------------------- */
 typedef struct sf_linear_args {
   int64_t M; int32_t N, K;
@@ -124,6 +129,7 @@ typedef struct sf_linear_args {
   int32_t post_sigmoid;
   void* y; int64_t y_rs; int32_t ycols;        /* y may be NULL when only yt is wanted */
   int32_t tcol0, tcols; void* yt; int64_t yt_rs;
+  int32_t glu;                                 /* 1: gated pairs (see above) */
 } sf_linear_args;
 
 int sf_hip_linear_fwd(const sf_linear_args* a, void* stream);
@@ -302,6 +308,37 @@ typedef struct sf_cross_attention_args {
 size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a);
 int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* Transition blocks, whole module, one call:
+ *   trunk transition (blocks.py:38-96, TransitionBlock.forward; vecops op transition_block,
+ *   native_ops name "evoformer_transition_block"):            h = LN(x) * ln_w + ln_b
+ *   diffusion transition (transformer.py:157-231; vecops op diffusion_transition_block,
+ *   "diffusion_transition_block"): h = AdaLN(x, cond) as in sf_self_attention_args, or
+ *                                   pre_scale * LN(x) + pre_shift (precomputed conditioning)
+ *   c = swish(h W_a^T) * (h W_b^T)            (the GatedLinearUnit, primitives.py:586-631)
+ *   out = (c W2^T) * (cond ? sigmoid(cond W_zc^T + b_zc) : 1) + (add_residual ? x : 0)
+ * x bf16 [S, N, C] (the condition [N, Cs] is shared by the S samples); w1 bf16 [2I, C] with
+ * interleaved rows: row 2i = column i of the reference's [C, 2I] weight (the swish half), row
+ * 2i + 1 = column I + i; w2 bf16 [C, I].  C % 64 == 0.  Workspace from
+ * sf_hip_transition_workspace_bytes. */
+typedef struct sf_transition_args {
+  int32_t S, N, C, I, Cs;
+  int32_t add_residual;
+  const void* x;                                /* bf16 [S, N, C] */
+  const void* cond;                             /* bf16 [N, Cs] or NULL */
+  const float* ln_w; const float* ln_b;         /* no condition: f32 [C] or NULL */
+  const float* lnc_w; const float* lnc_b;       /* condition: LN of cond, f32 [Cs] or NULL */
+  const void* w_scale; const float* b_scale;    /* bf16 [C, Cs], f32 [C] */
+  const void* w_shift;                          /* bf16 [C, Cs] */
+  const void* w1;                               /* bf16 [2I, C], interleaved */
+  const void* w2;                               /* bf16 [C, I] */
+  const void* w_zc; const float* b_zc;          /* bf16 [C, Cs], f32 [C] (condition only) */
+  void* out;                                    /* bf16 [S, N, C] */
+  const void* pre_scale; const void* pre_shift; const void* pre_zgate; int64_t pre_rs;
+} sf_transition_args;
+
+size_t sf_hip_transition_workspace_bytes(const sf_transition_args* a);
+int sf_hip_transition_fwd(const sf_transition_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Triangle multiplicative update, whole module (TriangleMultiplication.forward,
  * blocks.py:486-566, non-distributed), replacing the native triangle_multiplication op

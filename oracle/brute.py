@@ -248,3 +248,46 @@ def cross_attention(x_q, x_k, mask_q, mask_k, p, pair_logits=None, cond_q=None, 
         y = y * np.array([sigmoid(sum(cq[m] * wz[m, c] for m in range(len(cq))) + bz[c]) for c in range(C)])
       upd[u, i] = y
   return xq + upd, upd
+
+
+def _swish(v):
+  return v * sigmoid(v)
+
+
+def transition_block(act, p):
+  """blocks.py:84-96 per row and channel in float64: act ``[R, C]``.  Returns (act + upd, upd)."""
+  act = np.asarray(act, np.float64)
+  R, C = act.shape
+  w1 = np.asarray(p["transition1.weight"], np.float64)        # [C, 2I]: a = cols [0, I), b = [I, 2I)
+  w2 = np.asarray(p["transition2.weight"], np.float64)        # [I, C]
+  I = w2.shape[0]
+  upd = np.zeros_like(act)
+  for r in range(R):
+    x = layer_norm(act[r], p["input_layer_norm.weight"], p.get("input_layer_norm.bias"))
+    c = [_swish(sum(x[m] * w1[m, i] for m in range(C))) * sum(x[m] * w1[m, I + i] for m in range(C))
+         for i in range(I)]
+    upd[r] = [sum(c[i] * w2[i, n] for i in range(I)) for n in range(C)]
+  return act + upd, upd
+
+
+def diffusion_transition_block(x, cond, p):
+  """transformer.py:209-231 per row and channel in float64: x ``[R, C]``, cond ``[R, Cs]`` or
+  None.  Returns (x + upd, upd)."""
+  x = np.asarray(x, np.float64)
+  R, C = x.shape
+  w1 = np.asarray(p["transition.weight"], np.float64)
+  w2 = np.asarray(p["zero_init.transition2.weight"], np.float64)
+  I = w2.shape[0]
+  upd = np.zeros_like(x)
+  for r in range(R):
+    c_row = None if cond is None else np.asarray(cond[r], np.float64)
+    h = _adaln_row(x[r], c_row, p, "layer_norm.")
+    c = [_swish(sum(h[m] * w1[m, i] for m in range(C))) * sum(h[m] * w1[m, I + i] for m in range(C))
+         for i in range(I)]
+    y = np.array([sum(c[i] * w2[i, n] for i in range(I)) for n in range(C)])
+    if c_row is not None:
+        wz = np.asarray(p["zero_init.adaptive_zero_cond.weight"], np.float64)
+        bz = np.asarray(p["zero_init.adaptive_zero_cond.bias"], np.float64)
+        y = y * np.array([sigmoid(sum(c_row[m] * wz[m, n] for m in range(len(c_row))) + bz[n]) for n in range(C)])
+    upd[r] = y
+  return x + upd, upd

@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from oracle.primitives import layer_norm, linear
+from oracle.primitives import gated_linear_unit, layer_norm, linear
 from oracle.sdpa import dot_product_attention
 
 
@@ -256,6 +256,34 @@ def windowed_cross_attention(queries_act: torch.Tensor, queries_mask: torch.Tens
   return cross_attention(queries_act, keys_act, queries_mask, keys_mask, p, pair_logits=pair_logits,
                          single_cond_q=queries_single_cond, single_cond_k=keys_single_cond,
                          dtype=dtype, return_update=return_update)
+
+
+# --------------------------------------------------------------------------------------
+# Transitions: blocks.py:38-96 (trunk), transformer.py:157-231 (diffusion transformer)
+# --------------------------------------------------------------------------------------
+
+def transition_block(act: torch.Tensor, p: dict, *, return_update: bool = False) -> torch.Tensor:
+  """blocks.py:84-96 (TransitionBlock.forward): LN, SwiGLU of transition1 (its ``[C, 2I]`` weight
+  viewed as ``"a (i2 n) -> a i2 n"``), transition2 with the input as residual."""
+  x = layer_norm(act, p["input_layer_norm.weight"], _get(p, "input_layer_norm.bias"))
+  w1 = p["transition1.weight"]
+  c = gated_linear_unit(x, w1.reshape(w1.shape[0], 2, -1))
+  out = linear(c, p["transition2.weight"])
+  return out if return_update else act + out
+
+
+def diffusion_transition_block(x: torch.Tensor, single_cond: torch.Tensor | None, p: dict, *,
+                               dtype: torch.dtype | None = None, return_update: bool = False) -> torch.Tensor:
+  """transformer.py:209-231 (TransitionBlock.forward of the diffusion transformer): AdaLN with the
+  ``layer_norm.`` parameters, SwiGLU of ``transition``, AdaLN-zero output (``zero_init.``)."""
+  residual = x
+  orig = x.dtype
+  h = adaptive_layer_norm(x, single_cond, p, "layer_norm.", dtype)
+  h = h.to(dtype) if dtype is not None else h
+  w1 = p["transition.weight"]
+  c = gated_linear_unit(h, w1.reshape(w1.shape[0], 2, -1))
+  out = adaptive_zero_init(c.to(orig), single_cond, p, "zero_init.", dtype)
+  return out if return_update else residual + out
 
 
 # --------------------------------------------------------------------------------------

@@ -13,6 +13,9 @@ Follows ``src/sparsefold/model/layers/primitives.py``:
   bounded sigmoid, other devices ``torch.sigmoid``.
 * ``layer_norm``           -- ``LayerNorm.forward`` (:471-497): normalise in
   ``compute_dtype`` (input dtype when None), eps 1e-5, cast back.
+* ``swish`` / ``gated_linear_unit`` -- ``swish`` (:688-699, CPU form: bounded sigmoid, zero
+  below -20) and ``gated_linear_unit`` (:645-685): ``x @ W`` with ``W`` ``[K, 2, N]``
+  collapsed to ``[K, 2N]``, ``swish(first half) * second half``, cast to the input dtype.
 """
 from __future__ import annotations
 
@@ -80,3 +83,20 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
     bias = bias.to(y.dtype)
   out = F.layer_norm(y, (y.shape[-1],), weight, bias, eps)
   return out.to(dtype)
+
+
+def swish(x: torch.Tensor) -> torch.Tensor:
+  """primitives.py:688-699 on the CPU: x * bounded sigmoid(x), exactly 0 below -20."""
+  if x.device.type == "cpu":
+    return torch.where(x < -20, torch.zeros_like(x), x * cpu_bounded_sigmoid(x))
+  return x * torch.sigmoid(x)
+
+
+def gated_linear_unit(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+  """primitives.py:645-685 with the swish activation: weight ``[K, 2, N]`` (or ``[K, 2N]``)."""
+  w = weight.reshape(weight.shape[0], -1)
+  if x.dtype != w.dtype:
+    w = w.to(x.dtype)
+  y = torch.matmul(x, w)
+  a, b = torch.tensor_split(y, 2, dim=-1)
+  return (swish(a) * b).to(x.dtype)

@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -59,6 +59,7 @@ class LinearArgs(C.Structure):
       ("post_sigmoid", _i32),
       ("y", _vp), ("y_rs", _i64), ("ycols", _i32),
       ("tcol0", _i32), ("tcols", _i32), ("yt", _vp), ("yt_rs", _i64),
+      ("glu", _i32),
   ]
 
 
@@ -123,6 +124,16 @@ class DiffusionConditioningArgs(C.Structure):
   ]
 
 
+class TransitionArgs(C.Structure):
+  _fields_ = [
+      ("S", _i32), ("N", _i32), ("C", _i32), ("I", _i32), ("Cs", _i32), ("add_residual", _i32),
+      ("x", _vp), ("cond", _vp), ("ln_w", _vp), ("ln_b", _vp), ("lnc_w", _vp), ("lnc_b", _vp),
+      ("w_scale", _vp), ("b_scale", _vp), ("w_shift", _vp), ("w1", _vp), ("w2", _vp),
+      ("w_zc", _vp), ("b_zc", _vp), ("out", _vp),
+      ("pre_scale", _vp), ("pre_shift", _vp), ("pre_zgate", _vp), ("pre_rs", _i64),
+  ]
+
+
 class TriangleMultArgs(C.Structure):
   _fields_ = [
       ("N", _i32), ("C", _i32), ("incoming", _i32), ("add_residual", _i32),
@@ -142,6 +153,7 @@ STRUCTS = {
     "sf_cross_attention_args": CrossAttentionArgs,
     "sf_diffusion_conditioning_args": DiffusionConditioningArgs,
     "sf_triangle_mult_args": TriangleMultArgs,
+    "sf_transition_args": TransitionArgs,
 }
 
 # (name, restype, argtypes) of every exported entry point.
@@ -163,6 +175,8 @@ SIGNATURES = [
     ("sf_hip_cross_attention_fwd", C.c_int, [C.POINTER(CrossAttentionArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_diffusion_conditioning_workspace_bytes", C.c_size_t, [C.POINTER(DiffusionConditioningArgs)]),
     ("sf_hip_diffusion_conditioning_fwd", C.c_int, [C.POINTER(DiffusionConditioningArgs), _vp, C.c_size_t, _vp]),
+    ("sf_hip_transition_workspace_bytes", C.c_size_t, [C.POINTER(TransitionArgs)]),
+    ("sf_hip_transition_fwd", C.c_int, [C.POINTER(TransitionArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_triangle_mult_workspace_bytes", C.c_size_t, [_i32, _i32]),
     ("sf_hip_triangle_mult_fwd", C.c_int, [C.POINTER(TriangleMultArgs), _vp, C.c_size_t, _vp]),
 ]

@@ -27,6 +27,8 @@ _REPLACE_MAP = {
     "grid_self_attn": [("GridSelfAttention", "GridSelfAttentionHip")],
     "evoformer_single_act_update": [("SingleActUpdate", "SingleActUpdateHip")],
     "triangle_multiplication": [("TriangleMultiplication", "TriangleMultiplicationHip")],
+    "evoformer_transition_block": [("TransitionBlock", "TransitionBlockHip")],
+    "diffusion_transition_block": [("DiffusionTransitionBlock", "DiffusionTransitionBlockHip")],
     "diffusion_self_attention": [("SelfAttention", "SelfAttentionHip"),
                                  ("TransformerPairLogits", "TransformerPairLogitsHip")],
     "diffusion_cross_attention": [("CrossAttention", "CrossAttentionHip"),

@@ -15,6 +15,8 @@ Replaced reference forwards:
                                      gathers the key windows (transformer.py:671-673)
 * ``SingleActUpdateHip.forward``     blocks.py:739-763 (attention half)
 * ``TriangleMultiplicationHip.forward``  blocks.py:486-566 (outgoing and incoming edges, C = 128)
+* ``TransitionBlockHip.forward``     blocks.py:84-96 (trunk transition: pair / single)
+* ``DiffusionTransitionBlockHip.forward``  transformer.py:209-231 (diffusion transformer transition)
 * ``TransformerHipMixin``            transformer.py:430-447 -- the cached pair-logit pack
                                      ``[n_super, super_block, H, N, N]`` in one pass over pair_cond;
                                      with condition-only HIP attention blocks, also every block's
@@ -310,6 +312,77 @@ class CrossAttentionHipMixin:
 
 
 # ---------------------------------------------------------------------------------------
+# Transitions (trunk: blocks.py:38-96; diffusion transformer: transformer.py:157-231)
+# ---------------------------------------------------------------------------------------
+
+def _glu_rows(weight: torch.Tensor) -> torch.Tensor:
+  """The reference's ``[C, 2I]`` GLU weight (first I columns through swish) as the kernel's
+  ``[2I, C]`` K-contiguous rows, interleaved: row 2i = column i, row 2i + 1 = column I + i."""
+  wt = weight.detach().t()
+  I = wt.shape[0] // 2
+  return _bf(torch.stack([wt[:I], wt[I:]], 1).reshape(2 * I, wt.shape[1]))
+
+
+class TransitionBlockHipMixin:
+  """TransitionBlock.forward (blocks.py:84-96) as one library call."""
+
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    _buf(self, "_hip_ln_w", _f32(self.input_layer_norm.weight))
+    _buf(self, "_hip_ln_b", _f32(getattr(self.input_layer_norm, "bias", None)))
+    _buf(self, "_hip_w1", _glu_rows(self.transition1.weight))
+    _buf(self, "_hip_w2", _bf(self.transition2.weight.t()))           # [I, C] -> [C, I]
+    self._native_prepared = True
+    return True
+
+  @_require_native_preparation
+  @graphs.graphed
+  def forward(self, act: torch.Tensor, *, broadcast_dim: int | None = 0, add_residual: bool = True) -> torch.Tensor:
+    w = {"ln_w": self._hip_ln_w, "ln_b": self._hip_ln_b, "w1": self._hip_w1, "w2": self._hip_w2}
+    rows = act.reshape(-1, act.shape[-1])
+    out = ops.transition_module(rows, None, w, add_residual=add_residual)
+    return out.view(act.shape).to(act.dtype)
+
+
+class DiffusionTransitionHipMixin:
+  """TransitionBlock.forward of the diffusion transformer (transformer.py:209-231) as one call."""
+
+  def prepare_native(self) -> bool:
+    _begin_preparation(self)
+    _prepare_adaln(self, self.layer_norm, "_hip_ada_")
+    _buf(self, "_hip_w1", _glu_rows(self.transition.weight))
+    _prepare_zero_init(self, self.zero_init)                           # _hip_w_t2 = W2 [C, I]
+    self._native_prepared = True
+    return True
+
+  def _native_weights(self) -> dict:
+    w = {"w1": self._hip_w1, "w2": self._hip_w_t2, "w_zc": getattr(self, "_hip_w_zc", None),
+         "b_zc": getattr(self, "_hip_b_zc", None)}
+    for key in ("ln_w", "ln_b", "lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift"):
+      w[key] = getattr(self, "_hip_ada_" + key, None)
+    return w
+
+  @_require_native_preparation
+  @graphs.graphed
+  def forward(self, x: torch.Tensor, *, single_cond: torch.Tensor | None = None, add_residual: bool = True,
+              adaptive_scale: torch.Tensor | None = None, adaptive_bias: torch.Tensor | None = None,
+              zero_gate: torch.Tensor | None = None) -> torch.Tensor:
+    """``adaptive_scale`` / ``adaptive_bias`` / ``zero_gate`` ``[N, C]``: this layer's precomputed
+    conditioning (``TransformerHipMixin.diffusion_conditioning``), used in place of ``single_cond``."""
+    N = x.shape[-2]
+    pre = None
+    if adaptive_scale is not None:
+      pre = (adaptive_scale, adaptive_bias, zero_gate)
+    elif single_cond is not None and not (single_cond.dim() == 2 and single_cond.shape[0] == N):
+      raise ValueError(f"diffusion transition: single_cond must be [N, Cs], got {tuple(single_cond.shape)}")
+    if single_cond is None and pre is None and not hasattr(self, "_hip_ada_ln_w"):
+      raise ValueError("diffusion transition: this block is conditioned; pass single_cond")
+    out = ops.transition_module(x, None if pre else single_cond, self._native_weights(), add_residual=add_residual,
+                                pre=pre)
+    return out.to(x.dtype)
+
+
+# ---------------------------------------------------------------------------------------
 # SingleActUpdate: pair-logit prologue + single attention
 # ---------------------------------------------------------------------------------------
 
@@ -319,10 +392,9 @@ class SingleActUpdateHipMixin:
     _buf(self, "_hip_pl_ln_w", _f32(self.single_pair_logits_norm.weight))
     _buf(self, "_hip_pl_ln_b", _f32(getattr(self.single_pair_logits_norm, "bias", None)))
     _buf(self, "_hip_pl_w", _bf(self.single_pair_logits_projection.weight.t()))   # [Cz, H] -> [H, Cz]
-    prep = getattr(self.single_attention, "prepare_native", None)
-    if prep is None:
+    if getattr(self.single_attention, "prepare_native", None) is None:
       raise RuntimeError("single_attention is not a HIP module; select backend 'hip' before construction")
-    prep()
+    _prepare_hip_children(self)                                         # the attention and the transition
     self._native_prepared = True
     return True
 
@@ -409,21 +481,37 @@ class TransformerHipMixin:
                             for a in flat)
     return flat if ok else None
 
+  def _transition_layers(self) -> list | None:
+    """The transition blocks in call order when every one is a conditioned HIP transition (then
+    their AdaLN conditioning joins the attention blocks' one call), else None."""
+    try:
+      flat = [t for sb in self.transition_block for t in sb]
+    except (AttributeError, TypeError):
+      return None
+    ok = bool(flat) and all(isinstance(t, DiffusionTransitionHipMixin) and getattr(t, "_hip_ada_lnc_w", None) is not None
+                            and getattr(t, "_hip_ada_lnc_b", None) is None and getattr(t, "_hip_w_zc", None) is not None
+                            for t in flat)
+    return flat if ok else None
+
   def _prepare_conditioning(self) -> None:
-    """Stacks every block's AdaLN / AdaLN-zero condition weights so one call conditions them all
-    (the reference packs them per super-block, backends/vecops/modules.py:1040-1081)."""
+    """Stacks every block's AdaLN / AdaLN-zero condition weights -- the attention blocks', then the
+    transition blocks' when those are conditioned HIP transitions -- so that one call conditions
+    them all (the reference packs them per super-block, backends/vecops/modules.py:1040-1081)."""
     self._hip_dc = None
     flat = self._attention_layers()
     if flat is None:
       return
+    trans = self._transition_layers()
+    self._hip_dc_transitions = trans is not None
+    layers = flat + (trans or [])
     zeros = lambda a: torch.zeros(a._hip_ada_w_scale.shape[0], dtype=torch.float32, device=a._hip_ada_w_scale.device)
     self._hip_dc = {
-        "lnc_w": torch.stack([a._hip_ada_lnc_w for a in flat]).contiguous(),
-        "w_scale": torch.cat([a._hip_ada_w_scale for a in flat]).contiguous(),
-        "b_scale": torch.cat([a._hip_ada_b_scale if a._hip_ada_b_scale is not None else zeros(a) for a in flat]),
-        "w_shift": torch.cat([a._hip_ada_w_shift for a in flat]).contiguous(),
-        "w_zc": torch.cat([a._hip_w_zc for a in flat]).contiguous(),
-        "b_zc": torch.cat([a._hip_b_zc if a._hip_b_zc is not None else zeros(a) for a in flat]),
+        "lnc_w": torch.stack([a._hip_ada_lnc_w for a in layers]).contiguous(),
+        "w_scale": torch.cat([a._hip_ada_w_scale for a in layers]).contiguous(),
+        "b_scale": torch.cat([a._hip_ada_b_scale if a._hip_ada_b_scale is not None else zeros(a) for a in layers]),
+        "w_shift": torch.cat([a._hip_ada_w_shift for a in layers]).contiguous(),
+        "w_zc": torch.cat([a._hip_w_zc for a in layers]).contiguous(),
+        "b_zc": torch.cat([a._hip_b_zc if a._hip_b_zc is not None else zeros(a) for a in layers]),
     }
 
   @_require_native_preparation
@@ -463,11 +551,17 @@ class TransformerHipMixin:
     scale, shift, zgate = self.diffusion_conditioning(single_cond)
     x = act.to(self.dtype) if getattr(self, "dtype", None) is not None else act
     layer = 0
+    n_att = sum(len(sb) for sb in self.self_attention)
     for sb, (attentions, transitions) in enumerate(zip(self.self_attention, self.transition_block)):
       for b, (attention, transition) in enumerate(zip(attentions, transitions)):
         x = attention(x, mask, pair_logits=None if pack is None else pack[sb][b], single_cond=single_cond,
                       adaptive_scale=scale[layer], adaptive_bias=shift[layer], zero_gate=zgate[layer])
-        x = transition(x, single_cond=single_cond)
+        if self._hip_dc_transitions:
+          t = n_att + layer
+          x = transition(x, single_cond=single_cond, adaptive_scale=scale[t], adaptive_bias=shift[t],
+                         zero_gate=zgate[t])
+        else:
+          x = transition(x, single_cond=single_cond)
         layer += 1
     return x.to(act.dtype)
 
@@ -568,5 +662,14 @@ class TriangleMultiplicationHip(TriangleMultiplicationHipMixin, base.TriangleMul
   pass
 
 
-HIP_TYPES = (TriangleMultiplicationHipMixin, GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin, SingleActUpdateHipMixin,
-             TransformerHipMixin, CrossAttTransformerHipMixin)
+class TransitionBlockHip(TransitionBlockHipMixin, base.TransitionBlock):
+  pass
+
+
+class DiffusionTransitionBlockHip(DiffusionTransitionHipMixin, base.DiffusionTransitionBlock):
+  pass
+
+
+HIP_TYPES = (TriangleMultiplicationHipMixin, GridSelfAttentionHipMixin, SelfAttentionHipMixin, CrossAttentionHipMixin,
+             SingleActUpdateHipMixin, TransformerHipMixin, CrossAttTransformerHipMixin, TransitionBlockHipMixin,
+             DiffusionTransitionHipMixin)

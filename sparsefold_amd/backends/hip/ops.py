@@ -351,6 +351,43 @@ def self_attention_module(x: torch.Tensor, mask, bias, cond, w: dict, *, num_hea
   return out.view(x.shape)
 
 
+def transition_module(x: torch.Tensor, cond, w: dict, *, add_residual: bool = True, pre=None) -> torch.Tensor:
+  """A transition block as one call (sf_hip_transition_fwd).  ``x`` ``[..., N, C]`` (leading dims =
+  samples sharing the condition), ``cond`` ``[N, Cs]`` or None; ``w`` holds the packed weights
+  (``w1`` ``[2I, C]`` interleaved, ``w2`` ``[C, I]``, LayerNorm / AdaLN / zero-gate terms as in
+  the C struct).  ``pre`` = (scale, shift, zgate) ``[N, C]`` views with one row stride."""
+  _require_cuda(x, cond, *(pre or ()))
+  N, Cn = x.shape[-2], x.shape[-1]
+  S = x.numel() // max(N * Cn, 1)
+  w1, w2 = w["w1"], w["w2"]
+  I = w2.shape[1]
+  _require(tuple(w1.shape) == (2 * I, Cn) and tuple(w2.shape) == (Cn, I), "transition: weight shapes")
+  x3 = _bf16(x).reshape(S, N, Cn).contiguous()
+  out = torch.empty_like(x3)
+  a = _lib.TransitionArgs()
+  a.S, a.N, a.C, a.I = S, N, Cn, I
+  a.add_residual = int(bool(add_residual))
+  a.x, a.out = _vp(x3), _vp(out)
+  c2 = None
+  if cond is not None and pre is None:
+    c2 = _bf16(cond).contiguous()
+    _require(tuple(c2.shape[:-1]) == (N,), "transition: cond must be [N, Cs]")
+    a.cond, a.Cs = _vp(c2), c2.shape[-1]
+  for key in ("ln_w", "ln_b", "lnc_w", "lnc_b", "w_scale", "b_scale", "w_shift", "w1", "w2", "w_zc", "b_zc"):
+    setattr(a, key, _vp(w.get(key)))
+  if pre is not None:
+    ps, pb, pz = pre
+    rs = ps.stride(0)
+    for t in pre:
+      _require(t.dtype == torch.bfloat16 and tuple(t.shape) == (N, Cn) and t.stride() == (rs, 1),
+               "transition: precomputed conditioning must be bf16 [N, C] views with one row stride")
+    a.pre_scale, a.pre_shift, a.pre_zgate, a.pre_rs = _vp(ps), _vp(pb), _vp(pz), rs
+  lib = _lib.load()
+  ws = torch.empty(int(lib.sf_hip_transition_workspace_bytes(C.byref(a))), dtype=torch.uint8, device=x.device)
+  _lib.check(lib.sf_hip_transition_fwd(C.byref(a), _vp(ws), ws.numel(), _stream(x)), "sf_hip_transition_fwd")
+  return out.view(x.shape)
+
+
 def cross_attention_module(xq: torch.Tensor, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k,
                            w: dict, *, num_head: int, head_dim: int, add_residual: bool = True) -> torch.Tensor:
   """CrossAttention.forward as one call.  ``xq`` ``[..., U, Qw, C]``; keys either ``xk``

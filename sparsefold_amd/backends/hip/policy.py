@@ -4,12 +4,10 @@ from collections.abc import Sequence
 # native.ops names (src/sparsefold/config.py:24-35) that this backend replaces
 HIP_NATIVE_OPS = frozenset({
     "grid_self_attn", "evoformer_single_act_update", "diffusion_self_attention", "diffusion_cross_attention",
+    "evoformer_transition_block", "diffusion_transition_block", "triangle_multiplication",
 })
 # names the reference accepts that are outside the attention path: accepted, left on Torch
-OTHER_NATIVE_OPS = frozenset({
-    "linear", "evoformer_transition_block", "msa_attention", "outer_product_mean",
-    "triangle_multiplication", "diffusion_transition_block",
-})
+OTHER_NATIVE_OPS = frozenset({"linear", "msa_attention", "outer_product_mean"})
 
 
 def validate_hip_device(device) -> None:

@@ -361,6 +361,77 @@ extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void
 
 namespace {
 
+size_t transition_ws(const sf_transition_args* a) {
+  Arena ws{nullptr};
+  const int64_t rows = (int64_t)a->S * a->N;
+  const bool cond_gemms = a->cond && !a->pre_scale;
+  if (cond_gemms) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
+  ws.take((size_t)rows * a->C * 2);          // h
+  ws.take((size_t)rows * a->I * 2);          // gated intermediate
+  if (cond_gemms) ws.take((size_t)a->N * a->C * 2);
+  return ws.off;
+}
+
+}  // namespace
+
+extern "C" size_t sf_hip_transition_workspace_bytes(const sf_transition_args* a) {
+  return a == nullptr ? 0 : transition_ws(a);
+}
+
+extern "C" int sf_hip_transition_fwd(const sf_transition_args* a, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (a == nullptr || a->x == nullptr || a->out == nullptr || a->w1 == nullptr || a->w2 == nullptr) {
+    sf_set_error("transition: x, out, w1 and w2 must be non-null"); return 1;
+  }
+  if (a->S <= 0 || a->N <= 0 || a->C <= 0 || a->I <= 0 || a->C % 64 != 0 || a->I % 4 != 0 ||
+      (a->cond && !a->pre_scale && a->Cs <= 0)) {
+    sf_set_error("transition: need positive sizes, C %% 64 == 0 and I %% 4 == 0 (S=%d N=%d C=%d I=%d Cs=%d)",
+                 a->S, a->N, a->C, a->I, a->Cs);
+    return 1;
+  }
+  const bool pre = a->pre_scale != nullptr;
+  if (pre && (a->pre_shift == nullptr || a->pre_zgate == nullptr || a->pre_rs < a->C)) {
+    sf_set_error("transition: pre_scale needs pre_shift, pre_zgate and pre_rs >= C"); return 1;
+  }
+  if (!pre && a->cond && (a->w_scale == nullptr || a->w_shift == nullptr || a->w_zc == nullptr)) {
+    sf_set_error("transition: a condition needs w_scale, w_shift and w_zc"); return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < transition_ws(a)) {
+    sf_set_error("transition: workspace of %zu bytes needed, %zu given", transition_ws(a), workspace_bytes);
+    return 1;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Arena ws{static_cast<char*>(workspace)};
+  const int64_t rows = (int64_t)a->S * a->N;
+  int rc;
+  void* h = nullptr;
+  {
+    Arena probe = ws;                        // the AdaLN scratch first, as in transition_ws
+    if (a->cond && !pre) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
+    h = probe.take((size_t)rows * a->C * 2);
+    if (pre) {
+      sf_layer_norm_args ln{};
+      ln.M = rows; ln.C = a->C; ln.eps = 1e-5f;
+      ln.x = a->x; ln.x_rs = a->C; ln.y = h; ln.y_rs = a->C;
+      ln.scale = a->pre_scale; ln.shift = a->pre_shift; ln.cond_rows = a->N; ln.cond_rs = a->pre_rs;
+      if ((rc = sf_hip_layer_norm_fwd(&ln, st))) return rc;
+    } else if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b,
+                           a->w_scale, a->b_scale, a->w_shift, ws, h, st))) {
+      return rc;
+    }
+    ws = probe;
+  }
+  void* c = ws.take((size_t)rows * a->I * 2);
+  sf_linear_args g{};
+  g.M = rows; g.N = 2 * a->I; g.K = a->C; g.x = h; g.x_rs = a->C; g.wt = a->w1; g.mul_rows = 1;
+  g.y = c; g.y_rs = a->I; g.glu = 1;
+  if ((rc = sf_hip_linear_fwd(&g, st))) return rc;
+  return zero_init_out(rows, a->C, a->I, c, pre ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w2,
+                       a->add_residual ? a->x : nullptr, a->out, ws, st, a->pre_zgate, a->pre_rs);
+}
+
+namespace {
+
 // W'[j, k] = W[j, k] * g[j / C, k] for the scale and shift weights (blockIdx.y picks which),
 // eight bf16 per thread; Cs % 8 == 0 keeps each group of eight inside one row.
 __global__ void __launch_bounds__(256) fold_gamma_kernel(const uint16_t* __restrict__ w0,

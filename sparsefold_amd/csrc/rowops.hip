@@ -349,6 +349,19 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = cv[e] + bv[e];
+    if (a.glu) {
+      // gated pairs: columns 2j (swish) and 2j + 1 of the interleaved weight give output column j;
+      // N % 8 == 0 (checked on the host), so the 8 columns are 4 whole pairs
+      uint32_t w[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float g0 = v[4 * e] * sigmoidf_(v[4 * e]) * v[4 * e + 1];
+        const float g1 = v[4 * e + 2] * sigmoidf_(v[4 * e + 2]) * v[4 * e + 3];
+        w[e] = pack_bf2(g0, g1);
+      }
+      *reinterpret_cast<u32x2*>(yp + m * a.y_rs + n / 2) = u32x2{w[0], w[1]};
+      continue;
+    }
     if (a.post_sigmoid) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = sigmoidf_(v[e]);
@@ -708,6 +721,12 @@ extern "C" int sf_hip_linear_fwd(const sf_linear_args* a, void* stream) {
   if (a->mul && a->mul_rows <= 0) { sf_set_error("linear: mul_rows must be positive"); return 1; }
   if (a->yt && (a->tcol0 < 0 || a->tcols < 0 || a->tcol0 + a->tcols > a->N)) {
     sf_set_error("linear: transposed column range out of bounds"); return 1;
+  }
+  if (a->glu && (a->K % 64 != 0 || a->N % 8 != 0 || a->y == nullptr || a->yt || a->mul || a->residual ||
+                 a->post_sigmoid || a->ycols || !al16(a->y) || a->y_rs % 4)) {
+    sf_set_error("linear: the gated (glu) form needs K %% 64 == 0, N %% 8 == 0, an 8-byte aligned y with "
+                 "y_rs %% 4 == 0, and no mul / residual / sigmoid / transposed output (K=%d N=%d)", a->K, a->N);
+    return 1;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->K % 64 == 0) {

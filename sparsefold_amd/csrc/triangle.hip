@@ -732,6 +732,7 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       }
       // tile loads landed (the 8 Q loads of the last tile, the youngest, may stay in flight;
       // idle waves issued none and wait for everything)
+      static_assert(2 * kTR == 8, "the partial wait below leaves exactly the 2 * kTR Q reloads in flight");
       if (LAST && active) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();

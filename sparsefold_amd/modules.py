@@ -14,8 +14,10 @@ Mirrored layouts (reference file:line):
 * ``GridSelfAttention`` blocks.py:188-267
 * ``AdaptiveLayerNorm`` / ``AdaptiveZeroInit`` / ``SelfAttention`` transformer.py:27-304
 * ``CrossAttention``    transformer.py:480-547
-* ``SingleActUpdate``   blocks.py:692-737 (attention half; the transition is outside the
-                        attention path)
+* ``SingleActUpdate``   blocks.py:692-737 (pair-logit prologue, single attention and, with a
+                        ``transition_config``, the single transition)
+* ``TransitionBlock``   blocks.py:38-96 (trunk transition)
+* ``DiffusionTransitionBlock`` transformer.py:157-231 (the diffusion transformer's transition)
 * ``TransformerPairLogits``         transformer.py:398-419 -- the pair-conditioning sub-modules
                         of ``Transformer`` (``pair_input_layer_norm``, ``pair_logits_projection``)
 * ``CrossAttTransformerPairLogits`` transformer.py:611-620 -- the same for ``CrossAttTransformer``
@@ -264,6 +266,50 @@ class SingleActUpdate(_NoTorchPath, torch.nn.Module):
                                                 name="single_pair_logits_projection")
     self.single_attention = SelfAttention(attn_config, global_config, num_channels=seq_channels,
                                           name="single_attention_")
+    if transition_config is not None:
+      self.num_intermediate = int(seq_channels * transition_config.num_intermediate_factor)
+      self.single_transition = TransitionBlock(transition_config, global_config, num_channels=seq_channels,
+                                               name="single_transition")
+
+
+class TransitionBlock(_NoTorchPath, torch.nn.Module):
+  """blocks.py:38-96: the trunk transition -- LayerNorm, SwiGLU of ``transition1`` (``[C, 2I]``:
+  the first I columns through swish, times the last I), ``transition2`` plus the residual."""
+
+  @dataclasses.dataclass
+  class Config:
+    num_intermediate_factor: int = 4
+    use_glu_kernel: bool = True
+
+  def __init__(self, config: Config, global_config: GlobalConfig, *, num_channels: int, name: str = "", **kwargs):
+    super().__init__()
+    self.name = name
+    self.num_channels = num_channels
+    self.num_intermediate_factor = config.num_intermediate_factor
+    self.use_glu_kernel = config.use_glu_kernel
+    self.num_intermediate = int(num_channels * config.num_intermediate_factor)
+    self.input_layer_norm = LayerNorm(num_channels, name="input_layer_norm")
+    self.transition1 = Linear(num_channels, self.num_intermediate * 2, name="transition1")
+    self.transition2 = Linear(self.num_intermediate, num_channels, name="transition2")
+
+
+class DiffusionTransitionBlock(_NoTorchPath, torch.nn.Module):
+  """transformer.py:157-231 (``TransitionBlock`` of the diffusion transformer): AdaLN (``ffw_``),
+  SwiGLU of ``transition`` (``[C, 2I]``), AdaLN-zero output (``transition2`` times the sigmoid
+  gate of the condition) plus the residual."""
+
+  def __init__(self, global_config: GlobalConfig, *, num_channels: int, num_intermediate_factor: int,
+               single_cond_size: int | None = None, use_glu_kernel: bool = True, dtype=None, name: str = ""):
+    super().__init__()
+    self.name = name
+    self.dtype = dtype
+    self.use_glu_kernel = use_glu_kernel
+    self.num_intermediates = num_intermediate_factor * num_channels
+    self.layer_norm = AdaptiveLayerNorm(num_channels, single_cond_size, dtype=dtype, name="ffw_")
+    self.transition = Linear(num_channels, self.num_intermediates * 2, bias=False, dtype=dtype,
+                             name="ffw_transition1")
+    self.zero_init = AdaptiveZeroInit(global_config, num_channels=num_channels, hidden_size=self.num_intermediates,
+                                      single_cond_size=single_cond_size, dtype=dtype, name="ffw_")
 
 
 class TransformerPairLogits(_NoTorchPath, torch.nn.Module):

@@ -88,14 +88,15 @@ def make_trimul(N: int, *, C: int = 128, incoming: bool = False, padded: bool = 
 
 
 def make_single(N: int, *, C_s: int = 384, C_z: int = 128, H: int = 16, seed: int = 3, sharp: bool = False,
-                padded: bool = False, dtype=torch.bfloat16):
+                padded: bool = False, transition: bool = False, dtype=torch.bfloat16):
   g = _gen(seed)
   s = torch.randn(N, C_s, generator=g).to(dtype)
   z = torch.randn(N, N, C_z, generator=g).to(dtype)
   seq = torch.ones(N, dtype=torch.bool)
   if padded:
     seq[N - N // 10:] = False
-  mod = M.SingleActUpdate(M.GlobalConfig(), C_z, C_s, M.SelfAttention.Config(num_head=H))
+  mod = M.SingleActUpdate(M.GlobalConfig(), C_z, C_s, M.SelfAttention.Config(num_head=H),
+                          M.TransitionBlock.Config() if transition else None)
   fill_parameters(mod, seed + 1000, sharp=sharp)
   return mod, z, s, seq
 
@@ -126,6 +127,30 @@ def make_diffusion_stack(N: int, *, S: int = 5, L: int = 24, C: int = 768, C_con
                         single_cond_size=C_cond, name="diffusion_transformer")
     mods.append(fill_parameters(m, seed + 1000 + layer))
   return mods, act, cond, bias, mask
+
+
+def make_transition(rows: int, *, C: int = 384, factor: int = 4, lead=(), seed: int = 9, sharp: bool = True,
+                    dtype=torch.bfloat16):
+  """Trunk transition (blocks.py:38-96) and its input ``[*lead, rows, C]``: the single transition of
+  SingleActUpdate (C = 384, factor 4) or the pair transition (C = 128, lead = (N,))."""
+  act = torch.randn(*lead, rows, C, generator=_gen(seed)).to(dtype)
+  mod = M.TransitionBlock(M.TransitionBlock.Config(num_intermediate_factor=factor), M.GlobalConfig(),
+                          num_channels=C, name="transition")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, act
+
+
+def make_diffusion_transition(N: int, *, S: int = 5, C: int = 768, C_cond: int | None = 384, factor: int = 2,
+                              seed: int = 10, sharp: bool = True, dtype=torch.bfloat16):
+  """Diffusion-transformer transition (transformer.py:157-231), its act ``[S, N, C]`` and condition
+  ``[N, C_cond]`` (None: the unconditioned form)."""
+  g = _gen(seed)
+  act = torch.randn(S, N, C, generator=g).to(dtype)
+  cond = None if C_cond is None else torch.randn(N, C_cond, generator=g).to(dtype)
+  mod = M.DiffusionTransitionBlock(M.GlobalConfig(), num_channels=C, num_intermediate_factor=factor,
+                                   single_cond_size=C_cond, name="diffusion_transition")
+  fill_parameters(mod, seed + 1000, sharp=sharp)
+  return mod, act, cond
 
 
 @dataclasses.dataclass

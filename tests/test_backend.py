@@ -193,3 +193,18 @@ def test_graph_replay_flag_and_signature(monkeypatch, reset_runtime):
   for _ in range(3):
     m.forward(torch.zeros(2), flag=True)
   assert calls == [True] * 3 and "_hip_graph_cache" not in m.__dict__
+
+
+def test_transition_factories_are_replaced(reset_runtime):
+  original_trunk, original_diff = M.TransitionBlock, M.DiffusionTransitionBlock
+  config.configure_runtime(backend="hip", device="cuda",
+                           native_ops=["evoformer_transition_block", "diffusion_transition_block"])
+  backends.init()
+  assert M.TransitionBlock.__name__ == "TransitionBlockHip" and issubclass(M.TransitionBlock, original_trunk)
+  assert M.DiffusionTransitionBlock.__name__ == "DiffusionTransitionBlockHip"
+  t = M.TransitionBlock(M.TransitionBlock.Config(), M.GlobalConfig(), num_channels=64)
+  with pytest.raises(RuntimeError, match="not prepared"):
+    t(torch.zeros(3, 64))
+  config.configure_runtime(backend="torch")
+  backends.init()
+  assert M.TransitionBlock is original_trunk and M.DiffusionTransitionBlock is original_diff

@@ -447,6 +447,113 @@ def test_transformer_conditioned_block_loop():
 
 
 # --------------------------------------------------------------------------------------
+# Transitions (blocks.py:38-96, transformer.py:157-231)
+# --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("sharp", [False, True])
+@pytest.mark.parametrize("rows,C,lead", [(768, 384, ()), (37, 384, ()), (64, 128, (64,)), (5, 128, (3,))])
+def test_trunk_transition(rows, C, lead, sharp):
+  """The single transition of SingleActUpdate (C=384) and the pair transition (C=128 over [N, N]).
+  The module output is checked at the configurations' weights (std 0.02); with sharp weights
+  (std 1/sqrt(fan_in)) the update reaches magnitudes where a bf16 result's own rounding passes
+  2e-2, so there the update is checked against 2% of its largest magnitude, as for the attention
+  modules."""
+  mod, act = W.make_transition(rows, C=C, lead=lead, seed=60 + rows, sharp=sharp)
+  hip = _prepared(mod)
+  p = _params(hip)
+  if not sharp:
+    out = hip(act.to(DEV))
+    assert out.shape == act.shape and out.dtype == act.dtype
+    ref = OM.transition_block(act.float(), p)
+    assert_close_bf16(out, ref, f"trunk transition rows={rows} C={C}")
+  upd = hip(act.to(DEV), add_residual=False)
+  d_ref = OM.transition_block(act.float(), p, return_update=True)
+  assert_close_bf16(upd, d_ref, f"trunk transition update rows={rows} C={C} sharp={sharp}",
+                    max_abs=2e-2 * max(1.0, d_ref.abs().max().item()))
+
+
+@pytest.mark.parametrize("sharp", [False, True])
+@pytest.mark.parametrize("N,S,cond", [(100, 2, True), (1024, 5, True), (33, 1, False)])
+def test_diffusion_transition(N, S, cond, sharp):
+  mod, act, c = W.make_diffusion_transition(N, S=S, C_cond=384 if cond else None, seed=70 + N, sharp=sharp)
+  hip = _prepared(mod)
+  cd = None if c is None else c.to(DEV)
+  p = _params(hip)
+  cf = None if c is None else c.float()
+  if not sharp:
+    out = hip(act.to(DEV), single_cond=cd)
+    ref = OM.diffusion_transition_block(act.float(), cf, p)
+    assert_close_bf16(out, ref, f"diffusion transition N={N} S={S} cond={cond}")
+  upd = hip(act.to(DEV), single_cond=cd, add_residual=False)
+  d_ref = OM.diffusion_transition_block(act.float(), cf, p, return_update=True)
+  assert_close_bf16(upd, d_ref, f"diffusion transition update N={N} sharp={sharp}",
+                    max_abs=2e-2 * max(1.0, d_ref.abs().max().item()))
+
+
+def test_diffusion_transition_precomputed_conditioning_is_the_same_call():
+  """The transition's AdaLN from the one-call conditioning (pre_scale / pre_shift / pre_zgate)
+  equals the transition conditioned from single_cond."""
+  from sparsefold_amd.backends.hip import ops
+  N = 96
+  mod, act, c = W.make_diffusion_transition(N, S=2, seed=77)
+  hip = _prepared(mod)
+  lnc = hip._hip_ada_lnc_w[None]
+  scale, shift, zgate = ops.diffusion_conditioning(c.to(DEV), lnc, hip._hip_ada_w_scale, hip._hip_ada_b_scale,
+                                                   hip._hip_ada_w_shift, hip._hip_w_zc, hip._hip_b_zc)
+  got = hip(act.to(DEV), adaptive_scale=scale[0], adaptive_bias=shift[0], zero_gate=zgate[0], add_residual=False)
+  want = hip(act.to(DEV), single_cond=c.to(DEV), add_residual=False)
+  d_ref = OM.diffusion_transition_block(act.float(), c.float(), _params(hip), return_update=True)
+  tol = 2e-2 * d_ref.abs().max().item()
+  assert_close_bf16(got, d_ref, "precomputed-conditioning transition", max_abs=tol)
+  assert_close_bf16(got, want.float().cpu(), "precomputed vs per-call conditioning", max_abs=tol)
+
+
+def test_single_act_update_with_transition():
+  """SingleActUpdate.forward (blocks.py:739-763): pair-logit prologue, single attention, then
+  the single transition."""
+  N = 96
+  mod, z, s, seq = W.make_single(N, seed=81, padded=True, sharp=True, transition=True)
+  hip = _prepared(mod)
+  assert getattr(hip.single_transition, "_native_prepared", False)
+  out = hip(z.to(DEV), s.to(DEV), seq.to(DEV))
+  p = _params(hip)
+  mid = OM.single_act_update_attention(z.float(), s.float(), seq, p)
+  sub = {k[len("single_transition."):]: v for k, v in p.items() if k.startswith("single_transition.")}
+  ref = OM.transition_block(mid, sub)
+  assert_close_bf16(out, ref, "SingleActUpdate with transition", max_abs=2e-2 * max(1.0, ref.abs().max().item()))
+
+
+def test_transformer_conditioned_loop_with_hip_transitions():
+  """Transformer.forward with HIP attention and HIP transition blocks: one conditioning call for
+  all 8 layers (4 attention + 4 transition), against the oracle's block chain."""
+  N = 64
+  mod, pair_cond = W.make_transformer_pack(N, P=16, num_blocks=4, super_block_size=2, seed=90)
+  mod.self_attention = torch.nn.ModuleList(
+      [torch.nn.ModuleList([W.make_diffusion(N, S=1, seed=91 + 10 * i + j, sharp=True)[0] for j in range(2)])
+       for i in range(2)])
+  mod.transition_block = torch.nn.ModuleList(
+      [torch.nn.ModuleList([W.make_diffusion_transition(N, seed=95 + 10 * i + j)[0] for j in range(2)])
+       for i in range(2)])
+  mod._cache = _NoCache()
+  mod = _prepared(mod)
+  assert mod._hip_dc_transitions
+  _, act, cond, _, mask = W.make_diffusion(N, S=2, seed=99, padded=True)
+  calls = []
+  whole = mod.diffusion_conditioning
+  mod.diffusion_conditioning = lambda c: (calls.append(c), whole(c))[1]
+  out = mod(act.to(DEV), mask.to(DEV), cond.to(DEV), pair_cond.to(DEV))
+  assert len(calls) == 1
+  opack = OM.transformer_pair_logits(pair_cond.float(), _params(mod), 2, None)
+  ref = act.float()
+  for i in range(2):
+    for j in range(2):
+      ref = OM.self_attention(ref, mask, _params(mod.self_attention[i][j]), pair_logits=opack[i][j],
+                              single_cond=cond.float())
+      ref = OM.diffusion_transition_block(ref, cond.float(), _params(mod.transition_block[i][j]))
+  assert_close_bf16(out, ref, "Transformer loop with HIP transitions", max_abs=2e-2 * ref.abs().max().item())
+
+
+# --------------------------------------------------------------------------------------
 # Triangle multiplicative update (blocks.py:425-566)
 # --------------------------------------------------------------------------------------
 

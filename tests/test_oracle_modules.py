@@ -333,3 +333,43 @@ def test_windowed_cross_attention_matches_brute_force_over_converted_keys():
   _, upd = brute.cross_attention(xq.numpy(), keys, qmask.numpy(), kmask.numpy(), _npd(p), bias.numpy(),
                                  cq.numpy(), ck.numpy())
   np.testing.assert_allclose(out.numpy(), upd, rtol=1e-4, atol=1e-5)
+
+
+# --------------------------------------------------------------------------------------
+# Transitions (blocks.py:38-96, transformer.py:157-231) against float64 per-element loops
+# --------------------------------------------------------------------------------------
+
+def test_transition_block_matches_brute_force():
+  mod, act = W.make_transition(5, C=8, factor=2, seed=51, dtype=torch.float32)
+  p = _sd(mod)
+  out = OM.transition_block(act, p)
+  ref, upd = brute.transition_block(act.numpy(), _npd(p))
+  np.testing.assert_allclose(out.numpy(), ref, rtol=1e-4, atol=1e-5)
+  np.testing.assert_allclose(OM.transition_block(act, p, return_update=True).numpy(), upd, rtol=1e-4, atol=1e-5)
+  # a plant: the halves of transition1 swapped (swish on the second half) must be caught
+  w1 = p["transition1.weight"]
+  swapped = dict(p, **{"transition1.weight": torch.cat([w1[:, w1.shape[1] // 2:], w1[:, :w1.shape[1] // 2]], 1)})
+  assert not np.allclose(OM.transition_block(act, swapped, return_update=True).numpy(), upd, rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("cond", [True, False])
+def test_diffusion_transition_block_matches_brute_force(cond):
+  mod, act, c = W.make_diffusion_transition(4, S=2, C=8, C_cond=6 if cond else None, factor=2, seed=52,
+                                            dtype=torch.float32)
+  p = _sd(mod)
+  out = OM.diffusion_transition_block(act, c, p)
+  for s in range(2):
+    ref, upd = brute.diffusion_transition_block(act[s].numpy(), None if c is None else c.numpy(), _npd(p))
+    np.testing.assert_allclose(out[s].numpy(), ref, rtol=1e-4, atol=1e-5)
+  if cond:   # a plant: the AdaLN-zero gate taken from the normalised rows instead of the condition
+    bad = dict(p, **{"zero_init.adaptive_zero_cond.bias": p["zero_init.adaptive_zero_cond.bias"] + 3.0})
+    assert not np.allclose(OM.diffusion_transition_block(act, c, bad).numpy(), out.numpy(), rtol=1e-3, atol=1e-4)
+
+
+def test_swish_is_x_sigmoid_x_and_zero_below_minus_20():
+  from oracle.primitives import swish
+  x = torch.linspace(-30, 30, 601)
+  s = swish(x)
+  assert (s[x < -20] == 0).all()
+  keep = x >= -20
+  assert (s[keep] - x[keep] * torch.sigmoid(x[keep])).abs().max() < 1e-4
