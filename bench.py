@@ -214,6 +214,18 @@ def _config_builders() -> dict:
           "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
     return build
 
+  def trimul(n, incoming):  # triangle multiplicative update, z [n, n, 128], outgoing / incoming edges
+    def build():
+      mod, z, mask = W.make_trimul(n, incoming=incoming, padded=True, seed=13, sharp=False)
+      mod = mod.to(dev); backends.prepare(mod)
+      z, mask = z.to(dev), mask.to(dev)
+      c = 128
+      flop = 2 * n ** 3 * c + 2 * n * n * c * 4 * c + 2 * n * n * c * 2 * c
+      return (lambda: mod(z, mask)), (lambda t: {
+          "ms_per_call": round(t, 4), "tflops": round(flop / t / 1e9, 1),
+          "frac_bf16_peak": round(flop / t / 1e9 / PEAK_BF16_TFLOPS, 4), "bound": "mfma"})
+    return build
+
   def c5():    # windowed atom attention, 5 samples x 8192 atoms, 32-query / 128-key windows
     S, atoms, c, h, d = 5, 8192, 128, 4, 32
     mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5)
@@ -251,7 +263,9 @@ def _config_builders() -> dict:
           "single_n768": c3b, "diffusion_5x1024_block": c4,
           "diffusion_5x1024_24_blocks": c4_stack, "diffusion_transition_5x1024": c4_transition,
           "single_transition_n768": trunk_transition(768, 384, ()),
-          "pair_transition_n384": trunk_transition(384, 128, (384,)), "window_5x8192": c5,
+          "pair_transition_n384": trunk_transition(384, 128, (384,)),
+          "trimul_outgoing_n768": trimul(768, False), "trimul_incoming_n768": trimul(768, True),
+          "window_5x8192": c5,
           "transformer_pack_n1024": pack_tr, "cross_pack_8192": pack_x}
 
 

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 8
+#define SF_HIP_ABI_VERSION 9
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -130,6 +130,10 @@ typedef struct sf_linear_args {
   void* y; int64_t y_rs; int32_t ycols;        /* y may be NULL when only yt is wanted */
   int32_t tcol0, tcols; void* yt; int64_t yt_rs;
   int32_t glu;                                 /* 1: gated pairs (see above) */
+  /* Batched form (batch > 1, K % 64 == 0, no mul / residual / yt): member b reads x + b*x_bs and
+   * wt + b*w_bs and writes y + b*y_bs (element strides) -- the per-channel products of the
+   * triangle multiplicative update.  batch 0 or 1 = one product. */
+  int32_t batch; int64_t x_bs, w_bs, y_bs;
 } sf_linear_args;
 
 int sf_hip_linear_fwd(const sf_linear_args* a, void* stream);
@@ -355,9 +359,8 @@ int sf_hip_transition_fwd(const sf_transition_args* a, void* workspace, size_t w
  *          projection)
  *   w_out  [C, C] output_projection;  w_gate [C, C] gating_linear
  * Workspace from sf_hip_triangle_mult_workspace_bytes (0 = unsupported sizes).  out may not
- * alias z; z, out and the weights 16-byte aligned.
- * STATUS: the per-channel product stage is not implemented in this build; the call validates
- * its arguments and then returns an error without launching anything. */
+ * alias z; z, out and the weights 16-byte aligned.  N <= 8192.  The per-channel products run as one
+ * batched GEMM over zero-padded [128][Pn][Pn] planes (Pn = N rounded up to 64). */
 typedef struct sf_triangle_mult_args {
   int32_t N, C;
   int32_t incoming;                             /* 0 outgoing, 1 incoming edges */

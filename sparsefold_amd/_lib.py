@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -60,6 +60,7 @@ class LinearArgs(C.Structure):
       ("y", _vp), ("y_rs", _i64), ("ycols", _i32),
       ("tcol0", _i32), ("tcols", _i32), ("yt", _vp), ("yt_rs", _i64),
       ("glu", _i32),
+      ("batch", _i32), ("x_bs", _i64), ("w_bs", _i64), ("y_bs", _i64),
   ]
 
 

@@ -235,8 +235,9 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t m0 = (int64_t)blockIdx.x * BM;
   const int n0 = blockIdx.y * BN;
-  const uint16_t* xp = (const uint16_t*)a.x;
-  const uint16_t* wp = (const uint16_t*)a.wt;
+  const int64_t bz = blockIdx.z;                              // batch member (0 unless batched)
+  const uint16_t* xp = (const uint16_t*)a.x + bz * a.x_bs;
+  const uint16_t* wp = (const uint16_t*)a.wt + bz * a.w_bs;
   const int rsw = 8 * ((lane & 7) ^ ((lane >> 3) & 7));       // this lane's swizzled source piece
   const int64_t mlast = a.M - 1;
   const int nlast = a.N - 1;
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
         *reinterpret_cast<f32x4*>(&ct[(wm * WR + 32 * mb + li) * CP + wn * WC + 32 * nb + 8 * c + 4 * half]) =
             f32x4{acc[mb][nb][4 * c], acc[mb][nb][4 * c + 1], acc[mb][nb][4 * c + 2], acc[mb][nb][4 * c + 3]};
   __syncthreads();
-  uint16_t* yp = (uint16_t*)a.y;
+  uint16_t* yp = a.y ? (uint16_t*)a.y + bz * a.y_bs : nullptr;
   uint16_t* ytp = (uint16_t*)a.yt;
   const uint16_t* rp = (const uint16_t*)a.residual;
   const uint16_t* mp = (const uint16_t*)a.mul;
@@ -722,6 +723,13 @@ extern "C" int sf_hip_linear_fwd(const sf_linear_args* a, void* stream) {
   if (a->yt && (a->tcol0 < 0 || a->tcols < 0 || a->tcol0 + a->tcols > a->N)) {
     sf_set_error("linear: transposed column range out of bounds"); return 1;
   }
+  const int32_t batch = a->batch > 1 ? a->batch : 1;
+  if (batch > 1 && (a->K % 64 != 0 || batch > 65535 || a->yt || a->mul || a->residual || a->y == nullptr ||
+                    a->x_bs % 8 || a->w_bs % 8 || a->y_bs < 0)) {
+    sf_set_error("linear: the batched form needs K %% 64 == 0, batch <= 65535, 16-byte aligned batch strides and "
+                 "no mul / residual / transposed output (K=%d batch=%d)", a->K, a->batch);
+    return 1;
+  }
   if (a->glu && (a->K % 64 != 0 || a->N % 8 != 0 || a->y == nullptr || a->yt || a->mul || a->residual ||
                  a->post_sigmoid || a->ycols || !al16(a->y) || a->y_rs % 4)) {
     sf_set_error("linear: the gated (glu) form needs K %% 64 == 0, N %% 8 == 0, an 8-byte aligned y with "
@@ -731,13 +739,13 @@ extern "C" int sf_hip_linear_fwd(const sf_linear_args* a, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->K % 64 == 0) {
     // largest tile that still gives >= 512 workgroups (two per CU); else the smallest
-    auto tiles = [&](int bm, int bn) { return ((a->M + bm - 1) / bm) * (int64_t)((a->N + bn - 1) / bn); };
+    auto tiles = [&](int bm, int bn) { return ((a->M + bm - 1) / bm) * (int64_t)((a->N + bn - 1) / bn) * batch; };
     int bm = 64, bn = 64;
     if (tiles(128, 128) >= 512) bm = 128, bn = 128;
     else if (tiles(64, 128) >= 512) bm = 64, bn = 128;
     const int64_t gm = (a->M + bm - 1) / bm;
     if (gm > 0x7fffffff) { sf_set_error("linear: M too large"); return 1; }
-    const dim3 grid((unsigned)gm, (a->N + bn - 1) / bn);
+    const dim3 grid((unsigned)gm, (a->N + bn - 1) / bn, (unsigned)batch);
     if (bm == 128) hipLaunchKernelGGL((linear64_kernel<128, 128>), grid, dim3(256), 0, st, *a);
     else if (bn == 128) hipLaunchKernelGGL((linear64_kernel<64, 128>), grid, dim3(256), 0, st, *a);
     else hipLaunchKernelGGL((linear64_kernel<64, 64>), grid, dim3(256), 0, st, *a);

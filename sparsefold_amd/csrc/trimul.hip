@@ -4,10 +4,16 @@
 //   1. trimul_proj_kernel   x = LN(z) (left_norm_input) straight into MFMA operands; the gated
 //                           linear unit sigmoid(x W_g) * (x W_p) (primitives.py:586-631) for the
 //                           2C projected channels, zero where mask[i] & mask[k] is false
-//                           (blocks.py:516-530), written channel-major: a[c][i][k] = channel 2c,
-//                           b[c][i][k] = channel 2c + 1 ("(c i2) b n -> i2 c b n", :540).
-//   2. per-channel product  t[c] = a[c] b[c]^T (outgoing) or a[c]^T-contracted (incoming):
-//                           NOT IMPLEMENTED -- the entry point returns an error before any launch.
+//                           (blocks.py:516-530), written channel-major into zero-padded planes
+//                           [c][Pn][Pn] (Pn = N rounded up to 64): a = channel 2c, b = 2c + 1
+//                           ("(c i2) b n -> i2 c b n", :540).  Outgoing edges store position
+//                           (i, k) at row i, column k; incoming edges walk z column-wise and store
+//                           position (k, j) at row j, column k -- the transposed planes -- so that
+//                           both edges contract over the planes' contiguous dimension.
+//   2. per-channel product  t[c][i][j] = sum_k A[c][i][k] B[c][j][k] (blocks.py:555): one batched
+//                           NT GEMM over the 128 channels (sf_hip_linear_fwd, batched form) with
+//                           (A, B) = (a, b) for outgoing and (b^T, a^T) for incoming edges; the zero
+//                           padding of the contraction dimension adds nothing.
 //   3. trimul_out_kernel    LN over the channels of t (center_norm, dim=-3), output projection,
 //                           gate sigmoid(LN(z) W_gl) recomputed from z, out = z + update
 //                           (blocks.py:561-566).
@@ -27,6 +33,7 @@ constexpr int kGlu = 4 * kC;       // GLU rows: gate a, gate b, projection a, pr
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 int64_t plane_stride(int N) { return ((int64_t)N * N + 31) & ~(int64_t)31; }
+int padded_n(int N) { return (N + 63) & ~63; }
 
 // Folded weights and offsets, one block of rows each: GLU (left_norm), output (center_norm),
 // gate (left_norm).
@@ -58,15 +65,14 @@ __global__ __launch_bounds__(256) void trimul_fold_kernel(const FoldArgs a) {
 }
 
 struct ProjArgs {
-  int N;
-  int64_t P, Pp;                 // N*N; plane stride (multiple of 32)
-  const uint16_t* z;             // [P, 128]
+  int N, Pn, incoming;           // Pn: padded plane side (multiple of 64)
+  const uint16_t* z;             // [N*N, 128]
   const uint8_t* mask;           // [N] or NULL
   const uint16_t* w;             // folded GLU [512, 128]
   const float* off;              // [512]
-  uint16_t* a;                   // [128][Pp]
-  uint16_t* b;                   // [128][Pp]
-  int items, items_per_wave;     // 32-position blocks
+  uint16_t* a;                   // [128][Pn][Pn]
+  uint16_t* b;                   // [128][Pn][Pn]
+  int items, items_per_wave;     // blocks of 32 plane columns: Pn rows x Pn / 32
 };
 
 // D = X W^T per 32 positions x 32 channels: lane (li, half) ends with channel li of the tile at
@@ -93,25 +99,26 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
   __syncthreads();
   const int first = (blockIdx.x * kTW + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
+  const int cbs = a.Pn / 32;                            // column blocks per plane row
+  const int64_t plane = (int64_t)a.Pn * a.Pn;
   for (int item = first; item < last; ++item) {
-    const int64_t p = (int64_t)item * 32 + li;
-    const bool ok = p < a.P;
+    // plane row R, columns 32 cb .. 32 cb + 31; this lane's column col.  Outgoing: z position
+    // (R, col); incoming: (col, R), so that the planes hold a^T and b^T
+    const int R = item / cbs, cb = item - R * cbs, col = 32 * cb + li;
+    const int za = a.incoming ? col : R, zb = a.incoming ? R : col;
+    const bool ok = za < a.N && zb < a.N;
     u32x4 zn[8];
-    const uint16_t* zp = a.z + (ok ? p : 0) * kC + 8 * half;
+    const uint16_t* zp = a.z + (ok ? (int64_t)za * a.N + zb : 0) * kC + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
-    bool keep = ok;
-    if (ok && a.mask) {
-      const int i = (int)(p / a.N), k = (int)(p - (int64_t)i * a.N);
-      keep = a.mask[i] && a.mask[k];
-    }
-    const uint32_t kept = (uint32_t)__ballot(keep);        // bit q: position q of the block
+    const bool keep = ok && (a.mask == nullptr || (a.mask[za] && a.mask[zb]));
+    const uint32_t kept = (uint32_t)__ballot(keep);        // bit q: column 32 cb + q of the row
     bf16x8 xo[8];
     ln128_operands(zn, ok, xo);
-    const int64_t pbase = (int64_t)item * 32 + 4 * half;
+    const int64_t pbase = (int64_t)R * a.Pn + 32 * cb + 4 * half;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {              // 0: a (even channels), 1: b (odd)
-      uint16_t* plane = side ? a.b : a.a;
+      uint16_t* dstp = side ? a.b : a.a;
 #pragma unroll
       for (int nb = 0; nb < kC / 32; ++nb) {
         const int rg = side * kC + 32 * nb + li;        // gate row of this lane's channel
@@ -125,7 +132,7 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
           ap = mfma32(xo[kk], as_bf16x8(ld16(&sW[rp * kWS + 16 * kk + 8 * half])), ap);
         }
         const float og = sOff[rg], op = sOff[rp];
-        uint16_t* dst = plane + (int64_t)(32 * nb + li) * a.Pp + pbase;
+        uint16_t* dst = dstp + (int64_t)(32 * nb + li) * plane + pbase;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           float v[4];
@@ -250,30 +257,29 @@ struct Ws {
   uint16_t *wglu, *wout, *wgate;
   float *oglu, *oout, *ogate;
   uint16_t *a, *b, *t;
+  size_t bytes;
 };
 
 Ws carve(char* base, int N) {
   Ws w{};
   size_t off = 0;
   auto take = [&](size_t bytes) { char* p = base ? base + off : nullptr; off += align256(bytes); return p; };
-  const size_t plane = (size_t)plane_stride(N) * kC * 2;
+  const size_t ab = (size_t)padded_n(N) * padded_n(N) * kC * 2;      // a / b planes, [c][Pn][Pn]
+  const size_t tp = (size_t)plane_stride(N) * kC * 2;                 // t planes, [c][Pp]
   w.wglu = reinterpret_cast<uint16_t*>(take((size_t)kGlu * kC * 2));
   w.wout = reinterpret_cast<uint16_t*>(take((size_t)kC * kC * 2));
   w.wgate = reinterpret_cast<uint16_t*>(take((size_t)kC * kC * 2));
   w.oglu = reinterpret_cast<float*>(take(kGlu * 4));
   w.oout = reinterpret_cast<float*>(take(kC * 4));
   w.ogate = reinterpret_cast<float*>(take(kC * 4));
-  w.a = reinterpret_cast<uint16_t*>(take(plane));
-  w.b = reinterpret_cast<uint16_t*>(take(plane));
-  w.t = reinterpret_cast<uint16_t*>(take(plane));
+  w.a = reinterpret_cast<uint16_t*>(take(ab));
+  w.b = reinterpret_cast<uint16_t*>(take(ab));
+  w.t = reinterpret_cast<uint16_t*>(take(tp));
+  w.bytes = off;
   return w;
 }
 
-size_t ws_bytes(int N) {
-  const size_t plane = (size_t)plane_stride(N) * kC * 2;
-  return align256((size_t)kGlu * kC * 2) + 2 * align256((size_t)kC * kC * 2) + align256(kGlu * 4) +
-         2 * align256(kC * 4) + 3 * align256(plane);
-}
+size_t ws_bytes(int N) { return carve(nullptr, N).bytes; }
 
 int launch_grid(const void* kernel, int items) {
   const int waves = std::max(1, std::min(sf_resident_workgroups(kernel, 64 * kTW) * kTW, items));
@@ -294,8 +300,8 @@ extern "C" int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* wo
     sf_set_error("triangle_mult: z, out, the three weights, ln_w and cn_w must be non-null");
     return 1;
   }
-  if (a->C != kC || a->N <= 0 || (int64_t)a->N * a->N > ((int64_t)1 << 31) - 64) {
-    sf_set_error("triangle_mult: need C == %d and 0 < N*N < 2^31 (N=%d C=%d)", kC, a->N, a->C);
+  if (a->C != kC || a->N <= 0 || a->N > 8192) {
+    sf_set_error("triangle_mult: need C == %d and 0 < N <= 8192 (N=%d C=%d)", kC, a->N, a->C);
     return 1;
   }
   if (a->z == a->out) {
@@ -312,13 +318,8 @@ extern "C" int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* wo
     sf_set_error("triangle_mult: z, out and the weights must be 16-byte aligned");
     return 1;
   }
-  // The per-channel product stage is not implemented: its first implementation (a prebuilt
-  // BLAS batched GEMM) was followed by a GPU fault whose cause is not established, so the module
-  // refuses before any launch until a product kernel of this library's own replaces it.
-  sf_set_error("triangle_mult: the per-channel product stage is disabled (no batched GEMM in this build)");
-  return 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int N = a->N;
+  const int N = a->N, Pn = padded_n(N);
   const int64_t P = (int64_t)N * N, Pp = plane_stride(N);
   const Ws w = carve(static_cast<char*>(workspace), N);
 
@@ -333,18 +334,32 @@ extern "C" int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* wo
   int rc = sf_check_launch("trimul_fold_kernel");
   if (rc) return rc;
 
-  const int items = (int)((P + 31) / 32);
   {
     ProjArgs pa{};
-    pa.N = N; pa.P = P; pa.Pp = Pp; pa.z = static_cast<const uint16_t*>(a->z); pa.mask = a->mask;
-    pa.w = w.wglu; pa.off = w.oglu; pa.a = w.a; pa.b = w.b; pa.items = items;
-    const int waves = launch_grid(reinterpret_cast<const void*>(trimul_proj_kernel), items);
-    pa.items_per_wave = (items + waves - 1) / waves;
-    const int groups = (items + pa.items_per_wave * kTW - 1) / (pa.items_per_wave * kTW);
+    pa.N = N; pa.Pn = Pn; pa.incoming = a->incoming ? 1 : 0;
+    pa.z = static_cast<const uint16_t*>(a->z); pa.mask = a->mask;
+    pa.w = w.wglu; pa.off = w.oglu; pa.a = w.a; pa.b = w.b;
+    pa.items = Pn * (Pn / 32);                          // every plane row, padding included
+    const int waves = launch_grid(reinterpret_cast<const void*>(trimul_proj_kernel), pa.items);
+    pa.items_per_wave = (pa.items + waves - 1) / waves;
+    const int groups = (pa.items + pa.items_per_wave * kTW - 1) / (pa.items_per_wave * kTW);
     hipLaunchKernelGGL(trimul_proj_kernel, dim3(groups), dim3(64 * kTW), 0, st, pa);
     if ((rc = sf_check_launch("trimul_proj_kernel"))) return rc;
   }
 
+  // t[c][i][j] = sum_k A[c][i][k] B[c][j][k], rows i, j < N, contraction over the padded Pn
+  {
+    sf_linear_args g{};
+    g.M = N; g.N = N; g.K = Pn;
+    g.x = a->incoming ? w.b : w.a; g.x_rs = Pn;
+    g.wt = a->incoming ? w.a : w.b;
+    g.mul_rows = 1;
+    g.y = w.t; g.y_rs = N;
+    g.batch = kC; g.x_bs = (int64_t)Pn * Pn; g.w_bs = (int64_t)Pn * Pn; g.y_bs = Pp;
+    if ((rc = sf_hip_linear_fwd(&g, st))) return rc;
+  }
+
+  const int items = (int)((P + 31) / 32);              // 32-position blocks of the output
   OutArgs oa{};
   oa.P = P; oa.Pp = Pp; oa.t = w.t; oa.z = static_cast<const uint16_t*>(a->z);
   oa.wo = w.wout; oa.oo = w.oout; oa.wg = w.wgate; oa.og = w.ogate;

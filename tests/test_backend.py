@@ -208,3 +208,12 @@ def test_transition_factories_are_replaced(reset_runtime):
   config.configure_runtime(backend="torch")
   backends.init()
   assert M.TransitionBlock is original_trunk and M.DiffusionTransitionBlock is original_diff
+
+
+def test_trimul_incoming_edge_is_read_from_either_equation_form():
+  """The reference module keeps the per-channel einsum form (blocks.py:447-451); the config keeps
+  the pair form.  Both name the incoming edge."""
+  from sparsefold_amd.backends.hip import modules as HM
+  inc = HM.TriangleMultiplicationHipMixin.INCOMING_EQUATIONS
+  assert "...kjc,...kic->...ijc" in inc and "...ckj,...cki->...cij" in inc
+  assert "...ikc,...jkc->...ijc" not in inc and "...cik,...cjk->...cij" not in inc

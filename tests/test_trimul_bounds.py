@@ -1,0 +1,138 @@
+"""CPU model of every global memory access of the triangle multiplicative update's kernels
+(csrc/trimul.hip: the prologue, the batched NT product through the library's GEMM, the epilogue)
+and of the host's launch arithmetic, checked against the buffer sizes the host allocates, for
+N in {1, 37, 64, 384, 768} and both edges.  The index expressions are the kernels' own, restated;
+nothing here runs on a GPU."""
+import numpy as np
+import pytest
+
+from sparsefold_amd import _lib
+
+KC, KTW = 128, 8                 # channels, waves per workgroup of the position kernels
+RESIDENT = 256                   # resident workgroups of the position kernels (one per CU)
+
+
+def _pn(n):
+  return (n + 63) & ~63
+
+
+def _pp(n):
+  return (n * n + 31) & ~31
+
+
+def _grid(items):
+  """launch_grid + the host's items-per-wave / group arithmetic."""
+  waves = max(1, min(RESIDENT * KTW, items))
+  ipw = (items + waves - 1) // waves
+  groups = (items + ipw * KTW - 1) // (ipw * KTW)
+  return ipw, groups
+
+
+def _covered(items, ipw, groups):
+  """Every item is processed by exactly one wave."""
+  seen = np.zeros(items, np.int64)
+  for wave_id in range(groups * KTW):
+    first = wave_id * ipw
+    last = min(first + ipw, items)
+    if first < last:
+      seen[first:last] += 1
+  return bool((seen == 1).all())
+
+
+def _proj_accesses(N, incoming):
+  Pn = _pn(N)
+  items = Pn * (Pn // 32)
+  ipw, groups = _grid(items)
+  assert _covered(items, ipw, groups)
+  item = np.arange(items)[:, None]
+  lane = np.arange(64)[None, :]
+  half, li = lane >> 5, lane & 31
+  cbs = Pn // 32
+  R, cb = item // cbs, item % cbs
+  col = 32 * cb + li
+  za, zb = (col, R) if incoming else (R, col)
+  ok = (za < N) & (zb < N)
+  # z reads: 8 x 16 bytes at element (za * N + zb) * 128 + 8 * half + 16 kk (only where ok)
+  zfirst = (za * N + zb) * KC + 8 * half
+  zlast = zfirst + 16 * 7 + 7
+  z_max = int(zlast[ok].max()) if ok.any() else -1
+  # mask reads: mask[za], mask[zb] where ok
+  m_max = int(np.maximum(za, zb)[ok].max()) if ok.any() else -1
+  # plane stores: channel 32 nb + li, 4 groups of 4 elements at R * Pn + 32 cb + 4 half + 8 g
+  plane = Pn * Pn
+  pbase = R * Pn + 32 * cb + 4 * half
+  lo = (32 * 0 + li) * plane + pbase                      # nb = 0, g = 0
+  hi = (32 * 3 + li) * plane + pbase + 8 * 3 + 3          # nb = 3, g = 3
+  # the 4 x 8-byte stores of a lane and the 32 lanes' 8-element runs tile each plane row exactly
+  writes = np.zeros(Pn * Pn, np.int64)
+  for g in range(4):
+    for h in (0, 1):
+      idx = (R * Pn + 32 * cb + 4 * h + 8 * g)[:, 0]
+      for e in range(4):
+        np.add.at(writes, idx + e, 1)
+  return dict(items=items, z_max=z_max, m_max=m_max, plane_min=int(lo.min()), plane_max=int(hi.max()),
+              plane_elems=KC * plane, row_writes=writes, aligned8=bool(((pbase * 2) % 8 == 0).all()))
+
+
+def _gemm_accesses(N):
+  """linear64_kernel, batched: loads clamp rows to M-1 / N-1 and read k0 + swizzled piece < K
+  from rows of stride x_rs = K = Pn; stores y[b * y_bs + m * y_rs + n] for m < M, n < N."""
+  Pn = _pn(N)
+  M = Ng = N
+  K = Pn
+  x_rs, x_bs, y_rs, y_bs = Pn, Pn * Pn, N, _pp(N)
+  out = {}
+  for bm, bn in ((128, 128), (64, 128), (64, 64)):
+    gm, gn = (M + bm - 1) // bm, (Ng + bn - 1) // bn
+    # load rows: min(m0 + c * 8 + lane / 8, M - 1); columns k0 + rsw + 0..7 with k0 + 64 <= K
+    max_row = M - 1
+    max_col = K - 1                          # k0 <= K - 64, rsw + 7 <= 63
+    x_max = (KC - 1) * x_bs + max_row * x_rs + max_col
+    w_max = (KC - 1) * x_bs + (Ng - 1) * K + max_col
+    y_max = (KC - 1) * y_bs + (M - 1) * y_rs + (Ng - 1)
+    out[(bm, bn)] = (gm, gn, x_max, w_max, y_max)
+  return out, KC * Pn * Pn, KC * y_bs
+
+
+def _out_accesses(N):
+  P, Pp = N * N, _pp(N)
+  items = (P + 31) // 32
+  ipw, groups = _grid(items)
+  assert _covered(items, ipw, groups)
+  item = np.arange(items)[:, None]
+  lane = np.arange(64)[None, :]
+  half, li = lane >> 5, lane & 31
+  p = item * 32 + li
+  ok = p < P
+  t_max = int((p + 8 * half * Pp + (16 * 7 + 2 * 3 + 1) * Pp)[ok].max())
+  z_max = int((p * KC + 8 * half + 16 * 7 + 7)[ok].max())
+  q = lane + 64 * np.arange(8)[:, None, None]             # the row-store loop: u = 0..7
+  pos, c8 = q >> 4, (q & 15) * 8
+  pp = item[None] * 32 + pos
+  okw = pp < P
+  out_max = int((pp * KC + c8 + 7)[okw].max())
+  return dict(t_max=t_max, t_elems=KC * Pp, z_max=z_max, out_max=out_max, elems=P * KC)
+
+
+@pytest.mark.parametrize("incoming", [False, True])
+@pytest.mark.parametrize("N", [1, 37, 64, 384, 768])
+def test_trimul_kernel_accesses_stay_in_bounds(N, incoming):
+  pr = _proj_accesses(N, incoming)
+  assert pr["z_max"] < N * N * KC and pr["m_max"] < N
+  assert 0 <= pr["plane_min"] and pr["plane_max"] < pr["plane_elems"]
+  assert pr["aligned8"]
+  assert (pr["row_writes"] == 1).all(), "every padded plane element written exactly once (zeros included)"
+  gemm, ab_elems, t_elems = _gemm_accesses(N)
+  for (bm, bn), (gm, gn, x_max, w_max, y_max) in gemm.items():
+    assert x_max < ab_elems and w_max < ab_elems and y_max < t_elems, (bm, bn)
+    assert gm * gn * KC > 0 and gm < 2 ** 31 and KC <= 65535
+  o = _out_accesses(N)
+  assert o["t_max"] < o["t_elems"] and o["z_max"] < o["elems"] and o["out_max"] < o["elems"]
+
+
+@pytest.mark.parametrize("N", [1, 37, 64, 384, 768])
+def test_trimul_workspace_covers_the_modelled_buffers(N):
+  lib = _lib.load()
+  Pn, Pp = _pn(N), _pp(N)
+  need = 2 * KC * Pn * Pn * 2 + KC * Pp * 2 + (4 * KC * KC + 2 * KC * KC) * 2 + 6 * KC * 4
+  assert lib.sf_hip_triangle_mult_workspace_bytes(N, KC) >= need
