@@ -259,7 +259,40 @@ def _config_builders() -> dict:
         "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
         "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
 
+  def dense(n):  # triangle attention, starting node, all-ones mask (the block-sparse lines' baseline)
+    def build():
+      mod, z, seq = W.make_triangle(n, seed=9)
+      mod = mod.to(dev); backends.prepare(mod)
+      z, seq = z.to(dev), seq.to(dev)
+      f = module_flop(n)
+      return (lambda: mod(z, seq)), (lambda t: {"ms_per_call": round(t, 4), "tflops": round(f / t / 1e9, 1),
+                                                "frac_bf16_peak": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                                "bound": "mfma"})
+    return build
+
+  def ibs(n):  # block-sparse (IBS) triangle attention, starting node, default parameters
+    # (num_samples 16, num_rand_blocks 5, t_prob 0.9, tr_prob 0.95, u_prob 0.02): maps sampled on
+    # every call; `ms_per_call_reuse` reuses them (a later layer under an index-reuse policy)
+    from sparsefold_amd.backends.hip import ops as HO
+    def build():
+      mod, z, seq = W.make_triangle(n, seed=9)
+      mod = mod.to(dev); backends.prepare(mod)
+      z, seq = z.to(dev), seq.to(dev)
+      ws = torch.empty(HO.triangle_ibs_workspace_bytes(n, 128, 4, 32), dtype=torch.uint8, device=dev)
+      out = torch.empty_like(z)
+      kw = dict(num_head=4, transpose=False, num_samples=16, num_rand_blocks=5, t_prob=0.9, tr_prob=0.95,
+                u_prob=0.02, workspace=ws, out=out)
+      args = (z, seq, mod._hip_ln_w, mod._hip_ln_b, mod._hip_w_qkvgb, mod._hip_w_o)
+      _, im, wm = HO.triangle_attention_ibs(*args, seed=1, **kw)
+      frac = float((im >= 0).sum()) / (im.numel() / 16 * ((n + 31) // 32))
+      reuse_ms = _time_call(lambda: HO.triangle_attention_ibs(*args, index_map=im, weight_map=wm, **kw), 20)
+      return (lambda: HO.triangle_attention_ibs(*args, seed=1, **kw)), (lambda t: {
+          "ms_per_call": round(t, 4), "ms_per_call_reuse": round(reuse_ms, 4),
+          "key_blocks_attended": round(frac, 3), "bound": "mfma"})
+    return build
+
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
+          "triangle_ibs_n768": ibs(768), "triangle_n1536_start": dense(1536), "triangle_ibs_n1536": ibs(1536),
           "single_n768": c3b, "diffusion_5x1024_block": c4,
           "diffusion_5x1024_24_blocks": c4_stack, "diffusion_transition_5x1024": c4_transition,
           "single_transition_n768": trunk_transition(768, 384, ()),
@@ -279,7 +312,7 @@ def other_configs(iters: int) -> dict:
   for name, build in _config_builders().items():
     call, metrics = build()
     res[name] = metrics(_time_call(call, iters if "24_blocks" not in name else max(iters // 8, 5)))
-    if "pack" not in name and "24_blocks" not in name:
+    if "pack" not in name and "24_blocks" not in name and "ibs" not in name:
       config.configure_runtime(backend="hip", sdpa_implementation="hip", device="cuda", hip_graphs=True)
       try:
         res[name]["ms_per_call_hip_graphs"] = round(_time_call(call, iters), 4)

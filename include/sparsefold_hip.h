@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 9
+#define SF_HIP_ABI_VERSION 10
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -187,6 +187,30 @@ int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t 
 #define SF_TRI_STAGE_ALL 7
 int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* workspace,
                               size_t workspace_bytes, void* stream);
+
+/* Block-sparse (IBS) form of the same module (head dim 32: C = 128, H = 4, D = 32), the
+ * reference's native grid self-attention (vecops op grid_self_attention with index and weight
+ * maps, backends/vecops/kernels/registry.py:2946-3040; GridSelfAttention.cpp:134-142,290-306;
+ * parameters config.py:65-73): per (row r, head h, query tile t of 32 queries) num_samples slots
+ * of (key block of 32 keys, weight) in index_map / weight_map, int32 / f32 [N, H, T, S],
+ * T = ceil(N/32), index -1 = unused slot.  generate_maps = 1 samples them (this library's
+ * importance sampler: static heaviest blocks to t_prob, num_rand_blocks draws up to tr_prob with
+ * a u_prob floor, weight count / (R q); draws hashed from seed and (r, h, t)); 0 reuses the given
+ * maps.  At most num_samples valid blocks per tile: all selected, weight 1, i.e. dense attention.
+ * Masked rows follow the dense rule.  N <= 8192, num_samples <= 64.  Workspace from
+ * sf_hip_triangle_ibs_workspace_bytes (0 = unsupported sizes). */
+typedef struct sf_ibs_args {
+  int32_t num_samples, num_rand_blocks;
+  float t_prob, tr_prob, u_prob;
+  int32_t generate_maps;
+  uint64_t seed;
+  int32_t* index_map;                           /* [N, H, T, S] */
+  float* weight_map;                            /* [N, H, T, S] */
+} sf_ibs_args;
+
+size_t sf_hip_triangle_ibs_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t D);
+int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_ibs_args* p, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Pair logits: plane hp, position p holds (LN(z[p,:]) W)[hp]; z bf16 [P, C] contiguous

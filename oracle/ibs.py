@@ -16,13 +16,15 @@ what follows is this package's own sampler on the reference's interface:
   the reference's map shape ``[B, N, H, ceil(N/32), num_samples]`` (``registry.py:2982-2992``);
 * block mass: the tile's mean query against every valid key plus the tile's mean bias,
   ``m_b = sum_{j in b} 2^(qbar . k_j + bbar_j)`` (logits in log2 units), ``p_b = m_b / sum m``;
+  a block is valid when it holds at least one valid key (whatever its mass);
 * every valid block selected, weight 1, when there are at most ``num_samples`` of them: the
   attention is then exactly the dense one;
 * otherwise static blocks -- the heaviest in descending mass (ties: lower index first) until their
   mass reaches ``t_prob``, at most ``num_samples - num_rand_blocks`` -- with weight 1, then
   ``num_rand_blocks`` draws with replacement from the candidates (the next blocks in that order
   until the mass reaches ``tr_prob``) with proposal ``q_b`` proportional to
-  ``max(p_b / M_cand, u_prob)``; a block drawn ``c`` times gets weight ``c / (R q_b)`` (the
+  ``max(p_b / M_cand, u_prob)`` (uniform when ``M_cand`` is 0); a block drawn ``c`` times gets
+  weight ``c / (R q_b)`` (the
   importance-sampling estimate of the candidates' sum, ``sum_draws w q = 1``); blocks past
   ``tr_prob`` are dropped;
 * draws come from a counter-based hash of (seed, batch, row, head, tile, draw), so the maps are a
@@ -76,7 +78,8 @@ def block_masses(q: torch.Tensor, k: torch.Tensor, bias: torch.Tensor, key_valid
   """Per query tile and key block: the tile-mean query against each valid key plus the tile-mean
   bias (log2-domain logits, q already scaled), summed over the block as 2^x.  q, k ``[N, D]``
   (log2 units: q carries scale * log2 e), bias ``[N, N]`` (log2 units), key_valid ``[N]`` bool.
-  Returns ``[T, KB]`` float64 block masses relative to each tile's largest block (max 1)."""
+  Returns ``[T, KB]`` float64 block masses relative to each tile's largest block (max 1); -1 marks
+  a block without a valid key."""
   N = q.shape[0]
   T = (N + BLOCK - 1) // BLOCK
   out = torch.zeros(T, T, dtype=torch.float64)
@@ -94,6 +97,9 @@ def block_masses(q: torch.Tensor, k: torch.Tensor, bias: torch.Tensor, key_valid
     mx = out[t].max()
     if mx > 0:
       out[t] /= mx
+  for b in range(T):
+    if not bool(key_valid[BLOCK * b:BLOCK * b + BLOCK].any()):
+      out[:, b] = -1.0
   return out
 
 
@@ -105,7 +111,7 @@ def select_blocks(masses: torch.Tensor, params: IBSParams, seed: int, batch: int
   weight = np.zeros((T, S), np.float32)
   for t in range(T):
     m = masses[t].tolist()
-    valid = [b for b in range(KB) if m[b] > 0]
+    valid = [b for b in range(KB) if m[b] >= 0]
     if not valid:
       continue
     if len(valid) <= S:
@@ -132,7 +138,7 @@ def select_blocks(masses: torch.Tensor, params: IBSParams, seed: int, batch: int
     if not cand or R == 0:
       continue
     mc = sum(p[b] for b in cand)
-    raw = [max(p[b] / mc, params.u_prob) for b in cand]
+    raw = [max(p[b] / mc, params.u_prob) if mc > 0 else 1.0 for b in cand]
     zr = sum(raw)
     q = [r / zr for r in raw]
     counts = [0] * len(cand)

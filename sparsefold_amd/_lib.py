@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -73,6 +73,15 @@ class TriangleArgs(C.Structure):
       ("w_qkvgb", _vp), ("w_o", _vp),
       ("out", _vp),
       ("fixup_sum_limit", _f32),
+  ]
+
+
+class IbsArgs(C.Structure):
+  _fields_ = [
+      ("num_samples", _i32), ("num_rand_blocks", _i32),
+      ("t_prob", _f32), ("tr_prob", _f32), ("u_prob", _f32),
+      ("generate_maps", _i32), ("seed", C.c_uint64),
+      ("index_map", _vp), ("weight_map", _vp),
   ]
 
 
@@ -148,6 +157,7 @@ STRUCTS = {
     "sf_layer_norm_args": LayerNormArgs,
     "sf_linear_args": LinearArgs,
     "sf_triangle_args": TriangleArgs,
+    "sf_ibs_args": IbsArgs,
     "sf_pair_logits_args": PairLogitsArgs,
     "sf_window_gather_args": WindowGatherArgs,
     "sf_self_attention_args": SelfAttentionArgs,
@@ -167,6 +177,8 @@ SIGNATURES = [
     ("sf_hip_triangle_workspace_bytes", C.c_size_t, [_i32, _i32, _i32, _i32]),
     ("sf_hip_triangle_attn_fwd", C.c_int, [C.POINTER(TriangleArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_triangle_stage_fwd", C.c_int, [C.POINTER(TriangleArgs), _i32, _vp, C.c_size_t, _vp]),
+    ("sf_hip_triangle_ibs_workspace_bytes", C.c_size_t, [_i32, _i32, _i32, _i32]),
+    ("sf_hip_triangle_attn_ibs_fwd", C.c_int, [C.POINTER(TriangleArgs), C.POINTER(IbsArgs), _vp, C.c_size_t, _vp]),
     ("sf_hip_pair_logits_fwd", C.c_int, [C.POINTER(PairLogitsArgs), _vp]),
     ("sf_hip_window_gather_fwd", C.c_int, [C.POINTER(WindowGatherArgs), _vp]),
     ("sf_hip_self_attention_workspace_bytes", C.c_size_t, [C.POINTER(SelfAttentionArgs)]),

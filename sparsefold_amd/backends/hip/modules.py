@@ -35,6 +35,7 @@ import functools
 import torch
 
 from sparsefold_amd import modules as base
+from sparsefold_amd.runtime import config as runtime_config
 from sparsefold_amd.backends.hip import graphs, ops
 from sparsefold_amd.backends.hip.attention import dot_product_attention
 
@@ -75,6 +76,23 @@ def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
 # ---------------------------------------------------------------------------------------
 
 class GridSelfAttentionHipMixin:
+  """GridSelfAttention.forward (blocks.py:293-366) as one library call per pair block.  With the
+  runtime's ``hip_sparse_grid_attention`` on, the attention rows are block-sparse (IBS) with the
+  native backend's parameters and map reuse (backends/vecops/modules.py:1399-1640):
+  ``ibsa_params`` (parameters or a provider of them per layer-stack indices) and
+  ``index_reuse_policy``; otherwise they are dense, as in the reference's torch path."""
+
+  def __init__(self, *args, index_reuse_policy=base.default_reuse_policy,
+               ibsa_params=base.IBSAParameters.default, **kwargs):
+    super().__init__(*args, **kwargs)
+    if isinstance(ibsa_params, base.IBSAParameters):
+      self.ibsa_params_provider = lambda _indices: ibsa_params
+    else:
+      self.ibsa_params_provider = ibsa_params
+    self.index_reuse_policy = index_reuse_policy
+    self._hip_reusers: dict = {}          # (act shape, mask shape) -> IndexReuser
+    self.last_maps = None                 # (index_map, weight_map) of the last block-sparse call
+
   def prepare_native(self) -> bool:
     _begin_preparation(self)
     H, C, D = self.config.num_head, self.num_channels, self.qkv_dim
@@ -92,19 +110,52 @@ class GridSelfAttentionHipMixin:
     return True
 
   @_require_native_preparation
-  @graphs.graphed
   def forward(self, act: torch.Tensor, seq_mask: torch.Tensor, *, add_residual: bool = True) -> torch.Tensor:
     assert act.ndim >= 3
     N = act.shape[-2]
     assert act.shape[-1] == self.num_channels
     assert seq_mask.shape == (N,) and seq_mask.dtype == torch.bool
     assert act.shape[-3] == N, "triangle attention needs the full [N, N] pair block on one GPU"
+    if runtime_config.hip_sparse_grid_attention:    # per-call seeds and map reuse: never graphed
+      flat = act.reshape(-1, N, N, act.shape[-1])
+      outs = self._forward_sparse(act, flat, seq_mask, add_residual)
+      out = outs[0].unsqueeze(0) if len(outs) == 1 else torch.stack(outs)
+      return out.reshape(act.shape).to(act.dtype)
+    return self._forward_dense(act, seq_mask, add_residual=add_residual)
+
+  @graphs.graphed
+  def _forward_dense(self, act: torch.Tensor, seq_mask: torch.Tensor, *, add_residual: bool) -> torch.Tensor:
+    N = act.shape[-2]
     flat = act.reshape(-1, N, N, act.shape[-1])
     outs = [ops.triangle_attention(z, seq_mask, self._hip_ln_w, self._hip_ln_b, self._hip_w_qkvgb, self._hip_w_o,
                                    num_head=self.config.num_head, transpose=self.transpose,
                                    add_residual=add_residual) for z in flat]
     out = outs[0].unsqueeze(0) if len(outs) == 1 else torch.stack(outs)
     return out.reshape(act.shape).to(act.dtype)
+
+  def _forward_sparse(self, act, flat, seq_mask, add_residual):
+    """Block-sparse rows; maps ``[B, N, H, T, S]`` sampled or taken from the layer the reuse
+    policy names (modules.py:1589-1626 of the vecops backend)."""
+    indices = tuple(base.layer_stack_indices)
+    p = self.ibsa_params_provider(indices)
+    key = (tuple(act.shape), tuple(seq_mask.shape))
+    reuser = self._hip_reusers.setdefault(key, base.IndexReuser(self.index_reuse_policy))
+    maps, _ = reuser.get(indices)
+    outs, index_maps, weight_maps = [], [], []
+    for b, z in enumerate(flat):
+      im, wm = (None, None) if maps is None else (maps[0][b], maps[1][b])
+      o, im, wm = ops.triangle_attention_ibs(
+          z, seq_mask, self._hip_ln_w, self._hip_ln_b, self._hip_w_qkvgb, self._hip_w_o,
+          num_head=self.config.num_head, transpose=self.transpose, num_samples=p.num_samples,
+          num_rand_blocks=p.num_rand_blocks, t_prob=p.t_prob, tr_prob=p.tr_prob, u_prob=p.u_prob,
+          index_map=im, weight_map=wm, add_residual=add_residual)
+      outs.append(o)
+      index_maps.append(im)
+      weight_maps.append(wm)
+    self.last_maps = (torch.stack(index_maps), torch.stack(weight_maps))
+    if maps is None:
+      reuser.set(indices, self.last_maps)
+    return outs
 
 
 # ---------------------------------------------------------------------------------------

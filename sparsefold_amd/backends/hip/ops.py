@@ -8,6 +8,7 @@ Nothing here computes on the host: every numeric result comes from libsparsefold
 from __future__ import annotations
 
 import ctypes as C
+import itertools
 import math
 
 import torch
@@ -285,6 +286,74 @@ def triangle_attention(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qk
     rc = _lib.load().sf_hip_triangle_stage_fwd(C.byref(a), stages, _vp(workspace), workspace.numel(), _stream(z))
   _lib.check(rc, "sf_hip_triangle_attn_fwd")
   return out
+
+
+# per-call seeds of the block sampler when the caller gives none (the reference draws them from a
+# process-wide counter, backends/vecops/kernels/registry.py:3033)
+_ibs_seed_counter = itertools.count()
+
+
+def triangle_ibs_workspace_bytes(N: int, C_: int, H: int, D: int) -> int:
+  return int(_lib.load().sf_hip_triangle_ibs_workspace_bytes(N, C_, H, D))
+
+
+def triangle_attention_ibs(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, w_qkvgb: torch.Tensor,
+                           w_o: torch.Tensor, *, num_head: int, transpose: bool, num_samples: int,
+                           num_rand_blocks: int, t_prob: float, tr_prob: float, u_prob: float,
+                           index_map: torch.Tensor | None = None, weight_map: torch.Tensor | None = None,
+                           seed: int | None = None, add_residual: bool = True,
+                           workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+  """GridSelfAttention on ``z [N, N, C]`` with block-sparse (IBS) attention rows; returns
+  ``(out, index_map, weight_map)``, maps int32 / float32 ``[N, H, ceil(N/32), num_samples]``.
+  Given maps (both or neither, as backends/vecops/kernels/registry.py:2985-3002 requires) are
+  reused; otherwise they are sampled with ``seed`` (default: the next value of a process-wide
+  counter)."""
+  _require_cuda(z, seq_mask, ln_w, ln_b, w_qkvgb, w_o, workspace, index_map, weight_map)
+  _require(z.ndim == 3 and z.shape[0] == z.shape[1], f"triangle_ibs: z must be [N, N, C], got {tuple(z.shape)}")
+  _require((index_map is None) == (weight_map is None), "index_map and weight_map must be both present or both omitted")
+  N, _, Cn = z.shape
+  HD = w_o.shape[1]
+  _require(HD % num_head == 0, "triangle_ibs: output projection width not divisible by heads")
+  D = HD // num_head
+  _require(tuple(w_qkvgb.shape) == (4 * HD + num_head, Cn), f"triangle_ibs: w_qkvgb shape {tuple(w_qkvgb.shape)}")
+  _require(tuple(w_o.shape) == (Cn, HD), f"triangle_ibs: w_o shape {tuple(w_o.shape)}")
+  _require(seq_mask.shape == (N,), "triangle_ibs: seq_mask must be [N]")
+  need = triangle_ibs_workspace_bytes(N, Cn, num_head, D)
+  _require(need > 0, f"triangle_ibs: unsupported sizes N={N} C={Cn} H={num_head} D={D} "
+           "(block-sparse rows need C = 128, H = 4, D = 32, N <= 8192)")
+  T = (N + 31) // 32
+  shape = (N, num_head, T, int(num_samples))
+  generate = index_map is None
+  if generate:
+    index_map = torch.empty(shape, dtype=torch.int32, device=z.device)
+    weight_map = torch.empty(shape, dtype=torch.float32, device=z.device)
+  else:
+    _require(tuple(index_map.shape) == shape and tuple(weight_map.shape) == shape,
+             f"triangle_ibs: maps must be {shape}, got {tuple(index_map.shape)} / {tuple(weight_map.shape)}")
+    _require(index_map.dtype == torch.int32 and weight_map.dtype == torch.float32,
+             "triangle_ibs: index_map int32 and weight_map float32")
+    index_map, weight_map = index_map.contiguous(), weight_map.contiguous()
+  zc = _bf16(z).contiguous()
+  m8 = _u8(seq_mask).contiguous()
+  lw, lb = _f32(ln_w), _f32(ln_b)
+  if workspace is None or workspace.numel() < need:
+    workspace = torch.empty(need, dtype=torch.uint8, device=z.device)
+  if out is None:
+    out = torch.empty_like(zc)
+  a = _lib.TriangleArgs()
+  a.N, a.C, a.H, a.D = N, Cn, num_head, D
+  a.transpose, a.add_residual = int(bool(transpose)), int(bool(add_residual))
+  a.z, a.seq_mask, a.ln_w, a.ln_b = _vp(zc), _vp(m8), _vp(lw), _vp(lb)
+  a.w_qkvgb, a.w_o, a.out = _vp(w_qkvgb), _vp(w_o), _vp(out)
+  p = _lib.IbsArgs()
+  p.num_samples, p.num_rand_blocks = int(num_samples), int(num_rand_blocks)
+  p.t_prob, p.tr_prob, p.u_prob = float(t_prob), float(tr_prob), float(u_prob)
+  p.generate_maps = int(generate)
+  p.seed = (next(_ibs_seed_counter) if seed is None else int(seed)) & ((1 << 64) - 1)
+  p.index_map, p.weight_map = _vp(index_map), _vp(weight_map)
+  rc = _lib.load().sf_hip_triangle_attn_ibs_fwd(C.byref(a), C.byref(p), _vp(workspace), workspace.numel(), _stream(z))
+  _lib.check(rc, "sf_hip_triangle_attn_ibs_fwd")
+  return out, index_map, weight_map
 
 
 def default_scale(d: int) -> float:

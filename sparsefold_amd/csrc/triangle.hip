@@ -897,6 +897,293 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// IBS block-sparse attention (head dim 32 layouts; the projection, fix-up and output stages are
+// the dense path's).  Blocks of 32 queries x 32 keys; per (row, head, query tile) S slots of
+// (key block, weight).  The sampler:
+//   mass of key block b = sum over its valid keys of 2^(qbar . k_j + bbar_j)   (log2 units)
+//   qbar, bbar: the tile's mean query and mean bias over its queries (i < N)
+//   valid block: one with at least one valid key (whatever its mass)
+//   at most S valid blocks: all of them, weight 1 (the dense attention, exactly)
+//   else static blocks -- descending mass (ties: lower index), until the mass reaches t_prob, at
+//   most S - R -- weight 1; then R draws with replacement from the next blocks up to mass tr_prob,
+//   proposal q ~ max(p / M_cand, u_prob) (uniform if M_cand = 0); a block drawn c times gets
+//   weight c / (R q)
+//   draws: SplitMix64 hash of (seed, batch, row, head, tile, draw), 24 bits -> [0, 1)
+// The attention: o_i = sum_s w_s sum_{j in b_s} 2^(s_ij) v_j / sum_s w_s sum_{j in b_s} 2^(s_ij),
+// with an exact running maximum.
+// ---------------------------------------------------------------------------------------
+constexpr int kIbsMaxBlocks = 256;    // key blocks: N <= 8192 (the sampler's LDS: 256 T bytes)
+constexpr int kIbsMaxSamples = 64;
+
+struct IbsArgs {
+  int N, NP, H, T, S, R, transpose;
+  float t_prob, tr_prob, u_prob;
+  unsigned long long seed;
+  const uint16_t *q, *k, *vt, *bias;
+  const uint8_t* seq;
+  float* bmean;                       // [H][T][NP] tile-mean bias (log2 units), keys as the planes store them
+  int32_t* index; float* weight;      // [N][H][T][S]
+  uint16_t* o;                        // [H][N][N][32], as the dense attention stage writes it
+};
+
+__device__ __forceinline__ unsigned long long ibs_mix64(unsigned long long x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ float ibs_uniform(unsigned long long seed, int row, int head, int tile, int draw) {
+  unsigned long long x = ibs_mix64(seed);
+  x = ibs_mix64(x ^ 0ull);                                   // batch 0
+  x = ibs_mix64(x ^ (unsigned long long)(unsigned)row);
+  x = ibs_mix64(x ^ (unsigned long long)(unsigned)head);
+  x = ibs_mix64(x ^ (unsigned long long)(unsigned)tile);
+  x = ibs_mix64(x ^ (unsigned long long)(unsigned)draw);
+  return (float)(x >> 40) * (1.0f / 16777216.0f);
+}
+
+// Tile-mean bias: one thread per (head, tile, stored key position); the means keep the bias
+// planes' key order, so a lane reads its 16 S^T keys of a block as 64 contiguous bytes.
+__global__ __launch_bounds__(256) void tri_ibs_bias_mean_kernel(const IbsArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.H * a.T * a.NP) return;
+  const int jp = (int)(idx % a.NP), t = (int)((idx / a.NP) % a.T), h = (int)(idx / ((int64_t)a.NP * a.T));
+  const int i0 = 32 * t, i1 = min(a.N, i0 + 32);
+  float sum = 0.f;
+  for (int i = i0; i < i1; ++i) sum += bf2f(a.bias[((int64_t)h * a.NP + i) * a.NP + jp]);
+  a.bmean[idx] = sum / (float)(i1 - i0);
+}
+
+// The sampler: one wave per (row r, head h, group of 32 query tiles); lane (half, li) holds tile
+// 32 g + li.  Block logits S^T = K . qbar^T on the MFMA with the tile-mean query split into two
+// bf16 terms (hi + lo: about 16 significant bits), seeded with the tile-mean bias; per block the
+// log2 mass max + log2(sum 2^(x - max)) over its valid keys.  Each lane keeps its tile's column
+// of the LDS arrays (log2 masses [KB][32], then order | count << 16 [KB][32]) and selects alone.
+__global__ __launch_bounds__(64) void tri_ibs_index_kernel(const IbsArgs a) {
+  extern __shared__ float ibs_lds[];
+  const int lane = threadIdx.x, half = lane >> 5, li = lane & 31;
+  const int N = a.N, NP = a.NP, H = a.H, T = a.T, KB = a.T, S = a.S;
+  const int G = (T + 31) >> 5;
+  const int task = blockIdx.x;                               // the grid is N * H * G
+  const int g = task % G, h = (task / G) % H, r = task / (G * H);
+  const int t = 32 * g + li, tc = min(t, T - 1);            // tc: operand tile of idle lanes
+  const bool owner = half == 0 && t < T;                     // writes tile t's maps
+  int32_t* iout = a.index + (((int64_t)r * H + h) * T + tc) * S;
+  float* wout = a.weight + (((int64_t)r * H + h) * T + tc) * S;
+  int filled = 0;
+  if (a.seq[r] != 0) {                                       // masked rows keep empty maps
+    // tile-mean query, pieces (kk, half) of tiles' queries 32 tc .. 32 tc + 31
+    float qs[2][8];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qs[kk][e] = 0.f;
+    const uint16_t* qp = a.q + ql_off(r, h, H, NP, 32 * tc, 0, half);
+    for (int q0 = 0; q0 < 32; q0 += 8) {
+      u32x4 v[8][2];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) v[u][kk] = ld16(qp + (q0 + u) * 8 + kk * 512);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { qs[kk][2 * e] += bflo(v[u][kk][e]); qs[kk][2 * e + 1] += bfhi(v[u][kk][e]); }
+    }
+    const float qinv = 1.0f / (float)(min(N, 32 * tc + 32) - 32 * tc);   // queries past N hold 0
+    bf16x8 qh[2], ql[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = qs[kk][e] * qinv;
+        const __bf16 hv = (__bf16)v;
+        qh[kk][e] = hv;
+        ql[kk][e] = (__bf16)(v - (float)hv);
+      }
+    float* lm = ibs_lds;
+    const float* bm = a.bmean + ((int64_t)h * T + tc) * NP;
+    for (int b = 0; b < KB; ++b) {
+      const int j = 32 * b + li;
+      const uint32_t vm = (uint32_t)__ballot(j < N && a.seq[j] != 0);   // bit k: key 32 b + k valid
+      const bf16x8 k0 = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, j, 0, half)));
+      const bf16x8 k1 = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, j, 1, half)));
+      const float* bp = bm + 64 * (b >> 1) + 32 * (b & 1) + 16 * half;
+      f32x16 sc;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(bp + 4 * u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[4 * u + e] = v[e];
+      }
+      sc = mfma32(k0, qh[0], sc);
+      sc = mfma32(k1, qh[1], sc);
+      sc = mfma32(k0, ql[0], sc);
+      sc = mfma32(k1, ql[1], sc);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if ((vm >> (8 * (e >> 2) + 4 * half + (e & 3))) & 1u) mx = fmaxf(mx, sc[e]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float sum = 0.f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if ((vm >> (8 * (e >> 2) + 4 * half + (e & 3))) & 1u) sum += exp2f(sc[e] - mx);
+      }
+      sum += __shfl_xor(sum, 32);
+      const float l2 = mx + log2f(sum);
+      if (half == 0) lm[b * 32 + li] = (mx == -INFINITY || l2 != l2) ? -INFINITY : l2;   // NaN: no block
+    }
+    if (owner) {
+      float M = -INFINITY;
+      int nvalid = 0;
+      for (int b = 0; b < KB; ++b) {
+        const float v = lm[b * 32 + li];
+        M = fmaxf(M, v);
+        nvalid += v != -INFINITY;
+      }
+      if (nvalid <= S) {                                     // every valid block, weight 1
+        for (int b = 0; b < KB; ++b)
+          if (lm[b * 32 + li] != -INFINITY) { iout[filled] = b; wout[filled] = 1.f; ++filled; }
+      } else {
+        int* ord = reinterpret_cast<int*>(ibs_lds + KB * 32);
+        // descending mass, ties: lower index first; blocks without valid keys are not ranked
+        for (int b = 0; b < KB; ++b) {
+          const float v = lm[b * 32 + li];
+          if (v == -INFINITY) continue;
+          int rank = 0;
+          for (int c = 0; c < KB; ++c) {
+            const float u = lm[c * 32 + li];
+            rank += (u > v) || (u == v && c < b);
+          }
+          ord[rank * 32 + li] = b;
+        }
+        auto mass = [&](int k) { return exp2f(lm[(ord[k * 32 + li] & 0xFFFF) * 32 + li] - M); };
+        float total = 0.f;
+        for (int k = 0; k < nvalid; ++k) total += mass(k);
+        const float inv = 1.0f / total;
+        int ns = 0;
+        float cum = 0.f;
+        while (ns < nvalid && cum < a.t_prob && ns < S - a.R) { cum += mass(ns) * inv; ++ns; }
+        int nc = 0;
+        while (ns + nc < nvalid && cum < a.tr_prob) { cum += mass(ns + nc) * inv; ++nc; }
+        for (int k = 0; k < ns; ++k) { iout[k] = ord[k * 32 + li]; wout[k] = 1.f; }
+        filled = ns;
+        if (nc > 0 && a.R > 0) {
+          float mc = 0.f;
+          for (int c = 0; c < nc; ++c) mc += mass(ns + c) * inv;
+          auto raw = [&](int c) { return mc > 0.f ? fmaxf(mass(ns + c) * inv / mc, a.u_prob) : 1.0f; };
+          float zr = 0.f;
+          for (int c = 0; c < nc; ++c) zr += raw(c);
+          for (int d = 0; d < a.R; ++d) {
+            const float uu = ibs_uniform(a.seed, r, h, t, d);
+            float acc = 0.f;
+            int pick = nc - 1;
+            for (int c = 0; c < nc; ++c) {
+              acc += raw(c) / zr;
+              if (uu < acc) { pick = c; break; }
+            }
+            ord[(ns + pick) * 32 + li] += 1 << 16;
+          }
+          for (int c = 0; c < nc; ++c) {
+            const int cnt = ord[(ns + c) * 32 + li] >> 16;
+            if (cnt == 0) continue;
+            iout[filled] = ord[(ns + c) * 32 + li] & 0xFFFF;
+            wout[filled] = (float)cnt / ((float)a.R * (raw(c) / zr));
+            ++filled;
+          }
+        }
+      }
+    }
+  }
+  if (owner)
+    for (int s = filled; s < S; ++s) { iout[s] = -1; wout[s] = 0.f; }
+}
+
+// Sparse attention: one wave per (row, head, query tile); per selected block the S^T MFMAs seeded
+// with the bias, an exact running maximum, weights w 2^(s - m) as bf16, P.V on the MFMA.  Output in
+// the dense stage's o layout, so the output stage is shared.  Masked rows are left to the fix-up
+// kernel.
+__global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
+  const int64_t task = (int64_t)blockIdx.x * 4 + wave;
+  if (task >= (int64_t)a.N * a.H * a.T) return;
+  const int t = (int)(task % a.T), h = (int)((task / a.T) % a.H), r = (int)(task / ((int64_t)a.T * a.H));
+  if (a.seq[r] == 0) return;
+  const int N = a.N, NP = a.NP, H = a.H;
+  const int i = 32 * t + li;                                 // this lane's query (< NP)
+  bf16x8 qb[2];
+  const uint16_t* qp = a.q + ql_off(r, h, H, NP, i, 0, half);
+  qb[0] = as_bf16x8(ld16(qp));
+  qb[1] = as_bf16x8(ld16(qp + 512));
+  f32x16 o;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o[e] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const int32_t* idx = a.index + task * a.S;
+  const float* wts = a.weight + task * a.S;
+  for (int s = 0; s < a.S; ++s) {
+    const int b = idx[s];                                    // same address in every lane: uniform
+    if (b < 0 || b >= a.T) continue;                         // unused slot (or out of range)
+    const float w = wts[s];
+    bf16x8 kr[2], vr[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) kr[kk] = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, 32 * b + li, kk, half)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) vr[j] = as_bf16x8(ld16(a.vt + vl_off(r, h, H, NP, 2 * b + j, half, li)));
+    // bias of query i for keys 8(e/4) + 4 half + e%4 of the block: stored contiguously at
+    // 32 (b & 1) + 16 half + e within its 64-key tile
+    const uint16_t* bp = a.bias + ((int64_t)h * NP + i) * NP + 64 * (b >> 1) + 32 * (b & 1) + 16 * half;
+    const u32x4 b0 = ld16(bp), b1 = ld16(bp + 8);
+    f32x16 sd;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sd[2 * e] = bflo(b0[e]); sd[2 * e + 1] = bfhi(b0[e]);
+      sd[8 + 2 * e] = bflo(b1[e]); sd[8 + 2 * e + 1] = bfhi(b1[e]);
+    }
+    const f32x16 sc = mfma32(kr[1], qb[1], mfma32(kr[0], qb[0], sd));
+    float bmx = sc[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) bmx = fmaxf(bmx, sc[e]);
+    bmx = fmaxf(bmx, __shfl_xor(bmx, 32));
+    const float mn = fmaxf(m, bmx);
+    const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mn);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[e] *= alpha;
+    l *= alpha;
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 pb;
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        const bf16x2 pw = cvt_bf2(w * fast_exp2(sc[8 * j + 2 * q2] - mn), w * fast_exp2(sc[8 * j + 2 * q2 + 1] - mn));
+        pb[2 * q2] = pw[0];
+        pb[2 * q2 + 1] = pw[1];
+        l += (float)pw[0] + (float)pw[1];
+      }
+      o = mfma32(vr[j], pb, o);
+    }
+  }
+  const float lt = l + __shfl_xor(l, 32);
+  if (i >= N) return;
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
+  uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * half;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    uint32_t w4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w4[e] = pack_bf2(o[8 * kk + 2 * e] * inv, o[8 * kk + 2 * e + 1] * inv);
+    st16(op + 8 * kk, u32x4{w4[0], w4[1], w4[2], w4[3]});
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Generic path (any head dim): LN -> linear -> strided attention -> linear
 // ---------------------------------------------------------------------------------------
 struct TriWs {
@@ -1082,4 +1369,71 @@ extern "C" int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stag
     return 1;
   }
   return triangle_run(a, workspace, workspace_bytes, stream, stages);
+}
+
+namespace {
+size_t ibs_bmean_offset(int32_t N, int32_t H) { return carve_fast(nullptr, N, H).bytes; }
+size_t ibs_ws_bytes(int32_t N, int32_t H) {
+  const int NP = round_np(N), T = (N + 31) / 32;
+  return ibs_bmean_offset(N, H) + round_up((size_t)H * T * NP * 4);
+}
+}  // namespace
+
+extern "C" size_t sf_hip_triangle_ibs_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t D) {
+  if (N <= 0 || !fast_path(C, H, D) || N > 32 * kIbsMaxBlocks) return 0;
+  return ibs_ws_bytes(N, H);
+}
+
+extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_ibs_args* p, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  if (a == nullptr || p == nullptr || p->index_map == nullptr || p->weight_map == nullptr) {
+    sf_set_error("triangle_ibs: null arguments or maps"); return 1;
+  }
+  if (!fast_path(a->C, a->H, a->D)) {
+    sf_set_error("triangle_ibs: block-sparse attention needs C = 128, D = 32, H = 4 (C=%d H=%d D=%d)", a->C, a->H, a->D);
+    return 1;
+  }
+  if (a->N <= 0 || a->N > 32 * kIbsMaxBlocks) {
+    sf_set_error("triangle_ibs: N=%d outside [1, %d]", a->N, 32 * kIbsMaxBlocks); return 1;
+  }
+  if (p->num_samples < 1 || p->num_samples > kIbsMaxSamples || p->num_rand_blocks < 0 ||
+      p->num_rand_blocks > p->num_samples || !(p->t_prob >= 0.f && p->t_prob <= 1.f) ||
+      !(p->tr_prob >= 0.f && p->tr_prob <= 1.f) || !(p->u_prob >= 0.f && p->u_prob <= 1.f)) {
+    sf_set_error("triangle_ibs: need 1 <= num_samples <= %d, 0 <= num_rand_blocks <= num_samples and "
+                 "probabilities in [0, 1]", kIbsMaxSamples);
+    return 1;
+  }
+  if (workspace == nullptr || workspace_bytes < ibs_ws_bytes(a->N, a->H)) {
+    sf_set_error("triangle_ibs: workspace of %zu bytes needed, %zu given", ibs_ws_bytes(a->N, a->H), workspace_bytes);
+    return 1;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  if ((rc = triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_PROJECT))) return rc;
+  const FastWs ws = carve_fast(workspace, a->N, a->H);
+  IbsArgs ia{};
+  ia.N = a->N; ia.NP = round_np(a->N); ia.H = a->H; ia.T = (a->N + 31) / 32;
+  ia.S = p->num_samples; ia.R = p->num_rand_blocks; ia.transpose = a->transpose;
+  ia.t_prob = p->t_prob; ia.tr_prob = p->tr_prob; ia.u_prob = p->u_prob; ia.seed = p->seed;
+  ia.q = ws.q; ia.k = ws.k; ia.vt = ws.vt; ia.bias = ws.bias; ia.seq = a->seq_mask;
+  ia.bmean = reinterpret_cast<float*>(static_cast<char*>(workspace) + ibs_bmean_offset(a->N, a->H));
+  ia.index = p->index_map; ia.weight = p->weight_map; ia.o = ws.o;
+  const int64_t tasks = (int64_t)ia.N * ia.H * ia.T;
+  if (p->generate_maps) {
+    const int64_t nb = (int64_t)ia.H * ia.T * ia.NP;
+    hipLaunchKernelGGL(tri_ibs_bias_mean_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, ia);
+    if ((rc = sf_check_launch("tri_ibs_bias_mean_kernel"))) return rc;
+    const int groups = (ia.T + 31) / 32;
+    const size_t lds = (size_t)2 * ia.T * 32 * 4;          // <= 64 KB (T <= 256)
+    hipLaunchKernelGGL(tri_ibs_index_kernel, dim3((unsigned)(ia.N * ia.H * groups)), dim3(64), lds, st, ia);
+    if ((rc = sf_check_launch("tri_ibs_index_kernel"))) return rc;
+  }
+  hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
+  if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
+  TriAttnArgs fa{};
+  fa.N = a->N; fa.NP = ia.NP; fa.H = a->H; fa.transpose = a->transpose; fa.sum_limit = 0x1p100f;
+  fa.q = ws.q; fa.k = ws.k; fa.vt = ws.vt; fa.bias = ws.bias; fa.seq = a->seq_mask; fa.o = ws.o; fa.flags = ws.flags;
+  hipLaunchKernelGGL(tri_fixup_kernel, dim3(a->N), dim3(256), 0, st, fa);   // masked rows: mean of V
+  if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
+  return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);
 }

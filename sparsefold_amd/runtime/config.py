@@ -16,6 +16,7 @@ reference's (``src/sparsefold/config.py:271-285``) plus ``"hip"`` for both the n
 """
 from __future__ import annotations
 
+import ast
 import dataclasses
 import os
 import warnings
@@ -43,6 +44,14 @@ def _names(text: str) -> list[str]:
   return [item.strip() for item in str(text).split(",") if item.strip()]
 
 
+def _literal_dict(text) -> dict:
+  """A Python dict literal (the reference parses this setting with ast.literal_eval)."""
+  value = ast.literal_eval(text) if isinstance(text, str) else dict(text)
+  if not isinstance(value, dict):
+    raise ValueError(f"sparse_attention_parameters must be a dict, got {value!r}")
+  return dict(value)
+
+
 @dataclasses.dataclass(frozen=True)
 class _Setting:
   """One runtime setting: its environment suffix, default text and parser."""
@@ -58,8 +67,13 @@ _SETTINGS: dict[str, _Setting] = {
     "native_ops": _Setting("NATIVE_OPS", "*", _names),
     "sdpa_implementation": _Setting("SDPA_IMPLEMENTATION", "math"),
     "diffusion_precision": _Setting("DIFFUSION_PRECISION", "fp32"),
+    "sparse_attention_parameters": _Setting("SPARSE_ATTENTION_PARAMETERS", "{}", _literal_dict),
+    "enable_gsa_index_reuse": _Setting("ENABLE_GSA_INDEX_REUSE", "1", _flag),
     # no counterpart in the reference: replay repeated HIP module calls as captured graphs
     "hip_graphs": _Setting("HIP_GRAPHS", "0", _flag),
+    # no counterpart in the reference (whose native grid attention is always block-sparse and
+    # whose torch path is always dense): the HIP grid attention's rows are block-sparse (IBS)
+    "hip_sparse_grid_attention": _Setting("HIP_SPARSE_GRID_ATTENTION", "0", _flag),
 }
 
 _resolved: dict[str, Any] | None = None
@@ -97,6 +111,7 @@ def configure_runtime(**settings: Any) -> None:
   resolved = {name: settings[name] if name in settings else _from_environment(name) for name in _SETTINGS}
   resolved["acclib_implementation"] = normalize_backend(resolved["acclib_implementation"])
   resolved["native_ops"] = list(resolved["native_ops"])
+  resolved["sparse_attention_parameters"] = _literal_dict(resolved["sparse_attention_parameters"])
   _check(resolved)
   _resolved = resolved
 
@@ -107,7 +122,9 @@ def _value(name: str) -> Any:
 
 def get_runtime_options() -> dict[str, Any]:
   """A copy of the current settings that ``configure_runtime(**options)`` accepts back."""
-  return {name: (list(v) if isinstance(v, list) else v) for name, v in ((n, _value(n)) for n in _SETTINGS)}
+  def copy(v):
+    return list(v) if isinstance(v, list) else dict(v) if isinstance(v, dict) else v
+  return {name: copy(_value(name)) for name in _SETTINGS}
 
 
 def uses_hip() -> bool:

@@ -217,3 +217,44 @@ def test_trimul_incoming_edge_is_read_from_either_equation_form():
   inc = HM.TriangleMultiplicationHipMixin.INCOMING_EQUATIONS
   assert "...kjc,...kic->...ijc" in inc and "...ckj,...cki->...cij" in inc
   assert "...ikc,...jkc->...ijc" not in inc and "...cik,...cjk->...cij" not in inc
+
+
+def test_sparse_attention_settings_and_parameters(monkeypatch, reset_runtime):
+  """IBSAParameters.default reads the runtime's sparse_attention_parameters over the field
+  defaults (blocks.py:405-418, runtime/config.py:27,68 of the reference)."""
+  assert config.sparse_attention_parameters == {} and config.enable_gsa_index_reuse is True
+  assert M.IBSAParameters.default() == M.IBSAParameters(16, 6, 0.90, 0.95, 0.02)
+  monkeypatch.setenv("SPARSEFOLD_SPARSE_ATTENTION_PARAMETERS", "{'num_samples': 8, 'num_rand_blocks': 5}")
+  config.reset()
+  assert M.IBSAParameters.default() == M.IBSAParameters(8, 5, 0.90, 0.95, 0.02)
+  config.configure_runtime(sparse_attention_parameters={"t_prob": 0.5}, hip_sparse_grid_attention=True)
+  assert M.IBSAParameters.default().t_prob == 0.5 and config.hip_sparse_grid_attention is True
+  opts = config.get_runtime_options()
+  opts["sparse_attention_parameters"]["t_prob"] = 0.1
+  assert config.sparse_attention_parameters["t_prob"] == 0.5
+  with pytest.raises(ValueError, match="dict"):
+    config.configure_runtime(sparse_attention_parameters="[1, 2]")
+
+
+def test_index_reuser_follows_policy_and_switch(reset_runtime):
+  reuser = M.IndexReuser(lambda idx: (0,) if idx == (2,) else None)
+  reuser.set(0, "maps of layer 0")
+  assert reuser.get((2,)) == ("maps of layer 0", (0,))
+  assert reuser.get([1]) == (None, None)
+  config.configure_runtime(enable_gsa_index_reuse=False)
+  assert reuser.get((2,)) == (None, None)
+  assert M.default_reuse_policy((3,)) is None
+
+
+def test_grid_attention_takes_the_native_backends_sparse_arguments(reset_runtime):
+  config.configure_runtime(backend="hip", device="cuda", native_ops=["grid_self_attn"])
+  backends.init()
+  p = M.IBSAParameters(num_samples=4)
+  m = M.GridSelfAttention(M.GridSelfAttention.Config(), M.GlobalConfig(), True, num_channels=128,
+                          ibsa_params=p, index_reuse_policy=M.default_reuse_policy)
+  assert m.ibsa_params_provider((0,)) is p and m.index_reuse_policy is M.default_reuse_policy
+  provider = lambda indices: M.IBSAParameters(num_samples=len(indices))
+  m2 = M.GridSelfAttention(M.GridSelfAttention.Config(), M.GlobalConfig(), False, num_channels=128,
+                           ibsa_params=provider)
+  assert m2.ibsa_params_provider((0, 1)).num_samples == 2
+  assert m2.ibsa_params_provider is provider
