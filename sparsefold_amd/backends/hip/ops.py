@@ -302,13 +302,16 @@ def triangle_attention_ibs(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, 
                            num_rand_blocks: int, t_prob: float, tr_prob: float, u_prob: float,
                            index_map: torch.Tensor | None = None, weight_map: torch.Tensor | None = None,
                            seed: int | None = None, add_residual: bool = True,
-                           workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+                           workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                           fixup_sum_limit: float = 0.0):
   """GridSelfAttention on ``z [N, N, C]`` with block-sparse (IBS) attention rows; returns
   ``(out, index_map, weight_map)``, maps int32 / float32 ``[N, H, ceil(N/32), num_samples]``.
   Given maps (both or neither, as backends/vecops/kernels/registry.py:2985-3002 requires) are
   reused; otherwise they are sampled with ``seed`` (default: the next value of a process-wide
-  counter)."""
+  counter).  ``fixup_sum_limit`` > 0 lowers the weight-sum limit above which a (row, head) is
+  recomputed by the exact block-sparse kernel (0 = the default 2^100)."""
   _require_cuda(z, seq_mask, ln_w, ln_b, w_qkvgb, w_o, workspace, index_map, weight_map)
+  _require(fixup_sum_limit >= 0.0, "triangle_ibs: fixup_sum_limit must be >= 0")
   _require(z.ndim == 3 and z.shape[0] == z.shape[1], f"triangle_ibs: z must be [N, N, C], got {tuple(z.shape)}")
   _require((index_map is None) == (weight_map is None), "index_map and weight_map must be both present or both omitted")
   N, _, Cn = z.shape
@@ -345,6 +348,7 @@ def triangle_attention_ibs(z: torch.Tensor, seq_mask: torch.Tensor, ln_w, ln_b, 
   a.transpose, a.add_residual = int(bool(transpose)), int(bool(add_residual))
   a.z, a.seq_mask, a.ln_w, a.ln_b = _vp(zc), _vp(m8), _vp(lw), _vp(lb)
   a.w_qkvgb, a.w_o, a.out = _vp(w_qkvgb), _vp(w_o), _vp(out)
+  a.fixup_sum_limit = float(fixup_sum_limit)
   p = _lib.IbsArgs()
   p.num_samples, p.num_rand_blocks = int(num_samples), int(num_rand_blocks)
   p.t_prob, p.tr_prob, p.u_prob = float(t_prob), float(tr_prob), float(u_prob)

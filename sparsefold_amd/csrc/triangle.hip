@@ -463,12 +463,21 @@ struct TriAttnArgs {
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
   uint16_t* o;                        // [H][N][N][32] head-major, dims in epilogue order
-  uint8_t* flags;                     // [N][H]: 1 = recomputed exactly by tri_fixup_kernel
+  uint8_t* flags;                     // [N][H]: 1 = recomputed exactly (dense: tri_fixup_kernel)
+  // block-sparse rows (tri_ibs_tile_attn_kernel): maps [N][H][T][S] of (key block, weight);
+  // sparse != 0 also keeps tri_fixup_kernel to the masked rows (flagged rows are recomputed by
+  // the exact block-sparse kernel)
+  const int32_t* index; const float* weight;
+  int T, S, sparse;
 };
 
 constexpr int kTR = 4;                // rows per workgroup
 constexpr int kKT = 64;               // keys per tile
 constexpr int kAW = 8;                // waves per attention workgroup (256 queries)
+// Per-wave table of the block-sparse kernel: the weights of the selected key blocks of its query
+// tile for the task's 4 rows, [row][block] floats (0 = not selected), blocks < 128 (N <= 4096).
+constexpr int kIbsTabBlocks = 128;
+constexpr int kIbsTabBytes = kAW * kTR * kIbsTabBlocks * 4;
 
 typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
@@ -505,9 +514,15 @@ struct TileLayout {
 // Workgroup b is assumed to run on XCD b % 8 (round-robin dispatch) and takes the tasks
 // x * T/8 + b/8 + (G/8) j of XCD x's contiguous range, so the workgroups an XCD runs together
 // share one head's bias plane and neighbouring row groups' K/V tiles in its L2.
-__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) {
+//
+// SP (tri_ibs_tile_attn_kernel): block-sparse rows on the same pipeline.  At the start of a task
+// each wave fills its table from the maps; a unit (row rr, 32-key block b) whose weight w is 0 is
+// skipped (no S^T MFMAs, exponentials or P.V), and a selected one adds log2 w to its logits, so
+// that its weights are w 2^s.  Row sums, normalisation and the out-of-range flags are unchanged.
+template <bool SP>
+__device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   using TL = TileLayout;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes + (SP ? kIbsTabBytes : 0)];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar branches
   const int half = lane >> 5, li = lane & 31;
@@ -635,39 +650,86 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   // RELOAD (the last tile of a task): row rr's Q operands are replaced by the next task's (nq:
   // this lane's Q of that task) as soon as the S^T MFMA of unit 2rr+1 -- their last use -- has
   // been issued, so that those loads have most of a tile to land.
+  // SP: wu[u] = weight of unit u of the current tile (wave-uniform scalars), 0 = skipped
+  float wu[2 * kTR];
+  auto on = [&](int u) __attribute__((always_inline)) { return !SP || wu[u] != 0.f; };
   auto units = [&](int buf, auto reloadc, const uint16_t* nq) __attribute__((always_inline)) {
     constexpr bool RELOAD = decltype(reloadc)::value;
     f32x16 sc, sn;
     bf16x8 kr[2], vr[2];
-    load_k(0, 0, buf, kr);
-    qk(0, 0, kr, sc);
-    load_k(0, 1, buf, kr);
-    load_v(0, 0, buf, vr);
+    if (on(0)) {
+      load_k(0, 0, buf, kr);
+      qk(0, 0, kr, sc);
+    }
+    if (on(1)) load_k(0, 1, buf, kr);
+    if (on(0)) load_v(0, 0, buf, vr);
 #pragma unroll
     for (int u = 0; u < 2 * kTR; ++u) {
       const int rr = u >> 1;
-      if (u + 1 < 2 * kTR) qk((u + 1) >> 1, (u + 1) & 1, kr, sn);
-      if (u + 2 < 2 * kTR) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
+      if (u + 1 < 2 * kTR && on(u + 1)) qk((u + 1) >> 1, (u + 1) & 1, kr, sn);
+      if (u + 2 < 2 * kTR && on(u + 2)) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
       if (RELOAD && (u & 1) == 0) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(nq + rr * rstride + kk * 512));
       }
       __builtin_amdgcn_sched_barrier(0);
+      if (on(u)) {
+        if (SP && wu[u] != 1.0f) {     // a drawn block: weights w 2^s = 2^(s + log2 w)
+          const float lw = __builtin_amdgcn_logf(wu[u]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bf16x8 pb;                     // P^T chunk 2kb+j: weights 2^s as bf16 pairs
-#pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) {
-          const bf16x2 w = cvt_bf2(fast_exp2(sc[8 * j + 2 * q2]), fast_exp2(sc[8 * j + 2 * q2 + 1]));
-          pb[2 * q2] = w[0];
-          pb[2 * q2 + 1] = w[1];
+          for (int e = 0; e < 16; ++e) sc[e] += lw;
         }
-        o[rr] = mfma32(vr[j], pb, o[rr]);
-        lsum[rr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sel, pb, lsum[rr], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 pb;                     // P^T chunk 2kb+j: weights 2^s as bf16 pairs
+#pragma unroll
+          for (int q2 = 0; q2 < 4; ++q2) {
+            const bf16x2 w = cvt_bf2(fast_exp2(sc[8 * j + 2 * q2]), fast_exp2(sc[8 * j + 2 * q2 + 1]));
+            pb[2 * q2] = w[0];
+            pb[2 * q2 + 1] = w[1];
+          }
+          o[rr] = mfma32(vr[j], pb, o[rr]);
+          lsum[rr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sel, pb, lsum[rr], 0, 0, 0);
+        }
       }
-      if (u + 1 < 2 * kTR) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
+      if (u + 1 < 2 * kTR && on(u + 1)) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
       __builtin_amdgcn_sched_barrier(0);
       sc = sn;
+    }
+  };
+  // SP: this wave's table (weights of its query tile's selected blocks for the task's 4 rows)
+  float* tab = reinterpret_cast<float*>(smem + 2 * TL::kBytes) + wave * kTR * kIbsTabBlocks;
+  auto fill_table = [&](int r0, int h, int qb) __attribute__((always_inline)) {
+    asm volatile("" ::: "memory");
+    for (int e = lane; e < kTR * kIbsTabBlocks; e += 64) tab[e] = 0.f;
+    const int t = qb * kAW + wave;                           // this wave's query tile
+    const int ne = kTR * a.S;                                // <= 256 entries: 4 per lane
+    int bs[4];
+    float ws[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = lane + 64 * k, rr = e / a.S, r = r0 + rr;
+      bs[k] = -1;
+      ws[k] = 0.f;
+      if (e < ne && t < a.T && r < N) {
+        const int64_t m = (((int64_t)r * H + h) * a.T + t) * a.S + (e - rr * a.S);
+        bs[k] = a.index[m];
+        ws[k] = a.weight[m];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int rr = (lane + 64 * k) / a.S;
+      if (bs[k] >= 0 && bs[k] < a.T && ws[k] > 0.f) atomicAdd(&tab[rr * kIbsTabBlocks + bs[k]], ws[k]);
+    }
+    asm volatile("" ::: "memory");
+  };
+  auto tile_weights = [&](int tt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rr = 0; rr < kTR; ++rr) {
+      const f32x2 v = *reinterpret_cast<const f32x2*>(tab + rr * kIbsTabBlocks + 2 * tt);
+      wu[2 * rr] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v[0])));
+      wu[2 * rr + 1] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v[1])));
     }
   };
 
@@ -693,6 +755,7 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
     }
     const int i = qb * 32 * kAW + 32 * wave + li;          // this lane's query
     const bool active = qb * 32 * kAW + 32 * wave < NP;    // uniform: the wave has queries below NP
+    if constexpr (SP) fill_table(r0, h, qb);
 #pragma unroll
     for (int rr = 0; rr < kTR; ++rr) {
 #pragma unroll
@@ -727,7 +790,15 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
       // end of the last tile counts on it): no memory operation crosses this point
       if (LAST) asm volatile("" ::: "memory");
       if (active) {                                          // (idle waves need no Q operands)
-        load_bias(buf);
+        if constexpr (SP) {
+          tile_weights(tt);
+          bool any = false;
+#pragma unroll
+          for (int u = 0; u < 2 * kTR; ++u) any |= wu[u] != 0.f;
+          if (any) load_bias(buf);
+        } else {
+          load_bias(buf);
+        }
         units(buf, lastc, nq);
       }
       // tile loads landed (the 8 Q loads of the last tile, the youngest, may stay in flight;
@@ -776,6 +847,10 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a)
   }
   __builtin_amdgcn_s_waitcnt(0);                           // the last task's Q reloads
 }
+
+__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) { tri_attn_body<false>(a); }
+
+__global__ __launch_bounds__(64 * kAW) void tri_ibs_tile_attn_kernel(const TriAttnArgs a) { tri_attn_body<true>(a); }
 
 // ---------------------------------------------------------------------------------------
 // Rows the attention kernel cannot finish on its fast path, one workgroup per attention row:
@@ -841,6 +916,7 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
     }
     return;
   }
+  if (a.sparse) return;                                  // flagged block-sparse rows: not here
   for (int h = 0; h < H; ++h) {
     if (a.flags[r * H + h] == 0) continue;               // same address for every thread: uniform
     for (int i = tid; i < N; i += 256) {
@@ -924,6 +1000,7 @@ struct IbsArgs {
   float* bmean;                       // [H][T][NP] tile-mean bias (log2 units), keys as the planes store them
   int32_t* index; float* weight;      // [N][H][T][S]
   uint16_t* o;                        // [H][N][N][32], as the dense attention stage writes it
+  const uint8_t* flags;               // tri_ibs_attn_kernel: only (row, head) flagged here (null: all)
 };
 
 __device__ __forceinline__ unsigned long long ibs_mix64(unsigned long long x) {
@@ -955,43 +1032,61 @@ __global__ __launch_bounds__(256) void tri_ibs_bias_mean_kernel(const IbsArgs a)
   a.bmean[idx] = sum / (float)(i1 - i0);
 }
 
-// The sampler: one wave per (row r, head h, group of 32 query tiles); lane (half, li) holds tile
-// 32 g + li.  Block logits S^T = K . qbar^T on the MFMA with the tile-mean query split into two
-// bf16 terms (hi + lo: about 16 significant bits), seeded with the tile-mean bias; per block the
-// log2 mass max + log2(sum 2^(x - max)) over its valid keys.  Each lane keeps its tile's column
-// of the LDS arrays (log2 masses [KB][32], then order | count << 16 [KB][32]) and selects alone.
-__global__ __launch_bounds__(64) void tri_ibs_index_kernel(const IbsArgs a) {
+// The sampler: one workgroup of 4 waves per (row r, head h, group of 32 query tiles); lane
+// (half, li) of every wave holds tile 32 g + li.  The tile-mean query is summed over 8 of each
+// tile's queries per wave and reduced through LDS; block logits S^T = K . qbar^T on the MFMA with
+// the mean split into two bf16 terms (hi + lo: about 16 significant bits), seeded with the
+// tile-mean bias; per block the log2 mass max + log2(sum 2^(x - max)) over its valid keys.  Wave
+// w takes the key blocks b = w mod 4 and, for the ranking, the same blocks again; lane (0, li) of
+// wave 0 then selects tile li's blocks.  LDS: log2 masses [KB][32], order | count << 16 [KB][32],
+// partial query sums [4][64][16].
+constexpr int kIbsIndexWaves = 4;
+
+__global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(const IbsArgs a) {
   extern __shared__ float ibs_lds[];
-  const int lane = threadIdx.x, half = lane >> 5, li = lane & 31;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H, T = a.T, KB = a.T, S = a.S;
   const int G = (T + 31) >> 5;
   const int task = blockIdx.x;                               // the grid is N * H * G
   const int g = task % G, h = (task / G) % H, r = task / (G * H);
   const int t = 32 * g + li, tc = min(t, T - 1);            // tc: operand tile of idle lanes
-  const bool owner = half == 0 && t < T;                     // writes tile t's maps
+  const bool owner = wave == 0 && half == 0 && t < T;        // writes tile t's maps
   int32_t* iout = a.index + (((int64_t)r * H + h) * T + tc) * S;
   float* wout = a.weight + (((int64_t)r * H + h) * T + tc) * S;
+  float* lm = ibs_lds;
+  int* ord = reinterpret_cast<int*>(ibs_lds + KB * 32);
+  float* qpart = ibs_lds + 2 * KB * 32;
   int filled = 0;
-  if (a.seq[r] != 0) {                                       // masked rows keep empty maps
-    // tile-mean query, pieces (kk, half) of tiles' queries 32 tc .. 32 tc + 31
+  if (a.seq[r] != 0) {                                       // uniform over the workgroup
+    // partial tile-mean query: queries 8 wave .. 8 wave + 7 of tile tc, pieces (kk, half)
     float qs[2][8];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int e = 0; e < 8; ++e) qs[kk][e] = 0.f;
-    const uint16_t* qp = a.q + ql_off(r, h, H, NP, 32 * tc, 0, half);
-    for (int q0 = 0; q0 < 32; q0 += 8) {
+    const uint16_t* qp = a.q + ql_off(r, h, H, NP, 32 * tc, 0, half) + 8 * (8 * wave);
+    {
       u32x4 v[8][2];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) v[u][kk] = ld16(qp + (q0 + u) * 8 + kk * 512);
+        for (int kk = 0; kk < 2; ++kk) v[u][kk] = ld16(qp + u * 8 + kk * 512);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
           for (int e = 0; e < 4; ++e) { qs[kk][2 * e] += bflo(v[u][kk][e]); qs[kk][2 * e + 1] += bfhi(v[u][kk][e]); }
+    }
+#pragma unroll
+    for (int x = 0; x < 16; ++x) qpart[(wave * 64 + lane) * 16 + x] = qs[x >> 3][x & 7];
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kIbsIndexWaves; ++w) sum += qpart[(w * 64 + lane) * 16 + x];   // fixed order
+      qs[x >> 3][x & 7] = sum;
     }
     const float qinv = 1.0f / (float)(min(N, 32 * tc + 32) - 32 * tc);   // queries past N hold 0
     bf16x8 qh[2], ql[2];
@@ -1004,9 +1099,8 @@ __global__ __launch_bounds__(64) void tri_ibs_index_kernel(const IbsArgs a) {
         qh[kk][e] = hv;
         ql[kk][e] = (__bf16)(v - (float)hv);
       }
-    float* lm = ibs_lds;
     const float* bm = a.bmean + ((int64_t)h * T + tc) * NP;
-    for (int b = 0; b < KB; ++b) {
+    for (int b = wave; b < KB; b += kIbsIndexWaves) {
       const int j = 32 * b + li;
       const uint32_t vm = (uint32_t)__ballot(j < N && a.seq[j] != 0);   // bit k: key 32 b + k valid
       const bf16x8 k0 = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, j, 0, half)));
@@ -1038,30 +1132,33 @@ __global__ __launch_bounds__(64) void tri_ibs_index_kernel(const IbsArgs a) {
       const float l2 = mx + log2f(sum);
       if (half == 0) lm[b * 32 + li] = (mx == -INFINITY || l2 != l2) ? -INFINITY : l2;   // NaN: no block
     }
-    if (owner) {
-      float M = -INFINITY;
-      int nvalid = 0;
-      for (int b = 0; b < KB; ++b) {
+    __syncthreads();
+    float M = -INFINITY;
+    int nvalid = 0;
+    for (int b = 0; b < KB; ++b) {
+      const float v = lm[b * 32 + li];
+      M = fmaxf(M, v);
+      nvalid += v != -INFINITY;
+    }
+    // descending mass, ties: lower index first; blocks without valid keys are not ranked
+    if (nvalid > S && half == 0) {
+      for (int b = wave; b < KB; b += kIbsIndexWaves) {
         const float v = lm[b * 32 + li];
-        M = fmaxf(M, v);
-        nvalid += v != -INFINITY;
+        if (v == -INFINITY) continue;
+        int rank = 0;
+        for (int c = 0; c < KB; ++c) {
+          const float u = lm[c * 32 + li];
+          rank += (u > v) || (u == v && c < b);
+        }
+        ord[rank * 32 + li] = b;
       }
+    }
+    __syncthreads();
+    if (owner) {
       if (nvalid <= S) {                                     // every valid block, weight 1
         for (int b = 0; b < KB; ++b)
           if (lm[b * 32 + li] != -INFINITY) { iout[filled] = b; wout[filled] = 1.f; ++filled; }
       } else {
-        int* ord = reinterpret_cast<int*>(ibs_lds + KB * 32);
-        // descending mass, ties: lower index first; blocks without valid keys are not ranked
-        for (int b = 0; b < KB; ++b) {
-          const float v = lm[b * 32 + li];
-          if (v == -INFINITY) continue;
-          int rank = 0;
-          for (int c = 0; c < KB; ++c) {
-            const float u = lm[c * 32 + li];
-            rank += (u > v) || (u == v && c < b);
-          }
-          ord[rank * 32 + li] = b;
-        }
         auto mass = [&](int k) { return exp2f(lm[(ord[k * 32 + li] & 0xFFFF) * 32 + li] - M); };
         float total = 0.f;
         for (int k = 0; k < nvalid; ++k) total += mass(k);
@@ -1104,16 +1201,19 @@ __global__ __launch_bounds__(64) void tri_ibs_index_kernel(const IbsArgs a) {
     for (int s = filled; s < S; ++s) { iout[s] = -1; wout[s] = 0.f; }
 }
 
-// Sparse attention: one wave per (row, head, query tile); per selected block the S^T MFMAs seeded
-// with the bias, an exact running maximum, weights w 2^(s - m) as bf16, P.V on the MFMA.  Output in
-// the dense stage's o layout, so the output stage is shared.  Masked rows are left to the fix-up
-// kernel.
+// Exact sparse attention: one wave per (row, head, query tile); per selected block the S^T MFMAs
+// seeded with the bias, an exact running maximum, weights w 2^(s - m) as bf16, P.V on the MFMA.
+// Output in the dense stage's o layout, so the output stage is shared.  Masked rows are left to
+// the fix-up kernel.  It recomputes the (row, head) pairs tri_ibs_tile_attn_kernel flagged (a
+// weight sum out of range of its fixed reference point), or every row where that kernel's
+// per-wave table cannot hold the key blocks (N > 4096).
 __global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
   const int64_t task = (int64_t)blockIdx.x * 4 + wave;
   if (task >= (int64_t)a.N * a.H * a.T) return;
   const int t = (int)(task % a.T), h = (int)((task / a.T) % a.H), r = (int)(task / ((int64_t)a.T * a.H));
   if (a.seq[r] == 0) return;
+  if (a.flags != nullptr && a.flags[r * a.H + h] == 0) return;   // uniform over the wave
   const int N = a.N, NP = a.NP, H = a.H;
   const int i = 32 * t + li;                                 // this lane's query (< NP)
   bf16x8 qb[2];
@@ -1424,15 +1524,24 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
     hipLaunchKernelGGL(tri_ibs_bias_mean_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, ia);
     if ((rc = sf_check_launch("tri_ibs_bias_mean_kernel"))) return rc;
     const int groups = (ia.T + 31) / 32;
-    const size_t lds = (size_t)2 * ia.T * 32 * 4;          // <= 64 KB (T <= 256)
-    hipLaunchKernelGGL(tri_ibs_index_kernel, dim3((unsigned)(ia.N * ia.H * groups)), dim3(64), lds, st, ia);
+    const size_t lds = (size_t)2 * ia.T * 32 * 4 + kIbsIndexWaves * 64 * 16 * 4;   // <= 80 KB (T <= 256)
+    hipLaunchKernelGGL(tri_ibs_index_kernel, dim3((unsigned)(ia.N * ia.H * groups)), dim3(64 * kIbsIndexWaves), lds,
+                       st, ia);
     if ((rc = sf_check_launch("tri_ibs_index_kernel"))) return rc;
+  }
+  TriAttnArgs fa{};
+  fa.N = a->N; fa.NP = ia.NP; fa.H = a->H; fa.transpose = a->transpose; fa.sum_limit = sum_limit(a->fixup_sum_limit);
+  fa.q = ws.q; fa.k = ws.k; fa.vt = ws.vt; fa.bias = ws.bias; fa.seq = a->seq_mask; fa.o = ws.o; fa.flags = ws.flags;
+  fa.index = p->index_map; fa.weight = p->weight_map; fa.T = ia.T; fa.S = ia.S; fa.sparse = 1;
+  if (ia.T <= kIbsTabBlocks && ia.NP <= 32 * kIbsTabBlocks) {
+    // the tile pipeline with skipped units, then the exact kernel on the rows it flagged
+    const int total = ((ia.NP + 32 * kAW - 1) / (32 * kAW)) * (ia.NP / kTR) * a->H;
+    hipLaunchKernelGGL(tri_ibs_tile_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, fa);
+    if ((rc = sf_check_launch("tri_ibs_tile_attn_kernel"))) return rc;
+    ia.flags = ws.flags;
   }
   hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
   if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
-  TriAttnArgs fa{};
-  fa.N = a->N; fa.NP = ia.NP; fa.H = a->H; fa.transpose = a->transpose; fa.sum_limit = 0x1p100f;
-  fa.q = ws.q; fa.k = ws.k; fa.vt = ws.vt; fa.bias = ws.bias; fa.seq = a->seq_mask; fa.o = ws.o; fa.flags = ws.flags;
   hipLaunchKernelGGL(tri_fixup_kernel, dim3(a->N), dim3(256), 0, st, fa);   // masked rows: mean of V
   if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
   return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);

@@ -106,14 +106,16 @@ def _synthetic_maps(N, H, S, seed):
   return im, wm
 
 
-@pytest.mark.parametrize("transpose", [False, True])
-def test_ibs_given_maps_match_oracle(transpose):
+@pytest.mark.parametrize("transpose,limit", [(False, 0.0), (True, 0.0), (False, 1.0)])
+def test_ibs_given_maps_match_oracle(transpose, limit):
+  """limit 1 flags every (row, head) of the tile pipeline (weight sums exceed 1), so the exact
+  block-sparse kernel recomputes all of them."""
   N, S = 200, 4
   mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=33, sharp=True)
   hip = _prepared(mod)
   im, wm = _synthetic_maps(N, 4, S, seed=3)
   params = ibs.IBSParams(num_samples=S, num_rand_blocks=1)
-  upd, im_out, wm_out = _call(hip, z.to(DEV), seq.to(DEV), params,
+  upd, im_out, wm_out = _call(hip, z.to(DEV), seq.to(DEV), params, fixup_sum_limit=limit,
                               index_map=torch.from_numpy(im).to(DEV), weight_map=torch.from_numpy(wm).to(DEV))
   assert (im_out.cpu().numpy() == im).all() and (wm_out.cpu().numpy() == wm).all(), "given maps are not rewritten"
   rows = [0, 1, 63, 64, 150, N - 1]                    # N - 1: a masked row
@@ -121,7 +123,11 @@ def test_ibs_given_maps_match_oracle(transpose):
   ref = ibs.grid_self_attention_ibs(z.float(), seq, _params(hip), transpose=transpose, params=params, seed=0,
                                     maps=(im, wm), rows=rows).float()
   got = _rows_of(upd, rows, transpose).float().cpu()
-  assert_close_bf16(got, ref, f"IBS given maps transpose={transpose}", max_abs=2e-2 * ref.abs().max().item())
+  assert_close_bf16(got, ref, f"IBS given maps transpose={transpose} limit={limit}",
+                    max_abs=2e-2 * ref.abs().max().item())
+  if limit:
+    default, _, _ = _call(hip, z.to(DEV), seq.to(DEV), params, index_map=im_out, weight_map=wm_out)
+    assert not torch.equal(default, upd), "the exact kernel (fp32 weights) recomputed the rows"
 
 
 def _check_structure(im, wm, seq, S, R, T):
