@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SF_HIP_ABI_VERSION 10
+#define SF_HIP_ABI_VERSION 11
 
 /* ABI version of the loaded library (== SF_HIP_ABI_VERSION it was built with). */
 int sf_hip_abi_version(void);
@@ -80,6 +80,13 @@ typedef struct sf_attention_args {
    * (batch, head) share their K/V tiles; 2 = every 32-query block is an independent task.
    * Both give the same result up to fp32 summation order; tests select each explicitly. */
   int32_t schedule;
+  /* Key / value rows gathered by index (the key windows of CrossAttTransformer read from
+   * per-atom K / V, DiffusionCrossAttentionIndexed.cpp:376-411): with kv_index (int32), key j of
+   * batch (b0, b1) is row kv_index[b1 * kvi_s + j] of k / v at batch b0 (k_s[1] and v_s[1] are
+   * not applied), or row kv_zero_row -- a row of zeros the caller provides -- where kv_mask
+   * (u8 or NULL) is 0 or the index lies outside [0, kv_zero_row).  Needs 16-byte aligned q/k/v
+   * rows (the direct-to-LDS route). */
+  const int32_t* kv_index; const uint8_t* kv_mask; int64_t kvi_s; int32_t kv_zero_row;
 } sf_attention_args;
 
 int sf_hip_attention_fwd(const sf_attention_args* a, void* stream);
@@ -331,6 +338,16 @@ typedef struct sf_cross_attention_args {
   const void* w_t2;                             /* bf16 [C, H*D] */
   const void* w_zc; const float* b_zc;          /* bf16 [C, C], f32 [C] */
   void* out;                                    /* bf16 [S, U, Qw, C] */
+  /* Per-atom plan of the key windows (the native CrossAttTransformer's,
+   * backends/vecops/modules.py:1302-1400): with gather_idx and pre_q_scale, the keys' condition
+   * is the gathered queries' (keys_single_cond = convert(queries_to_keys, queries_single_cond),
+   * atom.py:279-281), so both sides' AdaLN terms are per atom, computed once per example
+   * (sf_hip_diffusion_conditioning_fwd) and given here: bf16 [U*Qw, C] each, row stride pre_rs.
+   * K / V are then projected once per atom and the attention gathers their rows by gather_idx
+   * (invalid keys: zero rows, as the gathered activations and conditions are zero there).
+   * cond_q, cond_k and the conditioning weights are not read. */
+  const void* pre_q_scale; const void* pre_q_shift; const void* pre_k_scale; const void* pre_k_shift;
+  const void* pre_zgate; int64_t pre_rs;
 } sf_cross_attention_args;
 
 size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attention_args* a);

@@ -10,7 +10,7 @@ import ctypes as C
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
@@ -33,6 +33,7 @@ class AttentionArgs(C.Structure):
       ("gate", _vp), ("g_s", _i64 * 4),
       ("out", _vp), ("o_s", _i64 * 4),
       ("schedule", _i32),
+      ("kv_index", _vp), ("kv_mask", _vp), ("kvi_s", _i64), ("kv_zero_row", _i32),
   ]
 
 
@@ -123,6 +124,8 @@ class CrossAttentionArgs(C.Structure):
       ("lnc_w_k", _vp), ("lnc_b_k", _vp), ("w_scale_k", _vp), ("b_scale_k", _vp), ("w_shift_k", _vp),
       ("w_qg", _vp), ("b_qg", _vp), ("w_kv", _vp), ("w_t2", _vp), ("w_zc", _vp), ("b_zc", _vp),
       ("out", _vp),
+      ("pre_q_scale", _vp), ("pre_q_shift", _vp), ("pre_k_scale", _vp), ("pre_k_shift", _vp),
+      ("pre_zgate", _vp), ("pre_rs", _i64),
   ]
 
 

@@ -293,8 +293,32 @@ class CrossAttentionHipMixin:
     _prepare_adaln(self, self.q_layernorm, "_hip_adq_")
     _prepare_adaln(self, self.k_layernorm, "_hip_adk_")
     _prepare_zero_init(self, self.zero_init)
+    self._hip_cond_cache = None
+    if self.q_layernorm.single_cond and self.k_layernorm.single_cond and self.zero_init.single_cond:
+      # both sides' conditioning as two layers of one diffusion_conditioning call (the k side's
+      # zero gate is computed and dropped, as the native plan does)
+      _buf(self, "_hip_pc_lnc_w", torch.stack([self._hip_adq_lnc_w, self._hip_adk_lnc_w]))
+      _buf(self, "_hip_pc_w_scale", torch.cat([self._hip_adq_w_scale, self._hip_adk_w_scale], 0))   # [2C, Cs]
+      _buf(self, "_hip_pc_b_scale", torch.cat([self._hip_adq_b_scale, self._hip_adk_b_scale]))
+      _buf(self, "_hip_pc_w_shift", torch.cat([self._hip_adq_w_shift, self._hip_adk_w_shift], 0))
+      _buf(self, "_hip_pc_w_zc", torch.cat([self._hip_w_zc, self._hip_w_zc], 0))
+      _buf(self, "_hip_pc_b_zc", torch.cat([self._hip_b_zc, self._hip_b_zc]))
     self._native_prepared = True
     return True
+
+  def cross_conditioning(self, queries_single_cond: torch.Tensor) -> dict:
+    """Both sides' AdaLN terms per atom from the queries' condition ``[U, Qw, C]``, cached per
+    condition tensor (the native plan's per-example conditioning, backends/vecops/modules.py:
+    1302-1351): q_scale, q_shift, k_scale, k_shift, zgate, each ``[U*Qw, C]``."""
+    key = (queries_single_cond.data_ptr(), tuple(queries_single_cond.shape), queries_single_cond._version)
+    if self._hip_cond_cache is not None and self._hip_cond_cache[0] == key:
+      return self._hip_cond_cache[1]
+    scale, shift, zgate = ops.diffusion_conditioning(queries_single_cond, self._hip_pc_lnc_w, self._hip_pc_w_scale,
+                                                     self._hip_pc_b_scale, self._hip_pc_w_shift, self._hip_pc_w_zc,
+                                                     self._hip_pc_b_zc)
+    terms = {"q_scale": scale[0], "q_shift": shift[0], "k_scale": scale[1], "k_shift": shift[1], "zgate": zgate[0]}
+    self._hip_cond_cache = (key, terms)
+    return terms
 
   def _native_weights(self) -> dict:
     w = {"w_qg": self._hip_w_qg, "b_qg": self._hip_b_qg, "w_kv": self._hip_w_kv, "w_t2": self._hip_w_t2,
@@ -343,10 +367,26 @@ class CrossAttentionHipMixin:
                       keys_single_cond: torch.Tensor, pair_logits: torch.Tensor | None = None, *,
                       add_residual: bool = True) -> torch.Tensor:
     """CrossAttTransformer block attention (transformer.py:668-682): keys are gathered from
-    the queries by ``queries_to_keys`` (flat index over ``[U, Qw]``, masked -> 0)."""
+    the queries by ``queries_to_keys`` (flat index over ``[U, Qw]``, masked -> 0).
+    ``keys_single_cond=None`` states that the keys' condition is the gathered queries' condition
+    (as CrossAttTransformer builds it, atom.py:279-281): the per-atom plan then runs, with both
+    sides' conditioning computed once per ``queries_single_cond`` (cross_conditioning)."""
     lead = queries_act.shape[:-3]
     U, Qw, Cn = queries_act.shape[-3:]
     Kw = gather_idxs.shape[-1]
+    if keys_single_cond is None:
+      ok = (hasattr(self, "_hip_pc_lnc_w") and queries_single_cond is not None
+            and tuple(queries_single_cond.shape) == (U, Qw, Cn) and tuple(gather_idxs.shape) == (U, Kw)
+            and self._native_ok(U, Qw, Kw, queries_mask, keys_mask, pair_logits, queries_single_cond,
+                                queries_single_cond.new_empty(U, Kw, Cn)))
+      if not ok:
+        raise ValueError("forward_indexed without keys_single_cond needs the conditioned module, "
+                         "queries_single_cond [U, Qw, C] and [U, Kw] gather indices")
+      out = ops.cross_attention_module(queries_act, None, gather_idxs, gather_mask, queries_mask, keys_mask,
+                                       pair_logits, None, None, self._native_weights(), num_head=self.num_head,
+                                       head_dim=self.key_dim, add_residual=add_residual,
+                                       pre=self.cross_conditioning(queries_single_cond))
+      return out.to(queries_act.dtype)
     if tuple(gather_idxs.shape) == (U, Kw) and self._native_ok(U, Qw, Kw, queries_mask, keys_mask, pair_logits,
                                                                queries_single_cond, keys_single_cond):
       out = ops.cross_attention_module(queries_act, None, gather_idxs, gather_mask, queries_mask, keys_mask,

@@ -462,12 +462,18 @@ def transition_module(x: torch.Tensor, cond, w: dict, *, add_residual: bool = Tr
 
 
 def cross_attention_module(xq: torch.Tensor, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k,
-                           w: dict, *, num_head: int, head_dim: int, add_residual: bool = True) -> torch.Tensor:
+                           w: dict, *, num_head: int, head_dim: int, add_residual: bool = True,
+                           pre: dict | None = None) -> torch.Tensor:
   """CrossAttention.forward as one call.  ``xq`` ``[..., U, Qw, C]``; keys either ``xk``
   ``[..., U, Kw, C]`` or gathered from the query rows by ``gather_idx`` / ``gather_mask``
   ``[U, Kw]``; masks ``[U, Qw]`` / ``[U, Kw]``; ``bias`` ``[U, H, Qw, Kw]``; conditions
-  ``[U, Qw, C]`` / ``[U, Kw, C]``."""
-  _require_cuda(xq, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k)
+  ``[U, Qw, C]`` / ``[U, Kw, C]``.  ``pre`` (with ``gather_idx``): the per-atom plan -- the
+  keys' condition is the gathered queries', and ``pre`` holds both sides' AdaLN terms per atom
+  (``q_scale``, ``q_shift``, ``k_scale``, ``k_shift``, ``zgate``: ``[U*Qw, C]`` views with one
+  row stride, as cross_conditioning returns them); the conditions are then not read."""
+  _require_cuda(xq, xk, gather_idx, gather_mask, mask_q, mask_k, bias, cond_q, cond_k,
+                *([] if pre is None else pre.values()))
+  _require(pre is None or gather_idx is not None, "cross_attention: the per-atom plan gathers its keys")
   U, Qw, Cn = xq.shape[-3:]
   S = xq.numel() // max(U * Qw * Cn, 1)
   Kw = gather_idx.shape[-1] if gather_idx is not None else xk.shape[-2]
@@ -492,8 +498,17 @@ def cross_attention_module(xq: torch.Tensor, xk, gather_idx, gather_mask, mask_q
   a.mask_q, a.mask_k = _vp(mq8), _vp(mk8)
   b = None if bias is None else _bf16(bias).contiguous()
   a.bias = _vp(b)
-  cq, ck = _bf16(cond_q).contiguous(), _bf16(cond_k).contiguous()
-  a.cond_q, a.cond_k = _vp(cq), _vp(ck)
+  if pre is None:
+    cq, ck = _bf16(cond_q).contiguous(), _bf16(cond_k).contiguous()
+    a.cond_q, a.cond_k = _vp(cq), _vp(ck)
+  else:
+    terms = [pre[k] for k in ("q_scale", "q_shift", "k_scale", "k_shift", "zgate")]
+    rs = terms[0].stride(0)
+    for t in terms:
+      _require(t.dtype == torch.bfloat16 and tuple(t.shape) == (U * Qw, Cn) and t.stride() == (rs, 1),
+               "cross_attention: pre terms must be bf16 [U*Qw, C] views with one row stride")
+    a.pre_q_scale, a.pre_q_shift, a.pre_k_scale, a.pre_k_shift, a.pre_zgate = (_vp(t) for t in terms)
+    a.pre_rs = rs
   for key in ("lnc_w_q", "lnc_b_q", "w_scale_q", "b_scale_q", "w_shift_q", "lnc_w_k", "lnc_b_k", "w_scale_k",
               "b_scale_k", "w_shift_k", "w_qg", "b_qg", "w_kv", "w_t2", "w_zc", "b_zc"):
     setattr(a, key, _vp(w.get(key)))

@@ -295,6 +295,9 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
                                     (int64_t)h * a.bias_s[2] + (int64_t)iq * a.bias_s[3]
                               : nullptr;
   const uint8_t* mkp = a.mask_k ? a.mask_k + b0 * a.mk_s[0] + b1 * a.mk_s[1] : nullptr;
+  // gathered K / V rows: key j -> row kvip[j] (or the zero row)
+  const int32_t* kvip = a.kv_index ? a.kv_index + (int64_t)b1 * a.kvi_s : nullptr;
+  const uint8_t* kvmp = a.kv_index && a.kv_mask ? a.kv_mask + (int64_t)b1 * a.kvi_s : nullptr;
   bool qvalid = i < Q;
   if (a.mask_q && i < Q) qvalid = a.mask_q[b0 * a.mq_s[0] + b1 * a.mq_s[1] + (int64_t)i * a.mq_s[2]] != 0;
   const bool any_qmasked = __any(!qvalid && i < Q);          // uniform
@@ -310,6 +313,17 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
 
   // ---- tile copy: chunk c of a tile, K chunks first ----
   uint8_t* wsm = smem + (SHARED ? 0 : wave * 2 * T::kBufBytes);
+  // gathered rows: lane L holds the row of key j0 + L of the next tile to copy (loaded one copy
+  // ahead, so that no copy waits for its index)
+  int kv_ix = 0, kv_ok = 1;
+  auto load_kvrow = [&](int j0) __attribute__((always_inline)) {
+    if (kvip != nullptr) {
+      const int j = min(j0 + lane, K - 1);
+      kv_ix = kvip[j];
+      kv_ok = kvmp == nullptr ? 1 : kvmp[j];
+    }
+  };
+  int kv_row = 0;                                            // kv_ix / kv_ok resolved for the copy
   auto copy_chunk = [&](int c, int j0, int buf) __attribute__((always_inline)) {
     const bool isk = c < T::kChunks / 2;
     const int cc = isk ? c : c - T::kChunks / 2;
@@ -317,11 +331,16 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     const int slot = lane % T::kPieces;
     int piece = slot ^ (isk ? T::kswz(key) : T::vswz(key));
     if (8 * piece >= (isk ? D : Dv)) piece = 0;              // dims past D: any finite data
-    const int row = min(j0 + key, K - 1);
+    int row = min(j0 + key, K - 1);
+    if (kvip != nullptr) row = __shfl(kv_row, key);
     const char* src = (isk ? kp + (int64_t)row * a.k_s[2] * 2 : vp + (int64_t)row * a.v_s[2] * 2) + piece * 16;
     __builtin_amdgcn_global_load_lds(src, (lds_u32a*)(wsm + buf * T::kBufBytes + c * 1024), 16, 0, 0);
   };
   auto copy_tile = [&](int j0, int buf) __attribute__((always_inline)) {
+    if (kvip != nullptr) {
+      kv_row = kv_ok == 0 || kv_ix < 0 || kv_ix >= a.kv_zero_row ? a.kv_zero_row : kv_ix;
+      load_kvrow(j0 + 64);                                   // the next copy's rows
+    }
     if (SHARED) {
 #pragma unroll
       for (int u = 0; u < T::kChunks / 4; ++u) copy_chunk(wave * (T::kChunks / 4) + u, j0, buf);
@@ -391,6 +410,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
 
   // Waits: the copies into LDS are ordinary loads to the compiler, so every wait is followed
   // by a compiler barrier (or __syncthreads) that keeps the LDS reads of the tile after it.
+  load_kvrow(t_begin * 64);
   copy_tile(t_begin * 64, 0);
   if (BL) load_bias_lds(t_begin * 64, 0);
   load_side(t_begin * 64);
@@ -670,6 +690,11 @@ int route(const sf_attention_args* a, bool allow_split, AttnRoute& r) {
   r.attn2 = r.vec && bias_vec;
   r.ksplit = 1;
   r.pl = Attn2Plan{};
+  if (a->kv_index != nullptr && (!r.attn2 || a->kv_zero_row < 0)) {
+    sf_set_error("attention: gathered K/V rows need 16-byte aligned q/k/v rows and strides, an 8-byte aligned "
+                 "bias and kv_zero_row >= 0");
+    return 1;
+  }
   if (!r.attn2) return 0;
   Attn2Plan& pl = r.pl;
   pl.QB = (a->Q + 31) / 32;

@@ -15,6 +15,7 @@
 //
 // Each stage is one of the library's own op entry points (LayerNorm, linear, attention, window
 // gather), so the numerics are exactly those of the op-level path.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <mutex>
@@ -139,6 +140,147 @@ sf_attention_args cross_attn_args(const sf_cross_attention_args* a, const void* 
   return t;
 }
 
+// Per-atom plan: q, g from yq [S*A, 2HD]; k, v from ykv [S][A + 1][2HD] (row A of each sample
+// is zero), gathered by the window index.
+bool cross_prepared(const sf_cross_attention_args* a) { return a->gather_idx != nullptr && a->pre_q_scale != nullptr; }
+
+sf_attention_args cross_prepared_attn_args(const sf_cross_attention_args* a, const void* yq, const void* ykv, void* o) {
+  sf_attention_args t = cross_attn_args(a, yq, ykv, o);
+  const int HD = a->H * a->D;
+  const int64_t A = (int64_t)a->U * a->Qw;
+  const int64_t ks[4] = {(A + 1) * 2 * HD, 0, 2 * HD, a->D};
+  for (int i = 0; i < 4; ++i) { t.k_s[i] = ks[i]; t.v_s[i] = ks[i]; }
+  t.v = static_cast<const uint16_t*>(ykv) + HD;
+  t.kv_index = a->gather_idx; t.kv_mask = a->gather_mask; t.kvi_s = a->Kw; t.kv_zero_row = (int32_t)A;
+  return t;
+}
+
+// zeroes `words` 16-byte pieces of `rows` rows (stride in 16-byte pieces)
+__global__ __launch_bounds__(256) void zero_rows_kernel(u32x4* __restrict__ p, int64_t stride, int rows, int words) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * words) return;
+  p[(int64_t)(t / words) * stride + t % words] = u32x4{0, 0, 0, 0};
+}
+
+// Per-atom AdaLN of both sides and the q/g and k/v projections of the key windows in one pass
+// (C = 128, 2HD = 256):
+//   hq = LN(x) * q_scale[a] + q_shift[a],   hk = LN(x) * k_scale[a] + k_shift[a]   (a = row % A)
+//   yq[row] = hq W_qg^T + b_qg,   ykv[s][a] = hk W_kv^T,   ykv[s][A] = 0
+// Persistent: every workgroup keeps both weights (512 rows, pitch 136) and b_qg in LDS and its
+// waves walk 32-row blocks.  Lane (half, li) holds channels 16 kk + 8 half .. +7 of row li for
+// kk = 0..7; the LN statistics are taken once per row for both sides, h is rounded to bf16 (the
+// operand the LayerNorm + linear chain would read), and the products are D^T = W h^T: lane li
+// keeps its row, registers 4g .. 4g+3 the columns 8g + 4 half .. +3 of each 32-column block.
+struct Adaln2Args {
+  int64_t rows, A; int S, blocks;
+  const uint16_t* x;
+  const uint16_t *q_scale, *q_shift, *k_scale, *k_shift; int64_t prs;
+  const uint16_t *wqg, *wkv; const float* bqg;
+  uint16_t *yq, *ykv;
+};
+constexpr int kA2Pitch = 136;
+
+__global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[2 * 256 * kA2Pitch];
+  __shared__ __attribute__((aligned(16))) float sB[256];   // b_qg (zeros without it)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
+  if (tid < 256) sB[tid] = a.bqg ? a.bqg[tid] : 0.f;
+  {
+    u32x4 st[16];                                      // 512 rows x 16 pieces: 16 per thread
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = tid + 512 * j, n = t >> 4, c8 = (t & 15) * 8;
+      st[j] = ld16((n < 256 ? a.wqg + n * 128 : a.wkv + (n - 256) * 128) + c8);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int t = tid + 512 * j, n = t >> 4, c8 = (t & 15) * 8;
+      st16(&sW[n * kA2Pitch + c8], st[j]);
+    }
+  }
+  if (blockIdx.x == 0)                                 // the zero row of every sample's K/V block
+    for (int e = tid; e < a.S * 32; e += 512)
+      st16(a.ykv + ((int64_t)(e >> 5) * (a.A + 1) + a.A) * 256 + 8 * (e & 31), u32x4{0, 0, 0, 0});
+  __syncthreads();
+  for (int blk = blockIdx.x * 8 + wave; blk < a.blocks; blk += gridDim.x * 8) {
+    const int64_t row = (int64_t)blk * 32 + li;
+    const bool valid = row < a.rows;
+    const int64_t rr = valid ? row : a.rows - 1;
+    const int64_t at = rr % a.A, smp = rr / a.A;
+    u32x4 x[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) x[kk] = ld16(a.x + rr * 128 + 16 * kk + 8 * half);
+    float sum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
+    sum += __shfl_xor(sum, 32);
+    const float mean = sum * (1.0f / 128);
+    float sq = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
+        sq += d0 * d0 + d1 * d1;
+      }
+    sq += __shfl_xor(sq, 32);
+    const float rstd = rsqrtf(sq * (1.0f / 128) + 1e-5f);
+#pragma unroll 1
+    for (int side = 0; side < 2; ++side) {
+      const uint16_t* sc = (side ? a.k_scale : a.q_scale) + at * a.prs + 8 * half;
+      const uint16_t* sh = (side ? a.k_shift : a.q_shift) + at * a.prs + 8 * half;
+      bf16x8 h[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const u32x4 s4 = ld16(sc + 16 * kk), h4 = ld16(sh + 16 * kk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd * bflo(s4[e]) + bflo(h4[e]),
+                                   (bfhi(x[kk][e]) - mean) * rstd * bfhi(s4[e]) + bfhi(h4[e]));
+          h[kk][2 * e] = v[0];
+          h[kk][2 * e + 1] = v[1];
+        }
+      }
+      uint16_t* dst = side ? a.ykv + (smp * (a.A + 1) + at) * 256 : a.yq + rr * 256;
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+          acc = mfma32(as_bf16x8(ld16(&sW[(side * 256 + 32 * cb + li) * kA2Pitch + 16 * kk + 8 * half])), h[kk], acc);
+        // lane half h' holds columns 8g + 4h' .. +3; after one exchange with the partner lane
+        // (li, 1 - h') half 0 holds columns 0..15 and half 1 columns 16..31: 32 contiguous bytes
+        uint32_t pk[4][2];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c0 = 32 * cb + 8 * g + 4 * half;
+          const f32x4 b4 = side == 0 ? *reinterpret_cast<const f32x4*>(&sB[c0]) : f32x4{0.f, 0.f, 0.f, 0.f};
+          pk[g][0] = pack_bf2(acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1]);
+          pk[g][1] = pack_bf2(acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
+        }
+        uint32_t rx[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(half ? pk[j][w] : pk[2 + j][w], 32);
+        if (valid) {
+          // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
+          // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
+          const u32x4 lo = half ? u32x4{rx[0][0], rx[0][1], pk[2][0], pk[2][1]} : u32x4{pk[0][0], pk[0][1], rx[0][0], rx[0][1]};
+          const u32x4 hi = half ? u32x4{rx[1][0], rx[1][1], pk[3][0], pk[3][1]} : u32x4{pk[1][0], pk[1][1], rx[1][0], rx[1][1]};
+          uint16_t* q = dst + 32 * cb + 16 * half;
+          st16(q, lo);
+          st16(q + 8, hi);
+        }
+      }
+    }
+  }
+}
+
 // Stand-in buffer address for sizing queries: the attention route depends on pointer alignment
 // only, and every arena slice is 256-byte aligned.
 void* const kArenaAligned = reinterpret_cast<void*>(static_cast<uintptr_t>(1) << 20);
@@ -163,6 +305,17 @@ size_t cross_ws(const sf_cross_attention_args* a) {
   Arena ws{nullptr};
   const int64_t qrows = (int64_t)a->S * a->U * a->Qw, krows = (int64_t)a->S * a->U * a->Kw;
   const int HD = a->H * a->D;
+  if (cross_prepared(a)) {                   // hq, hk, yq, ykv (+ a zero row per sample), o, slices
+    const int64_t A = (int64_t)a->U * a->Qw;
+    ws.take((size_t)qrows * a->C * 2);
+    ws.take((size_t)qrows * a->C * 2);
+    ws.take((size_t)qrows * 2 * HD * 2);
+    ws.take((size_t)a->S * (A + 1) * 2 * HD * 2);
+    ws.take((size_t)qrows * HD * 2);
+    const sf_attention_args t = cross_prepared_attn_args(a, kArenaAligned, kArenaAligned, kArenaAligned);
+    ws.take(sf_attention_workspace_bytes(&t));
+    return ws.off;
+  }
   for (int side = 0; side < 2; ++side) {
     const int64_t cr = (int64_t)a->U * (side ? a->Kw : a->Qw);
     ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2); ws.take((size_t)cr * a->C * 2);
@@ -304,8 +457,83 @@ extern "C" size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attentio
   return a == nullptr ? 0 : cross_ws(a);
 }
 
+namespace {
+// The per-atom plan: AdaLN of every atom for both sides from the given terms, q/g and k/v
+// projected once per atom, the attention gathering each window's K / V rows, AdaLN-zero output.
+int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t st) {
+  const int C = a->C, HD = a->H * a->D;
+  const int64_t A = (int64_t)a->U * a->Qw, rows = (int64_t)a->S * A;
+  int rc;
+  void* hq = ws.take((size_t)rows * C * 2);
+  void* hk = ws.take((size_t)rows * C * 2);
+  void* yq = ws.take((size_t)rows * 2 * HD * 2);
+  void* ykv = ws.take((size_t)a->S * (A + 1) * 2 * HD * 2);
+  void* o = ws.take((size_t)rows * HD * 2);
+  if (C == 128 && 2 * HD == 256) {                   // LN + both projections in one pass
+    Adaln2Args f{};
+    f.rows = rows; f.A = A; f.S = a->S; f.blocks = (int)((rows + 31) / 32);
+    f.x = static_cast<const uint16_t*>(a->xq);
+    f.q_scale = static_cast<const uint16_t*>(a->pre_q_scale); f.q_shift = static_cast<const uint16_t*>(a->pre_q_shift);
+    f.k_scale = static_cast<const uint16_t*>(a->pre_k_scale); f.k_shift = static_cast<const uint16_t*>(a->pre_k_shift);
+    f.prs = a->pre_rs;
+    f.wqg = static_cast<const uint16_t*>(a->w_qg); f.wkv = static_cast<const uint16_t*>(a->w_kv); f.bqg = a->b_qg;
+    f.yq = static_cast<uint16_t*>(yq); f.ykv = static_cast<uint16_t*>(ykv);
+    const int resident = sf_resident_workgroups(reinterpret_cast<const void*>(adaln2_proj_kernel), 512);
+    const int grid = std::max(1, std::min(resident, (f.blocks + 7) / 8));
+    hipLaunchKernelGGL(adaln2_proj_kernel, dim3(grid), dim3(512), 0, st, f);
+    if ((rc = sf_check_launch("adaln2_proj_kernel"))) return rc;
+  } else {
+  for (int side = 0; side < 2; ++side) {
+    sf_layer_norm_args ln{};
+    ln.M = rows; ln.C = C; ln.eps = 1e-5f;
+    ln.x = a->xq; ln.x_rs = C; ln.y = side ? hk : hq; ln.y_rs = C;
+    ln.scale = side ? a->pre_k_scale : a->pre_q_scale; ln.shift = side ? a->pre_k_shift : a->pre_q_shift;
+    ln.cond_rows = A; ln.cond_rs = a->pre_rs;
+    if ((rc = sf_hip_layer_norm_fwd(&ln, st))) return rc;
+  }
+  sf_linear_args p{};
+  p.M = rows; p.N = 2 * HD; p.K = C; p.x = hq; p.x_rs = C; p.wt = a->w_qg; p.bias = a->b_qg;
+  p.mul_rows = 1; p.y = yq; p.y_rs = 2 * HD;
+  if ((rc = sf_hip_linear_fwd(&p, st))) return rc;
+  sf_linear_args pk{};                       // per sample: rows 0..A-1 of its [A + 1] block
+  pk.M = A; pk.N = 2 * HD; pk.K = C; pk.x = hk; pk.x_rs = C; pk.wt = a->w_kv; pk.mul_rows = 1;
+  pk.y = ykv; pk.y_rs = 2 * HD; pk.batch = a->S; pk.x_bs = A * C; pk.y_bs = (A + 1) * 2 * HD;
+  if ((rc = sf_hip_linear_fwd(&pk, st))) return rc;
+  const int words = 2 * HD * 2 / 16;
+  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)((a->S * words + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<u32x4*>(static_cast<uint16_t*>(ykv) + A * 2 * HD), (A + 1) * 2 * HD * 2 / 16,
+                     a->S, words);
+  if ((rc = sf_check_launch("zero_rows_kernel"))) return rc;
+  }
+  const sf_attention_args t = cross_prepared_attn_args(a, yq, ykv, o);
+  const size_t split = sf_attention_workspace_bytes(&t);
+  void* split_ws = ws.take(split);
+  if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
+  return zero_init_out(rows, C, HD, o, nullptr, A, C, nullptr, nullptr, a->w_t2, a->add_residual ? a->xq : nullptr,
+                       a->out, ws, st, a->pre_zgate, a->pre_rs);
+}
+}  // namespace
+
 extern "C" int sf_hip_cross_attention_fwd(const sf_cross_attention_args* a, void* workspace,
                                           size_t workspace_bytes, void* stream) {
+  if (a != nullptr && cross_prepared(a)) {
+    if (a->xq == nullptr || a->out == nullptr || a->w_qg == nullptr || a->w_kv == nullptr || a->w_t2 == nullptr ||
+        a->gather_mask == nullptr || a->pre_q_shift == nullptr || a->pre_k_scale == nullptr ||
+        a->pre_k_shift == nullptr || a->pre_zgate == nullptr) {
+      sf_set_error("cross_attention: the per-atom plan needs xq, out, w_qg, w_kv, w_t2, gather_mask and all five "
+                   "pre_* terms");
+      return 1;
+    }
+    if (a->S <= 0 || a->U <= 0 || a->Qw <= 0 || a->Kw <= 0 || a->C <= 0 || a->H <= 0 || a->D <= 0 ||
+        a->pre_rs < a->C || (2 * a->H * a->D) % 8 != 0) {
+      sf_set_error("cross_attention: sizes must be positive, pre_rs >= C and 2HD a multiple of 8"); return 1;
+    }
+    if (workspace == nullptr || workspace_bytes < cross_ws(a)) {
+      sf_set_error("cross_attention: workspace of %zu bytes needed, %zu given", cross_ws(a), workspace_bytes);
+      return 1;
+    }
+    return cross_prepared_run(a, Arena{static_cast<char*>(workspace)}, reinterpret_cast<hipStream_t>(stream));
+  }
   if (a == nullptr || a->xq == nullptr || a->out == nullptr || a->w_qg == nullptr || a->w_kv == nullptr ||
       a->w_t2 == nullptr || a->w_zc == nullptr || a->cond_q == nullptr || a->cond_k == nullptr) {
     sf_set_error("cross_attention: xq, out, weights and both conditions must be non-null"); return 1;

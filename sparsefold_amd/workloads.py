@@ -182,7 +182,11 @@ def make_window(atoms: int, *, S: int = 5, C: int = 128, H: int = 4, pad: int = 
   U = atoms // 32
   act = torch.randn(S, U, 32, C, generator=g).to(dtype)
   qcond = torch.randn(U, 32, C, generator=g).to(dtype)
-  kcond = torch.randn(U, 128, C, generator=g).to(dtype)
+  torch.randn(U, 128, C, generator=g)              # (keeps the later draws of the seeded stream)
+  # the keys' condition is the queries' gathered into the windows, zero outside
+  # (keys_single_cond = convert(queries_to_keys, queries_single_cond), atom.py:279-281)
+  kcond = torch.where(lay.gather_mask[..., None], qcond.reshape(U * 32, C)[lay.gather_idxs.long()],
+                      torch.zeros((), dtype=dtype))
   bias = torch.randn(U, H, 32, 128, generator=g).to(dtype)
   mod = M.CrossAttention(M.CrossAttention.Config(num_head=H, key_dim=C, value_dim=C), M.GlobalConfig(),
                          num_channels=C, name="atom_transformer")

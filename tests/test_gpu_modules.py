@@ -270,6 +270,40 @@ def test_windowed_atom_attention(atoms, S, sharp):
   assert_close_bf16(upd, d_ref, "window update", max_abs=2e-2 * d_ref.abs().max().item())
 
 
+@pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False), (8192, 5, True)])
+def test_windowed_per_atom_plan(atoms, S, sharp):
+  """keys_single_cond=None: the keys' condition is the gathered queries' (as CrossAttTransformer
+  builds it), so both sides' AdaLN terms are per atom, K/V are projected per atom and the
+  attention gathers each window's rows (invalid keys: zero rows).  The workload's key condition is
+  that gather, so the oracle and the general path see the same inputs."""
+  mod, act, lay, qc, kc, bias = W.make_window(atoms, S=S, seed=5, sharp=sharp)
+  U = atoms // 32
+  ref_kc = OM.atom_layout_convert(lay.gather_idxs, lay.gather_mask, (U, 32), qc.float(), layout_axes=(-3, -2))
+  assert torch.equal(kc.float(), ref_kc)
+  hip = _prepared(mod)
+  ad, qcd, bd = act.to(DEV), qc.to(DEV), bias.to(DEV)
+  idx, gm = lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV)
+  qm, km = lay.queries_mask.to(DEV), lay.keys_mask.to(DEV)
+  out = hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd)
+  p = _params(hip)
+  oargs = (act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask, qc.float(), kc.float(),
+           bias.float(), p)
+  ref = OM.windowed_cross_attention(*oargs)
+  assert_close_bf16(out, ref, f"per-atom plan atoms={atoms} sharp={sharp}")
+  upd = hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd, add_residual=False)
+  d_ref = OM.windowed_cross_attention(*oargs, return_update=True)
+  assert_close_bf16(upd, d_ref, "per-atom plan update", max_abs=2e-2 * d_ref.abs().max().item())
+  general = hip.forward_indexed(ad, qm, idx, gm, km, qcd, kc.to(DEV), bd, add_residual=False)
+  assert_close_bf16(upd, general.float().cpu(), "per-atom plan vs general path", max_abs=2e-2 * d_ref.abs().max().item())
+  # the conditioning is computed once per condition tensor, again after it changes in place
+  first = hip._hip_cond_cache[1]
+  hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd)
+  assert hip._hip_cond_cache[1] is first
+  qcd.mul_(1.0)
+  hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd)
+  assert hip._hip_cond_cache[1] is not first
+
+
 @pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False)])
 def test_cross_attention_explicit_keys(atoms, S, sharp):
   """The reference's own call into CrossAttention (transformer.py:671-683): keys gathered by
