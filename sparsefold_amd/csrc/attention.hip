@@ -226,6 +226,12 @@ constexpr float kMassLimit = 1.152921504606846976e18f;   // 2^60: weight mass of
 
 struct Attn2Plan {
   int QB;            // 32-query blocks per (batch, head)
+  // The bias is shared across b0 (samples) and the workgroup count is a multiple of 8: XCD x
+  // (workgroup b runs on XCD b % 8) takes the contiguous eighth x of the tasks, ordered b1, head,
+  // b0, query block (SHARED) or b1, b0, head, query block (PRIVATE), so that an XCD's L2 holds
+  // the bias of the few heads / b1 it serves for all samples, and K/V stay shared between the
+  // query blocks (SHARED) or the heads (PRIVATE: neighbouring 64-byte head slices of a K/V row).
+  int xcd_order;
   int64_t tasks;     // B0 * B1 * H * QB * ksplit (PRIVATE) or groups of 4 blocks (SHARED)
   int vec_out;       // 8-byte stores of out / loads of gate
   int ksplit;        // PRIVATE: key-range slices per query block (1 = none)
@@ -261,15 +267,16 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   const int half = lane >> 5, li = lane & 31;
 
   // ---- task of this wave ----
+  const int64_t wg = pl.xcd_order ? (int64_t)(blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   int64_t task;
   int qblk;
   if (SHARED) {
-    task = blockIdx.x;                                       // (b, h, group of 4 blocks)
+    task = wg;                                               // (b, h, group of 4 blocks)
     const int groups = (pl.QB + 3) / 4;
     qblk = (int)(task % groups) * 4 + wave;
     task /= groups;
   } else {
-    const int64_t t = (int64_t)blockIdx.x * 4 + wave;
+    const int64_t t = wg * 4 + wave;
     if (t >= pl.tasks) return;                               // private waves never meet a barrier
     const int64_t tb = t / pl.ksplit;                        // (batch, head, query block)
     qblk = (int)(tb % pl.QB);
@@ -277,12 +284,19 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   }
   // key-range slice of this wave: tiles [t_begin, t_end)
   const int ntiles_all = (a.K + 63) / 64;
-  const int slice = SHARED ? 0 : (int)(((int64_t)blockIdx.x * 4 + wave) % pl.ksplit);
+  const int slice = SHARED ? 0 : (int)((wg * 4 + wave) % pl.ksplit);
   const int t_begin = (int)((int64_t)ntiles_all * slice / (SHARED ? 1 : pl.ksplit));
   const int t_end = (int)((int64_t)ntiles_all * (slice + 1) / (SHARED ? 1 : pl.ksplit));
-  const int h = (int)(task % a.H);
-  const int64_t b = task / a.H;
-  const int b0 = (int)(b / a.B1), b1 = (int)(b - (int64_t)b0 * a.B1);
+  int h, b0, b1;
+  if (pl.xcd_order && SHARED) {                              // b1, head, b0
+    b0 = (int)(task % a.B0); h = (int)((task / a.B0) % a.H); b1 = (int)(task / ((int64_t)a.B0 * a.H));
+  } else if (pl.xcd_order) {                                 // b1, b0, head
+    h = (int)(task % a.H); b0 = (int)((task / a.H) % a.B0); b1 = (int)(task / ((int64_t)a.H * a.B0));
+  } else {                                                   // b0, b1, head
+    h = (int)(task % a.H);
+    const int64_t b = task / a.H;
+    b0 = (int)(b / a.B1); b1 = (int)(b - (int64_t)b0 * a.B1);
+  }
   const int Q = a.Q, K = a.K, D = a.D, Dv = a.Dv;
   const int i = qblk * 32 + li;                              // this lane's query
   const int iq = min(i, Q - 1);
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   const float lt = l + __shfl_xor(l, 32);
   if (!SHARED && pl.ksplit > 1) {
     // one slice of the keys: unnormalised O, its reference point and weight sum, for the combine
-    const int64_t slot = ((int64_t)blockIdx.x * 4 + wave);  // (block, slice) in task order
+    const int64_t slot = wg * 4 + wave;                      // (block, slice) in task order
     float* po = pl.part + slot * 32 * (DP + 2);
 #pragma unroll
     for (int db = 0; db < DP / 32; ++db)
@@ -609,12 +623,17 @@ __global__ __launch_bounds__(256) void attn2_combine_kernel(const sf_attention_a
   if (t >= nblk * 32 * (DP / 4)) return;
   const int d0 = 4 * (int)(t % (DP / 4));
   const int li = (int)((t / (DP / 4)) % 32);
-  const int64_t blk = t / (32 * (DP / 4));
+  const int64_t blk = t / (32 * (DP / 4));                  // a PRIVATE task in the kernel's order
   const int qblk = (int)(blk % pl.QB);
   const int64_t task = blk / pl.QB;
-  const int h = (int)(task % a.H);
-  const int64_t b = task / a.H;
-  const int b0 = (int)(b / a.B1), b1 = (int)(b - (int64_t)b0 * a.B1);
+  int h, b0, b1;
+  if (pl.xcd_order) {                                        // b1, b0, head
+    h = (int)(task % a.H); b0 = (int)((task / a.H) % a.B0); b1 = (int)(task / ((int64_t)a.H * a.B0));
+  } else {
+    h = (int)(task % a.H);
+    const int64_t b = task / a.H;
+    b0 = (int)(b / a.B1); b1 = (int)(b - (int64_t)b0 * a.B1);
+  }
   const int i = qblk * 32 + li;
   if (i >= a.Q || d0 >= a.Dv) return;
   const float cs = a.scale * SF_LOG2E;
@@ -716,6 +735,8 @@ int route(const sf_attention_args* a, bool allow_split, AttnRoute& r) {
   }
   pl.ksplit = r.ksplit;
   pl.tasks = r.shared ? groups : bh * pl.QB * r.ksplit;
+  const int64_t wgs = r.shared ? pl.tasks : (pl.tasks + 3) / 4;
+  pl.xcd_order = a->bias != nullptr && a->bias_s[0] == 0 && a->B0 > 1 && wgs % 8 == 0 && (r.shared || pl.tasks % 4 == 0);
   r.kc = (a->D + 15) / 16;                                  // q.k chunks holding data
   // LDS bias tiles: always with shared tiles; per-wave tiles only for long key ranges, where the
   // saved load time outweighs the lower occupancy of the larger LDS footprint (atom windows,
