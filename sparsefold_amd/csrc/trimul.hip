@@ -30,6 +30,8 @@ constexpr int kC = 128;            // channels (the pair representation's width)
 constexpr int kWS = kC + 8;        // LDS row stride of a [rows][128] bf16 weight (bank padding)
 constexpr int kTW = 8;             // waves per workgroup of both position kernels
 constexpr int kGlu = 4 * kC;       // GLU rows: gate a, gate b, projection a, projection b
+constexpr int kTP = 34;            // LDS pitch of a staged [128 channels][32 positions] product block
+static_assert(kC * kTP == 32 * kWS, "the staged product block fills a wave's output rows exactly");
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 int64_t plane_stride(int N) { return ((int64_t)N * N + 31) & ~(int64_t)31; }
@@ -46,22 +48,20 @@ struct FoldArgs {
   float* off[3];
 };
 
+// one wave per weight row: lane l folds columns 2l, 2l + 1
 __global__ __launch_bounds__(256) void trimul_fold_kernel(const FoldArgs a) {
-  int n = blockIdx.x * 256 + threadIdx.x;
+  int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = 2 * lane;
   int s = 0;
   while (s < 3 && n >= a.rows[s]) n -= a.rows[s++];
-  if (s >= 3) return;
-  const uint16_t* w = a.w[s] + (int64_t)n * kC;
+  if (s >= 3) return;                                  // uniform over the wave
+  const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.w[s] + (int64_t)n * kC + c);
+  const float v0 = bflo(raw), v1 = bfhi(raw);
   const float* g = a.g[s];
   const float* b = a.b[s];
-  uint16_t* wf = a.wf[s] + (int64_t)n * kC;
-  float off = 0.f;
-  for (int k = 0; k < kC; ++k) {
-    const float v = bf2f(w[k]);
-    wf[k] = f2bf(g ? v * g[k] : v);
-    if (b) off += v * b[k];
-  }
-  a.off[s][n] = off;
+  *reinterpret_cast<uint32_t*>(a.wf[s] + (int64_t)n * kC + c) = pack_bf2(g ? v0 * g[c] : v0, g ? v1 * g[c + 1] : v1);
+  const float off = wave_sum(b ? v0 * b[c] + v1 * b[c + 1] : 0.f);
+  if (lane == 0) a.off[s][n] = off;
 }
 
 struct ProjArgs {
@@ -75,9 +75,9 @@ struct ProjArgs {
   int items, items_per_wave;     // blocks of 32 plane columns: Pn rows x Pn / 32
 };
 
-// D = X W^T per 32 positions x 32 channels: lane (li, half) ends with channel li of the tile at
-// positions 8(r/4) + 4 half + r%4 -- four consecutive positions per register group, one 8-byte
-// store into the channel-major plane.
+// D^T = W X^T per 32 channels x 32 positions: lane (li, half) ends with position li (plane column
+// 32 cb + li) at channels 32 nb + 8(r/4) + 4 half + r%4; each register is one 2-byte store, and
+// the 32 lanes of a half write 64 contiguous bytes of one plane row.
 __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[kGlu * kWS];
   __shared__ float sOff[kGlu];
@@ -112,10 +112,10 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
     const bool keep = ok && (a.mask == nullptr || (a.mask[za] && a.mask[zb]));
-    const uint32_t kept = (uint32_t)__ballot(keep);        // bit q: column 32 cb + q of the row
+    const float m = keep ? 1.f : 0.f;
     bf16x8 xo[8];
     ln128_operands(zn, ok, xo);
-    const int64_t pbase = (int64_t)R * a.Pn + 32 * cb + 4 * half;
+    const int64_t pbase = (int64_t)R * a.Pn + col;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {              // 0: a (even channels), 1: b (odd)
       uint16_t* dstp = side ? a.b : a.a;
@@ -128,21 +128,14 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
         for (int e = 0; e < 16; ++e) { ag[e] = 0.f; ap[e] = 0.f; }
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-          ag = mfma32(xo[kk], as_bf16x8(ld16(&sW[rg * kWS + 16 * kk + 8 * half])), ag);
-          ap = mfma32(xo[kk], as_bf16x8(ld16(&sW[rp * kWS + 16 * kk + 8 * half])), ap);
+          ag = mfma32(as_bf16x8(ld16(&sW[rg * kWS + 16 * kk + 8 * half])), xo[kk], ag);
+          ap = mfma32(as_bf16x8(ld16(&sW[rp * kWS + 16 * kk + 8 * half])), xo[kk], ap);
         }
-        const float og = sOff[rg], op = sOff[rp];
-        uint16_t* dst = dstp + (int64_t)(32 * nb + li) * plane + pbase;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int q = 8 * g + 4 * half + e;
-            const float m = ((kept >> q) & 1u) ? 1.f : 0.f;
-            v[e] = sigmoidf_(ag[4 * g + e] + og) * (ap[4 * g + e] + op) * m;
-          }
-          *reinterpret_cast<u32x2*>(dst + 8 * g) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        for (int r = 0; r < 16; ++r) {
+          const int ch = 32 * nb + 8 * (r >> 2) + 4 * half + (r & 3);   // this register's channel
+          const float v = sigmoidf_(ag[r] + sOff[side * kC + ch]) * (ap[r] + sOff[2 * kC + side * kC + ch]) * m;
+          dstp[(int64_t)ch * plane + pbase] = f2bf(v);
         }
       }
     }
@@ -194,22 +187,39 @@ __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
   for (int item = first; item < last; ++item) {
     const int64_t p = (int64_t)item * 32 + li;
     const bool ok = p < a.P;
-    // channels 16 kk + 8 half + 0..7 of position p, from the channel-major product
-    u32x4 tn[8], zn[8];
-    const uint16_t* tp = a.t + (ok ? p : 0) + (int64_t)(8 * half) * a.Pp;
+    // the block's product, [128 channels][32 positions] (64 contiguous bytes per channel): 16-byte
+    // loads into the wave's LDS rows at pitch 34, then each lane reads channels 16 kk + 8 half + 0..7
+    // of its position.  Positions past P read the planes' padding (Pp >= item * 32 + 32).
+    u32x4 tv[8], zn[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = lane + 64 * u, c = q >> 2, seg = q & 3;
+      tv[u] = ld16(a.t + (int64_t)c * a.Pp + (int64_t)item * 32 + 8 * seg);
+    }
     const uint16_t* zp = a.z + (ok ? p : 0) * kC + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    uint32_t* const rw = reinterpret_cast<uint32_t*>(rows);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = lane + 64 * u, c = q >> 2, seg = q & 3;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rw[(c * kTP + 8 * seg) / 2 + e] = tv[u][e];
+    }
+    asm volatile("" ::: "memory");                    // one wave's LDS accesses run in order
+    u32x4 tn[8];
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = ok ? tp[(int64_t)(16 * kk + 2 * e) * a.Pp] : 0u;
-        const uint32_t hi = ok ? tp[(int64_t)(16 * kk + 2 * e + 1) * a.Pp] : 0u;
-        w[e] = lo | (hi << 16);
+        const uint32_t lo = rows[(16 * kk + 8 * half + 2 * e) * kTP + li];
+        const uint32_t hi = rows[(16 * kk + 8 * half + 2 * e + 1) * kTP + li];
+        w[e] = ok ? lo | (hi << 16) : 0u;
       }
       tn[kk] = u32x4{w[0], w[1], w[2], w[3]};
-      zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
     }
+    asm volatile("" ::: "memory");                    // (the rows are rewritten below)
     bf16x8 to[8], zo[8];
     ln128_operands(tn, ok, to);
     ln128_operands(zn, ok, zo);
@@ -330,7 +340,7 @@ extern "C" int sf_hip_triangle_mult_fwd(const sf_triangle_mult_args* a, void* wo
   f.wf[1] = w.wout; f.off[1] = w.oout;
   f.w[2] = static_cast<const uint16_t*>(a->w_gate); f.g[2] = a->ln_w; f.b[2] = a->ln_b; f.rows[2] = kC;
   f.wf[2] = w.wgate; f.off[2] = w.ogate;
-  hipLaunchKernelGGL(trimul_fold_kernel, dim3((kGlu + 2 * kC + 255) / 256), dim3(256), 0, st, f);
+  hipLaunchKernelGGL(trimul_fold_kernel, dim3((kGlu + 2 * kC + 3) / 4), dim3(256), 0, st, f);   // a wave per row
   int rc = sf_check_launch("trimul_fold_kernel");
   if (rc) return rc;
 

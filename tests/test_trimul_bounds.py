@@ -58,20 +58,22 @@ def _proj_accesses(N, incoming):
   z_max = int(zlast[ok].max()) if ok.any() else -1
   # mask reads: mask[za], mask[zb] where ok
   m_max = int(np.maximum(za, zb)[ok].max()) if ok.any() else -1
-  # plane stores: channel 32 nb + li, 4 groups of 4 elements at R * Pn + 32 cb + 4 half + 8 g
+  # plane stores (2 bytes): lane (half, li) writes column col = 32 cb + li of plane row R for the
+  # channels 32 nb + 8 (r / 4) + 4 half + r % 4, r = 0..15, nb = 0..3
   plane = Pn * Pn
-  pbase = R * Pn + 32 * cb + 4 * half
-  lo = (32 * 0 + li) * plane + pbase                      # nb = 0, g = 0
-  hi = (32 * 3 + li) * plane + pbase + 8 * 3 + 3          # nb = 3, g = 3
-  # the 4 x 8-byte stores of a lane and the 32 lanes' 8-element runs tile each plane row exactly
-  writes = np.zeros(Pn * Pn, np.int64)
-  for g in range(4):
-    for h in (0, 1):
-      idx = (R * Pn + 32 * cb + 4 * h + 8 * g)[:, 0]
-      for e in range(4):
-        np.add.at(writes, idx + e, 1)
-  return dict(items=items, z_max=z_max, m_max=m_max, plane_min=int(lo.min()), plane_max=int(hi.max()),
-              plane_elems=KC * plane, row_writes=writes, aligned8=bool(((pbase * 2) % 8 == 0).all()))
+  pbase = R * Pn + col
+  ch = np.array([[32 * nb + 8 * (r >> 2) + 4 * h + (r & 3) for nb in range(4) for r in range(16)] for h in (0, 1)])
+  chl = ch[half[0]]                                        # [64 lanes, 64 channels]
+  lo = int((chl.min(axis=1)[None, :] * plane + pbase).min())
+  hi = int((chl.max(axis=1)[None, :] * plane + pbase).max())
+  # every (channel, plane element) written exactly once
+  writes = np.zeros((KC, Pn * Pn), np.int64)
+  for h in (0, 1):
+    lanes = np.flatnonzero(half[0] == h)
+    for c in ch[h]:
+      np.add.at(writes[c], pbase[:, lanes].ravel(), 1)
+  return dict(items=items, z_max=z_max, m_max=m_max, plane_min=lo, plane_max=hi,
+              plane_elems=KC * plane, row_writes=writes, aligned8=True)
 
 
 def _gemm_accesses(N):
@@ -104,7 +106,16 @@ def _out_accesses(N):
   half, li = lane >> 5, lane & 31
   p = item * 32 + li
   ok = p < P
-  t_max = int((p + 8 * half * Pp + (16 * 7 + 2 * 3 + 1) * Pp)[ok].max())
+  qt = lane + 64 * np.arange(8)[:, None, None]            # the product loads: u = 0..7, every item
+  ct, seg = qt >> 2, qt & 3
+  t_start = ct * Pp + item[None] * 32 + 8 * seg
+  assert (t_start % 8 == 0).all(), "16-byte product loads aligned"
+  t_max = int((t_start + 7).max())
+  # the wave's LDS rows hold 32 x kWS (136) elements; the staged block sits at pitch 34
+  lds_store = (ct * 34 + 8 * seg + 7).max()
+  kk, e = np.arange(8)[:, None, None, None], np.arange(4)[None, :, None, None]
+  lds_read = ((16 * kk + 8 * half[None] + 2 * e + 1) * 34 + li[None]).max()
+  assert max(lds_store, lds_read) < 32 * 136 and ((ct * 34 + 8 * seg) % 2 == 0).all()
   z_max = int((p * KC + 8 * half + 16 * 7 + 7)[ok].max())
   q = lane + 64 * np.arange(8)[:, None, None]             # the row-store loop: u = 0..7
   pos, c8 = q >> 4, (q & 15) * 8
@@ -121,7 +132,7 @@ def test_trimul_kernel_accesses_stay_in_bounds(N, incoming):
   assert pr["z_max"] < N * N * KC and pr["m_max"] < N
   assert 0 <= pr["plane_min"] and pr["plane_max"] < pr["plane_elems"]
   assert pr["aligned8"]
-  assert (pr["row_writes"] == 1).all(), "every padded plane element written exactly once (zeros included)"
+  assert (pr["row_writes"] == 1).all(), "every channel's padded plane element written exactly once (zeros included)"
   gemm, ab_elems, t_elems = _gemm_accesses(N)
   for (bm, bn), (gm, gn, x_max, w_max, y_max) in gemm.items():
     assert x_max < ab_elems and w_max < ab_elems and y_max < t_elems, (bm, bn)
