@@ -233,9 +233,22 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
-  const int64_t bz = blockIdx.z;                              // batch member (0 unless batched)
+  // Batched: workgroup L (x fastest) is assumed to run on XCD L % 8 (round-robin dispatch) and
+  // takes tile (L % 8) * total/8 + L / 8, so that every XCD works through a contiguous range of
+  // whole batch members and their operands stay in its own L2.  In dispatch order the batched
+  // product of 128 planes of 768 x 768 read its operands 5x over from HBM.
+  uint64_t bx = blockIdx.x, by = blockIdx.y, bzu = blockIdx.z;
+  if (gridDim.z > 1) {
+    const uint64_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+    if ((total & 7) == 0) {
+      const uint64_t L = blockIdx.x + gx * (blockIdx.y + gy * (uint64_t)blockIdx.z);
+      const uint64_t t = (L & 7) * (total >> 3) + (L >> 3);
+      bx = t % gx; by = (t / gx) % gy; bzu = t / (gx * gy);
+    }
+  }
+  const int64_t m0 = (int64_t)bx * BM;
+  const int n0 = (int)by * BN;
+  const int64_t bz = (int64_t)bzu;                            // batch member (0 unless batched)
   const uint16_t* xp = (const uint16_t*)a.x + bz * a.x_bs;
   const uint16_t* wp = (const uint16_t*)a.wt + bz * a.w_bs;
   const int rsw = 8 * ((lane & 7) ^ ((lane >> 3) & 7));       // this lane's swizzled source piece

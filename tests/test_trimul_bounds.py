@@ -147,3 +147,20 @@ def test_trimul_workspace_covers_the_modelled_buffers(N):
   Pn, Pp = _pn(N), _pp(N)
   need = 2 * KC * Pn * Pn * 2 + KC * Pp * 2 + (4 * KC * KC + 2 * KC * KC) * 2 + 6 * KC * 4
   assert lib.sf_hip_triangle_mult_workspace_bytes(N, KC) >= need
+
+
+@pytest.mark.parametrize("grid", [(6, 6, 128), (12, 12, 128), (1, 1, 8), (3, 2, 5), (320, 2, 5), (7, 3, 8)])
+def test_batched_gemm_tile_remap_is_a_permutation(grid):
+  """linear64_kernel's batched tile order (XCD-contiguous ranges when the tile count is a multiple
+  of 8, dispatch order otherwise) visits every (x, y, z) tile exactly once."""
+  gx, gy, gz = grid
+  total = gx * gy * gz
+  L = np.arange(total, dtype=np.int64)
+  t = (L & 7) * (total >> 3) + (L >> 3) if total % 8 == 0 else L
+  bx, by, bz = t % gx, (t // gx) % gy, t // (gx * gy)
+  assert np.unique(bx + gx * (by + gy * bz)).size == total and bz.max() < gz
+  if total % 8 == 0 and gz % 8 == 0:
+    # each XCD (L % 8) holds whole batch members
+    for x in range(8):
+      members = np.unique(bz[(L & 7) == x])
+      assert members.size == gz // 8
