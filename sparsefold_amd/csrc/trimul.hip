@@ -97,11 +97,15 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
   }
   for (int n = tid; n < kGlu; n += 64 * kTW) sOff[n] = a.off[n];
   __syncthreads();
-  const int first = (blockIdx.x * kTW + wave) * a.items_per_wave;
-  const int last = min(first + a.items_per_wave, a.items);
   const int cbs = a.Pn / 32;                            // column blocks per plane row
   const int64_t plane = (int64_t)a.Pn * a.Pn;
-  for (int item = first; item < last; ++item) {
+  // the workgroup's items are base .. base + kTW * items_per_wave - 1, wave w taking every kTW-th:
+  // neighbouring column blocks, whose stores fill the two halves of each 128-byte plane line, are
+  // written together (one wave walking consecutive items came back to a line too late for L2)
+  const int base = blockIdx.x * kTW * a.items_per_wave;
+  for (int k = 0; k < a.items_per_wave; ++k) {
+    const int item = base + k * kTW + wave;
+    if (item >= a.items) break;
     // plane row R, columns 32 cb .. 32 cb + 31; this lane's column col.  Outgoing: z position
     // (R, col); incoming: (col, R), so that the planes hold a^T and b^T
     const int R = item / cbs, cb = item - R * cbs, col = 32 * cb + li;
@@ -156,8 +160,9 @@ struct OutArgs {
 };
 
 // D^T = W X^T per 32 output channels x 32 positions: lane (li, half) ends with position li at
-// channels 32 nb + 8(r/4) + 4 half + r%4; the gated update goes through a per-wave LDS row block
-// so that every lane then writes whole 16-byte runs of the position-major output.
+// channels 32 nb + 8(r/4) + 4 half + r%4; the gated update (plus the residual, taken from the z
+// registers the gate's LayerNorm loaded) goes through a per-wave LDS row block so that every lane
+// then writes whole 16-byte runs of the position-major output.
 __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sWo[kC * kWS];
   __shared__ __attribute__((aligned(16))) uint16_t sWg[kC * kWS];
@@ -182,9 +187,13 @@ __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
   for (int n = tid; n < kC; n += 64 * kTW) { sOo[n] = a.oo[n]; sOg[n] = a.og[n]; }
   __syncthreads();
   uint16_t* const rows = sOut[wave];
-  const int first = (blockIdx.x * kTW + wave) * a.items_per_wave;
-  const int last = min(first + a.items_per_wave, a.items);
-  for (int item = first; item < last; ++item) {
+  // the workgroup's items are base .. base + kTW * items_per_wave - 1, wave w taking every kTW-th:
+  // neighbouring blocks read the two 64-byte halves of each 128-byte line of t together (one wave
+  // walking consecutive items came back to a line after L2 had dropped it: t was fetched twice)
+  const int base = blockIdx.x * kTW * a.items_per_wave;
+  for (int k = 0; k < a.items_per_wave; ++k) {
+    const int item = base + k * kTW + wave;
+    if (item >= a.items) break;
     const int64_t p = (int64_t)item * 32 + li;
     const bool ok = p < a.P;
     // the block's product, [128 channels][32 positions] (64 contiguous bytes per channel): 16-byte
@@ -225,6 +234,18 @@ __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
     ln128_operands(zn, ok, zo);
 #pragma unroll
     for (int nb = 0; nb < kC / 32; ++nb) {
+      // residual z of this lane's update channels: channel 32 nb + 8 g + 4 half + e is word
+      // 2 half + e/2 of zn[2 nb + g/2] in the lane of half g%2 -- this lane's own registers for
+      // g%2 == half, the partner lane's (lane ^ 32) otherwise
+      uint32_t zown[2][2], zrcv[2][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const u32x4 zw = zn[2 * nb + j];
+          zown[j][w] = half ? zw[2 + w] : zw[w];
+          zrcv[j][w] = (uint32_t)__shfl_xor((int)(half ? zw[w] : zw[2 + w]), 32);
+        }
       f32x16 ao, ag;
 #pragma unroll
       for (int e = 0; e < 16; ++e) { ao[e] = 0.f; ag[e] = 0.f; }
@@ -240,7 +261,15 @@ __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = (ao[4 * g + e] + sOo[c0 + e]) * sigmoidf_(ag[4 * g + e] + sOg[c0 + e]);
-        *reinterpret_cast<u32x2*>(&rows[li * kWS + c0]) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+        uint32_t u0 = pack_bf2(v[0], v[1]), u1 = pack_bf2(v[2], v[3]);   // the bf16 update
+        if (a.add_residual) {                                            // out = update + z
+          const bool mine = half == (g & 1);
+          const uint32_t z0 = mine ? zown[g >> 1][0] : zrcv[g >> 1][0];
+          const uint32_t z1 = mine ? zown[g >> 1][1] : zrcv[g >> 1][1];
+          u0 = pack_bf2(bflo(u0) + bflo(z0), bfhi(u0) + bfhi(z0));
+          u1 = pack_bf2(bflo(u1) + bflo(z1), bfhi(u1) + bfhi(z1));
+        }
+        *reinterpret_cast<u32x2*>(&rows[li * kWS + c0]) = u32x2{u0, u1};
       }
     }
     asm volatile("" ::: "memory");                    // one wave's LDS accesses run in order
@@ -249,15 +278,7 @@ __global__ __launch_bounds__(64 * kTW) void trimul_out_kernel(const OutArgs a) {
       const int q = lane + 64 * u, pos = q >> 4, c8 = (q & 15) * 8;
       const int64_t pp = (int64_t)item * 32 + pos;
       const u32x4 v = ld16(&rows[pos * kWS + c8]);
-      if (pp < a.P) {
-        u32x4 r = v;
-        if (a.add_residual) {
-          const u32x4 zr = ld16(a.z + pp * kC + c8);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = pack_bf2(bflo(v[e]) + bflo(zr[e]), bfhi(v[e]) + bfhi(zr[e]));
-        }
-        st16(a.out + pp * kC + c8, r);
-      }
+      if (pp < a.P) st16(a.out + pp * kC + c8, v);
     }
     asm volatile("" ::: "memory");                    // one wave's LDS accesses run in order
   }

@@ -607,6 +607,9 @@ def test_triangle_multiplication(N, incoming, padded):
   d_ref = OM.triangle_multiplication(z.float(), mask, _params(hip), equation=eq, return_update=True)
   assert_close_bf16(upd, d_ref, f"trimul update N={N} incoming={incoming} padded={padded}",
                     max_abs=2e-2 * max(1.0, d_ref.abs().max().item()))
+  # the residual form adds z to the same bf16 update in fp32 and rounds once more: bit-exact
+  out = hip(z.to(DEV), mask.to(DEV))
+  assert torch.equal(out, (upd.float() + z.to(DEV).float()).to(z.dtype)), "trimul residual != bf16(update + z)"
 
 
 @pytest.mark.parametrize("N,incoming", [(768, False), (768, True), (96, False), (96, True)])

@@ -29,13 +29,16 @@ def _grid(items):
 
 
 def _covered(items, ipw, groups):
-  """Every item is processed by exactly one wave."""
+  """Every item is processed by exactly one wave: workgroup g's wave w takes items
+  g * KTW * ipw + k * KTW + w, k < ipw, until the first one past the end."""
   seen = np.zeros(items, np.int64)
-  for wave_id in range(groups * KTW):
-    first = wave_id * ipw
-    last = min(first + ipw, items)
-    if first < last:
-      seen[first:last] += 1
+  for g in range(groups):
+    for w in range(KTW):
+      for k in range(ipw):
+        item = g * KTW * ipw + k * KTW + w
+        if item >= items:
+          break
+        seen[item] += 1
   return bool((seen == 1).all())
 
 
