@@ -365,7 +365,11 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   };
   // ---- bias tile (this lane's query, its 32 keys) and key-mask bits ----
   u32x2 bnext[8];
-  uint64_t mnext = ~0ull;
+  // key-mask byte of key j0 + lane of the next tile, kept raw until the tile's wait: a ballot
+  // right after the load waited for it -- and, the vector memory counter being in order, for the
+  // next tile's copies issued just before, which serialised the prefetch with the compute
+  // (diffusion 5 x 1024: 0.155 -> 0.140 ms per block)
+  uint32_t mbyte = 1;
   uint8_t* bsm = smem + kKVRegion + wave * 2 * 4096;        // BL: this wave's two bias buffers
   // BL source rows: lane L copies row 8u + L%8 of the wave's 32 queries, piece L/8 (keys 8p .. 8p+7)
   const uint16_t* brow0 = nullptr;
@@ -407,9 +411,11 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
         bnext[q] = u32x2{(uint32_t)t[0] | ((uint32_t)t[1] << 16), (uint32_t)t[2] | ((uint32_t)t[3] << 16)};
       }
     }
-    const int jl = j0 + lane;
-    const bool kv = jl < K && (mkp == nullptr || mkp[(int64_t)jl * a.mk_s[2]] != 0);
-    mnext = __ballot(kv);
+    if (mkp != nullptr) mbyte = mkp[(int64_t)min(j0 + lane, K - 1) * a.mk_s[2]];
+  };
+  // valid keys of the tile at j0, once its mask bytes (load_side(j0)) have landed
+  auto mask_bits = [&](int j0) __attribute__((always_inline)) -> uint64_t {
+    return __ballot(j0 + lane < K && mbyte != 0);
   };
 
   f32x16 o[DP / 32];
@@ -445,7 +451,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
 #pragma unroll
       for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
     }
-    const uint64_t mbits = mnext;
+    const uint64_t mbits = mask_bits(j0);
     if (t + 1 < t_end) {
       copy_tile(j0 + 64, buf ^ 1);
       if (BL) load_bias_lds(j0 + 64, buf ^ 1);
