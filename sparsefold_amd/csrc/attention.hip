@@ -254,13 +254,15 @@ struct Attn2Tile {
 // (rows 16-byte aligned, K % 8 == 0): each wave copies its 32 query rows x 64 keys with four
 // direct-to-LDS loads of 8 rows x 128 bytes, slot-major [row/8][piece][row%8], and every lane
 // then reads its keys with conflict-free 8-byte LDS reads.  Loaded lane by lane from global
-// memory instead, every bias instruction touched 32 rows: 40% of the kernel's time.
+// memory instead, every bias instruction touched 32 rows: 40% of the kernel's time.  One buffer
+// per wave: the wave reads the tile's bias into registers first, waits for those reads, and only
+// then copies the next tile's into the same buffer (48 KB per shared-tile workgroup, three per CU).
 template <int DP, bool SHARED, int KC, bool BL>
 __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, const Attn2Plan pl) {
   using T = Attn2Tile<DP>;
   constexpr int kWaveBufs = SHARED ? 1 : 4;                 // tile sets in LDS (shared or per wave)
   constexpr int kKVRegion = kWaveBufs * 2 * T::kBufBytes;
-  constexpr int kBiasRegion = BL ? 4 * 2 * 4096 : 0;        // per wave: 2 buffers x 32 rows x 128 B
+  constexpr int kBiasRegion = BL ? 4 * 4096 : 0;            // per wave: 32 rows x 128 B
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kKVRegion + kBiasRegion];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -370,7 +372,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // next tile's copies issued just before, which serialised the prefetch with the compute
   // (diffusion 5 x 1024: 0.155 -> 0.140 ms per block)
   uint32_t mbyte = 1;
-  uint8_t* bsm = smem + kKVRegion + wave * 2 * 4096;        // BL: this wave's two bias buffers
+  uint8_t* bsm = smem + kKVRegion + wave * 4096;            // BL: this wave's bias buffer
   // BL source rows: lane L copies row 8u + L%8 of the wave's 32 queries, piece L/8 (keys 8p .. 8p+7)
   const uint16_t* brow0 = nullptr;
   int64_t brs8 = 0;                                          // elements between rows 8 apart
@@ -380,7 +382,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     brs8 = 8 * a.bias_s[3];
   }
   const bool brows_clamped = qblk * 32 + 32 > Q;            // uniform: the last query block
-  auto load_bias_lds = [&](int j0, int buf) __attribute__((always_inline)) {
+  auto load_bias_lds = [&](int j0) __attribute__((always_inline)) {
     const int jc = min(j0, K - 8 - 8 * (lane >> 3)) - j0;   // pieces past K re-read the last one
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
         const uint16_t* bh = (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] + (int64_t)h * a.bias_s[2];
         src = bh + (int64_t)min(qblk * 32 + 8 * u + (lane & 7), Q - 1) * a.bias_s[3] + 8 * (lane >> 3);
       }
-      __builtin_amdgcn_global_load_lds(src + j0 + jc, (lds_u32a*)(bsm + buf * 4096 + u * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(src + j0 + jc, (lds_u32a*)(bsm + u * 1024), 16, 0, 0);
     }
   };
   auto load_side = [&](int j0) __attribute__((always_inline)) {
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // by a compiler barrier (or __syncthreads) that keeps the LDS reads of the tile after it.
   load_kvrow(t_begin * 64);
   copy_tile(t_begin * 64, 0);
-  if (BL) load_bias_lds(t_begin * 64, 0);
+  if (BL) load_bias_lds(t_begin * 64);
   load_side(t_begin * 64);
   __builtin_amdgcn_s_waitcnt(0);
   if (SHARED) __syncthreads();
@@ -446,7 +448,10 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     if (BL) {                                                // keys 32(q/4) + 8(q%4) + 4half .. +3 = piece q
 #pragma unroll
       for (int q = 0; q < 8; ++q)
-        bcur[q] = *reinterpret_cast<const u32x2*>(bsm + buf * 4096 + (li >> 3) * 1024 + q * 128 + (li & 7) * 16 + half * 8);
+        bcur[q] = *reinterpret_cast<const u32x2*>(bsm + (li >> 3) * 1024 + q * 128 + (li & 7) * 16 + half * 8);
+      // the buffer is refilled below: these reads complete first (the copies are ordinary loads
+      // to the compiler, so the wait carries a memory clobber)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     } else {
 #pragma unroll
       for (int q = 0; q < 8; ++q) bcur[q] = bnext[q];
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     const uint64_t mbits = mask_bits(j0);
     if (t + 1 < t_end) {
       copy_tile(j0 + 64, buf ^ 1);
-      if (BL) load_bias_lds(j0 + 64, buf ^ 1);
+      if (BL) load_bias_lds(j0 + 64);
       load_side(j0 + 64);
     }
     if (wactive) {
