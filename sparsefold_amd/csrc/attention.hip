@@ -749,10 +749,10 @@ int route(const sf_attention_args* a, bool allow_split, AttnRoute& r) {
   const int64_t wgs = r.shared ? pl.tasks : (pl.tasks + 3) / 4;
   pl.xcd_order = a->bias != nullptr && a->bias_s[0] == 0 && a->B0 > 1 && wgs % 8 == 0 && (r.shared || pl.tasks % 4 == 0);
   r.kc = (a->D + 15) / 16;                                  // q.k chunks holding data
-  // LDS bias tiles: always with shared tiles; per-wave tiles only for long key ranges, where the
-  // saved load time outweighs the lower occupancy of the larger LDS footprint (atom windows,
-  // K = 128: 31 us without, 41 us with; single attention, K = 768: 30 us without, 25 us with)
-  r.bl = a->bias != nullptr && aligned16(a->bias) && a->K % 8 == 0 && (r.shared || a->K >= 256);
+  // LDS bias tiles: always with shared tiles; per-wave tiles from two key tiles on (with one
+  // bias buffer per wave a per-wave-tile workgroup takes 80 KB, two per CU as without the bias
+  // tiles: atom windows, K = 128, 34.7 -> 30.5 us; single attention, K = 768, 30 -> 25 us)
+  r.bl = a->bias != nullptr && aligned16(a->bias) && a->K % 8 == 0 && (r.shared || a->K >= 128);
   for (int s2 = 0; s2 < 4 && r.bl; ++s2) r.bl = a->bias_s[s2] % 8 == 0;
   return 0;
 }
