@@ -166,11 +166,16 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(u32x4* __restrict__ p, i
 // (C = 128, 2HD = 256):
 //   hq = LN(x) * q_scale[a] + q_shift[a],   hk = LN(x) * k_scale[a] + k_shift[a]   (a = row % A)
 //   yq[row] = hq W_qg^T + b_qg,   ykv[s][a] = hk W_kv^T,   ykv[s][A] = 0
-// Persistent: every workgroup keeps both weights (512 rows, pitch 136) and b_qg in LDS and its
-// waves walk 32-row blocks.  Lane (half, li) holds channels 16 kk + 8 half .. +7 of row li for
-// kk = 0..7; the LN statistics are taken once per row for both sides, h is rounded to bf16 (the
-// operand the LayerNorm + linear chain would read), and the products are D^T = W h^T: lane li
-// keeps its row, registers 4g .. 4g+3 the columns 8g + 4 half .. +3 of each 32-column block.
+// Persistent: every workgroup keeps both weights (512 rows, pitch 136) and b_qg in LDS and walks
+// blocks of 32 rows.  Per block:
+//   1. all 512 threads read the block's x, scale and shift rows as contiguous 16-byte pieces
+//      (thread t: row t/16, channels 8 (t%16) .. +7; 4 rows per instruction), reduce each row's
+//      LayerNorm statistics over its 16 lanes and write hq, hk (bf16, the operand the LayerNorm +
+//      linear chain would read) to LDS;
+//   2. wave w forms output columns 32w .. 32w+31 of both sides, D^T = W h^T: lane (li, half)
+//      keeps row li, registers 4g .. 4g+3 the columns 8g + 4 half .. +3.
+// The next block's rows are requested before step 2.  (With a wave per 32 rows, every load
+// instruction touched 32 rows in 16-byte pieces: the loads took half of the kernel's time.)
 struct Adaln2Args {
   int64_t rows, A; int S, blocks;
   const uint16_t* x;
@@ -182,8 +187,10 @@ constexpr int kA2Pitch = 136;
 
 __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[2 * 256 * kA2Pitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * 32 * kA2Pitch];   // hq, hk of the block
   __shared__ __attribute__((aligned(16))) float sB[256];   // b_qg (zeros without it)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
+  const int prow = tid >> 4, pc = tid & 15;           // step 1: this thread's row and 8 channels
   if (tid < 256) sB[tid] = a.bqg ? a.bqg[tid] : 0.f;
   {
     u32x4 st[16];                                      // 512 rows x 16 pieces: 16 per thread
@@ -201,81 +208,88 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
   if (blockIdx.x == 0)                                 // the zero row of every sample's K/V block
     for (int e = tid; e < a.S * 32; e += 512)
       st16(a.ykv + ((int64_t)(e >> 5) * (a.A + 1) + a.A) * 256 + 8 * (e & 31), u32x4{0, 0, 0, 0});
-  __syncthreads();
-  for (int blk = blockIdx.x * 8 + wave; blk < a.blocks; blk += gridDim.x * 8) {
+  // step 1 loads of a block: x, q scale / shift, k scale / shift of row prow, channels 8 pc .. +7
+  u32x4 lx, lsq, lhq, lsk, lhk;
+  auto load_rows = [&](int blk) __attribute__((always_inline)) {
+    const int64_t row = min((int64_t)blk * 32 + prow, a.rows - 1), at = row % a.A;
+    lx = ld16(a.x + row * 128 + 8 * pc);
+    lsq = ld16(a.q_scale + at * a.prs + 8 * pc); lhq = ld16(a.q_shift + at * a.prs + 8 * pc);
+    lsk = ld16(a.k_scale + at * a.prs + 8 * pc); lhk = ld16(a.k_shift + at * a.prs + 8 * pc);
+  };
+  const int stride = gridDim.x;
+  int blk = blockIdx.x;
+  if (blk < a.blocks) load_rows(blk);
+  for (; blk < a.blocks; blk += stride) {
+    // ---- step 1: LayerNorm statistics over the row's 16 lanes, modulation, hq / hk to LDS ----
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum += bflo(lx[e]) + bfhi(lx[e]);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) sum += __shfl_xor(sum, m);
+    const float mean = sum * (1.0f / 128);
+    float sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d0 = bflo(lx[e]) - mean, d1 = bfhi(lx[e]) - mean;
+      sq += d0 * d0 + d1 * d1;
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) sq += __shfl_xor(sq, m);
+    const float rstd = rsqrtf(sq * (1.0f / 128) + 1e-5f);
+    u32x4 hq, hk;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float n0 = (bflo(lx[e]) - mean) * rstd, n1 = (bfhi(lx[e]) - mean) * rstd;
+      hq[e] = pack_bf2(n0 * bflo(lsq[e]) + bflo(lhq[e]), n1 * bfhi(lsq[e]) + bfhi(lhq[e]));
+      hk[e] = pack_bf2(n0 * bflo(lsk[e]) + bflo(lhk[e]), n1 * bfhi(lsk[e]) + bfhi(lhk[e]));
+    }
+    __syncthreads();                                   // the previous block's step 2 is done with sH
+    st16(&sH[prow * kA2Pitch + 8 * pc], hq);
+    st16(&sH[(32 + prow) * kA2Pitch + 8 * pc], hk);
+    __syncthreads();
+    if (blk + stride < a.blocks) load_rows(blk + stride);   // lands during step 2
+    // ---- step 2: this wave's 32 columns of both sides ----
     const int64_t row = (int64_t)blk * 32 + li;
     const bool valid = row < a.rows;
     const int64_t rr = valid ? row : a.rows - 1;
     const int64_t at = rr % a.A, smp = rr / a.A;
-    u32x4 x[8];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) x[kk] = ld16(a.x + rr * 128 + 16 * kk + 8 * half);
-    float sum = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
-    sum += __shfl_xor(sum, 32);
-    const float mean = sum * (1.0f / 128);
-    float sq = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
-        sq += d0 * d0 + d1 * d1;
-      }
-    sq += __shfl_xor(sq, 32);
-    const float rstd = rsqrtf(sq * (1.0f / 128) + 1e-5f);
-#pragma unroll 1
     for (int side = 0; side < 2; ++side) {
-      const uint16_t* sc = (side ? a.k_scale : a.q_scale) + at * a.prs + 8 * half;
-      const uint16_t* sh = (side ? a.k_shift : a.q_shift) + at * a.prs + 8 * half;
-      bf16x8 h[8];
+      f32x16 acc;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const u32x4 s4 = ld16(sc + 16 * kk), h4 = ld16(sh + 16 * kk);
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd * bflo(s4[e]) + bflo(h4[e]),
-                                   (bfhi(x[kk][e]) - mean) * rstd * bfhi(s4[e]) + bfhi(h4[e]));
-          h[kk][2 * e] = v[0];
-          h[kk][2 * e + 1] = v[1];
-        }
+      for (int kk = 0; kk < 8; ++kk)
+        acc = mfma32(as_bf16x8(ld16(&sW[(side * 256 + 32 * wave + li) * kA2Pitch + 16 * kk + 8 * half])),
+                     as_bf16x8(ld16(&sH[(32 * side + li) * kA2Pitch + 16 * kk + 8 * half])), acc);
+      // lane half h' holds columns 8g + 4h' .. +3; after one exchange with the partner lane
+      // (li, 1 - h') half 0 holds columns 0..15 and half 1 columns 16..31: 32 contiguous bytes
+      uint32_t pk[4][2];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = 32 * wave + 8 * g + 4 * half;
+        const f32x4 b4 = side == 0 ? *reinterpret_cast<const f32x4*>(&sB[c0]) : f32x4{0.f, 0.f, 0.f, 0.f};
+        pk[g][0] = pack_bf2(acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1]);
+        pk[g][1] = pack_bf2(acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
       }
-      uint16_t* dst = side ? a.ykv + (smp * (a.A + 1) + at) * 256 : a.yq + rr * 256;
+      // (selects by half as bitwise blends of values: a select between array elements became a
+      // run-time index into a stack copy of the array)
+      const uint32_t hm = half ? ~0u : 0u;
+      auto blend = [&](uint32_t if1, uint32_t if0) __attribute__((always_inline)) { return (if1 & hm) | (if0 & ~hm); };
+      uint32_t rx[2][2];
 #pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        f32x16 acc;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-          acc = mfma32(as_bf16x8(ld16(&sW[(side * 256 + 32 * cb + li) * kA2Pitch + 16 * kk + 8 * half])), h[kk], acc);
-        // lane half h' holds columns 8g + 4h' .. +3; after one exchange with the partner lane
-        // (li, 1 - h') half 0 holds columns 0..15 and half 1 columns 16..31: 32 contiguous bytes
-        uint32_t pk[4][2];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c0 = 32 * cb + 8 * g + 4 * half;
-          const f32x4 b4 = side == 0 ? *reinterpret_cast<const f32x4*>(&sB[c0]) : f32x4{0.f, 0.f, 0.f, 0.f};
-          pk[g][0] = pack_bf2(acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1]);
-          pk[g][1] = pack_bf2(acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
-        }
-        uint32_t rx[2][2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(half ? pk[j][w] : pk[2 + j][w], 32);
-        if (valid) {
-          // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
-          // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
-          const u32x4 lo = half ? u32x4{rx[0][0], rx[0][1], pk[2][0], pk[2][1]} : u32x4{pk[0][0], pk[0][1], rx[0][0], rx[0][1]};
-          const u32x4 hi = half ? u32x4{rx[1][0], rx[1][1], pk[3][0], pk[3][1]} : u32x4{pk[1][0], pk[1][1], rx[1][0], rx[1][1]};
-          uint16_t* q = dst + 32 * cb + 16 * half;
-          st16(q, lo);
-          st16(q + 8, hi);
-        }
+        for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(blend(pk[j][w], pk[2 + j][w]), 32);
+      if (valid) {
+        // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
+        // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
+        const u32x4 lo = {blend(rx[0][0], pk[0][0]), blend(rx[0][1], pk[0][1]), blend(pk[2][0], rx[0][0]), blend(pk[2][1], rx[0][1])};
+        const u32x4 hi = {blend(rx[1][0], pk[1][0]), blend(rx[1][1], pk[1][1]), blend(pk[3][0], rx[1][0]), blend(pk[3][1], rx[1][1])};
+        uint16_t* dst = side ? a.ykv + (smp * (a.A + 1) + at) * 256 : a.yq + rr * 256;
+        uint16_t* q = dst + 32 * wave + 16 * half;
+        st16(q, lo);
+        st16(q + 8, hi);
       }
     }
   }
@@ -479,7 +493,7 @@ int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t s
     f.wqg = static_cast<const uint16_t*>(a->w_qg); f.wkv = static_cast<const uint16_t*>(a->w_kv); f.bqg = a->b_qg;
     f.yq = static_cast<uint16_t*>(yq); f.ykv = static_cast<uint16_t*>(ykv);
     const int resident = sf_resident_workgroups(reinterpret_cast<const void*>(adaln2_proj_kernel), 512);
-    const int grid = std::max(1, std::min(resident, (f.blocks + 7) / 8));
+    const int grid = std::max(1, std::min(resident, f.blocks));
     hipLaunchKernelGGL(adaln2_proj_kernel, dim3(grid), dim3(512), 0, st, f);
     if ((rc = sf_check_launch("adaln2_proj_kernel"))) return rc;
   } else {
