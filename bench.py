@@ -65,6 +65,22 @@ def _events_time(fn, iters: int, stream) -> float:
   return start.elapsed_time(end) / iters
 
 
+def _median_call_ms(fn, iters: int, stream) -> float:
+  """Median duration of single calls, each bracketed by its own pair of HIP events on `stream`
+  (the rule for the parity configurations' timings; `value` stays the mean over a block of calls,
+  as the step contract has it)."""
+  pairs = []
+  for _ in range(iters):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    fn()
+    e1.record(stream)
+    pairs.append((e0, e1))
+  torch.cuda.synchronize()
+  times = sorted(e0.elapsed_time(e1) for e0, e1 in pairs)
+  return times[len(times) // 2]
+
+
 def stage_ms(z, seq, mod, iters: int) -> dict:
   """Average duration of each triangle stage (projection, attention core, output projection),
   launched through sf_hip_triangle_stage_fwd on the current stream and timed with HIP events
@@ -266,9 +282,10 @@ def _config_builders(side_timings: bool = True) -> dict:
         "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
         "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
 
-  def dense(n):  # triangle attention, starting node, all-ones mask (the block-sparse lines' baseline)
+  def dense(n, padded=False):  # triangle attention, starting node; all-ones mask (the block-sparse
+    # lines' baseline), or the last n//10 tokens padded
     def build():
-      mod, z, seq = W.make_triangle(n, seed=9)
+      mod, z, seq = W.make_triangle(n, seed=9, padded=padded)
       mod = mod.to(dev); backends.prepare(mod)
       z, seq = z.to(dev), seq.to(dev)
       f = module_flop(n)
@@ -300,6 +317,7 @@ def _config_builders(side_timings: bool = True) -> dict:
     return build
 
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
+          "triangle_n768_padded": dense(768, padded=True),
           "triangle_ibs_n768": ibs(768), "triangle_n1536_start": dense(1536), "triangle_ibs_n1536": ibs(1536),
           "single_n768": c3b, "diffusion_5x1024_block": c4,
           "diffusion_5x1024_24_blocks": c4_stack, "diffusion_transition_5x1024": c4_transition,
@@ -439,6 +457,7 @@ def main():
   torch.cuda.synchronize()
   ms = _events_time(lambda: mod(z, seq), args.steps, stream)
   torch.cuda.synchronize()
+  median_ms = _median_call_ms(lambda: mod(z, seq), max(args.steps, 20), stream)
   stages = stage_ms(z, seq, mod, max(args.steps, 10))
   core_ms = stages["attend"]
   flop = module_flop()
@@ -467,6 +486,7 @@ def main():
       "warmup": args.warmup,
       "clock_warmup": {"calls": extra, "min_seconds": CLOCK_WARMUP_S},
       "ms_per_step": round(ms, 4),
+      "ms_per_call_median": round(median_ms, 4),
       "higher_is_better": False,
       "scaling": "weak",
       "vs_baseline": None,

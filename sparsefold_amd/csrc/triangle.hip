@@ -869,8 +869,9 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
   // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
   if (a.seq[r] == 0) {
-    // sum over the keys: thread (part, head, dim), part p of the 16-key chunks; four loads in
-    // flight per thread (H * 32 = 128 on this path)
+    // sum over the keys: thread (part, head, dim), part p of the 16-key chunks; sixteen loads in
+    // flight per thread (H * 32 = 128 on this path).  With four, each masked row took a dozen
+    // dependent round trips: 40 us of tail for the 76 padded rows of N = 768.
     __shared__ float part[2][4 * 32];
     __shared__ float mean[4 * 32];
     {
@@ -878,6 +879,15 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
       const int nc = NP / 16, c0 = pp * (nc / 2), c1 = pp ? nc : nc / 2;
       float s0 = 0.f, s1 = 0.f;
       int c16 = c0;
+      for (; c16 + 8 <= c1; c16 += 8) {
+        u32x4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = ld16(a.vt + vl_off(r, h, H, NP, c16 + (u >> 1), u & 1, d));
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
+      }
       for (; c16 + 2 <= c1; c16 += 2) {
         u32x4 v[4];
 #pragma unroll
