@@ -23,8 +23,9 @@
 //                        so nothing is transposed in memory (blocks.py:345-346, :362-363).
 //   2. tri_attn_kernel   one workgroup per (4 rows, head, 256 queries); K / V^T tiles of 64
 //                        keys for the 4 rows double-buffered in LDS; each wave keeps the
-//                        softmax sums of its 32 queries for all 4 rows and feeds the bias tile
-//                        -- identical for every row -- as the accumulator input of the S^T MFMA;
+//                        softmax sums of its 32 queries for all 4 rows and feeds its bias tile
+//                        -- identical for every row, loaded a tile ahead into its registers --
+//                        as the accumulator input of the S^T MFMA;
 //                        output written at its pair position, rows with an out-of-range
 //                        weight sum flagged.
 //      tri_fixup_kernel  rows whose token is masked attend uniformly to every key (the
@@ -485,28 +486,25 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 // global_load_lds_dwordx4 (lane L -> bytes 16L..16L+15):
 //   K    [row rr][key block 2][k-chunk 2][lane half 2][key 32]   copied as stored     16 KB
 //   V^T  [row rr][16-key chunk 4][lane half 2][dim 32]          copied as stored     16 KB
-//   bias [query/8][key-piece 0..7][query%8]                                          32 KB
 // The operand reads of consecutive lanes are consecutive slots (bank-conflict free), and
-// every read of a lane is one per-lane base plus a compile-time offset.
+// every read of a lane is one per-lane base plus a compile-time offset.  The bias tile is not
+// staged here: each wave's 32 query rows of it are its own (no other wave reads them), so every
+// wave loads them a tile ahead straight into registers, which takes them off the LDS (a DMA
+// write and a read per byte) and out of the barrier's wait.
 struct TileLayout {
   static constexpr int kKBytes = kTR * kKT * 32 * 2;
   static constexpr int kVBytes = kTR * kKT * 32 * 2;
-  static constexpr int kBBytes = kAW * 32 * kKT * 2;
   static constexpr int kKVBytes = kKBytes + kVBytes;
-  static constexpr int kBytes = kKVBytes + kBBytes;
-  // K / V^T of both buffers first, then the two bias buffers: every operand read is one of
-  // two per-lane bases plus an offset that fits the 16-bit LDS immediate
-  static constexpr int kBiasBase = 2 * kKVBytes;
-  __device__ static constexpr int chunk_offset(int buf, int c) {
-    return c * 1024 < kKVBytes ? buf * kKVBytes + c * 1024 : kBiasBase + buf * kBBytes + c * 1024 - kKVBytes;
-  }
+  static constexpr int kBytes = kKVBytes;
+  __device__ static constexpr int chunk_offset(int buf, int c) { return buf * kKVBytes + c * 1024; }
   static constexpr int kChunks = kBytes / 1024;
   static constexpr int kChunksPerWave = kChunks / kAW;
   static_assert(kChunks % kAW == 0, "tile chunks must split evenly over the waves");
+  static_assert(kChunksPerWave == 4 && kAW == 2 * kTR, "waves 0-3 copy K rows, waves 4-7 V^T rows, 4 chunks each");
 };
 
 // Task = (head, row group of 4 rows, block of 256 queries).  The grid is persistent: at most
-// one workgroup per CU (the double-buffered LDS tiles leave room for no second one), each walking
+// one workgroup per CU (its 8 waves use 2 waves' worth of registers on every SIMD), each walking
 // its tasks with the tile pipeline running straight through task boundaries -- the last tile of a
 // task loads the first tile of the next one, and the next task's Q operands are loaded while the
 // last tile computes.  With one short-lived workgroup per task the prologue (Q and first-tile
@@ -540,38 +538,21 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
     h = t / (QB * RG);
   };
 
-  // ---- tile loader: this wave's 1 KB chunks of a tile, straight into LDS.  K and V^T chunks
-  //      are 1 KB of contiguous memory; bias chunks are 8 query rows of 128 bytes.  Every chunk
-  //      address is a wave-uniform base plus one of two per-lane offsets. ----
+  // ---- tile loader: this wave's 1 KB chunks of a tile, straight into LDS.  Wave w < 4 copies
+  //      the K tile of row r0 + w, wave w >= 4 the V^T tile of row r0 + w - 4: four 1 KB quarters
+  //      of 4 KB of contiguous memory. ----
   const int64_t rstride = (int64_t)H * NP * 32;             // row stride of the Q/K/G and V^T layouts
-  const uint32_t lane16 = (uint32_t)lane * 16u;             // byte offsets: K / V^T chunks ...
-  const uint32_t roffb = (uint32_t)((lane & 7) * NP + 8 * (lane >> 3)) * 2u;   // ... bias: row L%8, piece L/8
-  // Waves 0-1 fetch K (rows 2w, 2w+1), waves 2-3 V^T (rows 2(w-2), 2(w-2)+1), waves 4-7 the bias
-  // rows of queries 64(w-4) .. +63 of the block; chunk u of a wave is then a uniform base plus
-  // a compile-time multiple of the wave's two strides.
-  const int64_t wrow = wave < 4 ? rstride * 2 : 0;          // bytes between chunks 4 apart (K / V^T rows)
-  const int wq = wave < 4 ? 1024 : 16 * NP;                 // bytes per quarter (K / V^T) or 8 bias rows
-  const int wj = wave < 4 ? 64 : 2;                         // bytes per key
-  const uint32_t woff = wave < 4 ? lane16 : roffb;
-  auto loader_src = [&](int r0, int h, int qb, int& wlim) __attribute__((always_inline)) -> const char* {
-    if (wave < 4) {
-      wlim = 0;
-      return wave < 2 ? (const char*)(a.k + ql_off(r0 + 2 * wave, h, H, NP, 0, 0, 0))
-                      : (const char*)(a.vt + vl_off(r0 + 2 * (wave - 2), h, H, NP, 0, 0, 0));
-    }
-    const int q0 = qb * 32 * kAW + (wave - 4) * 64;
-    wlim = NP - 8 - q0;                  // query rows past NP - 8 are clamped (idle waves only)
-    return (const char*)(a.bias + ((int64_t)h * NP + q0) * NP);
+  const uint32_t lane16 = (uint32_t)lane * 16u;
+  auto loader_src = [&](int r0, int h) __attribute__((always_inline)) -> const char* {
+    return wave < 4 ? (const char*)(a.k + ql_off(r0 + wave, h, H, NP, 0, 0, 0))
+                    : (const char*)(a.vt + vl_off(r0 + wave - 4, h, H, NP, 0, 0, 0));
   };
-  auto load_tile = [&](const char* wsrc, int wlim, int j0, int buf) __attribute__((always_inline)) {
-    const char* src = wsrc + (int64_t)j0 * wj;
+  auto load_tile = [&](const char* wsrc, int j0, int buf) __attribute__((always_inline)) {
+    const char* src = wsrc + (int64_t)j0 * 64;
 #pragma unroll
-    for (int u = 0; u < TL::kChunksPerWave; ++u) {
-      const char* cs = wave < 4 ? src + (u >> 2) * wrow + (u & 3) * wq
-                                : src + (int64_t)min(8 * u, wlim) * (2 * NP);
-      __builtin_amdgcn_global_load_lds(cs + woff, (lds_u32*)(smem + TL::chunk_offset(buf, wave * TL::kChunksPerWave + u)),
-                                       16, 0, 0);
-    }
+    for (int u = 0; u < TL::kChunksPerWave; ++u)
+      __builtin_amdgcn_global_load_lds(src + u * 1024 + lane16,
+                                       (lds_u32*)(smem + TL::chunk_offset(buf, wave * TL::kChunksPerWave + u)), 16, 0, 0);
   };
   auto kslot = [&](int buf, int rr, int kb, int kk) __attribute__((always_inline)) -> const uint8_t* {
     return smem + buf * TL::kKVBytes + rr * 4096 + (kb * 4 + kk * 2 + half) * 512 + li * 16;
@@ -579,8 +560,20 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   auto vslot = [&](int buf, int rr, int c2) __attribute__((always_inline)) -> const uint8_t* {
     return smem + buf * TL::kKVBytes + TL::kKBytes + rr * 4096 + (c2 * 2 + half) * 512 + li * 16;
   };
-  auto bslot = [&](int buf, int row, int pc) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + TL::kBiasBase + buf * TL::kBBytes + (row >> 3) * 1024 + pc * 128 + (row & 7) * 16;
+  // ---- this lane's bias of a tile, straight into registers: the 128 bytes of its query row are
+  //      8 pieces of 8 keys, and lane half h' holds pieces 4kb + 2h' and 4kb + 2h' + 1 of 32-key
+  //      half kb (the keys its S^T registers hold).  Rows past NP - 1 are clamped (idle waves). ----
+  u32x4 breg[4];
+  auto bias_src = [&](int h, int qb) __attribute__((always_inline)) -> const char* {
+    const int q = min(qb * 32 * kAW + 32 * wave + li, NP - 1);
+    return (const char*)(a.bias + ((int64_t)h * NP + q) * NP) + 32 * half;
+  };
+  auto load_bias_regs = [&](const char* bsrc, int j0) __attribute__((always_inline)) {
+    const char* p = bsrc + (int64_t)j0 * 2;
+    breg[0] = ld16(p);
+    breg[1] = ld16(p + 16);
+    breg[2] = ld16(p + 64);
+    breg[3] = ld16(p + 80);
   };
 
   // Q operands (B of S^T = K Q^T) of a task's 4 rows.  Rows past N hold zeros and are never stored.
@@ -610,14 +603,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) sel[e] = (__bf16)((((lane & 15) < 8) == (((lane >> 4) & 1) == 0)) ? 1.0f : 0.0f);
 
-  // bias tile of this wave's 32 queries -> fp32 accumulator seed in S^T register order
+  // bias tile of this wave's 32 queries (in breg) -> fp32 accumulator seed in S^T register order
   f32x16 bseed[2];
-  auto load_bias = [&](int buf) __attribute__((always_inline)) {
-    const int row = 32 * wave + li;
+  auto load_bias = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const u32x4 b0 = ld16(bslot(buf, row, 4 * kb + 2 * half));
-      const u32x4 b1 = ld16(bslot(buf, row, 4 * kb + 2 * half + 1));
+      const u32x4 b0 = breg[2 * kb];
+      const u32x4 b1 = breg[2 * kb + 1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         bseed[kb][2 * e] = bflo(b0[e]);
@@ -736,10 +728,12 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   const int ntiles = NP / kKT;
   const int q32 = lane & 31;
   const int src_lane = q32 < 16 ? q32 : q32 + 16;   // a lane whose row-sum output holds query q32
-  int r0, h, qb, wlim;
+  int r0, h, qb;
   decode(task, r0, h, qb);
-  const char* wsrc = loader_src(r0, h, qb, wlim);
-  load_tile(wsrc, wlim, 0, 0);
+  const char* wsrc = loader_src(r0, h);
+  const char* bsrc = bias_src(h, qb);
+  load_tile(wsrc, 0, 0);
+  load_bias_regs(bsrc, 0);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
   load_q(r0, h, qb, qb8);
@@ -747,11 +741,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   for (;;) {
     const int next = task + G8;
     const bool has_next = next < per;                      // uniform
-    int nr0 = 0, nh = 0, nqb = 0, nwlim = 0;
-    const char* nsrc = nullptr;
+    int nr0 = 0, nh = 0, nqb = 0;
+    const char* nsrc = wsrc;
+    const char* nbsrc = bsrc;
     if (has_next) {
       decode(next, nr0, nh, nqb);
-      nsrc = loader_src(nr0, nh, nqb, nwlim);
+      nsrc = loader_src(nr0, nh);
+      nbsrc = bias_src(nh, nqb);
     }
     const int i = qb * 32 * kAW + 32 * wave + li;          // this lane's query
     const bool active = qb * 32 * kAW + 32 * wave < NP;    // uniform: the wave has queries below NP
@@ -763,8 +759,11 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) lsum[rr][e] = 0.f;
     }
-    // One tile: the loads of the tile after it (or of the next task's first tile) are issued
-    // first and land while it computes.  The first and last tiles of a task are separate code
+    // One tile: its bias registers are turned into the S^T seed, then the loads of the tile after
+    // it (or of the next task's first tile) are issued -- K/V^T chunks into the other LDS buffer,
+    // then the bias into the registers just freed -- and land while it computes.  At its end
+    // every wave waits for its chunks and the barrier makes everybody's visible; the bias loads,
+    // the youngest, stay in flight.  The first and last tiles of a task are separate code
     // instances: the last one loads the next task's Q operands (into the registers of rows it has
     // finished with), the first one waits for them -- with a wait the compiler sees, so that it
     // puts no conservative wait of its own in front of the first S^T MFMA, where it would also
@@ -780,31 +779,36 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
                                                              // aliases the loads into the other
       if (FIRST) {
         if (!qready) load_q(r0, h, qb, qb8);
-        __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0): this task's Q operands
+        __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0): this task's Q operands and bias
       }
-      // the tile after this one; after the last tile, the next task's first tile (the last task
-      // loads its own first tile again: unused, but the code stays branch-free)
-      if (!LAST) load_tile(wsrc, wlim, (tt + 1) * kKT, buf ^ 1);
-      else load_tile(has_next ? nsrc : wsrc, has_next ? nwlim : wlim, 0, buf ^ 1);
-      // the Q reloads below must stay younger than these tile loads (the vmcnt(8) wait at the
-      // end of the last tile counts on it): no memory operation crosses this point
-      if (LAST) asm volatile("" ::: "memory");
-      if (active) {                                          // (idle waves need no Q operands)
+      if (active) {                                          // (idle waves need no Q operands or bias)
         if constexpr (SP) {
           tile_weights(tt);
           bool any = false;
 #pragma unroll
           for (int u = 0; u < 2 * kTR; ++u) any |= wu[u] != 0.f;
-          if (any) load_bias(buf);
+          if (any) load_bias();
         } else {
-          load_bias(buf);
+          load_bias();
         }
-        units(buf, lastc, nq);
       }
-      // tile loads landed (the 8 Q loads of the last tile, the youngest, may stay in flight;
-      // idle waves issued none and wait for everything)
-      static_assert(2 * kTR == 8, "the partial wait below leaves exactly the 2 * kTR Q reloads in flight");
-      if (LAST && active) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+      // the seed is read out of breg before the loads below overwrite it
+      __builtin_amdgcn_sched_barrier(0);
+      // the tile after this one; after the last tile, the next task's first tile (the last task
+      // loads its own first tile again: unused, but the code stays branch-free)
+      if (!LAST) load_tile(wsrc, (tt + 1) * kKT, buf ^ 1);
+      else load_tile(nsrc, 0, buf ^ 1);
+      if (active) load_bias_regs(LAST ? nbsrc : bsrc, LAST ? 0 : (tt + 1) * kKT);
+      // the Q reloads below must stay younger than these loads (the partial waits at the end of
+      // the tile count on it): no memory operation crosses this point
+      asm volatile("" ::: "memory");
+      if (active) units(buf, lastc, nq);
+      // this wave's chunks landed: the 4 bias loads and, on the last tile, the 2 * kTR Q reloads
+      // after them, the youngest, may stay in flight (idle waves issued neither and wait for all)
+      static_assert(2 * kTR == 8 && TL::kChunksPerWave == 4,
+                    "the partial waits below leave exactly 4 bias loads (+ 2 * kTR Q reloads) in flight");
+      if (LAST && active) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)" ::: "memory");
+      else if (active) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
@@ -843,7 +847,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       }
     }
     if (!has_next) break;
-    task = next; r0 = nr0; h = nh; qb = nqb; wsrc = nsrc; wlim = nwlim;
+    task = next; r0 = nr0; h = nh; qb = nqb; wsrc = nsrc; bsrc = nbsrc;
   }
   __builtin_amdgcn_s_waitcnt(0);                           // the last task's Q reloads
 }
