@@ -16,7 +16,8 @@
 //                                   scale * log2(e), so logits land in log2 units
 //                          V^T      per (row r, head h), 16-key chunks of
 //                                   [lane half 2][dim 32][8 keys in PV slot order]
-//                          bias     [h][i][j''] bias * log2(e), bf16, untransposed orientation
+//                          bias     per (h, 32 queries, 64 keys) 4 KB blocks in the attention
+//                                   loads' order (bias_off), bias * log2(e), bf16, untransposed orientation
 //                                   (blocks.py:329), masked keys = SF_MASKED_LOGIT, keys past
 //                                   N = -inf, keys in S^T register order
 //                        For the ending node the workgroup walks z's column instead of its row,
@@ -50,6 +51,22 @@ int round_np(int n) { return (n + 127) & ~127; }
 __host__ __device__ inline int bias_pos64(int j) {
   const int j32 = j & 31;
   return (j & 32) + 16 * ((j32 >> 2) & 1) + 4 * (j32 >> 3) + (j32 & 3);
+}
+// Bias planes of the head-dim-32 path, in the order the attention kernel loads them: per (head h,
+// tile of 32 queries, tile of 64 keys) one 4 KB block [piece k 4][lane 64][8 keys], where lane
+// 32 h' + i%32 holds, as piece k, stored piece 4(k/2) + 2h' + k%2 (8 keys) of query i's 64 keys
+// in stored (bias_pos64) order -- the keys its S^T registers hold.  Each of a wave's four
+// 16-byte loads then reads 1 KB of contiguous memory: with a query row per lane (32 rows, each
+// read in 16-byte pieces) the same loads ran at a third of the L2 bandwidth.
+// js = stored key position in the row: (j & ~63) + bias_pos64(j & 63).
+__host__ __device__ inline int64_t bias_off_stored(int h, int i, int js, int NP) {
+  const int jp = js & 63, pc = jp >> 3;
+  const int k = 2 * (pc >> 2) + (pc & 1), hf = (pc >> 1) & 1;
+  return ((((int64_t)h * (NP >> 5) + (i >> 5)) * (NP >> 6) + (js >> 6)) << 11)
+         + ((k * 64 + 32 * hf + (i & 31)) << 3) + (jp & 7);
+}
+__host__ __device__ inline int64_t bias_off(int h, int i, int j, int NP) {
+  return bias_off_stored(h, i, (j & ~63) + bias_pos64(j & 63), NP);
 }
 // Q / K / G of (row r, head h): position p, k-chunk kk, lane half hf.  The 8 values at the
 // returned offset are dims 16*kk + 8*(t/4) + 4*hf + t%4 for t = 0..7 -- what lane (p%32, hf)
@@ -279,13 +296,11 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
             else if (a.seq[zb] == 0) b = SF_MASKED_LOGIT;
             v[e] = b;
           }
-          if (!a.transpose) {   // za = r: four consecutive keys of one bias row
-            const int64_t base = ((int64_t)li * NP + r) * NP + (pb & ~63) + bias_pos64(pb & 63);
-            *reinterpret_cast<u32x2*>(a.bias + base) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+          if (!a.transpose) {   // za = r: four consecutive keys of one bias row (stored together)
+            *reinterpret_cast<u32x2*>(a.bias + bias_off(li, r, pb, NP)) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
           } else {              // zb = r: one key of four bias rows
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              a.bias[((int64_t)li * NP + pb + e) * NP + (r & ~63) + bias_pos64(r & 63)] = f2bf(v[e]);
+            for (int e = 0; e < 4; ++e) a.bias[bias_off(li, pb + e, r, NP)] = f2bf(v[e]);
           }
         }
       }
@@ -560,20 +575,18 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   auto vslot = [&](int buf, int rr, int c2) __attribute__((always_inline)) -> const uint8_t* {
     return smem + buf * TL::kKVBytes + TL::kKBytes + rr * 4096 + (c2 * 2 + half) * 512 + li * 16;
   };
-  // ---- this lane's bias of a tile, straight into registers: the 128 bytes of its query row are
-  //      8 pieces of 8 keys, and lane half h' holds pieces 4kb + 2h' and 4kb + 2h' + 1 of 32-key
-  //      half kb (the keys its S^T registers hold).  Rows past NP - 1 are clamped (idle waves). ----
+  // ---- this lane's bias of a tile, straight into registers: piece k of the wave's 4 KB block
+  //      (bias_off_stored) is pieces 4(k/2) + 2 half + k%2 of its query's 64 keys, 8 keys each:
+  //      the keys its S^T registers hold.  Query tiles past the last are clamped (idle waves). ----
   u32x4 breg[4];
   auto bias_src = [&](int h, int qb) __attribute__((always_inline)) -> const char* {
-    const int q = min(qb * 32 * kAW + 32 * wave + li, NP - 1);
-    return (const char*)(a.bias + ((int64_t)h * NP + q) * NP) + 32 * half;
+    const int qt = min(qb * kAW + wave, (NP >> 5) - 1);
+    return (const char*)(a.bias + (((int64_t)h * (NP >> 5) + qt) * (NP >> 6) << 11)) + lane16;
   };
   auto load_bias_regs = [&](const char* bsrc, int j0) __attribute__((always_inline)) {
-    const char* p = bsrc + (int64_t)j0 * 2;
-    breg[0] = ld16(p);
-    breg[1] = ld16(p + 16);
-    breg[2] = ld16(p + 64);
-    breg[3] = ld16(p + 80);
+    const char* p = bsrc + (int64_t)j0 * 64;             // 4 KB per 64-key tile
+#pragma unroll
+    for (int k = 0; k < 4; ++k) breg[k] = ld16(p + 1024 * k);
   };
 
   // Q operands (B of S^T = K Q^T) of a task's 4 rows.  Rows past N hold zeros and are never stored.
@@ -942,9 +955,8 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) { q[8 * c + 2 * e] = bflo(v[e]); q[8 * c + 2 * e + 1] = bfhi(v[e]); }
       }
-      const uint16_t* brow = a.bias + ((int64_t)h * NP + i) * NP;
       auto logit = [&](int j) {
-        float s = bf2f(brow[(j & ~63) + bias_pos64(j & 63)]);
+        float s = bf2f(a.bias[bias_off(h, i, j, NP)]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const u32x4 v = ld16(a.k + ql_off(r, h, H, NP, j, c >> 1, c & 1));
@@ -1042,7 +1054,7 @@ __global__ __launch_bounds__(256) void tri_ibs_bias_mean_kernel(const IbsArgs a)
   const int jp = (int)(idx % a.NP), t = (int)((idx / a.NP) % a.T), h = (int)(idx / ((int64_t)a.NP * a.T));
   const int i0 = 32 * t, i1 = min(a.N, i0 + 32);
   float sum = 0.f;
-  for (int i = i0; i < i1; ++i) sum += bf2f(a.bias[((int64_t)h * a.NP + i) * a.NP + jp]);
+  for (int i = i0; i < i1; ++i) sum += bf2f(a.bias[bias_off_stored(h, i, jp, a.NP)]);
   a.bmean[idx] = sum / (float)(i1 - i0);
 }
 
@@ -1249,10 +1261,10 @@ __global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
     for (int kk = 0; kk < 2; ++kk) kr[kk] = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, 32 * b + li, kk, half)));
 #pragma unroll
     for (int j = 0; j < 2; ++j) vr[j] = as_bf16x8(ld16(a.vt + vl_off(r, h, H, NP, 2 * b + j, half, li)));
-    // bias of query i for keys 8(e/4) + 4 half + e%4 of the block: stored contiguously at
-    // 32 (b & 1) + 16 half + e within its 64-key tile
-    const uint16_t* bp = a.bias + ((int64_t)h * NP + i) * NP + 64 * (b >> 1) + 32 * (b & 1) + 16 * half;
-    const u32x4 b0 = ld16(bp), b1 = ld16(bp + 8);
+    // bias of query i for keys 8(e/4) + 4 half + e%4 of the block: stored positions
+    // 32 (b & 1) + 16 half + e of its 64-key tile, two pieces of 8
+    const int js = 64 * (b >> 1) + 32 * (b & 1) + 16 * half;
+    const u32x4 b0 = ld16(a.bias + bias_off_stored(h, i, js, NP)), b1 = ld16(a.bias + bias_off_stored(h, i, js + 8, NP));
     f32x16 sd;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

@@ -188,7 +188,9 @@ def _bias_pos64(j):
 def _decode_operands(ws, N, H):
   """Q, K [r][h][NP][32] and bias [h][NP][NP] (keys in natural order) from the workspace of the
   projection stage: Q / K pieces of 8 dims 16 kk + 8 (t / 4) + 4 hf + t % 4 per (32-position
-  block, kk, hf, position), bias planes with keys permuted within 64-key tiles."""
+  block, kk, hf, position); bias as 4 KB blocks per (head, 32 queries, 64 keys) of
+  [k 4][hf 2][query 32][8 keys], piece k of lane half hf holding stored piece
+  4 (k / 2) + 2 hf + k % 2, with keys permuted within 64-key tiles."""
   NP = _round_np(N)
   E = NP * NP * H * 32
   rup = lambda x: (x + 255) & ~255
@@ -206,7 +208,8 @@ def _decode_operands(ws, N, H):
   q = layout(0)
   k = layout(rup(E * 2))
   bias_off = 3 * rup(E * 2)
-  planes = bf(bias_off, H * NP * NP).reshape(H, NP, NP)
+  blocks = bf(bias_off, H * NP * NP).reshape(H, NP // 32, NP // 64, 2, 2, 2, 32, 8)  # h qt kt k2 k1 hf i e
+  planes = blocks.permute(0, 1, 6, 2, 3, 5, 4, 7).reshape(H, NP, NP)                # h (qt i) (kt k2 hf k1 e)
   j = torch.arange(NP)
   stored = (j & ~63) + torch.tensor([_bias_pos64(int(x) & 63) for x in j])
   return q, k, planes[:, :, stored]
