@@ -373,23 +373,28 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
   // (diffusion 5 x 1024: 0.155 -> 0.140 ms per block)
   uint32_t mbyte = 1;
   uint8_t* bsm = smem + kKVRegion + wave * 4096;            // BL: this wave's bias buffer
-  // BL source rows: lane L copies row 8u + L%8 of the wave's 32 queries, piece L/8 (keys 8p .. 8p+7)
+  // BL source rows: lane L copies row 8u + L/8 of the wave's 32 queries, piece (L%8) ^ (L/8)
+  // (keys 8p .. 8p+7): the 8 lanes of a row read its 128 bytes, so every 4 consecutive lanes read
+  // 64 contiguous bytes (with a query row per lane, consecutive lanes on different rows, the same
+  // copies ran at a third of the L2 bandwidth), and the XOR spreads a column of pieces over the
+  // LDS banks for the reads below.
+  const int bpiece = (lane & 7) ^ (lane >> 3);
   const uint16_t* brow0 = nullptr;
   int64_t brs8 = 0;                                          // elements between rows 8 apart
   if (BL) {
     const uint16_t* bh = (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] + (int64_t)h * a.bias_s[2];
-    brow0 = bh + (int64_t)min(qblk * 32 + (lane & 7), Q - 1) * a.bias_s[3] + 8 * (lane >> 3);
+    brow0 = bh + (int64_t)min(qblk * 32 + (lane >> 3), Q - 1) * a.bias_s[3] + 8 * bpiece;
     brs8 = 8 * a.bias_s[3];
   }
   const bool brows_clamped = qblk * 32 + 32 > Q;            // uniform: the last query block
   auto load_bias_lds = [&](int j0) __attribute__((always_inline)) {
-    const int jc = min(j0, K - 8 - 8 * (lane >> 3)) - j0;   // pieces past K re-read the last one
+    const int jc = min(j0, K - 8 - 8 * bpiece) - j0;         // pieces past K re-read the last one
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const uint16_t* src = brow0 + u * brs8;
       if (brows_clamped) {
         const uint16_t* bh = (const uint16_t*)a.bias + b0 * a.bias_s[0] + b1 * a.bias_s[1] + (int64_t)h * a.bias_s[2];
-        src = bh + (int64_t)min(qblk * 32 + 8 * u + (lane & 7), Q - 1) * a.bias_s[3] + 8 * (lane >> 3);
+        src = bh + (int64_t)min(qblk * 32 + 8 * u + (lane >> 3), Q - 1) * a.bias_s[3] + 8 * bpiece;
       }
       __builtin_amdgcn_global_load_lds(src + j0 + jc, (lds_u32a*)(bsm + u * 1024), 16, 0, 0);
     }
@@ -447,8 +452,8 @@ __global__ __launch_bounds__(256) void attn2_kernel(const sf_attention_args a, c
     u32x2 bcur[8];
     if (BL) {                                                // keys 32(q/4) + 8(q%4) + 4half .. +3 = piece q
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        bcur[q] = *reinterpret_cast<const u32x2*>(bsm + (li >> 3) * 1024 + q * 128 + (li & 7) * 16 + half * 8);
+      for (int q = 0; q < 8; ++q)                            // row li: slot 8 (li%8) + (q ^ li%8) of chunk li/8
+        bcur[q] = *reinterpret_cast<const u32x2*>(bsm + (li >> 3) * 1024 + (li & 7) * 128 + (q ^ (li & 7)) * 16 + half * 8);
       // the buffer is refilled below: these reads complete first (the copies are ordinary loads
       // to the compiler, so the wait carries a memory clobber)
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
