@@ -490,6 +490,7 @@ struct TriAttnArgs {
 constexpr int kTR = 4;                // rows per workgroup
 constexpr int kKT = 64;               // keys per tile
 constexpr int kAW = 8;                // waves per attention workgroup (256 queries)
+constexpr int kPrioUnits = 4;         // units of a tile the younger wave of each SIMD runs at raised priority
 // Per-wave table of the block-sparse kernel: the weights of the selected key blocks of its query
 // tile for the task's 4 rows, [row][block] floats (0 = not selected), blocks < 128 (N <= 4096).
 constexpr int kIbsTabBlocks = 128;
@@ -658,7 +659,9 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   // SP: wu[u] = weight of unit u of the current tile (wave-uniform scalars), 0 = skipped
   float wu[2 * kTR];
   auto on = [&](int u) __attribute__((always_inline)) { return !SP || wu[u] != 0.f; };
-  auto units = [&](int buf, auto reloadc, const uint16_t* nq) __attribute__((always_inline)) {
+  // ISSUE(u), u < 4: the next tile's loads, one K/V^T chunk and one bias piece per unit (see the
+  // tile below).  PRIO: the wave's raised issue priority is dropped at unit kPrioUnits.
+  auto units = [&](int buf, auto reloadc, const uint16_t* nq, auto issue) __attribute__((always_inline)) {
     constexpr bool RELOAD = decltype(reloadc)::value;
     f32x16 sc, sn;
     bf16x8 kr[2], vr[2];
@@ -671,6 +674,11 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
     for (int u = 0; u < 2 * kTR; ++u) {
       const int rr = u >> 1;
+      if (u < TL::kChunksPerWave) {
+        issue(u);
+        asm volatile("" ::: "memory");   // keeps the loads in issue order (the tile's waits count them)
+      }
+      if (u == kPrioUnits && wave >= 4) __builtin_amdgcn_s_setprio(0);
       if (u + 1 < 2 * kTR && on(u + 1)) qk((u + 1) >> 1, (u + 1) & 1, kr, sn);
       if (u + 2 < 2 * kTR && on(u + 2)) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
       if (RELOAD && (u & 1) == 0) {
@@ -808,20 +816,40 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       // the seed is read out of breg before the loads below overwrite it
       __builtin_amdgcn_sched_barrier(0);
       // the tile after this one; after the last tile, the next task's first tile (the last task
-      // loads its own first tile again: unused, but the code stays branch-free)
-      if (!LAST) load_tile(wsrc, (tt + 1) * kKT, buf ^ 1);
-      else load_tile(nsrc, 0, buf ^ 1);
-      if (active) load_bias_regs(LAST ? nbsrc : bsrc, LAST ? 0 : (tt + 1) * kKT);
-      // the Q reloads below must stay younger than these loads (the partial waits at the end of
-      // the tile count on it): no memory operation crosses this point
+      // loads its own first tile again: unused, but the code stays branch-free).  A wave issues
+      // them one K/V^T chunk and one bias piece per unit over the first 4 units: all 64 issued at
+      // the tile start, the later ones waited for room in the CU's memory-instruction queue,
+      // holding their waves for ~1000 cycles per tile.
+      const char* tsrc = LAST ? nsrc : wsrc;
+      const char* tbsrc = LAST ? nbsrc : bsrc;
+      const int tj = LAST ? 0 : (tt + 1) * kKT;
+      auto issue = [&](int u) __attribute__((always_inline)) {
+        __builtin_amdgcn_global_load_lds(tsrc + (int64_t)tj * 64 + u * 1024 + lane16,
+                                         (lds_u32*)(smem + TL::chunk_offset(buf ^ 1, wave * TL::kChunksPerWave + u)), 16, 0, 0);
+        asm volatile("" ::: "memory");   // the chunk before the bias piece (left alone, the compiler
+                                         // put the bias load first, and the partial waits below
+                                         // then let the last chunk stay in flight past the barrier)
+        breg[u] = ld16(tbsrc + (int64_t)tj * 64 + 1024 * u);
+      };
+      if (!active) load_tile(tsrc, tj, buf ^ 1);
+      // On each SIMD the wave launched first (w < 4) has the older age, so it won every issue
+      // slot it competed for, finished its units ~25% sooner and then waited at the barrier
+      // while the younger one (w + 4) ran alone (19% of the kernel at the barrier).  The younger
+      // wave gets the higher priority for the first kPrioUnits units of a tile instead.
+      if (wave >= 4) __builtin_amdgcn_s_setprio(1);
+      // the loads of the tile must stay in issue order with the Q reloads (the partial waits at
+      // the end of the tile count on it): no memory operation crosses this point
       asm volatile("" ::: "memory");
-      if (active) units(buf, lastc, nq);
-      // this wave's chunks landed: the 4 bias loads and, on the last tile, the 2 * kTR Q reloads
-      // after them, the youngest, may stay in flight (idle waves issued neither and wait for all)
-      static_assert(2 * kTR == 8 && TL::kChunksPerWave == 4,
-                    "the partial waits below leave exactly 4 bias loads (+ 2 * kTR Q reloads) in flight");
-      if (LAST && active) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)" ::: "memory");
-      else if (active) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+      if (active) units(buf, lastc, nq, issue);
+      __builtin_amdgcn_s_setprio(0);
+      // this wave's chunks landed.  Issue order (unit: loads) is 0: D0 B0 [Q0 Q0], 1: D1 B1,
+      // 2: D2 B2 [Q1 Q1], 3: D3 B3, 4: [Q2 Q2], 6: [Q3 Q3] -- D chunk, B bias piece, [Q] the last
+      // tile's reloads of the next task's Q operands -- so the bias piece of unit 3 and the Q
+      // reloads after it may stay in flight (idle waves issued no bias or Q loads: they wait for all)
+      static_assert(2 * kTR == 8 && TL::kChunksPerWave == 4 && kPrioUnits >= 0,
+                    "the partial waits below count the loads of the unit schedule above");
+      if (LAST && active) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)" ::: "memory");
+      else if (active) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
