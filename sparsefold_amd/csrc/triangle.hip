@@ -68,6 +68,17 @@ __host__ __device__ inline int64_t bias_off_stored(int h, int i, int js, int NP)
 __host__ __device__ inline int64_t bias_off(int h, int i, int j, int NP) {
   return bias_off_stored(h, i, (j & ~63) + bias_pos64(j & 63), NP);
 }
+// Attention output o of (head h, attention row r, query i): per (h, r, block of 32 queries) one
+// 2 KB block [piece 4][query 32][8 dims], piece 2 hf + kk holding the 8 dims the attention
+// epilogue's lane half hf stores as its k-chunk kk (dims 16 kk + 8 (t/4) + 4 hf + t%4 of the
+// head, t = 0..7).  Each store
+// of the epilogue (a piece of 32 queries per lane half) and each load of the output stage (a
+// piece of 32 positions) then covers 512 contiguous bytes; with a query's 64 bytes contiguous,
+// consecutive lanes were 64 bytes apart.  Indexed by attention row and query, not by pair
+// position, so both nodes write whole blocks.
+__host__ __device__ inline int64_t o_off(int h, int r, int i, int hf, int kk, int N, int NP) {
+  return ((((int64_t)h * N + r) * (NP >> 5) + (i >> 5)) << 10) + ((((2 * hf + kk) << 5) + (i & 31)) << 3);
+}
 // Q / K / G of (row r, head h): position p, k-chunk kk, lane half hf.  The 8 values at the
 // returned offset are dims 16*kk + 8*(t/4) + 4*hf + t%4 for t = 0..7 -- what lane (p%32, hf)
 // of a 32x32x16 MFMA holds for k-chunk kk, both as the A operand of S^T = K Q^T and, for Q,
@@ -106,7 +117,7 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.k = (uint16_t*)(p + off); off += round_up(E * 2);
   w.vt = (uint16_t*)(p + off); off += round_up(E * 2);
   w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
-  w.o = (uint16_t*)(p + off); off += round_up((size_t)N * N * H * 32 * 2);
+  w.o = (uint16_t*)(p + off); off += round_up((size_t)N * NP * H * 32 * 2);   // o_off blocks
   w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
   w.off = (float*)(p + off); off += round_up((size_t)kPCols * 4);
   w.flags = (uint8_t*)(p + off); off += round_up((size_t)N * H);
@@ -319,15 +330,15 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 //    element e -> dim 8c + 4hf + e); W_o's columns are permuted to match when staged.
 // ---------------------------------------------------------------------------------------
 struct TriOutArgs {
-  int64_t P;                          // N * N
-  const uint16_t* o;                  // [4 heads][P][32]
+  int N, NP, transpose;
+  const uint16_t* o;                  // o_off blocks
   const uint16_t* wo;                 // [128 out, 128 in]
   const uint16_t* wg;                 // folded gate rows [128, 128]
   const float* goff;                  // [128]
   const uint16_t* z;                  // [P, 128]
   int add_residual;
   uint16_t* out;
-  int items, items_per_wave;          // 32-position blocks
+  int items, items_per_wave;          // blocks of 32 queries of one attention row: N * ceil(N / 32)
 };
 
 __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs a) {
@@ -364,26 +375,31 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   __syncthreads();
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
-  auto load = [&](int item, u32x4 (&xo)[8], u32x4 (&xz)[8], int64_t& p) {
-    p = (int64_t)item * 32 + li;
-    const bool ok = p < a.P;
-    // o is head-major [head][P][32]: feature 16kk + 8half + 0..7 is head kk/2, dims
-    // 16(kk%2) + 8half + 0..7
-    const uint16_t* op = a.o + (ok ? p : 0) * 32 + 8 * half;
-    const uint16_t* zp = a.z + (ok ? p : 0) * kPC + 8 * half;
+  // item = (attention row r, block ib of 32 queries); lane li takes query i = 32 ib + li, at pair
+  // position (r, i) (starting node) or (i, r) (ending node)
+  const int IB = (a.N + 31) >> 5;
+  auto pos = [&](int r, int i) -> int64_t { return a.transpose ? (int64_t)i * a.N + r : (int64_t)r * a.N + i; };
+  auto load = [&](int item, u32x4 (&xo)[8], u32x4 (&xz)[8], int& rn, int& in) {
+    rn = item / IB;
+    in = (item - rn * IB) * 32 + li;
+    const bool ok = in < a.N;
+    const int i = ok ? in : 0;
+    // feature 16kk + 8half + 0..7 of o is head kk/2, dims 16(kk%2) + 8half + 0..7: piece
+    // (hf = kk%2, k-chunk = half) of the epilogue's order
+    const uint16_t* zp = a.z + pos(rn, i) * kPC + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      xo[kk] = ok ? ld16(op + (kk >> 1) * a.P * 32 + 16 * (kk & 1)) : u32x4{0, 0, 0, 0};
+      xo[kk] = ok ? ld16(a.o + o_off(kk >> 1, rn, i, kk & 1, half, a.N, a.NP)) : u32x4{0, 0, 0, 0};
       xz[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
     }
   };
   u32x4 on[8], zn[8];
-  int64_t pn = 0;
-  if (first < last) load(first, on, zn, pn);
+  int rn = 0, in = 0;
+  if (first < last) load(first, on, zn, rn, in);
   for (int item = first; item < last; ++item) {
     asm volatile("" ::: "memory");                      // LDS weights are re-read every item
-    const int64_t p = pn;
-    const bool ok = p < a.P;                             // only the last block has idle lanes
+    const int r = rn, i0 = in - li;
+    const bool ok = in < a.N;                            // only a row's last block has idle lanes
     bf16x8 zo[8];
     ln128_operands(zn, ok, zo);
     // residual: output features 8c + 4h + e (c even / odd) of lane half h sit in z chunk
@@ -436,7 +452,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
         }
       }
     }
-    if (item + 1 < last) load(item + 1, on, zn, pn);    // lands during the output projection
+    if (item + 1 < last) load(item + 1, on, zn, rn, in);   // lands during the output projection
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       f32x16 acc;
@@ -458,17 +474,17 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
         *reinterpret_cast<u32x2*>(orow + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
       }
     }
-    // the wave's 32 output rows are 8 KB of contiguous memory: lane (row 4i + lane/16, chunk
-    // lane%16) stores 16 bytes, four whole 256-byte rows per streaming store (the LDS rows were
-    // written by other lanes of this wave; LDS executes a wave's accesses in order).  Against
-    // 8-byte stores straight from the MFMA layout: 0.128 -> 0.106 ms at N=768.
+    // the wave's 32 output rows (8 KB of contiguous memory for the starting node, 32 rows of
+    // 256 bytes for the ending node): lane (row 4u + lane/16, chunk lane%16) stores 16 bytes,
+    // four whole 256-byte rows per streaming store (the LDS rows were written by other lanes of
+    // this wave; LDS executes a wave's accesses in order).  Against 8-byte stores straight from
+    // the MFMA layout: 0.128 -> 0.106 ms at N=768.
     asm volatile("" ::: "memory");
-    const int64_t p0 = p - li;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 4 * i + (lane >> 4), ch = lane & 15;
+    for (int u = 0; u < 8; ++u) {
+      const int row = 4 * u + (lane >> 4), ch = lane & 15;
       const u32x4 v = ld16(so + row * kWP + 8 * ch);
-      if (p0 + row < a.P) st16_stream(a.out + (p0 + row) * kPC + 8 * ch, v);
+      if (i0 + row < a.N) st16_stream(a.out + pos(r, i0 + row) * kPC + 8 * ch, v);
     }
   }
 }
@@ -875,15 +891,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
         if (r >= N) continue;
         if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
         const float inv = fast_rcp(lt);
-        const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-        uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * half;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
-          st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+          st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
@@ -955,18 +969,16 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
     if (tid < 128) mean[tid] = (part[0][tid] + part[1][tid]) / (float)N;
     __syncthreads();
     // one (query, head, lane half) per thread: 16 dims in epilogue order; consecutive threads
-    // write consecutive positions of one head's plane
+    // write consecutive queries of one piece
     for (int t = tid; t < N * H * 2; t += 256) {
-      const int hf = t & 1, i = (t >> 1) % N, h = (t >> 1) / N;
-      const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-      uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * hf;
+      const int i = t % N, hf = (t / N) & 1, h = t / (2 * N);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           w[e] = pack_bf2(mean[h * 32 + slot_dim(hf, kk, 2 * e)], mean[h * 32 + slot_dim(hf, kk, 2 * e + 1)]);
-        st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+        st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
       }
     }
     return;
@@ -1007,17 +1019,15 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
         for (int d = 0; d < 32; ++d) acc[d] += w * bf2f(a.vt[vl_off(r, h, H, NP, c16, hf, d) + t]);
       }
       const float inv = 1.0f / l;
-      const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * hf;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             w[e] = pack_bf2(acc[slot_dim(hf, kk, 2 * e)] * inv, acc[slot_dim(hf, kk, 2 * e + 1)] * inv);
-          st16(op + 8 * kk, u32x4{w[0], w[1], w[2], w[3]});
+          st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
@@ -1326,14 +1336,12 @@ __global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
   const float lt = l + __shfl_xor(l, 32);
   if (i >= N) return;
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  const int za = a.transpose ? i : r, zb = a.transpose ? r : i;
-  uint16_t* op = a.o + ((int64_t)h * N * N + (int64_t)za * N + zb) * 32 + 16 * half;
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     uint32_t w4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) w4[e] = pack_bf2(o[8 * kk + 2 * e] * inv, o[8 * kk + 2 * e + 1] * inv);
-    st16(op + 8 * kk, u32x4{w4[0], w4[1], w4[2], w4[3]});
+    st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w4[0], w4[1], w4[2], w4[3]});
   }
 }
 
@@ -1431,12 +1439,12 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
 
   TriOutArgs oa{};
-  oa.P = (int64_t)N * N;
+  oa.N = N; oa.NP = NP; oa.transpose = a->transpose;
   oa.o = ws.o; oa.wo = (const uint16_t*)a->w_o;
   oa.wg = ws.wf + (size_t)12 * 32 * kPC; oa.goff = ws.off + 12 * 32;   // folded gate rows 384..511
   oa.z = (const uint16_t*)a->z; oa.add_residual = a->add_residual;
   oa.out = (uint16_t*)a->out;
-  oa.items = (int)((oa.P + 31) / 32);
+  oa.items = N * ((N + 31) / 32);
   const int ogroups = persistent_groups(oa.items, &oa.items_per_wave);
   hipLaunchKernelGGL(tri_out_kernel, dim3(ogroups), dim3(64 * kPWaves), 0, st, oa);
   return sf_check_launch("tri_out_kernel");
