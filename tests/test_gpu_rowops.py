@@ -34,10 +34,12 @@ def test_layer_norm_adaptive_rows_broadcast():
 
 
 # Shapes cover both GEMM kernels (K % 64 != 0 and == 0), each tile size of the K % 64 == 0
-# kernel (64x64, 64x128 at >= 512 tiles, 128x128 at >= 512 tiles), odd K-step counts and
-# ragged M / N edges (N % 4 != 0 exercises the partial 4-column epilogue group).
+# kernel (64x64, 64x128 at >= 512 tiles, 128x128 at >= 512 tiles), odd K-step counts, ragged
+# M / N edges (N % 4 != 0 exercises the partial 4-column epilogue group) and the diffusion
+# projection's 5120 x 3072 x 768.
 @pytest.mark.parametrize("M,N,K", [(1, 8, 8), (100, 96, 128), (257, 516, 128), (1030, 384, 384), (64, 3072, 768),
-                                   (1, 8, 64), (130, 70, 64), (4100, 1030, 192), (32773, 256, 128), (77, 3, 320)])
+                                   (1, 8, 64), (130, 70, 64), (4100, 1030, 192), (32773, 256, 128), (77, 3, 320),
+                                   (4100, 3610, 192), (5120, 3072, 768), (14700, 1030, 64)])
 def test_linear_plain(M, N, K):
   g = torch.Generator().manual_seed(M * 7 + N)
   x = torch.randn(M, K, generator=g).to(torch.bfloat16)
@@ -66,6 +68,43 @@ def test_linear_epilogue_bias_sigmoid_mul_residual_and_transposed_columns(K):
   y2 = ops.linear(x.to(DEV), w.to(DEV), ycols=64)
   assert y2.shape == (M, 64)
   assert_close_bf16(y2, x.float() @ w.float()[:64].t(), "linear ycols")
+
+
+def test_linear_large_epilogues():
+  """A large ragged product (4100 x 3608, 128x128 tiles) under every epilogue: bias, sigmoid,
+  row-broadcast multiplier, residual, transposed columns and ycols, and the gated pairs."""
+  g = torch.Generator().manual_seed(11)
+  M, N, K = 4100, 3608, 128
+  x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+  w = (torch.randn(N, K, generator=g) / 8).to(torch.bfloat16)
+  bias = torch.randn(N, generator=g)
+  mul = torch.randn(41, N, generator=g).to(torch.bfloat16)
+  res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+  yt = torch.empty(16, M, dtype=torch.bfloat16, device=DEV)
+  out = ops.linear(x.to(DEV), w.to(DEV), bias.to(DEV), post_sigmoid=True, mul=mul.to(DEV), residual=res.to(DEV),
+                   yt=yt, tcol0=3000)
+  pre = torch.sigmoid(x.float() @ w.float().t() + bias)
+  ref = pre * mul.float().repeat(M // 41 + 1, 1)[:M] + res.float()
+  assert_close_bf16(out, ref, "linear large epilogue")
+  assert_close_bf16(yt, ref[:, 3000:3016].t(), "linear large transposed columns")
+  y2 = ops.linear(x.to(DEV), w.to(DEV), ycols=3500)
+  assert y2.shape == (M, 3500)
+  assert_close_bf16(y2, x.float() @ w.float()[:3500].t(), "linear large ycols")
+  # gated pairs (C ABI): output column j = swish(col 2j) * col 2j + 1
+  import ctypes
+  from sparsefold_amd import _lib
+  w = (w.float() / 4).to(torch.bfloat16)           # products of O(1) gates and values
+  bias = bias / 4
+  xd, wd, bd = x.to(DEV), w.to(DEV), bias.to(DEV)
+  yg = torch.empty(M, N // 2, dtype=torch.bfloat16, device=DEV)
+  a = _lib.LinearArgs()
+  a.M, a.N, a.K = M, N, K
+  a.x, a.x_rs, a.wt, a.bias = xd.data_ptr(), K, wd.data_ptr(), bd.data_ptr()
+  a.y, a.y_rs, a.mul_rows, a.glu = yg.data_ptr(), N // 2, 1, 1
+  _lib.check(_lib.load().sf_hip_linear_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+             "sf_hip_linear_fwd")
+  h = x.float() @ w.float().t() + bias
+  assert_close_bf16(yg, torch.nn.functional.silu(h[:, 0::2]) * h[:, 1::2], "linear large glu")
 
 
 # C = 128 runs the MFMA kernel (P = 1320: a ragged last 32-position step; P = 1517: P % 4 != 0,
