@@ -677,7 +677,10 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   auto on = [&](int u) __attribute__((always_inline)) { return !SP || wu[u] != 0.f; };
   // ISSUE(u), u < 4: the next tile's loads, one K/V^T chunk and one bias piece per unit (see the
   // tile below).  PRIO: the wave's raised issue priority is dropped at unit kPrioUnits.
-  auto units = [&](int buf, auto reloadc, const uint16_t* nq, auto issue) __attribute__((always_inline)) {
+  // FIN(rr): row rr's result is final (its last P.V MFMA was issued a unit earlier): the last tile
+  // of a task normalises and stores rows 0..2 there, spread over the tile, instead of all four
+  // rows of all eight waves storing together after it.
+  auto units = [&](int buf, auto reloadc, const uint16_t* nq, auto issue, auto fin) __attribute__((always_inline)) {
     constexpr bool RELOAD = decltype(reloadc)::value;
     f32x16 sc, sn;
     bf16x8 kr[2], vr[2];
@@ -724,6 +727,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       if (u + 1 < 2 * kTR && on(u + 1)) load_v((u + 1) >> 1, (u + 1) & 1, buf, vr);
       __builtin_amdgcn_sched_barrier(0);
       sc = sn;
+      if ((u & 1) == 0 && u >= 2) fin((u >> 1) - 1);
     }
   };
   // SP: this wave's table (weights of its query tile's selected blocks for the task's 4 rows)
@@ -788,6 +792,24 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
     }
     const int i = qb * 32 * kAW + 32 * wave + li;          // this lane's query
     const bool active = qb * 32 * kAW + 32 * wave < NP;    // uniform: the wave has queries below NP
+    // normalise row rr of the task and store it at the pair position (the gate is applied by the
+    // output kernel, which recomputes it from z)
+    auto finish_row = [&](int rr) __attribute__((always_inline)) {
+      if (i >= N) return;
+      const int r = r0 + rr;
+      const float lt = __shfl(lsum[rr][0], src_lane);
+      if (r >= N) return;
+      if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
+      const float inv = fast_rcp(lt);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
+        st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+      }
+    };
     if constexpr (SP) fill_table(r0, h, qb);
 #pragma unroll
     for (int rr = 0; rr < kTR; ++rr) {
@@ -856,7 +878,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       // the loads of the tile must stay in issue order with the Q reloads (the partial waits at
       // the end of the tile count on it): no memory operation crosses this point
       asm volatile("" ::: "memory");
-      if (active) units(buf, lastc, nq, issue);
+      // rows 0..2 of the last tile are finished inside its units (the stores join the loads in the
+      // memory counter; the partial waits below still cover the K/V^T chunks, since the loads
+      // return in issue order and the stores only add to the count)
+      auto fin = [&](int rr) __attribute__((always_inline)) {
+        if constexpr (LAST && !SP) finish_row(rr);
+      };
+      if (active) units(buf, lastc, nq, issue, fin);
       __builtin_amdgcn_s_setprio(0);
       // this wave's chunks landed.  Issue order (unit: loads) is 0: D0 B0 [Q0 Q0], 1: D1 B1,
       // 2: D2 B2 [Q1 Q1], 3: D3 B3, 4: [Q2 Q2], 6: [Q3 Q3] -- D chunk, B bias piece, [Q] the last
@@ -881,26 +909,9 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
     tile(ntiles - 1, F{}, T{}, B1{});
     qready = active;                 // an idle wave loaded no Q operands for the next task
 
-    // ---- epilogue: normalise and store at the pair position (the gate is applied by the
-    //      output kernel, which recomputes it from z) ----
-    if (i < N) {
+    // ---- epilogue: the rows the last tile did not finish (idle waves have no queries below N) ----
 #pragma unroll
-      for (int rr = 0; rr < kTR; ++rr) {
-        const int r = r0 + rr;
-        const float lt = __shfl(lsum[rr][0], src_lane);
-        if (r >= N) continue;
-        if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
-        const float inv = fast_rcp(lt);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
-          st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
-        }
-      }
-    }
+    for (int rr = SP ? 0 : kTR - 1; rr < kTR; ++rr) finish_row(rr);
     if (!has_next) break;
     task = next; r0 = nr0; h = nh; qb = nqb; wsrc = nsrc; bsrc = nbsrc;
   }
