@@ -807,7 +807,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
-        st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        st16_stream(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
       }
     };
     if constexpr (SP) fill_table(r0, h, qb);
