@@ -506,7 +506,7 @@ struct TriAttnArgs {
 constexpr int kTR = 4;                // rows per workgroup
 constexpr int kKT = 64;               // keys per tile
 constexpr int kAW = 8;                // waves per attention workgroup (256 queries)
-constexpr int kPrioUnits = 4;         // units of a tile the younger wave of each SIMD runs at raised priority
+constexpr int kPrioUnits = 6;         // units of a tile the younger wave of each SIMD runs at raised priority
 // Per-wave table of the block-sparse kernel: the weights of the selected key blocks of its query
 // tile for the task's 4 rows, [row][block] floats (0 = not selected), blocks < 128 (N <= 4096).
 constexpr int kIbsTabBlocks = 128;
