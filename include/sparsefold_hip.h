@@ -200,7 +200,8 @@ int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* w
  * maps, backends/vecops/kernels/registry.py:2946-3040; GridSelfAttention.cpp:134-142,290-306;
  * parameters config.py:65-73): per (row r, head h, query tile t of 32 queries) num_samples slots
  * of (key block of 32 keys, weight) in index_map / weight_map, int32 / f32 [N, H, T, S],
- * T = ceil(N/32), index -1 = unused slot.  generate_maps = 1 samples them (this library's
+ * T = ceil(N/32); a slot whose index lies outside [0, T) (-1 by convention) or whose weight is
+ * <= 0 is unused, and a query tile with no used slot gets o = 0.  generate_maps = 1 samples them (this library's
  * importance sampler: static heaviest blocks to t_prob, num_rand_blocks draws up to tr_prob with
  * a u_prob floor, weight count / (R q); draws hashed from seed and (r, h, t)); 0 reuses the given
  * maps.  At most num_samples valid blocks per tile: all selected, weight 1, i.e. dense attention.

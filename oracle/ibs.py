@@ -163,14 +163,17 @@ def sparse_attention(q, k, v, bias, key_valid, index, weight) -> torch.Tensor:
   """One attention row: q, k ``[N, D]`` (log2 units), v ``[N, Dv]``, bias ``[N, N]`` (log2
   units), key_valid ``[N]``, maps ``[T, S]``.  Returns ``[N, Dv]`` float64."""
   N = q.shape[0]
-  out = torch.zeros(N, v.shape[1], dtype=torch.float64)
+  dev = q.device                          # the oracle runs where its inputs live (CPU, or the GPU for large N)
+  out = torch.zeros(N, v.shape[1], dtype=torch.float64, device=dev)
   qd, kd, vd, bd = q.double(), k.double(), v.double(), bias.double()
   for t in range(index.shape[0]):
-    blocks = [(int(b), float(w)) for b, w in zip(index[t], weight[t]) if b >= 0]
+    # a slot is used when its index names a key block and its weight is positive
+    blocks = [(int(b), float(w)) for b, w in zip(index[t], weight[t]) if 0 <= b < index.shape[0] and w > 0]
     if not blocks:
       continue
-    keys = torch.cat([torch.arange(BLOCK * b, min(N, BLOCK * b + BLOCK)) for b, _ in blocks])
-    wk = torch.cat([torch.full((min(N, BLOCK * b + BLOCK) - BLOCK * b,), w, dtype=torch.float64) for b, w in blocks])
+    keys = torch.cat([torch.arange(BLOCK * b, min(N, BLOCK * b + BLOCK), device=dev) for b, _ in blocks])
+    wk = torch.cat([torch.full((min(N, BLOCK * b + BLOCK) - BLOCK * b,), w, dtype=torch.float64, device=dev)
+                    for b, w in blocks])
     ok = key_valid[keys]
     for i in range(BLOCK * t, min(N, BLOCK * t + BLOCK)):
       x = kd[keys] @ qd[i] + bd[i, keys]
@@ -207,7 +210,7 @@ def grid_self_attention_ibs(act: torch.Tensor, seq_mask: torch.Tensor, p: dict, 
     v = linear(xr, p["v_projection.weight"])
     g = linear(xr, p["gating_query.weight"], transpose_weights=True, post_op="sigmoid")
     key_valid = seq & seq[r]
-    o = torch.zeros(N, H, D, dtype=torch.float64)
+    o = torch.zeros(N, H, D, dtype=torch.float64, device=act.device)
     for h in range(H):
       if not bool(seq[r]):
         o[:, h] = v[:, h].double().mean(0)                  # every logit is -max: uniform over all keys

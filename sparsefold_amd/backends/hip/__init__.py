@@ -20,8 +20,6 @@ from sparsefold_amd import _lib
 from sparsefold_amd import modules as _modules
 from sparsefold_amd.runtime import config
 
-_PATCHED_FACTORIES: list[tuple[object, str, object]] = []
-
 # native.ops name -> [(factory attribute, HIP class attribute in backends.hip.modules)]
 _REPLACE_MAP = {
     "grid_self_attn": [("GridSelfAttention", "GridSelfAttentionHip")],
@@ -36,16 +34,31 @@ _REPLACE_MAP = {
 }
 
 
-def _replace_factory(module, name: str, implementation) -> None:
-  if not any(owner is module and attr == name for owner, attr, _ in _PATCHED_FACTORIES):
-    _PATCHED_FACTORIES.append((module, name, getattr(module, name)))
-  setattr(module, name, implementation)
+class _FactoryPatches:
+  """The module factories this backend has replaced, each with the original to put back.
+
+  Keyed by (owner identity, attribute name): the first replacement of a factory records the
+  original, later ones (``apply`` called again) only swap the implementation, so ``restore``
+  always returns the reference's own class."""
+
+  def __init__(self) -> None:
+    self._originals: dict[tuple[int, str], tuple[object, object]] = {}
+
+  def replace(self, owner, name: str, implementation) -> None:
+    self._originals.setdefault((id(owner), name), (owner, getattr(owner, name)))
+    setattr(owner, name, implementation)
+
+  def restore(self) -> None:
+    originals, self._originals = self._originals, {}
+    for (_, name), (owner, original) in originals.items():
+      setattr(owner, name, original)
+
+
+_patches = _FactoryPatches()
 
 
 def unapply() -> None:
-  for module, name, original in reversed(_PATCHED_FACTORIES):
-    setattr(module, name, original)
-  _PATCHED_FACTORIES.clear()
+  _patches.restore()
 
 
 def apply() -> None:
@@ -57,7 +70,7 @@ def apply() -> None:
   for key, pairs in _REPLACE_MAP.items():
     if key in selected:
       for factory, impl in pairs:
-        _replace_factory(_modules, factory, getattr(hip_modules, impl))
+        _patches.replace(_modules, factory, getattr(hip_modules, impl))
 
 
 def manual_seed(seed: int) -> None:

@@ -309,15 +309,21 @@ class CrossAttentionHipMixin:
   def cross_conditioning(self, queries_single_cond: torch.Tensor) -> dict:
     """Both sides' AdaLN terms per atom from the queries' condition ``[U, Qw, C]``, cached per
     condition tensor (the native plan's per-example conditioning, backends/vecops/modules.py:
-    1302-1351): q_scale, q_shift, k_scale, k_shift, zgate, each ``[U*Qw, C]``."""
-    key = (queries_single_cond.data_ptr(), tuple(queries_single_cond.shape), queries_single_cond._version)
-    if self._hip_cond_cache is not None and self._hip_cond_cache[0] == key:
-      return self._hip_cond_cache[1]
+    1302-1351): q_scale, q_shift, k_scale, k_shift, zgate, each ``[U*Qw, C]``.
+
+    The cache holds the condition tensor itself and matches it by identity and version counter:
+    while it is held, its memory cannot be handed to another tensor, so a new condition that
+    happens to land at a freed address is never mistaken for the cached one, and an in-place
+    change bumps the version."""
+    cached = self._hip_cond_cache
+    if (cached is not None and cached[0] is queries_single_cond
+        and cached[1] == queries_single_cond._version):
+      return cached[2]
     scale, shift, zgate = ops.diffusion_conditioning(queries_single_cond, self._hip_pc_lnc_w, self._hip_pc_w_scale,
                                                      self._hip_pc_b_scale, self._hip_pc_w_shift, self._hip_pc_w_zc,
                                                      self._hip_pc_b_zc)
     terms = {"q_scale": scale[0], "q_shift": shift[0], "k_scale": scale[1], "k_shift": shift[1], "zgate": zgate[0]}
-    self._hip_cond_cache = (key, terms)
+    self._hip_cond_cache = (queries_single_cond, queries_single_cond._version, terms)
     return terms
 
   def _native_weights(self) -> dict:

@@ -494,7 +494,7 @@ struct TriAttnArgs {
   float sum_limit;                    // weight sums outside [2^-100, sum_limit] flag the (row, head)
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
-  uint16_t* o;                        // [H][N][N][32] head-major, dims in epilogue order
+  uint16_t* o;                        // o_off blocks: per (head, attention row, 32 queries), N * NP * H * 32
   uint8_t* flags;                     // [N][H]: 1 = recomputed exactly (dense: tri_fixup_kernel)
   // block-sparse rows (tri_ibs_tile_attn_kernel): maps [N][H][T][S] of (key block, weight);
   // sparse != 0 also keeps tri_fixup_kernel to the masked rows (flagged rows are recomputed by
@@ -753,6 +753,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int rr = (lane + 64 * k) / a.S;
+      // unused slot: index out of range or weight <= 0 (the exact kernel skips the same)
       if (bs[k] >= 0 && bs[k] < a.T && ws[k] > 0.f) atomicAdd(&tab[rr * kIbsTabBlocks + bs[k]], ws[k]);
     }
     asm volatile("" ::: "memory");
@@ -861,6 +862,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       const char* tsrc = LAST ? nsrc : wsrc;
       const char* tbsrc = LAST ? nbsrc : bsrc;
       const int tj = LAST ? 0 : (tt + 1) * kKT;
+      // The end-of-tile waits `vmcnt(1)` / `vmcnt(5)` below are counts of this lambda's loads in
+      // the order they are issued: chunk D_u, then bias piece B_u, for u = 0..3 (plus the last
+      // tile's Q reloads).  The vector memory counter retires loads in issue order, so the wait
+      // covers every K/V^T chunk only if no chunk is issued after a load the wait leaves in
+      // flight.  The compiler fence between D_u and B_u (and the one after each issue(u) in the
+      // unit loop) is what fixes that order; without it the compiler may reorder the two loads
+      // and the last chunk can still be in flight when the barrier releases the other waves.
       auto issue = [&](int u) __attribute__((always_inline)) {
         __builtin_amdgcn_global_load_lds(tsrc + (int64_t)tj * 64 + u * 1024 + lane16,
                                          (lds_u32*)(smem + TL::chunk_offset(buf ^ 1, wave * TL::kChunksPerWave + u)), 16, 0, 0);
@@ -1074,7 +1082,7 @@ struct IbsArgs {
   const uint8_t* seq;
   float* bmean;                       // [H][T][NP] tile-mean bias (log2 units), keys as the planes store them
   int32_t* index; float* weight;      // [N][H][T][S]
-  uint16_t* o;                        // [H][N][N][32], as the dense attention stage writes it
+  uint16_t* o;                        // o_off blocks (per head, attention row, 32 queries), as the dense stage writes them
   const uint8_t* flags;               // tri_ibs_attn_kernel: only (row, head) flagged here (null: all)
 };
 
@@ -1303,8 +1311,9 @@ __global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
   const float* wts = a.weight + task * a.S;
   for (int s = 0; s < a.S; ++s) {
     const int b = idx[s];                                    // same address in every lane: uniform
-    if (b < 0 || b >= a.T) continue;                         // unused slot (or out of range)
     const float w = wts[s];
+    // unused slot: index out of range or weight <= 0 (the tile kernel's table skips the same)
+    if (b < 0 || b >= a.T || !(w > 0.f)) continue;
     bf16x8 kr[2], vr[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) kr[kk] = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, 32 * b + li, kk, half)));

@@ -180,8 +180,17 @@ class GridSelfAttention(_NoTorchPath, torch.nn.Module):
     self.v_projection = Linear(num_channels, (H, qkv_dim), name="v_projection")
     self.gating_query = Linear(num_channels, H * qkv_dim, transpose_weights=True, name="gating_query")
     self.output_projection = Linear(H * qkv_dim, num_channels, name="output_projection")
-    self.act_norm = LayerNorm(num_channels, bias=kwargs.pop("act_norm_bias", True), name="act_norm")
+    # bias-free as in the reference (blocks.py:260-264); a checkpoint that carries an
+    # act_norm.bias still loads (see _load_from_state_dict)
+    self.act_norm = LayerNorm(num_channels, bias=kwargs.pop("act_norm_bias", False), name="act_norm")
     self.pair_bias_projection = Linear(num_channels, H, name="pair_bias_projection")
+
+  def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+    key = prefix + "act_norm.bias"
+    if key in state_dict and self.act_norm.bias is None:
+      w = self.act_norm.weight
+      self.act_norm.bias = torch.nn.Parameter(torch.empty(w.shape, dtype=w.dtype, device=w.device))
+    super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
 
 
 class TriangleMultiplication(_NoTorchPath, torch.nn.Module):

@@ -60,14 +60,16 @@ def state_dict_f32(module: torch.nn.Module) -> dict[str, torch.Tensor]:
 # ---------------------------------------------------------------------------------------
 
 def make_triangle(N: int, *, C: int = 128, H: int = 4, transpose: bool = False, padded: bool = False,
-                  seed: int = 1, sharp: bool = False, dtype=torch.bfloat16):
+                  seed: int = 1, sharp: bool = False, dtype=torch.bfloat16, act_norm_bias: bool = False):
+  """GridSelfAttention (blocks.py:188-366) and its z [N, N, C], mask [N].  ``act_norm_bias`` adds
+  the LayerNorm offset the reference module does not have (a checkpoint may still carry one)."""
   g = _gen(seed)
   z = torch.randn(N, N, C, generator=g).to(dtype)
   seq = torch.ones(N, dtype=torch.bool)
   if padded:
     seq[N - N // 10:] = False
   mod = M.GridSelfAttention(M.GridSelfAttention.Config(num_head=H), M.GlobalConfig(), transpose,
-                            num_channels=C, name="pair_attention")
+                            num_channels=C, name="pair_attention", act_norm_bias=act_norm_bias)
   fill_parameters(mod, seed + 1000, sharp=sharp)
   return mod, z, seq
 

@@ -72,7 +72,8 @@ def oracle_cases():
     for name, t in (("q", q), ("k", k), ("v", v), ("bias", bias), ("out", o)):
       out[f"sdpa808_{tag}_{name}"] = t.numpy()
   for tr in (False, True):
-    mod, z, seq = W.make_triangle(20, seed=21, sharp=True, padded=True, transpose=tr, dtype=torch.float32)
+    mod, z, seq = W.make_triangle(20, seed=21, sharp=True, padded=True, transpose=tr, dtype=torch.float32,
+                                   act_norm_bias=True)
     p = W.state_dict_f32(mod)
     upd = OM.grid_self_attention(z, seq, p, transpose=tr, return_update=True)
     tag = "end" if tr else "start"

@@ -83,7 +83,7 @@ def test_reference_parameter_layouts():
   assert shapes == {
       "q_projection.weight": (4, 32, 128), "k_projection.weight": (4, 32, 128), "v_projection.weight": (128, 4, 32),
       "gating_query.weight": (128, 128), "output_projection.weight": (128, 128), "act_norm.weight": (128,),
-      "act_norm.bias": (128,), "pair_bias_projection.weight": (128, 4)}
+      "pair_bias_projection.weight": (128, 4)}
   s = M.SelfAttention(M.SelfAttention.Config(num_head=16), M.GlobalConfig(), num_channels=768, single_cond_size=384)
   shapes = {k: tuple(v.shape) for k, v in s.state_dict().items()}
   assert shapes["layer_norm.single_cond_scale.weight"] == (384, 768)

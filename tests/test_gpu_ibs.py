@@ -271,3 +271,48 @@ def test_ibs_module_switch_and_reuse():
   dense = hip(zd, sd, add_residual=False)[0]
   ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=False, return_update=True)
   assert_close_bf16(dense, ref, "switch off: dense", max_abs=2e-2 * ref.abs().max().item())
+
+
+def _large_maps(N, H, S, seed):
+  """Vectorised synthetic maps for large N: slot 0 = block 0 and slot 1 = the last block (so the
+  tile kernel's per-wave table is filled to its last entry), the others random (repeats allowed:
+  a repeated block is the same as one slot with the summed weight); weights in [0.5, 3], except
+  that slot S-1 is unused -- index -1, weight 0 or a negative weight, by tile."""
+  rng = np.random.default_rng(seed)
+  T = (N + 31) // 32
+  im = rng.integers(0, T, size=(N, H, T, S), dtype=np.int32)
+  im[..., 0] = 0
+  im[..., 1] = T - 1
+  wm = rng.uniform(0.5, 3.0, size=(N, H, T, S)).astype(np.float32)
+  kind = rng.integers(0, 3, size=(N, H, T))
+  im[..., S - 1] = np.where(kind == 0, -1, im[..., S - 1])
+  wm[..., S - 1] = np.where(kind == 1, 0.0, np.where(kind == 2, -1.5, wm[..., S - 1]))
+  return im, wm
+
+
+@pytest.mark.parametrize("N", [4096, 4100])
+def test_ibs_given_maps_large(N):
+  """N=4096: the tile kernel with its per-wave block table full (T = 128 blocks, the last one
+  selected everywhere).  N=4100: above the table's limit, so every row runs on the exact
+  block-sparse kernel alone.  Slots with a negative or zero weight count as unused in both.  A
+  few rows against the oracle, which runs on the GPU here (its LayerNorm and bias planes over the
+  N^2 positions would take minutes on the host)."""
+  H, S = 4, 4
+  print(f"[case] IBS given maps N={N}", flush=True)
+  mod, _, _ = W.make_triangle(1, seed=41, sharp=True)       # the weights do not depend on N
+  hip = _prepared(mod)
+  g = torch.Generator(device=DEV).manual_seed(41)
+  zd = torch.randn(N, N, 128, generator=g, device=DEV).to(torch.bfloat16)   # 4.3 GB: made on the GPU
+  seq = torch.ones(N, dtype=torch.bool)
+  im, wm = _large_maps(N, H, S, seed=4)
+  params = ibs.IBSParams(num_samples=S, num_rand_blocks=1)
+  upd, _, _ = _call(hip, zd, seq.to(DEV), params, index_map=torch.from_numpy(im).to(DEV),
+                    weight_map=torch.from_numpy(wm).to(DEV))
+  torch.cuda.synchronize()
+  rows = [0, N // 2 + 1, N - 1]
+  got = upd[rows].float().cpu()
+  del upd
+  pd = {k: v.to(DEV) for k, v in _params(hip).items()}
+  ref = ibs.grid_self_attention_ibs(zd.float(), seq.to(DEV), pd, transpose=False, params=params, seed=0,
+                                    maps=(im, wm), rows=rows).float().cpu()
+  assert_close_bf16(got, ref, f"IBS given maps N={N}", max_abs=2e-2 * ref.abs().max().item())

@@ -56,7 +56,7 @@ def test_triangle_c1_n20_fp32(transpose):
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("N", [64, 97])
 def test_triangle_sharp_update_padded(transpose, N):
-  mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=7, sharp=True)
+  mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=7, sharp=True, act_norm_bias=True)
   hip = _prepared(mod)
   upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
   ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
@@ -157,7 +157,7 @@ def _n768_sharp_padded(transpose: bool):
     upd = hip(z.to(DEV), seq.to(DEV), add_residual=False).float().cpu()
     p = _params(hip)
     zf = z.float()
-    x = layer_norm(zf, p["act_norm.weight"], p["act_norm.bias"])
+    x = layer_norm(zf, p["act_norm.weight"], p.get("act_norm.bias"))
     bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
     _N768_CACHE.clear()
     _N768_CACHE[transpose] = (upd.transpose(0, 1) if transpose else upd, zf, seq, p, bias)
@@ -190,6 +190,41 @@ def test_triangle_c3_n768_sharp_padded_rows(transpose, rows):
   masked = [i for i, r in enumerate(sel) if not bool(seq[r])]
   if masked:                          # padded tokens attend uniformly: the mean of V, gated and projected
     assert got[masked].abs().max() > 0
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_n768_sharp_padded_repeatable(transpose):
+  """Two calls on the same inputs give the same bits.  At N=768 every persistent attention
+  workgroup runs 9 tasks, so the last tile of each task -- which loads the next task's first tile
+  and Q operands behind partial waits -- runs 8 times per workgroup; a wait that let a load land
+  late would show up as differing bits between calls."""
+  mod, z, seq = W.make_triangle(768, transpose=transpose, padded=True, seed=17, sharp=True)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  first = hip(zd, sd, add_residual=False)
+  for _ in range(3):
+    assert torch.equal(hip(zd, sd, add_residual=False), first)
+  assert torch.equal(hip(zd, sd), hip(zd, sd))
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("N,padded,sharp", [(96, True, True), (200, True, False), (37, False, True)])
+def test_triangle_template_stack_shape(transpose, N, padded, sharp):
+  """The template stack's PairFormer triangle attention (model/embeddings/template.py:122-127,
+  304-313): C=64, H=4, so D=16 -- the generic path (LayerNorm, one projection GEMM, strided
+  attention with the gate in its epilogue, output GEMM with the residual)."""
+  mod, z, seq = W.make_triangle(N, C=64, H=4, transpose=transpose, padded=padded, seed=23, sharp=sharp)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  p = _params(hip)
+  upd = hip(zd, sd, add_residual=False)
+  ref_u = OM.grid_self_attention(z.float(), seq, p, transpose=transpose, return_update=True)
+  assert torch.isfinite(upd).all()
+  assert_close_bf16(upd, ref_u, f"template triangle N={N} transpose={transpose} update",
+                    max_abs=2e-2 * ref_u.abs().max().item())
+  out = hip(zd, sd)
+  ref = OM.grid_self_attention(z.float(), seq, p, transpose=transpose)
+  assert_close_bf16(out, ref, f"template triangle N={N} transpose={transpose}")
 
 
 @pytest.mark.parametrize("transpose", [False, True])
@@ -296,12 +331,33 @@ def test_windowed_per_atom_plan(atoms, S, sharp):
   general = hip.forward_indexed(ad, qm, idx, gm, km, qcd, kc.to(DEV), bd, add_residual=False)
   assert_close_bf16(upd, general.float().cpu(), "per-atom plan vs general path", max_abs=2e-2 * d_ref.abs().max().item())
   # the conditioning is computed once per condition tensor, again after it changes in place
-  first = hip._hip_cond_cache[1]
+  first = hip._hip_cond_cache[2]
   hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd)
-  assert hip._hip_cond_cache[1] is first
+  assert hip._hip_cond_cache[2] is first
   qcd.mul_(1.0)
   hip.forward_indexed(ad, qm, idx, gm, km, qcd, None, bd)
-  assert hip._hip_cond_cache[1] is not first
+  assert hip._hip_cond_cache[2] is not first
+
+
+def test_windowed_per_atom_plan_new_condition_at_a_freed_address():
+  """A later example's condition is a new tensor of the same shape.  Even if the allocator would
+  hand it the memory of the previous (freed) condition, the per-atom plan must not reuse that
+  condition's cached AdaLN terms: the output follows the new values."""
+  mod, act, lay, qc, kc, bias = W.make_window(256, S=2, seed=5, sharp=True)
+  hip = _prepared(mod)
+  ad, bd = act.to(DEV), bias.to(DEV)
+  idx, gm = lay.gather_idxs.to(DEV), lay.gather_mask.to(DEV)
+  qm, km = lay.queries_mask.to(DEV), lay.keys_mask.to(DEV)
+  first = hip.forward_indexed(ad, qm, idx, gm, km, qc.to(DEV), None, bd, add_residual=False).float().cpu()
+  torch.cuda.synchronize()
+  qc2 = torch.randn(qc.shape, generator=torch.Generator().manual_seed(77)).to(qc.dtype)
+  second = hip.forward_indexed(ad, qm, idx, gm, km, qc2.to(DEV), None, bd, add_residual=False).float().cpu()
+  p = _params(hip)
+  kc2 = OM.atom_layout_convert(lay.gather_idxs, lay.gather_mask, (256 // 32, 32), qc2.float(), layout_axes=(-3, -2))
+  ref2 = OM.windowed_cross_attention(act.float(), lay.queries_mask, lay.gather_idxs, lay.gather_mask, lay.keys_mask,
+                                     qc2.float(), kc2, bias.float(), p, return_update=True)
+  assert not torch.equal(first, second)
+  assert_close_bf16(second, ref2, "per-atom plan, new condition", max_abs=2e-2 * ref2.abs().max().item())
 
 
 @pytest.mark.parametrize("atoms,S,sharp", [(256, 2, True), (8192, 5, False)])

@@ -32,7 +32,7 @@ def test_ending_node_is_starting_node_on_transpose_with_untransposed_bias():
   seq[-1] = False
   p = _sd(mod)
   end = OM.grid_self_attention(z, seq, p, transpose=True, return_update=True)
-  x = layer_norm(z, p["act_norm.weight"], p["act_norm.bias"])
+  x = layer_norm(z, p["act_norm.weight"], p.get("act_norm.bias"))
   bias_untransposed = torch.einsum("abc,ch->hab", x, p["pair_bias_projection.weight"])
   start_rows = OM.grid_self_attention_rows(z.transpose(0, 1).contiguous(), seq, p, transpose=False,
                                            rows=range(7), bias=bias_untransposed)
