@@ -126,11 +126,24 @@ def traffic_from_profile() -> float | None:
   return None
 
 
+CONFIG_MIN_TIMED_S = 0.05           # minimum GPU time of a configuration's timed calls
+
+
 def _time_call(fn, iters: int) -> float:
-  for _ in range(20):
+  """Mean ms of one call: the same clock warm-up as the headline (calls for at least
+  CLOCK_WARMUP_S of wall time, then 20 more), then at least `iters` timed calls and at least
+  CONFIG_MIN_TIMED_S of them, by HIP events on the current stream."""
+  t0 = time.perf_counter()
+  calls = 0
+  while time.perf_counter() - t0 < CLOCK_WARMUP_S or calls < 20:
     fn()
+    calls += 1
+    if calls % 10 == 0:
+      torch.cuda.synchronize()
   torch.cuda.synchronize()
-  return _events_time(fn, iters, torch.cuda.current_stream())
+  per_call_s = (time.perf_counter() - t0) / calls
+  n = max(iters, int(CONFIG_MIN_TIMED_S / max(per_call_s, 1e-6)) + 1)
+  return _events_time(fn, n, torch.cuda.current_stream())
 
 
 def _config_builders(side_timings: bool = True) -> dict:

@@ -187,11 +187,16 @@ int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t 
  *   SF_TRI_STAGE_ATTEND   attention core (reads the projected operands)
  *   SF_TRI_STAGE_OUTPUT   sigmoid gate (recomputed from LN(z)), output projection (+ residual)
  * Stages run in that order when several bits are set; sf_hip_triangle_attn_fwd == all three.
- * A stage reads what the earlier stages left in the same workspace. */
+ * A stage reads what the earlier stages left in the same workspace.
+ *   SF_TRI_STAGE_FUSE     with ATTEND and OUTPUT: one attention kernel whose epilogue runs the
+ *                         output stage per (row group, 256 queries) once its four heads are done
+ *                         (results identical; measured slower on MI355X, so not the default).
+ *                         ATTEND needs a workspace a PROJECT stage has initialised. */
 #define SF_TRI_STAGE_PROJECT 1
 #define SF_TRI_STAGE_ATTEND 2
 #define SF_TRI_STAGE_OUTPUT 4
 #define SF_TRI_STAGE_ALL 7
+#define SF_TRI_STAGE_FUSE 8
 int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* workspace,
                               size_t workspace_bytes, void* stream);
 

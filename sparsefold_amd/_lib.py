@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsparsefold_hip.so"
 ABI_VERSION = 11
-TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL = 1, 2, 4, 7
+TRI_STAGE_PROJECT, TRI_STAGE_ATTEND, TRI_STAGE_OUTPUT, TRI_STAGE_ALL, TRI_STAGE_FUSE = 1, 2, 4, 7, 8
 NOALLOC_SCRATCH_BYTES = 64 << 20           # SF_HIP_NOALLOC_SCRATCH_BYTES
 
 _i32, _i64, _f32, _vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p

@@ -105,8 +105,18 @@ struct FastWs {
   uint16_t *q, *k, *vt, *bias, *o, *wf;
   float* off;
   uint8_t* flags;                     // [N][H] rows for the exact fix-up
+  int* ctr;                           // fused epilogue: [G] per (row group, query block) heads done, then
+                                      // the error word (see TriAttnArgs)
+  uint8_t* defer;                     // [N] rows whose output the post kernel writes
+  int nctr;                           // G + 4
   size_t bytes;
 };
+
+// Groups of the fused epilogue: (row group of 4 rows, block of 256 queries).
+int fused_groups(int32_t N) {
+  const int NP = round_np(N);
+  return (NP / 4) * ((NP + 255) / 256);
+}
 
 FastWs carve_fast(void* base, int32_t N, int32_t H) {
   const size_t NP = (size_t)round_np(N), E = NP * NP * H * 32;
@@ -121,6 +131,9 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
   w.off = (float*)(p + off); off += round_up((size_t)kPCols * 4);
   w.flags = (uint8_t*)(p + off); off += round_up((size_t)N * H);
+  w.nctr = fused_groups(N) + 4;
+  w.ctr = (int*)(p + off); off += round_up((size_t)w.nctr * 4);
+  w.defer = (uint8_t*)(p + off); off += round_up((size_t)N);
   w.bytes = off;
   return w;
 }
@@ -136,11 +149,15 @@ struct TriFoldArgs {
   const float* ln_w; const float* ln_b;
   uint16_t* wf; float* off;           // [544, 128], [544]
   uint8_t* flags; int nflags;         // [N * H], cleared
+  int* ctr; int nctr;                 // fused epilogue counters, cleared
+  uint8_t* defer; int ndefer;         // fused epilogue deferred rows, cleared
 };
 
 __global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
   const int lane = threadIdx.x & 63;
   for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nflags; f += gridDim.x * blockDim.x) a.flags[f] = 0;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nctr; f += gridDim.x * blockDim.x) a.ctr[f] = 0;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.ndefer; f += gridDim.x * blockDim.x) a.defer[f] = 0;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= kPCols) return;
   const int c = 2 * lane;
@@ -341,6 +358,123 @@ struct TriOutArgs {
   int items, items_per_wave;          // blocks of 32 queries of one attention row: N * ceil(N / 32)
 };
 
+// W_o (its columns permuted to the attention epilogue's dim order) and the folded gate rows into
+// LDS rows of pitch kWP, by NTHR threads: every load first, then the stores (one memory latency).
+template <int NTHR>
+__device__ __forceinline__ void stage_out_weights(uint16_t* sW, uint16_t* sG, float* sGoff, const uint16_t* wo,
+                                                  const uint16_t* wg, const float* goff, int tid) {
+  constexpr int kStage = kPC * (kPC / 8) / NTHR;
+  static_assert(kPC * (kPC / 8) % NTHR == 0, "whole staging rounds");
+  u32x2 wlo[kStage], whi[kStage];
+  u32x4 gst[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * NTHR, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
+    // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head
+    const int hd = c8 & ~31, hf = (c8 >> 4) & 1, j = (c8 >> 3) & 1;
+    const uint16_t* src = wo + (int64_t)n * kPC + hd + 16 * j + 4 * hf;
+    wlo[u] = *reinterpret_cast<const u32x2*>(src);
+    whi[u] = *reinterpret_cast<const u32x2*>(src + 8);
+    gst[u] = ld16(wg + (int64_t)n * kPC + c8);
+  }
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int t = tid + u * NTHR, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    st16(&sW[n * kWP + c8], u32x4{wlo[u][0], wlo[u][1], whi[u][0], whi[u][1]});
+    st16(&sG[n * kWP + c8], gst[u]);
+  }
+  for (int n = tid; n < kPC; n += NTHR) sGoff[n] = goff[n];
+}
+
+// Gate of 32 pair positions (lane = position li, half = channel half): from this lane's z
+// channels 16 kk + 8 half + 0..7 (zn) and o pieces (on: feature 16 kk + 8 half + 0..7 of o is head
+// kk/2, piece (hf = kk%2, k-chunk = half) of the epilogue's order) it forms the gated o operands
+// xg of the output projection and, with add_residual, the residual pieces zr its accumulator
+// layout needs (output features 8c + 4h + e of lane half h sit in z chunk 2nb + c/2 of lane half
+// c%2, elements 4h + e: two permlane32 swaps per chunk bring them over).
+//   g = LN(z[p]) . W_g^T   (gamma folded into W_g, beta into its offset)
+__device__ __forceinline__ void out_gate(const u32x4 (&on)[8], const u32x4 (&zn)[8], bool ok, bool add_residual,
+                                         const uint16_t* sG, const float* sGoff, int lane, bf16x8 (&xg)[8],
+                                         uint32_t (&zr)[8][2][2]) {
+  const int half = lane >> 5, li = lane & 31;
+  bf16x8 zo[8];
+  ln128_operands(zn, ok, zo);
+  if (add_residual) {   // (add_residual false: the caller supplies the residual another way, or none)
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const auto s02 = __builtin_amdgcn_permlane32_swap(zn[kk][0], zn[kk][2], false, false);
+      const auto s13 = __builtin_amdgcn_permlane32_swap(zn[kk][1], zn[kk][3], false, false);
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        zr[kk][par][0] = s02[par];
+        zr[kk][par][1] = s13[par];
+      }
+    }
+  }
+  // gate of head nb: D^T = W_g . X^T -> lane (position, half hf) holds natural dims
+  // 8c + 4hf + e in register 4c + e; o operand chunk kk = 2nb + j of lane half h needs the
+  // gate of half j, register 8h + t -- one permlane32 swap per register pair gets it
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      acc = mfma32(as_bf16x8(ld16(&sG[(32 * nb + li) * kWP + 16 * kk + 8 * half])), zo[kk], acc);
+    float sg[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sg[r] = sigmoidf_(acc[r] + sGoff[32 * nb + 8 * (r >> 2) + 4 * half + (r & 3)]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(sg[t]), __float_as_uint(sg[t + 8]), false, false);
+      // sw[0]: gate for chunk 2nb (j = 0), sw[1]: for chunk 2nb + 1 (j = 1), element t
+      sg[t] = __uint_as_float(sw[0]);
+      sg[t + 8] = __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 w = on[2 * nb + j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2 v = cvt_bf2(bflo(w[e]) * sg[8 * j + 2 * e], bfhi(w[e]) * sg[8 * j + 2 * e + 1]);
+        xg[2 * nb + j][2 * e] = v[0];
+        xg[2 * nb + j][2 * e + 1] = v[1];
+      }
+    }
+  }
+}
+
+// Output projection + residual of the 32 positions: out[p] = z[p] + (o[p] * g[p]) . W_o^T
+// (blocks.py:286-291, :366).  st(nb, c, v) receives output channels 32 nb + 8 c + 4 half .. +3 of
+// position li as two bf16 pairs; resid(nb, c) gives the same channels of z.
+template <class Store, class Resid>
+__device__ __forceinline__ void out_proj(const bf16x8 (&xg)[8], bool add_residual, const uint16_t* sW, int lane,
+                                         Resid resid, Store st) {
+  const int half = lane >> 5, li = lane & 31;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
+      if (add_residual) {   // output channels 32 nb + 8 c + 4 half .. +3 of z
+        const u32x2 zz = resid(nb, c);
+        v[0] += bflo(zz[0]); v[1] += bfhi(zz[0]); v[2] += bflo(zz[1]); v[3] += bfhi(zz[1]);
+      }
+      st(nb, c, u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])});
+    }
+  }
+}
+
 __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
   __shared__ __attribute__((aligned(16))) uint16_t sG[kPC * kWP];
@@ -349,29 +483,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   uint16_t* const so = sOut[wave];
-  // all loads first, then the LDS stores: one memory latency for the staging
-  constexpr int kStage = kPC * (kPC / 8) / (64 * kPWaves);
-  static_assert(kPC * (kPC / 8) % (64 * kPWaves) == 0, "whole staging rounds");
-  u32x2 wlo[kStage], whi[kStage];
-  u32x4 gst[kStage];
-#pragma unroll
-  for (int u = 0; u < kStage; ++u) {
-    const int t = tid + u * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
-    // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head
-    const int hd = c8 & ~31, hf = (c8 >> 4) & 1, j = (c8 >> 3) & 1;
-    const uint16_t* src = a.wo + (int64_t)n * kPC + hd + 16 * j + 4 * hf;
-    wlo[u] = *reinterpret_cast<const u32x2*>(src);
-    whi[u] = *reinterpret_cast<const u32x2*>(src + 8);
-    gst[u] = ld16(a.wg + (int64_t)n * kPC + c8);
-  }
-#pragma unroll
-  for (int u = 0; u < kStage; ++u) {
-    const int t = tid + u * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    st16(&sW[n * kWP + c8], u32x4{wlo[u][0], wlo[u][1], whi[u][0], whi[u][1]});
-    st16(&sG[n * kWP + c8], gst[u]);
-  }
-  for (int n = tid; n < kPC; n += 64 * kPWaves) sGoff[n] = a.goff[n];
+  stage_out_weights<64 * kPWaves>(sW, sG, sGoff, a.wo, a.wg, a.goff, tid);
   __syncthreads();
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
@@ -384,8 +496,6 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
     in = (item - rn * IB) * 32 + li;
     const bool ok = in < a.N;
     const int i = ok ? in : 0;
-    // feature 16kk + 8half + 0..7 of o is head kk/2, dims 16(kk%2) + 8half + 0..7: piece
-    // (hf = kk%2, k-chunk = half) of the epilogue's order
     const uint16_t* zp = a.z + pos(rn, i) * kPC + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
@@ -400,80 +510,13 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
     asm volatile("" ::: "memory");                      // LDS weights are re-read every item
     const int r = rn, i0 = in - li;
     const bool ok = in < a.N;                            // only a row's last block has idle lanes
-    bf16x8 zo[8];
-    ln128_operands(zn, ok, zo);
-    // residual: output features 8c + 4h + e (c even / odd) of lane half h sit in z chunk
-    // 2nb + c/2 of lane half c%2, elements 4h + e -- two permlane32 swaps per chunk bring
-    // them over before the registers are reused by the next item's loads
-    uint32_t zr[8][2][2];
-    if (a.add_residual) {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const auto s02 = __builtin_amdgcn_permlane32_swap(zn[kk][0], zn[kk][2], false, false);
-        const auto s13 = __builtin_amdgcn_permlane32_swap(zn[kk][1], zn[kk][3], false, false);
-#pragma unroll
-        for (int par = 0; par < 2; ++par) {
-          zr[kk][par][0] = s02[par];
-          zr[kk][par][1] = s13[par];
-        }
-      }
-    }
-
-    // gate of head nb: D^T = W_g . X^T -> lane (position, half hf) holds natural dims
-    // 8c + 4hf + e in register 4c + e; o operand chunk kk = 2nb + j of lane half h needs the
-    // gate of half j, register 8h + t -- one permlane32 swap per register pair gets it
     bf16x8 xg[8];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      f32x16 acc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(as_bf16x8(ld16(&sG[(32 * nb + li) * kWP + 16 * kk + 8 * half])), zo[kk], acc);
-      float sg[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sg[r] = sigmoidf_(acc[r] + sGoff[32 * nb + 8 * (r >> 2) + 4 * half + (r & 3)]);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(sg[t]), __float_as_uint(sg[t + 8]), false, false);
-        // sw[0]: gate for chunk 2nb (j = 0), sw[1]: for chunk 2nb + 1 (j = 1), element t
-        sg[t] = __uint_as_float(sw[0]);
-        sg[t + 8] = __uint_as_float(sw[1]);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const u32x4 w = on[2 * nb + j];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16x2 v = cvt_bf2(bflo(w[e]) * sg[8 * j + 2 * e], bfhi(w[e]) * sg[8 * j + 2 * e + 1]);
-          xg[2 * nb + j][2 * e] = v[0];
-          xg[2 * nb + j][2 * e + 1] = v[1];
-        }
-      }
-    }
+    uint32_t zr[8][2][2];
+    out_gate(on, zn, ok, a.add_residual, sG, sGoff, lane, xg, zr);
     if (item + 1 < last) load(item + 1, on, zn, rn, in);   // lands during the output projection
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      f32x16 acc;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
-      uint16_t* orow = so + li * kWP + 32 * nb + 4 * half;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[4 * c + e];
-        if (a.add_residual) {
-          const uint32_t z0 = zr[2 * nb + (c >> 1)][c & 1][0], z1 = zr[2 * nb + (c >> 1)][c & 1][1];
-          v[0] += bflo(z0); v[1] += bfhi(z0); v[2] += bflo(z1); v[3] += bfhi(z1);
-        }
-        *reinterpret_cast<u32x2*>(orow + 8 * c) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-      }
-    }
+    out_proj(xg, a.add_residual, sW, lane,
+             [&](int nb, int c) { return u32x2{zr[2 * nb + (c >> 1)][c & 1][0], zr[2 * nb + (c >> 1)][c & 1][1]}; },
+             [&](int nb, int c, u32x2 v) { *reinterpret_cast<u32x2*>(so + li * kWP + 32 * nb + 4 * half + 8 * c) = v; });
     // the wave's 32 output rows (8 KB of contiguous memory for the starting node, 32 rows of
     // 256 bytes for the ending node): lane (row 4u + lane/16, chunk lane%16) stores 16 bytes,
     // four whole 256-byte rows per streaming store (the LDS rows were written by other lanes of
@@ -501,6 +544,17 @@ struct TriAttnArgs {
   // the exact block-sparse kernel)
   const int32_t* index; const float* weight;
   int T, S, sparse;
+  // fused epilogue (tri_attn_fused_kernel / tri_post_kernel): gate, output projection and residual
+  const uint16_t* wo;                 // [128 out, 128 in]
+  const uint16_t* wg;                 // folded gate rows [128, 128]
+  const float* goff;                  // [128]
+  const uint16_t* z;                  // [N, N, 128]
+  uint16_t* out;                      // [N, N, 128]
+  int add_residual;
+  int* ctr;                           // [G] heads published per group (1 + XCD id << 8 each), then
+                                      // [G] the error word (a wait timed out, or a group spanned XCDs)
+  uint8_t* defer;                     // [N] 1: row left to tri_post_kernel (a head of the row was flagged)
+  int groups;                         // G
 };
 
 constexpr int kTR = 4;                // rows per workgroup
@@ -511,6 +565,14 @@ constexpr int kPrioUnits = 6;         // units of a tile the younger wave of eac
 // tile for the task's 4 rows, [row][block] floats (0 = not selected), blocks < 128 (N <= 4096).
 constexpr int kIbsTabBlocks = 128;
 constexpr int kIbsTabBytes = kAW * kTR * kIbsTabBlocks * 4;
+// LDS of the fused epilogue: W_o (permuted), W_g (folded), the gate offsets, and the partial sums
+// and mean of V of a fully masked row.
+constexpr int kFusedW = kPC * kWP * 2;
+constexpr int kFusedBytes = 2 * kFusedW + kPC * 4 + 5 * kPC * 4;
+// Bound of a fused epilogue wait (iterations of a 64-cycle sleep, ~0.1 s): every wait is for
+// work that resident workgroups finish on their own, so only a broken assumption (a workgroup
+// that never runs) reaches it; the rows concerned are then written as NaN and the error word set.
+constexpr int kFusedSpin = 1 << 20;
 
 typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
@@ -549,10 +611,11 @@ struct TileLayout {
 // each wave fills its table from the maps; a unit (row rr, 32-key block b) whose weight w is 0 is
 // skipped (no S^T MFMAs, exponentials or P.V), and a selected one adds log2 w to its logits, so
 // that its weights are w 2^s.  Row sums, normalisation and the out-of-range flags are unchanged.
-template <bool SP>
+template <bool SP, bool FUSED>
 __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
+  static_assert(!(SP && FUSED), "the block-sparse rows use the separate output stage");
   using TL = TileLayout;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes + (SP ? kIbsTabBytes : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes + (SP ? kIbsTabBytes : 0) + (FUSED ? kFusedBytes : 0)];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar branches
   const int half = lane >> 5, li = lane & 31;
@@ -563,11 +626,21 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   const int xcd = blockIdx.x & 7, G8 = gridDim.x >> 3;
   int task = blockIdx.x >> 3;                       // index within the XCD's range
   if (task >= per) return;                          // uniform over the workgroup
+  // FUSED: the heads are innermost, so that the 4 tasks of a group (row group, query block) are
+  // tasks 4m .. 4m+3 of an XCD's range, run in the same round by workgroups 4m' .. 4m'+3 of that
+  // XCD (G8 is a multiple of 4): one L2 holds the o of all 4 heads for the group's epilogue.
+  // (Measured on the attention alone: +3%, the bias planes of all heads then share the L2.)
   auto decode = [&](int tl, int& r0, int& h, int& qb) __attribute__((always_inline)) {
     const int t = xcd * per + tl;
-    qb = t % QB;
-    r0 = ((t / QB) % RG) * kTR;
-    h = t / (QB * RG);
+    if constexpr (FUSED) {
+      h = t & 3;
+      qb = (t >> 2) % QB;
+      r0 = ((t >> 2) / QB) * kTR;
+    } else {
+      qb = t % QB;
+      r0 = ((t / QB) % RG) * kTR;
+      h = t / (QB * RG);
+    }
   };
 
   // ---- tile loader: this wave's 1 KB chunks of a tile, straight into LDS.  Wave w < 4 copies
@@ -770,16 +843,126 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   const int ntiles = NP / kKT;
   const int q32 = lane & 31;
   const int src_lane = q32 < 16 ? q32 : q32 + 16;   // a lane whose row-sum output holds query q32
+
+  // ---- FUSED: the gate, output projection and residual of a group's rows, in the epilogue ----
+  // A task publishes its group (row group, query block) once its o stores are in L2: the group's
+  // count grows by 1 + (XCD id << 8).  One task later -- when the group's other three heads,
+  // started in the same round, are done as well -- the workgroup that ran head h writes the
+  // output of the group's row r0 + h (256 queries, one 32-query item per wave): o of the four
+  // heads from this XCD's L2, z for the gate and the residual, out = z + (o * g) W_o.
+  uint16_t* const sWo = reinterpret_cast<uint16_t*>(smem + 2 * TL::kBytes);
+  uint16_t* const sWg = sWo + kPC * kWP;
+  float* const sGoff = reinterpret_cast<float*>(sWg + kPC * kWP);
+  float* const sPart = sGoff + kPC;                          // [4][128] partial sums of V
+  float* const sMean = sPart + 4 * kPC;                      // [128] mean of V (head-major)
+  const int xcc = FUSED ? (int)__builtin_amdgcn_s_getreg((3 << 11) | 20) : 0;   // HW_REG_XCC_ID[3:0]
+  auto pos_of = [&](int r, int i) __attribute__((always_inline)) -> int64_t {
+    return a.transpose ? (int64_t)i * N + r : (int64_t)r * N + i;
+  };
+  auto publish = [&](int gid) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0);                           // this wave's o stores and flags are in L2
+    __syncthreads();                                         // ... and every other wave's
+    if (tid == 0) __hip_atomic_fetch_add(a.ctr + gid, 1 + (xcc << 8), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto outwork = [&](int gid, int r, int oqb) __attribute__((always_inline)) {
+    int v = 0;
+    for (int it = 0; it < kFusedSpin; ++it) {                // uniform: every lane reads the same word
+      v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(a.ctr + gid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      if ((v & 0xff) >= 4) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (r >= N) return;                                      // a padding row of the group
+    const int i0 = (oqb * kAW + wave) * 32, i = i0 + li;
+    const bool ok = i < N;
+    auto store = [&](int nb, int c, u32x2 val) __attribute__((always_inline)) {
+      if (ok) *reinterpret_cast<u32x2*>(a.out + pos_of(r, i) * kPC + 32 * nb + 8 * c + 4 * half) = val;
+    };
+    if (v != 4 + ((4 * xcc) << 8)) {
+      // the wait timed out, or the group's heads ran on different XCDs (no common L2): the rows
+      // are written as NaN and the error word is set, never a stale or partial result
+      if (tid == 0) a.ctr[a.groups] = 1;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) store(nb, c, u32x2{0x7fc07fc0u, 0x7fc07fc0u});
+      return;
+    }
+    // a flagged head: tri_post_kernel recomputes the row exactly and writes its output (all of
+    // its query blocks: each of the row's groups marks it, the mark is idempotent)
+    const uint32_t fl = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(reinterpret_cast<uint32_t*>(a.flags + r * 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (fl != 0) {
+      if (tid == 0) a.defer[r] = 1;
+      return;
+    }
+    u32x4 on[8];
+    if (a.seq[r] == 0) {
+      // every logit of a masked row is the masked value, so the reference's softmax is uniform:
+      // o = mean of V over all N keys (keys past N hold V = 0); thread (part, head, dim)
+      {
+        const int hd = tid & 127, hh = hd >> 5, d = hd & 31, pp = tid >> 7;
+        const int per_part = NP / 64;                        // 16-key chunks per part, even
+        float s0 = 0.f, s1 = 0.f;
+        for (int c16 = pp * per_part; c16 < (pp + 1) * per_part; c16 += 2) {
+          u32x4 vv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) vv[u] = ld16(a.vt + vl_off(r, hh, H, NP, c16 + (u >> 1), u & 1, d));
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { s0 += bflo(vv[u][e]); s1 += bfhi(vv[u][e]); }
+        }
+        sPart[pp * kPC + hd] = s0 + s1;
+      }
+      __syncthreads();
+      if (tid < kPC) sMean[tid] = (sPart[tid] + sPart[kPC + tid] + sPart[2 * kPC + tid] + sPart[3 * kPC + tid]) / (float)N;
+      __syncthreads();
+      // piece (hf = kk%2, k-chunk = half) of head kk/2: dims 16 half + 8 (t/4) + 4 hf + t%4
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const float* mh = sMean + 32 * (kk >> 1) + 16 * half + 4 * (kk & 1);
+        on[kk] = u32x4{pack_bf2(mh[0], mh[1]), pack_bf2(mh[2], mh[3]), pack_bf2(mh[8], mh[9]), pack_bf2(mh[10], mh[11])};
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        on[kk] = ok ? ld16(a.o + o_off(kk >> 1, r, i, kk & 1, half, N, NP)) : u32x4{0, 0, 0, 0};
+    }
+    if (i0 < N) {
+      u32x4 zn[8];
+      const uint16_t* zp = a.z + pos_of(r, ok ? i : 0) * kPC + 8 * half;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+      // The weights lie above the first 64 KB of LDS, past a ds_read's immediate offset: left
+      // alone, the compiler hoisted one base register per weight row block out of the persistent
+      // loop and spilled.  An opaque zero makes the bases local to this item.
+      int lz = 0;
+      asm volatile("" : "+v"(lz));
+      const uint16_t* wg_l = sWg + lz;
+      const uint16_t* wo_l = sWo + lz;
+      bf16x8 xg[8];
+      uint32_t zr[8][2][2];                                  // unused: the residual is re-read below
+      out_gate(on, zn, ok, false, wg_l, sGoff, lane, xg, zr);
+      // the residual straight from z in the accumulator layout (the lines were just read)
+      const uint16_t* zq = a.z + pos_of(r, ok ? i : 0) * kPC + 4 * half;
+      out_proj(xg, a.add_residual, wo_l, lane,
+               [&](int nb, int c) { return ok ? *reinterpret_cast<const u32x2*>(zq + 32 * nb + 8 * c) : u32x2{0, 0}; },
+               store);
+    }
+  };
+
   int r0, h, qb;
   decode(task, r0, h, qb);
   const char* wsrc = loader_src(r0, h);
   const char* bsrc = bias_src(h, qb);
   load_tile(wsrc, 0, 0);
   load_bias_regs(bsrc, 0);
+  if constexpr (FUSED) stage_out_weights<64 * kAW>(sWo, sWg, sGoff, a.wo, a.wg, a.goff, tid);
   __builtin_amdgcn_s_waitcnt(0);                           // this wave's chunks have landed
   __syncthreads();                                         // ... and everybody else's
   load_q(r0, h, qb, qb8);
   bool qready = true;                                      // qb8 holds this task's Q operands (uniform)
+  int prev_gid = -1, prev_row = 0, prev_qb = 0;            // FUSED: the previous task's group
   for (;;) {
     const int next = task + G8;
     const bool has_next = next < per;                      // uniform
@@ -808,7 +991,9 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
-        st16_stream(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        // FUSED: plain stores, so that the group's epilogue finds them in L2
+        if constexpr (FUSED) st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        else st16_stream(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
       }
     };
     if constexpr (SP) fill_table(r0, h, qb);
@@ -920,15 +1105,86 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
     // ---- epilogue: the rows the last tile did not finish (idle waves have no queries below N) ----
 #pragma unroll
     for (int rr = SP ? 0 : kTR - 1; rr < kTR; ++rr) finish_row(rr);
+    if constexpr (FUSED) {
+      // publish this task's group, then write the output row of the previous task's group (its
+      // other heads ran in the previous round: no wait in practice); the next task's first
+      // tile and Q operands are loading meanwhile
+      const int gid = (xcd * per + task) >> 2;
+      publish(gid);
+      if (prev_gid >= 0) outwork(prev_gid, prev_row, prev_qb);
+      prev_gid = gid; prev_row = r0 + h; prev_qb = qb;
+    }
     if (!has_next) break;
     task = next; r0 = nr0; h = nh; qb = nqb; wsrc = nsrc; bsrc = nbsrc;
   }
+  if constexpr (FUSED) outwork(prev_gid, prev_row, prev_qb);   // the last task's group
   __builtin_amdgcn_s_waitcnt(0);                           // the last task's Q reloads
 }
 
-__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) { tri_attn_body<false>(a); }
+__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) { tri_attn_body<false, false>(a); }
 
-__global__ __launch_bounds__(64 * kAW) void tri_ibs_tile_attn_kernel(const TriAttnArgs a) { tri_attn_body<true>(a); }
+__global__ __launch_bounds__(64 * kAW) void tri_ibs_tile_attn_kernel(const TriAttnArgs a) { tri_attn_body<true, false>(a); }
+
+__global__ __launch_bounds__(64 * kAW) void tri_attn_fused_kernel(const TriAttnArgs a) { tri_attn_body<false, true>(a); }
+
+// (row, head) pairs flagged by the attention kernel (a weight sum out of range) of attention row r:
+// recomputed with an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from
+// the same Q, K, V^T and bias operands, one query per thread of a 256-thread workgroup; each flag
+// is cleared afterwards.
+__device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
+  const int N = a.N, NP = a.NP, H = a.H;
+  auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
+  for (int h = 0; h < H; ++h) {
+    if (a.flags[r * H + h] == 0) continue;               // same address for every thread: uniform
+    for (int i = tid; i < N; i += 256) {
+      // q.k is invariant under the common dim permutation of the Q / K layouts: dot in storage order
+      float q[32];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 v = ld16(a.q + ql_off(r, h, H, NP, i, c >> 1, c & 1));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { q[8 * c + 2 * e] = bflo(v[e]); q[8 * c + 2 * e + 1] = bfhi(v[e]); }
+      }
+      auto logit = [&](int j) {
+        float s = bf2f(a.bias[bias_off(h, i, j, NP)]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32x4 v = ld16(a.k + ql_off(r, h, H, NP, j, c >> 1, c & 1));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += q[8 * c + 2 * e] * bflo(v[e]) + q[8 * c + 2 * e + 1] * bfhi(v[e]);
+        }
+        return s;
+      };
+      float m = -INFINITY;
+      for (int j = 0; j < N; ++j) m = fmaxf(m, logit(j));
+      float l = 0.f, acc[32];
+#pragma unroll
+      for (int d = 0; d < 32; ++d) acc[d] = 0.f;
+      for (int j = 0; j < N; ++j) {
+        const float w = exp2f(logit(j) - m);
+        l += w;
+        // V^T piece of key j: chunk j/16, lane half (j/4)%2, element 4((j%16)/8) + j%4
+        const int c16 = j >> 4, hf = (j >> 2) & 1, t = 4 * ((j & 15) >> 3) + (j & 3);
+#pragma unroll
+        for (int d = 0; d < 32; ++d) acc[d] += w * bf2f(a.vt[vl_off(r, h, H, NP, c16, hf, d) + t]);
+      }
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = pack_bf2(acc[slot_dim(hf, kk, 2 * e)] * inv, acc[slot_dim(hf, kk, 2 * e + 1)] * inv);
+          st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        }
+      }
+    }
+    __syncthreads();                                     // every thread has read the flag
+    if (tid == 0) a.flags[r * H + h] = 0;
+  }
+}
 
 // ---------------------------------------------------------------------------------------
 // Rows the attention kernel cannot finish on its fast path, one workgroup per attention row:
@@ -1003,55 +1259,54 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
     return;
   }
   if (a.sparse) return;                                  // flagged block-sparse rows: not here
-  for (int h = 0; h < H; ++h) {
-    if (a.flags[r * H + h] == 0) continue;               // same address for every thread: uniform
-    for (int i = tid; i < N; i += 256) {
-      // q.k is invariant under the common dim permutation of the Q / K layouts: dot in storage order
-      float q[32];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 v = ld16(a.q + ql_off(r, h, H, NP, i, c >> 1, c & 1));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { q[8 * c + 2 * e] = bflo(v[e]); q[8 * c + 2 * e + 1] = bfhi(v[e]); }
-      }
-      auto logit = [&](int j) {
-        float s = bf2f(a.bias[bias_off(h, i, j, NP)]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32x4 v = ld16(a.k + ql_off(r, h, H, NP, j, c >> 1, c & 1));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) s += q[8 * c + 2 * e] * bflo(v[e]) + q[8 * c + 2 * e + 1] * bfhi(v[e]);
-        }
-        return s;
-      };
-      float m = -INFINITY;
-      for (int j = 0; j < N; ++j) m = fmaxf(m, logit(j));
-      float l = 0.f, acc[32];
-#pragma unroll
-      for (int d = 0; d < 32; ++d) acc[d] = 0.f;
-      for (int j = 0; j < N; ++j) {
-        const float w = exp2f(logit(j) - m);
-        l += w;
-        // V^T piece of key j: chunk j/16, lane half (j/4)%2, element 4((j%16)/8) + j%4
-        const int c16 = j >> 4, hf = (j >> 2) & 1, t = 4 * ((j & 15) >> 3) + (j & 3);
-#pragma unroll
-        for (int d = 0; d < 32; ++d) acc[d] += w * bf2f(a.vt[vl_off(r, h, H, NP, c16, hf, d) + t]);
-      }
-      const float inv = 1.0f / l;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            w[e] = pack_bf2(acc[slot_dim(hf, kk, 2 * e)] * inv, acc[slot_dim(hf, kk, 2 * e + 1)] * inv);
-          st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
-        }
-      }
+  tri_exact_heads(a, r, tid);
+}
+
+// Rows the fused epilogue left to this kernel (a head of the row was flagged): those heads are
+// recomputed exactly, as tri_fixup_kernel does, then the row's output is written (gate, output
+// projection, residual) for all its queries.  Grid-strided over the rows; also clears the group
+// counts, the marks and (through the recompute) the flags for the next call.
+__global__ __launch_bounds__(256) void tri_post_kernel(const TriAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
+  __shared__ __attribute__((aligned(16))) uint16_t sG[kPC * kWP];
+  __shared__ __attribute__((aligned(16))) float sGoff[kPC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
+  const int N = a.N, NP = a.NP;
+  for (int f = blockIdx.x * 256 + tid; f < a.groups; f += gridDim.x * 256) a.ctr[f] = 0;
+  bool staged = false;
+  for (int r = blockIdx.x; r < N; r += gridDim.x) {
+    if (a.defer[r] == 0) continue;                       // same address for every thread: uniform
+    if (!staged) {
+      stage_out_weights<256>(sW, sG, sGoff, a.wo, a.wg, a.goff, tid);
+      staged = true;
     }
-    __syncthreads();                                     // every thread has read the flag
-    if (tid == 0) a.flags[r * H + h] = 0;
+    tri_exact_heads(a, r, tid);
+    // the recomputed o rows are read by other waves below: __syncthreads waits only for LDS
+    // traffic, so the global stores are waited for explicitly first
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int ib = wave; ib * 32 < N; ib += 4) {
+      const int i = ib * 32 + li;
+      const bool ok = i < N;
+      const int64_t p = a.transpose ? (int64_t)(ok ? i : 0) * N + r : (int64_t)r * N + (ok ? i : 0);
+      u32x4 on[8], zn[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        on[kk] = ok ? ld16(a.o + o_off(kk >> 1, r, i, kk & 1, half, N, NP)) : u32x4{0, 0, 0, 0};
+        zn[kk] = ok ? ld16(a.z + p * kPC + 8 * half + 16 * kk) : u32x4{0, 0, 0, 0};
+      }
+      bf16x8 xg[8];
+      uint32_t zr[8][2][2];                                  // unused: the residual is re-read below
+      out_gate(on, zn, ok, false, sG, sGoff, lane, xg, zr);
+      const uint16_t* zq = a.z + p * kPC + 4 * half;
+      out_proj(xg, a.add_residual, sW, lane,
+               [&](int nb, int c) { return ok ? *reinterpret_cast<const u32x2*>(zq + 32 * nb + 8 * c) : u32x2{0, 0}; },
+               [&](int nb, int c, u32x2 v) {
+                 if (ok) *reinterpret_cast<u32x2*>(a.out + p * kPC + 32 * nb + 8 * c + 4 * half) = v;
+               });
+    }
+    __syncthreads();                                     // every thread has read the mark
+    if (tid == 0) a.defer[r] = 0;
   }
 }
 
@@ -1429,6 +1684,8 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     fa.w = (const uint16_t*)a->w_qkvgb; fa.ln_w = a->ln_w; fa.ln_b = a->ln_b;
     fa.wf = ws.wf; fa.off = ws.off;
     fa.flags = ws.flags; fa.nflags = N * H;
+    fa.ctr = ws.ctr; fa.nctr = ws.nctr;
+    fa.defer = ws.defer; fa.ndefer = N;
     hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4), dim3(256), 0, st, fa);
     if (int rc = sf_check_launch("tri_fold_kernel")) return rc;
 
@@ -1451,6 +1708,21 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     aa.flags = ws.flags;
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;   // a multiple of 64
+    // attention with the gate, output projection and residual in its epilogue: the workgroups
+    // of a group's four heads must be resident together on one XCD, so the grid is a multiple of
+    // 32 (each XCD's share a multiple of 4) no larger than the resident count
+    const int fgrid = std::min(std::min(total, 256),
+                               sf_resident_workgroups((const void*)tri_attn_fused_kernel, 64 * kAW) / 32 * 32);
+    if ((stages & SF_TRI_STAGE_FUSE) && (stages & SF_TRI_STAGE_OUTPUT) && fgrid >= 32) {
+      aa.wo = (const uint16_t*)a->w_o;
+      aa.wg = ws.wf + (size_t)12 * 32 * kPC; aa.goff = ws.off + 12 * 32;   // folded gate rows 384..511
+      aa.z = (const uint16_t*)a->z; aa.out = (uint16_t*)a->out; aa.add_residual = a->add_residual;
+      aa.ctr = ws.ctr; aa.defer = ws.defer; aa.groups = fused_groups(N);
+      hipLaunchKernelGGL(tri_attn_fused_kernel, dim3(fgrid), dim3(64 * kAW), 0, st, aa);
+      if (int rc = sf_check_launch("tri_attn_fused_kernel")) return rc;
+      hipLaunchKernelGGL(tri_post_kernel, dim3(std::min(N, 128)), dim3(256), 0, st, aa);
+      return sf_check_launch("tri_post_kernel");
+    }
     hipLaunchKernelGGL(tri_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
     hipLaunchKernelGGL(tri_fixup_kernel, dim3(N), dim3(256), 0, st, aa);
@@ -1485,7 +1757,7 @@ static int triangle_run(const sf_triangle_args* a, void* workspace, size_t works
   if (a->out == a->z) { sf_set_error("triangle: out must not alias z"); return 1; }
   if (fast_path(C, H, D))
     return triangle_fast(a, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), stages);
-  if (stages != SF_TRI_STAGE_ALL) {
+  if ((stages & SF_TRI_STAGE_ALL) != SF_TRI_STAGE_ALL) {
     sf_set_error("triangle: single stages are available on the head-dim-32 path only (C=%d H=%d D=%d)", C, H, D);
     return 1;
   }
@@ -1546,7 +1818,7 @@ extern "C" int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspa
 
 extern "C" int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stages, void* workspace,
                                          size_t workspace_bytes, void* stream) {
-  if (stages <= 0 || (stages & ~SF_TRI_STAGE_ALL)) {
+  if (stages <= 0 || (stages & ~(SF_TRI_STAGE_ALL | SF_TRI_STAGE_FUSE)) || stages == SF_TRI_STAGE_FUSE) {
     sf_set_error("triangle: invalid stage mask %d", stages);
     return 1;
   }

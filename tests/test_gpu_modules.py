@@ -78,12 +78,13 @@ def test_triangle_edge_sizes(transpose, N, padded):
   assert_close_bf16(upd, ref, f"triangle N={N} transpose={transpose}", max_abs=2e-2 * ref.abs().max().item())
 
 
-def _triangle_update(hip, z, seq, **kw):
+def _triangle_update(hip, z, seq, add_residual=False, **kw):
   """The module's update through the C entry point with its packed weights (the module's own
   forward, plus the explicit test controls of ops.triangle_attention)."""
   from sparsefold_amd.backends.hip import ops
   return ops.triangle_attention(z, seq, hip._hip_ln_w, hip._hip_ln_b, hip._hip_w_qkvgb, hip._hip_w_o,
-                                num_head=hip.config.num_head, transpose=hip.transpose, add_residual=False, **kw)
+                                num_head=hip.config.num_head, transpose=hip.transpose, add_residual=add_residual,
+                                **kw)
 
 
 @pytest.mark.parametrize("limit", [1.0, 1500.0])
@@ -205,6 +206,30 @@ def test_triangle_n768_sharp_padded_repeatable(transpose):
   for _ in range(3):
     assert torch.equal(hip(zd, sd, add_residual=False), first)
   assert torch.equal(hip(zd, sd), hip(zd, sd))
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("N,limit", [(768, 0.0), (768, 1.0), (384, 0.0), (200, 1500.0), (257, 0.0), (20, 0.0)])
+def test_triangle_fused_output_stage(transpose, N, limit):
+  """The opt-in fused kernel (SF_TRI_STAGE_FUSE: the attention epilogue writes each group's
+  output rows once its four heads are done, flagged rows go to the post kernel) gives the same bits
+  as the separate stages: every row and node, padded rows (mean of V in the epilogue), and rows
+  recomputed by the exact fix-up (limit 1: every row deferred; 1500: some)."""
+  from sparsefold_amd import _lib
+  mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=29, sharp=True)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  print(f"[case] fused output stage N={N} limit={limit} transpose={transpose}", flush=True)
+  for residual in (False, True):
+    ref = _triangle_update(hip, zd, sd, fixup_sum_limit=limit, add_residual=residual)
+    fused = _triangle_update(hip, zd, sd, fixup_sum_limit=limit, add_residual=residual,
+                             stages=_lib.TRI_STAGE_ALL | _lib.TRI_STAGE_FUSE)
+    assert torch.isfinite(fused).all()
+    assert torch.equal(fused, ref), f"max diff {(fused.float() - ref.float()).abs().max().item():.3e}"
+  # the counters are reset for the next call: a second fused call gives the same bits
+  again = _triangle_update(hip, zd, sd, fixup_sum_limit=limit, add_residual=True,
+                           stages=_lib.TRI_STAGE_ALL | _lib.TRI_STAGE_FUSE)
+  assert torch.equal(again, ref)
 
 
 @pytest.mark.parametrize("transpose", [False, True])
