@@ -108,6 +108,7 @@ struct FastWs {
   int* ctr;                           // fused epilogue: [G] per (row group, query block) heads done, then
                                       // the error word (see TriAttnArgs)
   uint8_t* defer;                     // [N] rows whose output the post kernel writes
+  int* rgl;                           // [1 + NP/4]: count, then the row groups with a valid row
   int nctr;                           // G + 4
   size_t bytes;
 };
@@ -134,6 +135,7 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.nctr = fused_groups(N) + 4;
   w.ctr = (int*)(p + off); off += round_up((size_t)w.nctr * 4);
   w.defer = (uint8_t*)(p + off); off += round_up((size_t)N);
+  w.rgl = (int*)(p + off); off += round_up((size_t)(1 + NP / 4) * 4);
   w.bytes = off;
   return w;
 }
@@ -151,13 +153,44 @@ struct TriFoldArgs {
   uint8_t* flags; int nflags;         // [N * H], cleared
   int* ctr; int nctr;                 // fused epilogue counters, cleared
   uint8_t* defer; int ndefer;         // fused epilogue deferred rows, cleared
+  // the attention rows worth computing: row groups (4 rows) with a row r < N and seq[r] != 0,
+  // listed in rgl[1..count], count in rgl[0] (null: no list)
+  int* rgl; int rg, N; const uint8_t* seq;
 };
 
 __global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
   const int lane = threadIdx.x & 63;
-  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nflags; f += gridDim.x * blockDim.x) a.flags[f] = 0;
-  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nctr; f += gridDim.x * blockDim.x) a.ctr[f] = 0;
-  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.ndefer; f += gridDim.x * blockDim.x) a.defer[f] = 0;
+  if (blockIdx.x == gridDim.x - 1) {                       // the extra last workgroup compacts the row groups
+    if (a.rgl == nullptr) return;
+    __shared__ int part[256];
+    const int tid = threadIdx.x, per_t = (a.rg + 255) / 256;
+    const int g0 = min(tid * per_t, a.rg), g1 = min(g0 + per_t, a.rg);
+    auto valid = [&](int g) {
+      bool v = false;
+      for (int r = 4 * g; r < 4 * g + 4 && r < a.N; ++r) v |= a.seq[r] != 0;
+      return v;
+    };
+    int cnt = 0;
+    for (int g = g0; g < g1; ++g) cnt += valid(g);
+    int inc = cnt;                                         // inclusive prefix within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o);
+      if (lane >= o) inc += v;
+    }
+    if (lane == 63) part[tid >> 6] = inc;                  // wave totals
+    __syncthreads();
+    int base = inc - cnt;                                  // exclusive prefix of the counts
+    for (int w = 0; w < (tid >> 6); ++w) base += part[w];
+    for (int g = g0; g < g1; ++g)
+      if (valid(g)) a.rgl[1 + base++] = g;
+    if (tid == 255) a.rgl[0] = base;
+    return;
+  }
+  const int zstride = (gridDim.x - 1) * blockDim.x;         // the folding workgroups clear the flags
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nflags; f += zstride) a.flags[f] = 0;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nctr; f += zstride) a.ctr[f] = 0;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.ndefer; f += zstride) a.defer[f] = 0;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= kPCols) return;
   const int c = 2 * lane;
@@ -555,6 +588,9 @@ struct TriAttnArgs {
                                       // [G] the error word (a wait timed out, or a group spanned XCDs)
   uint8_t* defer;                     // [N] 1: row left to tri_post_kernel (a head of the row was flagged)
   int groups;                         // G
+  // row groups to compute (rgl[0] = count, then their indices; null: all NP/4): tasks of row
+  // groups whose rows are all masked or past N are not run (the fix-up kernel writes masked rows)
+  const int* rgl;
 };
 
 constexpr int kTR = 4;                // rows per workgroup
@@ -622,10 +658,15 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   const int N = a.N, NP = a.NP, H = a.H;
 
   const int QB = (NP + 32 * kAW - 1) / (32 * kAW), RG = NP / kTR;
-  const int per = QB * RG * H / 8;                  // tasks per XCD (RG is a multiple of 16)
+  // row groups to run: the list of those with a valid row, or all (FUSED: the epilogue writes
+  // every row, masked ones included)
+  const int nrg = (!FUSED && a.rgl != nullptr) ? __builtin_amdgcn_readfirstlane(a.rgl[0]) : RG;
+  const int total = QB * nrg * H;
+  const int per = (total + 7) / 8;                  // tasks per XCD (FUSED: exact, a multiple of 4)
   const int xcd = blockIdx.x & 7, G8 = gridDim.x >> 3;
+  const int xper = max(0, min(per, total - xcd * per));   // this XCD's tasks (the last may have fewer)
   int task = blockIdx.x >> 3;                       // index within the XCD's range
-  if (task >= per) return;                          // uniform over the workgroup
+  if (task >= xper) return;                         // uniform over the workgroup
   // FUSED: the heads are innermost, so that the 4 tasks of a group (row group, query block) are
   // tasks 4m .. 4m+3 of an XCD's range, run in the same round by workgroups 4m' .. 4m'+3 of that
   // XCD (G8 is a multiple of 4): one L2 holds the o of all 4 heads for the group's epilogue.
@@ -638,8 +679,9 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       r0 = ((t >> 2) / QB) * kTR;
     } else {
       qb = t % QB;
-      r0 = ((t / QB) % RG) * kTR;
-      h = t / (QB * RG);
+      const int k = (t / QB) % nrg;
+      r0 = ((!FUSED && a.rgl != nullptr) ? __builtin_amdgcn_readfirstlane(a.rgl[1 + k]) : k) * kTR;
+      h = t / (QB * nrg);
     }
   };
 
@@ -965,7 +1007,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   int prev_gid = -1, prev_row = 0, prev_qb = 0;            // FUSED: the previous task's group
   for (;;) {
     const int next = task + G8;
-    const bool has_next = next < per;                      // uniform
+    const bool has_next = next < xper;                     // uniform
     int nr0 = 0, nh = 0, nqb = 0;
     const char* nsrc = wsrc;
     const char* nbsrc = bsrc;
@@ -1686,7 +1728,8 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     fa.flags = ws.flags; fa.nflags = N * H;
     fa.ctr = ws.ctr; fa.nctr = ws.nctr;
     fa.defer = ws.defer; fa.ndefer = N;
-    hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4), dim3(256), 0, st, fa);
+    fa.rgl = ws.rgl; fa.rg = NP / 4; fa.N = N; fa.seq = a->seq_mask;
+    hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4 + 1), dim3(256), 0, st, fa);
     if (int rc = sf_check_launch("tri_fold_kernel")) return rc;
 
     TriProjArgs pa{};
@@ -1707,6 +1750,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     aa.sum_limit = sum_limit(a->fixup_sum_limit);
     aa.q = ws.q; aa.k = ws.k; aa.vt = ws.vt; aa.bias = ws.bias; aa.seq = a->seq_mask; aa.o = ws.o;
     aa.flags = ws.flags;
+    aa.rgl = ws.rgl;                // (the fused kernel ignores it: its epilogue writes every row)
     const int total = ((NP + 32 * kAW - 1) / (32 * kAW)) * (NP / kTR) * H;   // a multiple of 64
     // attention with the gate, output projection and residual in its epilogue: the workgroups
     // of a group's four heads must be resident together on one XCD, so the grid is a multiple of

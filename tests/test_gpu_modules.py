@@ -78,6 +78,27 @@ def test_triangle_edge_sizes(transpose, N, padded):
   assert_close_bf16(upd, ref, f"triangle N={N} transpose={transpose}", max_abs=2e-2 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("N,masked", [(100, "all"), (300, "leading"), (257, "every_other_group")])
+def test_triangle_masked_row_groups(transpose, N, masked):
+  """Row groups (4 attention rows) whose rows are all masked or past N are not scheduled: every
+  token masked (no attention task runs; the fix-up writes every row), a masked prefix, and masks
+  that leave every other row group empty."""
+  mod, z, seq = W.make_triangle(N, transpose=transpose, seed=43, sharp=True)
+  if masked == "all":
+    seq[:] = False
+  elif masked == "leading":
+    seq[:37] = False
+  else:
+    seq[:] = torch.tensor([(i // 4) % 2 == 0 for i in range(N)])
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert torch.isfinite(upd).all()
+  assert_close_bf16(upd, ref, f"triangle N={N} masked={masked} transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
 def _triangle_update(hip, z, seq, add_residual=False, **kw):
   """The module's update through the C entry point with its packed weights (the module's own
   forward, plus the explicit test controls of ops.triangle_attention)."""
