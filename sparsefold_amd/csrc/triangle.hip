@@ -1377,7 +1377,8 @@ struct IbsArgs {
   unsigned long long seed;
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
-  float* bmean;                       // [H][T][NP] tile-mean bias (log2 units), keys as the planes store them
+  float* bmean;                       // tile-mean bias (log2 units), ibs_bmean_off order; -inf for keys
+                                      // past N or masked (no valid row attends them) and tiles past T
   int32_t* index; float* weight;      // [N][H][T][S]
   uint16_t* o;                        // o_off blocks (per head, attention row, 32 queries), as the dense stage writes them
   const uint8_t* flags;               // tri_ibs_attn_kernel: only (row, head) flagged here (null: all)
@@ -1390,44 +1391,85 @@ __device__ __forceinline__ unsigned long long ibs_mix64(unsigned long long x) {
   return x ^ (x >> 31);
 }
 
-__device__ __forceinline__ float ibs_uniform(unsigned long long seed, int row, int head, int tile, int draw) {
+// The hash of (seed, batch 0, row, head, tile): the part of a draw's hash all its draws share.
+__device__ __forceinline__ unsigned long long ibs_tile_hash(unsigned long long seed, int row, int head, int tile) {
   unsigned long long x = ibs_mix64(seed);
   x = ibs_mix64(x ^ 0ull);                                   // batch 0
   x = ibs_mix64(x ^ (unsigned long long)(unsigned)row);
   x = ibs_mix64(x ^ (unsigned long long)(unsigned)head);
-  x = ibs_mix64(x ^ (unsigned long long)(unsigned)tile);
-  x = ibs_mix64(x ^ (unsigned long long)(unsigned)draw);
+  return ibs_mix64(x ^ (unsigned long long)(unsigned)tile);
+}
+// Uniform in [0, 1) of draw `draw`: 24 bits of mix64(tile hash ^ draw).
+__device__ __forceinline__ float ibs_uniform(unsigned long long tile_hash, int draw) {
+  const unsigned long long x = ibs_mix64(tile_hash ^ (unsigned long long)(unsigned)draw);
   return (float)(x >> 40) * (1.0f / 16777216.0f);
 }
 
-// Tile-mean bias: one thread per (head, tile, stored key position); the means keep the bias
-// planes' key order, so a lane reads its 16 S^T keys of a block as 64 contiguous bytes.
+// Tile-mean bias of (head h, tile t, key j) at [h][t / 32][key block j / 32][quad][t % 32][j % 4]
+// with quad = 2 ((j % 32) / 8) + (j / 4) % 2: the sampler's lane (hf, li) seeds its S^T registers
+// 4u .. 4u + 3 (keys 32 b + 8u + 4 hf + 0..3) of tile 32 g + li from one 16-byte load, and the 32
+// lanes of a half read 512 contiguous bytes.
+__host__ __device__ __forceinline__ int64_t ibs_bmean_off(int h, int G, int KB, int t, int j) {
+  const int q4 = 2 * ((j & 31) >> 3) + ((j >> 2) & 1);
+  return (((((int64_t)h * G + (t >> 5)) * KB + (j >> 5)) * 8 + q4) * 32 + (t & 31)) * 4 + (j & 3);
+}
+
+// Tile-mean bias: one thread per (head, tile, key), in ibs_bmean_off order.  A key past N or
+// masked gets -inf: the sampler's logits then drop it with no per-key mask test (in a row with
+// seq[r] = 1 the valid keys are those with seq[j] = 1; masked rows are not sampled); tiles past T
+// (the last group's idle lanes) get -inf as well.
 __global__ __launch_bounds__(256) void tri_ibs_bias_mean_kernel(const IbsArgs a) {
+  const int KB = a.T, G = (a.T + 31) >> 5;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)a.H * a.T * a.NP) return;
-  const int jp = (int)(idx % a.NP), t = (int)((idx / a.NP) % a.T), h = (int)(idx / ((int64_t)a.NP * a.T));
+  if (idx >= (int64_t)a.H * G * KB * 1024) return;
+  const int c = (int)(idx & 3), tl = (int)((idx >> 2) & 31), q4 = (int)((idx >> 7) & 7);
+  const int64_t rest = idx >> 10;                            // (h, g, key block)
+  const int b = (int)(rest % KB), g = (int)((rest / KB) % G), h = (int)(rest / ((int64_t)KB * G));
+  const int t = 32 * g + tl, j = 32 * b + 8 * (q4 >> 1) + 4 * (q4 & 1) + c;
+  if (t >= a.T || j >= a.N || a.seq[j] == 0) { a.bmean[idx] = -INFINITY; return; }
+  const int js = (j & ~63) + bias_pos64(j & 63);
   const int i0 = 32 * t, i1 = min(a.N, i0 + 32);
   float sum = 0.f;
-  for (int i = i0; i < i1; ++i) sum += bf2f(a.bias[bias_off_stored(h, i, jp, a.NP)]);
+  for (int i = i0; i < i1; ++i) sum += bf2f(a.bias[bias_off_stored(h, i, js, a.NP)]);
   a.bmean[idx] = sum / (float)(i1 - i0);
 }
 
 // The sampler: one workgroup of 4 waves per (row r, head h, group of 32 query tiles); lane
-// (half, li) of every wave holds tile 32 g + li.  The tile-mean query is summed over 8 of each
-// tile's queries per wave and reduced through LDS; block logits S^T = K . qbar^T on the MFMA with
-// the mean split into two bf16 terms (hi + lo: about 16 significant bits), seeded with the
-// tile-mean bias; per block the log2 mass max + log2(sum 2^(x - max)) over its valid keys.  Wave
-// w takes the key blocks b = w mod 4 and, for the ranking, the same blocks again; lane (0, li) of
-// wave 0 then selects tile li's blocks.  LDS: log2 masses [KB][32], order | count << 16 [KB][32],
-// partial query sums [4][64][16].
+// (half, li) of every wave holds tile 32 g + li.  The tile sums of the query are read a whole
+// 2 KB tile at a time and reduced across lanes; block logits S^T = K . qbar^T on the MFMA with the
+// mean split into two bf16 terms (hi + lo: about 16 significant bits), seeded with the tile-mean
+// bias; per block the log2 mass max + log2(sum 2^(x - max)) over its valid keys.  Wave w takes
+// the key blocks b = w mod 4; for the ranking lane (hf, li) of wave w takes blocks b = w + 4 hf
+// mod 8, writing each block's mass 2^(l2 - M) at its rank.  Lane (0, li) of wave 0 then selects
+// tile li's blocks with running sums over those masses and the draw probabilities, each
+// computed once.  LDS: log2 masses [KB][32] (later the draw probabilities), order | count << 16
+// [KB][32], masses by rank [KB][32], and first, in the same bytes, the tile query sums
+// [32 tiles][4 pieces][8 dims].
 constexpr int kIbsIndexWaves = 4;
 
-__global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(const IbsArgs a) {
+// Sum over the 16 lanes of a DPP row, in every lane of it: mirror, half mirror, then the two
+// quad permutations pair each lane with the other 15.
+__device__ __forceinline__ float row16_sum(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xF, 0xF, true));
+  };
+  x += dpp(x, std::integral_constant<int, 0x140>{});       // row_mirror
+  x += dpp(x, std::integral_constant<int, 0x141>{});       // row_half_mirror
+  x += dpp(x, std::integral_constant<int, 0x1B>{});        // quad_perm [3, 2, 1, 0]
+  x += dpp(x, std::integral_constant<int, 0xB1>{});        // quad_perm [1, 0, 3, 2]
+  return x;
+}
+
+__global__ __launch_bounds__(64 * kIbsIndexWaves) __attribute__((amdgpu_waves_per_eu(8))) void tri_ibs_index_kernel(const IbsArgs a) {
   extern __shared__ float ibs_lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H, T = a.T, KB = a.T, S = a.S;
   const int G = (T + 31) >> 5;
-  const int task = blockIdx.x;                               // the grid is N * H * G
+  // the grid is N * H * G.  Workgroup i runs on XCD i mod 8: tasks are dealt so that each XCD
+  // takes a contiguous run of them, and the G tile groups of a (row, head), which read the same
+  // keys, meet in one L2
+  const int ntask = N * H * G, per = ntask >> 3;
+  const int task = (int)blockIdx.x < 8 * per ? (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
   const int g = task % G, h = (task / G) % H, r = task / (G * H);
   const int t = 32 * g + li, tc = min(t, T - 1);            // tc: operand tile of idle lanes
   const bool owner = wave == 0 && half == 0 && t < T;        // writes tile t's maps
@@ -1435,39 +1477,45 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
   float* wout = a.weight + (((int64_t)r * H + h) * T + tc) * S;
   float* lm = ibs_lds;
   int* ord = reinterpret_cast<int*>(ibs_lds + KB * 32);
-  float* qpart = ibs_lds + 2 * KB * 32;
+  float* smass = ibs_lds + 2 * KB * 32;                      // masses in rank order
   int filled = 0;
   if (a.seq[r] != 0) {                                       // uniform over the workgroup
-    // partial tile-mean query: queries 8 wave .. 8 wave + 7 of tile tc, pieces (kk, half)
+    // tile sums of the query: wave w sums tiles 32 g + 8 w .. + 7, one 2 KB tile (4 pieces of 32
+    // positions x 8 dims) per step: lane (row pc, p) adds positions p and p + 16 of piece pc, its
+    // 16-lane row then reduces (DPP); lane p = 0 stores the piece's 8 sums to qsum[tile][piece]
+    float* qsum = ibs_lds;                                   // [32][4][8], before lm / ord / smass
+    {
+      const int pc = lane >> 4, p = lane & 15;
+#pragma unroll 2
+      for (int it = 0; it < 8; ++it) {
+        const int tl = 8 * wave + it, tq = min(32 * g + tl, T - 1);
+        const uint16_t* qt = a.q + ql_off(r, h, H, NP, 32 * tq, 0, 0) + pc * 256 + p * 8;
+        const u32x4 v0 = ld16(qt), v1 = ld16(qt + 128);
+        float sv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[2 * e] = bflo(v0[e]) + bflo(v1[e]);
+          sv[2 * e + 1] = bfhi(v0[e]) + bfhi(v1[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[e] = row16_sum(sv[e]);
+        if (p == 0) {
+          f32x4* dst = reinterpret_cast<f32x4*>(qsum + (tl * 4 + pc) * 8);
+          dst[0] = f32x4{sv[0], sv[1], sv[2], sv[3]};
+          dst[1] = f32x4{sv[4], sv[5], sv[6], sv[7]};
+        }
+      }
+    }
+    __syncthreads();
     float qs[2][8];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < 2; ++kk) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(qsum + (li * 4 + 2 * kk + half) * 8);
+      const f32x4 x0 = src[0], x1 = src[1];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qs[kk][e] = 0.f;
-    const uint16_t* qp = a.q + ql_off(r, h, H, NP, 32 * tc, 0, half) + 8 * (8 * wave);
-    {
-      u32x4 v[8][2];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) v[u][kk] = ld16(qp + u * 8 + kk * 512);
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { qs[kk][2 * e] += bflo(v[u][kk][e]); qs[kk][2 * e + 1] += bfhi(v[u][kk][e]); }
+      for (int e = 0; e < 4; ++e) { qs[kk][e] = x0[e]; qs[kk][4 + e] = x1[e]; }
     }
-#pragma unroll
-    for (int x = 0; x < 16; ++x) qpart[(wave * 64 + lane) * 16 + x] = qs[x >> 3][x & 7];
-    __syncthreads();
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kIbsIndexWaves; ++w) sum += qpart[(w * 64 + lane) * 16 + x];   // fixed order
-      qs[x >> 3][x & 7] = sum;
-    }
+    __syncthreads();                                         // qsum read: lm may be written
     const float qinv = 1.0f / (float)(min(N, 32 * tc + 32) - 32 * tc);   // queries past N hold 0
     bf16x8 qh[2], ql[2];
 #pragma unroll
@@ -1479,34 +1527,39 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
         qh[kk][e] = hv;
         ql[kk][e] = (__bf16)(v - (float)hv);
       }
-    const float* bm = a.bmean + ((int64_t)h * T + tc) * NP;
-    for (int b = wave; b < KB; b += kIbsIndexWaves) {
+    const float* bm = a.bmean + ibs_bmean_off(h, G, KB, t, 0);   // tile t's column (past T: -inf)
+    // block b's operands: K (two k-chunks) and the tile-mean bias of its 16 keys in this lane
+    auto load_block = [&](int b, u32x4 (&kv)[2], f32x16& bv) {
       const int j = 32 * b + li;
-      const uint32_t vm = (uint32_t)__ballot(j < N && a.seq[j] != 0);   // bit k: key 32 b + k valid
-      const bf16x8 k0 = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, j, 0, half)));
-      const bf16x8 k1 = as_bf16x8(ld16(a.k + ql_off(r, h, H, NP, j, 1, half)));
-      const float* bp = bm + 64 * (b >> 1) + 32 * (b & 1) + 16 * half;
-      f32x16 sc;
+      kv[0] = ld16(a.k + ql_off(r, h, H, NP, j, 0, half));
+      kv[1] = ld16(a.k + ql_off(r, h, H, NP, j, 1, half));
+      const float* bp = bm + (int64_t)b * 8 * 128 + half * 128;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(bp + 4 * u);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(bp + u * 256);   // quad 2u + hf
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sc[4 * u + e] = v[e];
+        for (int e = 0; e < 4; ++e) bv[4 * u + e] = v[e];
       }
+    };
+    for (int b = wave; b < KB; b += kIbsIndexWaves) {
+      u32x4 kn[2];
+      f32x16 sc;                                             // seeded with the tile-mean bias
+      load_block(b, kn, sc);
+      const bf16x8 k0 = as_bf16x8(kn[0]), k1 = as_bf16x8(kn[1]);
       sc = mfma32(k0, qh[0], sc);
       sc = mfma32(k1, qh[1], sc);
       sc = mfma32(k0, ql[0], sc);
       sc = mfma32(k1, ql[1], sc);
+      // invalid keys hold -inf (their tile-mean bias): they add exactly 0.  The hardware exp2
+      // (no denormal range reduction): a term below 2^-126 is lost against the block maximum's 1
       float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if ((vm >> (8 * (e >> 2) + 4 * half + (e & 3))) & 1u) mx = fmaxf(mx, sc[e]);
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[e]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       float sum = 0.f;
       if (mx != -INFINITY) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if ((vm >> (8 * (e >> 2) + 4 * half + (e & 3))) & 1u) sum += exp2f(sc[e] - mx);
+        for (int e = 0; e < 16; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
       }
       sum += __shfl_xor(sum, 32);
       const float l2 = mx + log2f(sum);
@@ -1521,16 +1574,27 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
       nvalid += v != -INFINITY;
     }
     // descending mass, ties: lower index first; blocks without valid keys are not ranked
-    if (nvalid > S && half == 0) {
-      for (int b = wave; b < KB; b += kIbsIndexWaves) {
-        const float v = lm[b * 32 + li];
-        if (v == -INFINITY) continue;
+    if (nvalid > S) {
+      // half hf ranks block b0 + 4 hf; the loop bounds stay wave-uniform: blocks c < b0 count when
+      // at least as heavy (ties: the lower index first), c > b0 + 4 when heavier
+      const int w0 = __builtin_amdgcn_readfirstlane(wave);
+      for (int b0 = w0; b0 < KB; b0 += 2 * kIbsIndexWaves) {
+        const int b = b0 + kIbsIndexWaves * half;
+        const float v = b < KB ? lm[b * 32 + li] : -INFINITY;
         int rank = 0;
-        for (int c = 0; c < KB; ++c) {
+#pragma unroll 8
+        for (int c = 0; c < b0; ++c) rank += lm[c * 32 + li] >= v;
+        const int c1 = min(b0 + kIbsIndexWaves + 1, KB);
+        for (int c = b0; c < c1; ++c) {
           const float u = lm[c * 32 + li];
           rank += (u > v) || (u == v && c < b);
         }
-        ord[rank * 32 + li] = b;
+#pragma unroll 8
+        for (int c = c1; c < KB; ++c) rank += lm[c * 32 + li] > v;
+        if (v != -INFINITY) {
+          ord[rank * 32 + li] = b;
+          smass[rank * 32 + li] = exp2f(v - M);
+        }
       }
     }
     __syncthreads();
@@ -1539,7 +1603,7 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
         for (int b = 0; b < KB; ++b)
           if (lm[b * 32 + li] != -INFINITY) { iout[filled] = b; wout[filled] = 1.f; ++filled; }
       } else {
-        auto mass = [&](int k) { return exp2f(lm[(ord[k * 32 + li] & 0xFFFF) * 32 + li] - M); };
+        auto mass = [&](int k) { return smass[k * 32 + li]; };
         float total = 0.f;
         for (int k = 0; k < nvalid; ++k) total += mass(k);
         const float inv = 1.0f / total;
@@ -1553,15 +1617,23 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
         if (nc > 0 && a.R > 0) {
           float mc = 0.f;
           for (int c = 0; c < nc; ++c) mc += mass(ns + c) * inv;
-          auto raw = [&](int c) { return mc > 0.f ? fmaxf(mass(ns + c) * inv / mc, a.u_prob) : 1.0f; };
+          // the draw probabilities q_c = raw_c / sum raw once, in the (now free) log2-mass
+          // column of this tile
+          float* qc = lm;
           float zr = 0.f;
-          for (int c = 0; c < nc; ++c) zr += raw(c);
+          for (int c = 0; c < nc; ++c) {
+            const float rc = mc > 0.f ? fmaxf(mass(ns + c) * inv / mc, a.u_prob) : 1.0f;
+            qc[c * 32 + li] = rc;
+            zr += rc;
+          }
+          for (int c = 0; c < nc; ++c) qc[c * 32 + li] = qc[c * 32 + li] / zr;
+          const unsigned long long th = ibs_tile_hash(a.seed, r, h, t);
           for (int d = 0; d < a.R; ++d) {
-            const float uu = ibs_uniform(a.seed, r, h, t, d);
+            const float uu = ibs_uniform(th, d);
             float acc = 0.f;
             int pick = nc - 1;
             for (int c = 0; c < nc; ++c) {
-              acc += raw(c) / zr;
+              acc += qc[c * 32 + li];
               if (uu < acc) { pick = c; break; }
             }
             ord[(ns + pick) * 32 + li] += 1 << 16;
@@ -1570,7 +1642,7 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) void tri_ibs_index_kernel(cons
             const int cnt = ord[(ns + c) * 32 + li] >> 16;
             if (cnt == 0) continue;
             iout[filled] = ord[(ns + c) * 32 + li] & 0xFFFF;
-            wout[filled] = (float)cnt / ((float)a.R * (raw(c) / zr));
+            wout[filled] = (float)cnt / ((float)a.R * qc[c * 32 + li]);
             ++filled;
           }
         }
@@ -1872,8 +1944,8 @@ extern "C" int sf_hip_triangle_stage_fwd(const sf_triangle_args* a, int32_t stag
 namespace {
 size_t ibs_bmean_offset(int32_t N, int32_t H) { return carve_fast(nullptr, N, H).bytes; }
 size_t ibs_ws_bytes(int32_t N, int32_t H) {
-  const int NP = round_np(N), T = (N + 31) / 32;
-  return ibs_bmean_offset(N, H) + round_up((size_t)H * T * NP * 4);
+  const int T = (N + 31) / 32, G = (T + 31) / 32;
+  return ibs_bmean_offset(N, H) + round_up((size_t)H * G * T * 1024 * 4);
 }
 }  // namespace
 
@@ -1918,11 +1990,11 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
   ia.index = p->index_map; ia.weight = p->weight_map; ia.o = ws.o;
   const int64_t tasks = (int64_t)ia.N * ia.H * ia.T;
   if (p->generate_maps) {
-    const int64_t nb = (int64_t)ia.H * ia.T * ia.NP;
+    const int64_t nb = (int64_t)ia.H * ((ia.T + 31) / 32) * ia.T * 1024;
     hipLaunchKernelGGL(tri_ibs_bias_mean_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, ia);
     if ((rc = sf_check_launch("tri_ibs_bias_mean_kernel"))) return rc;
     const int groups = (ia.T + 31) / 32;
-    const size_t lds = (size_t)2 * ia.T * 32 * 4 + kIbsIndexWaves * 64 * 16 * 4;   // <= 80 KB (T <= 256)
+    const size_t lds = std::max((size_t)3 * ia.T * 32 * 4, (size_t)32 * 4 * 8 * 4);   // <= 96 KB (T <= 256)
     hipLaunchKernelGGL(tri_ibs_index_kernel, dim3((unsigned)(ia.N * ia.H * groups)), dim3(64 * kIbsIndexWaves), lds,
                        st, ia);
     if ((rc = sf_check_launch("tri_ibs_index_kernel"))) return rc;
