@@ -472,6 +472,230 @@ extern "C" size_t sf_hip_cross_attention_workspace_bytes(const sf_cross_attentio
 }
 
 namespace {
+// ---------------------------------------------------------------------------------------
+// Window attention and the output stage in one kernel (per-atom plan; 32-query / 128-key
+// windows, H = 4, D = 32, C = 128): one workgroup per (sample s, window u), wave h runs head h.
+// CrossAttention.forward (transformer.py:549-585) after the q/g, k/v projections:
+//   S^T  = K Q^T + bias / scale (+ SF_MASKED_LOGIT for masked keys; a masked query weighs every
+//          key equally), K gathered row by row straight into the MFMA A operand
+//   P    = 2^(scale log2e (S^T - m)), m the exact maximum over the 128 keys, as bf16; l = sum P
+//   O^T  = V^T P^T, the window's 128 V rows of head h copied into LDS (global_load_lds) and read
+//          transposed (ds_read_b64_tr_b16)
+//   og   = O / l * sigmoid(g) -> LDS [query][h * 32 + d] (over the V rows, after a barrier)
+//   out  = og W_t2^T * zgate + x: wave w takes output channels 32w .. 32w + 31
+// Against the separate attention and output-projection kernels this drops the o round trip
+// (the attention's store and the projection's load) and a launch; every window's bias tile is
+// read by its 5 samples from one L2 (task order below).
+// ---------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint32_t lds_u32w;
+typedef short v4i16w __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16w lds_v4i16w;
+
+struct WinFusedArgs {
+  int S, U, A;                          // samples, windows, atoms per sample (= 32 U)
+  const uint16_t* yq;                   // [S * A][256]: q (h * 32 + d) | g (128 + h * 32 + d)
+  const uint16_t* ykv;                  // [S][A + 1][256]: k | v, row A zero
+  const int32_t* gidx; const uint8_t* gmask;   // [U][128] key -> atom, gather mask
+  const uint8_t *mask_q, *mask_k;       // [U][32], [U][128] (null: all valid)
+  const uint16_t* bias;                 // [U][4][32][128] (null: none)
+  const uint16_t* w_t2;                 // [128][128]: output channel x (h * 32 + d)
+  const uint16_t* zgate; int64_t zrs;   // [A] rows of 128, row stride zrs
+  const uint16_t* x;                    // residual [S * A][128] (null: none)
+  uint16_t* out;                        // [S * A][128]
+  float cs, inv_scale;                  // scale * log2 e, 1 / scale
+};
+constexpr int kWinOgPitch = 136;        // og rows in LDS (bf16): 272 bytes apart, conflict-free
+
+// (at most 128 registers: four workgroups per CU)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void window_attn_out_kernel(const WinFusedArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * 8192];   // V rows per wave, then og
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int h = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, li = lane & 31;
+  // Workgroup b runs on XCD b mod 8: each XCD takes a contiguous run of (window, sample) tasks,
+  // so the samples of a window (one bias tile) meet in one L2.
+  const int ntask = a.S * a.U, per = ntask >> 3;
+  const int task = (int)blockIdx.x < 8 * per ? (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int u = task / a.S, s = task - u * a.S;
+  const int64_t qrow = (int64_t)s * a.A + 32 * u;            // row of query 0 in yq / x / out
+  const uint16_t* kv = a.ykv + (int64_t)s * (a.A + 1) * 256;
+
+  // rows of keys lane and lane + 64: the zero row A for a gather-masked or out-of-range key
+  int rowA, rowB;
+  {
+    const int32_t i0 = a.gidx[(int64_t)u * 128 + lane], i1 = a.gidx[(int64_t)u * 128 + lane + 64];
+    const uint8_t m0 = a.gmask[(int64_t)u * 128 + lane], m1 = a.gmask[(int64_t)u * 128 + lane + 64];
+    rowA = (m0 == 0 || i0 < 0 || i0 >= a.A) ? a.A : i0;
+    rowB = (m1 == 0 || i1 < 0 || i1 >= a.A) ? a.A : i1;
+  }
+  // V rows of head h -> LDS [key][32 dims] (64 bytes a row): copy c moves keys 16c .. 16c + 15
+  uint8_t* vsm = smem + h * 8192;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int key = 16 * c + (lane >> 2);
+    const int row = __shfl(c < 4 ? rowA : rowB, key & 63);
+    __builtin_amdgcn_global_load_lds(kv + (int64_t)row * 256 + 128 + h * 32 + 8 * (lane & 3),
+                                     (lds_u32w*)(vsm + c * 1024), 16, 0, 0);
+  }
+  // K (A operand of S^T, lane (half, li): key 32 kb + li, dims 16 kk + 8 half ..) and Q (B operand)
+  u32x4 kr[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const int row = __shfl(kb < 2 ? rowA : rowB, (32 * kb + li) & 63);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) kr[kb][kk] = ld16(kv + (int64_t)row * 256 + h * 32 + 16 * kk + 8 * half);
+  }
+  const uint16_t* qp = a.yq + (qrow + li) * 256 + h * 32 + 8 * half;
+  const bf16x8 qb0 = as_bf16x8(ld16(qp)), qb1 = as_bf16x8(ld16(qp + 16));
+  // bias of query li, keys 32 kb + 8 j + 4 half .. + 3 (S^T registers 4 j .. 4 j + 3 of block kb)
+  u32x2 br[4][4];
+  if (a.bias != nullptr) {
+    const uint16_t* bp = a.bias + (((int64_t)u * 4 + h) * 32 + li) * 128 + 4 * half;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) br[kb][j] = *reinterpret_cast<const u32x2*>(bp + 32 * kb + 8 * j);
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) br[kb][j] = u32x2{0, 0};
+  }
+  const bool kvalid0 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane] != 0;
+  const bool kvalid1 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane + 64] != 0;
+  const uint64_t mk0 = __ballot(kvalid0), mk1 = __ballot(kvalid1);
+  const bool qvalid = a.mask_q == nullptr || a.mask_q[(int64_t)u * 32 + li] != 0;
+
+  // ---- S^T = K Q^T + bias / scale, masks ----
+  f32x16 sc[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        sc[kb][4 * j + 2 * e] = bflo(br[kb][j][e]) * a.inv_scale;
+        sc[kb][4 * j + 2 * e + 1] = bfhi(br[kb][j][e]) * a.inv_scale;
+      }
+    sc[kb] = mfma32(as_bf16x8(kr[kb][0]), qb0, sc[kb]);
+    sc[kb] = mfma32(as_bf16x8(kr[kb][1]), qb1, sc[kb]);
+  }
+  if ((mk0 & mk1) != ~0ull) {                               // uniform: some key masked
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      // bit 8 j + i: key 32 kb + 8 j + 4 half + i, S^T register 4 j + i
+      const uint32_t mw = (uint32_t)((kb < 2 ? mk0 : mk1) >> (32 * (kb & 1) + 4 * half));
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (((mw >> (8 * (r >> 2) + (r & 3))) & 1u) == 0) sc[kb][r] += SF_MASKED_LOGIT;
+    }
+  }
+  if (!qvalid) {                                            // masked query: every key alike
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
+  }
+  // ---- P against the exact row maximum ----
+  float m = sc[0][0];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[kb][r]);
+  m = fmaxf(m, __shfl_xor(m, 32));
+  const float mb = m * a.cs;
+  bf16x2 pw[32];
+  float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(sc[kb][2 * e], a.cs, -mb)),
+                               fast_exp2(__builtin_fmaf(sc[kb][2 * e + 1], a.cs, -mb)));
+      if (e & 1) l1 = add_bf2(pw[8 * kb + e], l1); else l0 = add_bf2(pw[8 * kb + e], l0);
+    }
+  float l = l0 + l1;
+  l += __shfl_xor(l, 32);
+
+  // ---- O^T = V^T P^T ----
+  __builtin_amdgcn_s_waitcnt(0);                            // this wave's V copies have landed
+  asm volatile("" ::: "memory");
+  // gate of query li, dims 8 j + 4 half .. + 3 (O^T registers 4 j .. 4 j + 3), and W_t2 rows
+  // 32 h + li (A operand of the projection; L2-resident): in flight during P.V
+  u32x2 gr[4];
+  const uint16_t* gp = a.yq + (qrow + li) * 256 + 128 + h * 32 + 4 * half;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) gr[j] = *reinterpret_cast<const u32x2*>(gp + 8 * j);
+  u32x4 wr[8];
+  const uint16_t* wp = a.w_t2 + (int64_t)(32 * h + li) * 128 + 8 * half;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) wr[kk] = ld16(wp + 16 * kk);
+  // zero-gate and residual of the output channels 32 h + 8 j + 4 half .. + 3 of query li
+  const int64_t orow = qrow + li;
+  const uint16_t* zp = a.zgate + (int64_t)(32 * u + li) * a.zrs + 32 * h + 4 * half;
+  u32x2 zg[4], xr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    zg[j] = *reinterpret_cast<const u32x2*>(zp + 8 * j);
+    xr[j] = a.x != nullptr ? *reinterpret_cast<const u32x2*>(a.x + orow * 128 + 32 * h + 8 * j + 4 * half) : u32x2{0, 0};
+  }
+  f32x16 o;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o[r] = 0.f;
+  {
+    const int grp = lane >> 4, gi = lane & 15, ekey = gi >> 2, q4 = gi & 3;
+    const int d = 16 * (grp & 1) + 4 * q4;
+#pragma unroll
+    for (int c2 = 0; c2 < 8; ++c2) {
+      bf16x8 pb;
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        pb[2 * q2] = pw[4 * c2 + q2][0];
+        pb[2 * q2 + 1] = pw[4 * c2 + q2][1];
+      }
+      u32x2 part[2];
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd) {
+        const int key = 16 * c2 + 8 * rd + 4 * (grp >> 1) + ekey;
+        const int off = key * 64 + ((d >> 3) << 4) + ((d >> 2) & 1) * 8;
+        part[rd] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16w*)(vsm + off)));
+      }
+      o = mfma32(as_bf16x8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]}), pb, o);
+    }
+  }
+  // ---- og = O / l * sigmoid(g) -> LDS (the V rows of every wave are then dead) ----
+  const float inv = 1.0f / l;
+  __syncthreads();
+  uint16_t* og = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float v0 = o[4 * j] * inv * sigmoidf_(bflo(gr[j][0]));
+    const float v1 = o[4 * j + 1] * inv * sigmoidf_(bfhi(gr[j][0]));
+    const float v2 = o[4 * j + 2] * inv * sigmoidf_(bflo(gr[j][1]));
+    const float v3 = o[4 * j + 3] * inv * sigmoidf_(bfhi(gr[j][1]));
+    *reinterpret_cast<u32x2*>(og + li * kWinOgPitch + 32 * h + 8 * j + 4 * half) =
+        u32x2{pack_bf2(v0, v1), pack_bf2(v2, v3)};
+  }
+  __syncthreads();
+  // ---- out^T (channels 32 h .. + 31, this wave) = W_t2 og^T; * zgate + x ----
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    acc = mfma32(as_bf16x8(wr[kk]), as_bf16x8(ld16(og + li * kWinOgPitch + 16 * kk + 8 * half)), acc);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v[4] = {acc[4 * j] * bflo(zg[j][0]), acc[4 * j + 1] * bfhi(zg[j][0]),
+                  acc[4 * j + 2] * bflo(zg[j][1]), acc[4 * j + 3] * bfhi(zg[j][1])};
+    if (a.x != nullptr) {                                   // uniform
+      v[0] += bflo(xr[j][0]); v[1] += bfhi(xr[j][0]); v[2] += bflo(xr[j][1]); v[3] += bfhi(xr[j][1]);
+    }
+    *reinterpret_cast<u32x2*>(a.out + orow * 128 + 32 * h + 8 * j + 4 * half) =
+        u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+  }
+}
+
 // The per-atom plan: AdaLN of every atom for both sides from the given terms, q/g and k/v
 // projected once per atom, the attention gathering each window's K / V rows, AdaLN-zero output.
 int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t st) {
@@ -518,6 +742,20 @@ int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t s
                      reinterpret_cast<u32x4*>(static_cast<uint16_t*>(ykv) + A * 2 * HD), (A + 1) * 2 * HD * 2 / 16,
                      a->S, words);
   if ((rc = sf_check_launch("zero_rows_kernel"))) return rc;
+  }
+  if (a->Qw == 32 && a->Kw == 128 && a->H == 4 && a->D == 32 && C == 128 && (int64_t)a->S * a->U < (1ll << 31)) {
+    WinFusedArgs f{};
+    f.S = a->S; f.U = a->U; f.A = (int)A;
+    f.yq = static_cast<const uint16_t*>(yq); f.ykv = static_cast<const uint16_t*>(ykv);
+    f.gidx = a->gather_idx; f.gmask = a->gather_mask; f.mask_q = a->mask_q; f.mask_k = a->mask_k;
+    f.bias = static_cast<const uint16_t*>(a->bias); f.w_t2 = static_cast<const uint16_t*>(a->w_t2);
+    f.zgate = static_cast<const uint16_t*>(a->pre_zgate); f.zrs = a->pre_rs;
+    f.x = a->add_residual ? static_cast<const uint16_t*>(a->xq) : nullptr;
+    f.out = static_cast<uint16_t*>(a->out);
+    const float scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
+    f.cs = scale * SF_LOG2E; f.inv_scale = 1.0f / scale;
+    hipLaunchKernelGGL(window_attn_out_kernel, dim3((unsigned)(a->S * a->U)), dim3(256), 0, st, f);
+    return sf_check_launch("window_attn_out_kernel");
   }
   const sf_attention_args t = cross_prepared_attn_args(a, yq, ykv, o);
   const size_t split = sf_attention_workspace_bytes(&t);
