@@ -1229,77 +1229,70 @@ __device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Rows the attention kernel cannot finish on its fast path, one workgroup per attention row:
+// Rows the attention kernel cannot finish on its fast path, one workgroup per (attention row,
+// head):
 //  * rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
 //    reference's softmax is uniform over the N keys: o = mean_k V[r, k] (gated later, like
 //    every other row).  Keys past N hold V = 0.
 //  * (row, head) pairs flagged by tri_attn_kernel (a weight sum out of range): recomputed with
 //    an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from the same
-//    Q, K, V^T and bias operands, one query per thread; the flag is cleared afterwards.
-// Rows with nothing to do return at once.
+//    Q, K, V^T and bias operands, one query per thread, by the row's head-0 workgroup; the flag
+//    is cleared afterwards.
+// Workgroups with nothing to do return at once.
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
-  const int r = blockIdx.x;
+  const int H = a.H, r = blockIdx.x / H, hb = blockIdx.x - r * H;   // the grid is N * H
   if (r >= a.N) return;
-  const int tid = threadIdx.x, N = a.N, NP = a.NP, H = a.H;
+  const int tid = threadIdx.x, N = a.N, NP = a.NP;
   // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
   if (a.seq[r] == 0) {
-    // sum over the keys: thread (part, head, dim), part p of the 16-key chunks; sixteen loads in
-    // flight per thread (H * 32 = 128 on this path).  With four, each masked row took a dozen
-    // dependent round trips: 40 us of tail for the 76 padded rows of N = 768.
-    __shared__ float part[2][4 * 32];
-    __shared__ float mean[4 * 32];
+    // head hb of a masked row.  Sum over the keys: thread (part p, dim d), part p of the 16-key
+    // chunks, all of its loads in flight; then the mean, and the N queries' o of the head.
+    // (One workgroup per row, all heads, took 8.5 us for the 38 padded rows of N = 384: a
+    // single workgroup's load, reduce and store chain per row is the whole kernel.)
+    __shared__ float part[8][32];
+    __shared__ float mean[32];
     {
-      const int hd = tid & 127, h = hd >> 5, d = hd & 31, pp = tid >> 7;
-      const int nc = NP / 16, c0 = pp * (nc / 2), c1 = pp ? nc : nc / 2;
+      const int d = tid & 31, pp = tid >> 5, nc = NP / 16;
       float s0 = 0.f, s1 = 0.f;
-      int c16 = c0;
-      for (; c16 + 8 <= c1; c16 += 8) {
-        u32x4 v[16];
+      for (int c0 = pp; c0 < nc; c0 += 8 * 4) {              // chunks c0 + 8u, u < 4: all loads issued together
+        u32x4 v[8];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = ld16(a.vt + vl_off(r, h, H, NP, c16 + (u >> 1), u & 1, d));
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
-      }
-      for (; c16 + 2 <= c1; c16 += 2) {
-        u32x4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = ld16(a.vt + vl_off(r, h, H, NP, c16 + (u >> 1), u & 1, d));
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
-      }
-      for (; c16 < c1; ++c16)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const u32x4 v = ld16(a.vt + vl_off(r, h, H, NP, c16, hf, d));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { s0 += bflo(v[e]); s1 += bfhi(v[e]); }
+        for (int u = 0; u < 8; ++u) {
+          const int c16 = c0 + 8 * (u >> 1);
+          v[u] = c16 < nc ? ld16(a.vt + vl_off(r, hb, H, NP, c16, u & 1, d)) : u32x4{0, 0, 0, 0};
         }
-      part[pp][hd] = s0 + s1;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
+      }
+      part[pp][d] = s0 + s1;
     }
     __syncthreads();
-    if (tid < 128) mean[tid] = (part[0][tid] + part[1][tid]) / (float)N;
+    if (tid < 32) {
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) t += part[q][tid];
+      mean[tid] = t / (float)N;
+    }
     __syncthreads();
-    // one (query, head, lane half) per thread: 16 dims in epilogue order; consecutive threads
-    // write consecutive queries of one piece
-    for (int t = tid; t < N * H * 2; t += 256) {
-      const int i = t % N, hf = (t / N) & 1, h = t / (2 * N);
+    // one (query, lane half) per thread: 16 dims in epilogue order; consecutive threads write
+    // consecutive queries of one piece
+    for (int t = tid; t < N * 2; t += 256) {
+      const int i = t % N, hf = t / N;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = pack_bf2(mean[h * 32 + slot_dim(hf, kk, 2 * e)], mean[h * 32 + slot_dim(hf, kk, 2 * e + 1)]);
-        st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        for (int e = 0; e < 4; ++e) w[e] = pack_bf2(mean[slot_dim(hf, kk, 2 * e)], mean[slot_dim(hf, kk, 2 * e + 1)]);
+        st16(a.o + o_off(hb, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
       }
     }
     return;
   }
+  if (hb != 0) return;                                   // flagged heads: one workgroup per row
   if (a.sparse) return;                                  // flagged block-sparse rows: not here
   tri_exact_heads(a, r, tid);
 }
@@ -1841,7 +1834,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     }
     hipLaunchKernelGGL(tri_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
-    hipLaunchKernelGGL(tri_fixup_kernel, dim3(N), dim3(256), 0, st, aa);
+    hipLaunchKernelGGL(tri_fixup_kernel, dim3(N * a->H), dim3(256), 0, st, aa);
     if (int rc = sf_check_launch("tri_fixup_kernel")) return rc;
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
@@ -2012,7 +2005,7 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
   }
   hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
   if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
-  hipLaunchKernelGGL(tri_fixup_kernel, dim3(a->N), dim3(256), 0, st, fa);   // masked rows: mean of V
+  hipLaunchKernelGGL(tri_fixup_kernel, dim3(a->N * a->H), dim3(256), 0, st, fa);   // masked rows: mean of V
   if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
   return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);
 }
