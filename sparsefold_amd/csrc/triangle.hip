@@ -1173,11 +1173,11 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_fused_kernel(const TriAttnA
 // recomputed with an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from
 // the same Q, K, V^T and bias operands, one query per thread of a 256-thread workgroup; each flag
 // is cleared afterwards.
-__device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
+__device__ void tri_exact_head(const TriAttnArgs& a, int r, int h, int tid) {
   const int N = a.N, NP = a.NP, H = a.H;
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
-  for (int h = 0; h < H; ++h) {
-    if (a.flags[r * H + h] == 0) continue;               // same address for every thread: uniform
+  {
+    if (a.flags[r * H + h] == 0) return;                 // same address for every thread: uniform
     for (int i = tid; i < N; i += 256) {
       // q.k is invariant under the common dim permutation of the Q / K layouts: dot in storage order
       float q[32];
@@ -1227,74 +1227,93 @@ __device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
     if (tid == 0) a.flags[r * H + h] = 0;
   }
 }
+__device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
+  for (int h = 0; h < a.H; ++h) tri_exact_head(a, r, h, tid);
+}
 
 // ---------------------------------------------------------------------------------------
-// Rows the attention kernel cannot finish on its fast path, one workgroup per (attention row,
-// head):
+// Rows the attention kernel cannot finish on its fast path, per (attention row, head) item, the
+// items dealt over a fixed grid (a launch of one workgroup per row cost ~4.6 us when every row
+// was a no-op):
 //  * rows whose token is masked (seq[r] == 0): every logit of the row is masked, so the
 //    reference's softmax is uniform over the N keys: o = mean_k V[r, k] (gated later, like
 //    every other row).  Keys past N hold V = 0.
 //  * (row, head) pairs flagged by tri_attn_kernel (a weight sum out of range): recomputed with
 //    an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from the same
-//    Q, K, V^T and bias operands, one query per thread, by the row's head-0 workgroup; the flag
-//    is cleared afterwards.
-// Workgroups with nothing to do return at once.
+//    Q, K, V^T and bias operands, one query per thread; the flag is cleared afterwards.
 // ---------------------------------------------------------------------------------------
+constexpr int kFixupGrid = 512;       // workgroups of tri_fixup_kernel (items strided over them)
 __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
-  const int H = a.H, r = blockIdx.x / H, hb = blockIdx.x - r * H;   // the grid is N * H
-  if (r >= a.N) return;
-  const int tid = threadIdx.x, N = a.N, NP = a.NP;
+  const int H = a.H, tid = threadIdx.x, N = a.N, NP = a.NP, items = N * H;
   // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
-  if (a.seq[r] == 0) {
-    // head hb of a masked row.  Sum over the keys: thread (part p, dim d), part p of the 16-key
-    // chunks, all of its loads in flight; then the mean, and the N queries' o of the head.
-    // (One workgroup per row, all heads, took 8.5 us for the 38 padded rows of N = 384: a
-    // single workgroup's load, reduce and store chain per row is the whole kernel.)
-    __shared__ float part[8][32];
-    __shared__ float mean[32];
+  __shared__ float part[8][32];
+  __shared__ float mean[32];
+  __shared__ int list[256];
+  __shared__ int nlist;
+  // this workgroup's items are blockIdx.x + k gridDim.x; 256 of them are checked at once, one per
+  // thread (checked one after another, each a dependent load, a no-op launch took 9 us)
+  const int K = (items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  for (int k0 = 0; k0 < K; k0 += 256) {
+    if (tid == 0) nlist = 0;
+    __syncthreads();
     {
-      const int d = tid & 31, pp = tid >> 5, nc = NP / 16;
-      float s0 = 0.f, s1 = 0.f;
-      for (int c0 = pp; c0 < nc; c0 += 8 * 4) {              // chunks c0 + 8u, u < 4: all loads issued together
-        u32x4 v[8];
+      const int k = k0 + tid, item = (int)blockIdx.x + k * (int)gridDim.x;
+      if (k < K && (a.seq[item / H] == 0 || (!a.sparse && a.flags[item] != 0))) list[atomicAdd(&nlist, 1)] = item;
+    }
+    __syncthreads();
+    const int n = nlist;
+    for (int w = 0; w < n; ++w) {                          // (row r, head hb)
+      const int item = list[w], r = item / H, hb = item - r * H;
+      if (a.seq[r] != 0) {                               // a flagged (row, head): exact recompute
+        tri_exact_head(a, r, hb, tid);
+        continue;
+      }
+      // head hb of a masked row.  Sum over the keys: thread (part p, dim d), part p of the 16-key
+      // chunks, all of its loads in flight; then the mean, and the N queries' o of the head.
+      // (One workgroup per row, all heads, took 8.5 us for the 38 padded rows of N = 384: a
+      // single workgroup's load, reduce and store chain per row is the whole kernel.)
+      {
+        const int d = tid & 31, pp = tid >> 5, nc = NP / 16;
+        float s0 = 0.f, s1 = 0.f;
+        for (int c0 = pp; c0 < nc; c0 += 8 * 4) {        // chunks c0 + 8u, u < 4: all loads issued together
+          u32x4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int c16 = c0 + 8 * (u >> 1);
-          v[u] = c16 < nc ? ld16(a.vt + vl_off(r, hb, H, NP, c16, u & 1, d)) : u32x4{0, 0, 0, 0};
+          for (int u = 0; u < 8; ++u) {
+            const int c16 = c0 + 8 * (u >> 1);
+            v[u] = c16 < nc ? ld16(a.vt + vl_off(r, hb, H, NP, c16, u & 1, d)) : u32x4{0, 0, 0, 0};
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { s0 += bflo(v[u][e]); s1 += bfhi(v[u][e]); }
+        part[pp][d] = s0 + s1;
       }
-      part[pp][d] = s0 + s1;
-    }
-    __syncthreads();
-    if (tid < 32) {
-      float t = 0.f;
+      __syncthreads();
+      if (tid < 32) {
+        float t = 0.f;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) t += part[q][tid];
-      mean[tid] = t / (float)N;
-    }
-    __syncthreads();
-    // one (query, lane half) per thread: 16 dims in epilogue order; consecutive threads write
-    // consecutive queries of one piece
-    for (int t = tid; t < N * 2; t += 256) {
-      const int i = t % N, hf = t / N;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = pack_bf2(mean[slot_dim(hf, kk, 2 * e)], mean[slot_dim(hf, kk, 2 * e + 1)]);
-        st16(a.o + o_off(hb, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        for (int q = 0; q < 8; ++q) t += part[q][tid];
+        mean[tid] = t / (float)N;
       }
+      __syncthreads();
+      // one (query, lane half) per thread: 16 dims in epilogue order; consecutive threads write
+      // consecutive queries of one piece
+      for (int t = tid; t < N * 2; t += 256) {
+        const int i = t % N, hf = t / N;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          uint32_t wv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wv[e] = pack_bf2(mean[slot_dim(hf, kk, 2 * e)], mean[slot_dim(hf, kk, 2 * e + 1)]);
+          st16(a.o + o_off(hb, r, i, hf, kk, N, NP), u32x4{wv[0], wv[1], wv[2], wv[3]});
+        }
+      }
+      __syncthreads();                                   // mean is read: the next item may refill it
     }
-    return;
+    __syncthreads();                                     // nlist is read
   }
-  if (hb != 0) return;                                   // flagged heads: one workgroup per row
-  if (a.sparse) return;                                  // flagged block-sparse rows: not here
-  tri_exact_heads(a, r, tid);
 }
 
 // Rows the fused epilogue left to this kernel (a head of the row was flagged): those heads are
@@ -1834,7 +1853,7 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     }
     hipLaunchKernelGGL(tri_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
-    hipLaunchKernelGGL(tri_fixup_kernel, dim3(N * a->H), dim3(256), 0, st, aa);
+    hipLaunchKernelGGL(tri_fixup_kernel, dim3(std::min(N * a->H, kFixupGrid)), dim3(256), 0, st, aa);
     if (int rc = sf_check_launch("tri_fixup_kernel")) return rc;
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
@@ -2005,7 +2024,7 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
   }
   hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
   if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
-  hipLaunchKernelGGL(tri_fixup_kernel, dim3(a->N * a->H), dim3(256), 0, st, fa);   // masked rows: mean of V
+  hipLaunchKernelGGL(tri_fixup_kernel, dim3(std::min(a->N * a->H, kFixupGrid)), dim3(256), 0, st, fa);   // masked rows: mean of V
   if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
   return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);
 }
