@@ -95,6 +95,151 @@ int zero_init_out(int64_t rows, int C, int HD, const void* o, const void* cond, 
   return sf_hip_linear_fwd(&l, st);
 }
 
+// ---------------------------------------------------------------------------------------
+// The AdaLN conditioning terms of one layer in one launch (transformer.py:80-96, 138-154):
+//   scale = sigmoid(LN(c) W_s^T + b_s),  shift = LN(c) W_sh^T,  zgate = sigmoid(c W_zc^T + b_zc)
+// with LN(c) the LayerNorm of the condition rows (lnc_w / lnc_b, eps 1e-5), rounded to bf16 as
+// the LayerNorm kernel writes it.  It replaces a LayerNorm and three GEMM launches that each
+// fill a fraction of the GPU (1024 x 384 -> 768: 4.8 + 6.2 + 6.3 + 6.6 us in the diffusion
+// block).  Workgroup (64-row block, 64-channel block, term): the block's condition rows --
+// normalised unless term 2 -- staged in LDS, then wave w forms the 32 x 32 quadrant of channels
+// 32 (w & 1) .. and rows 32 (w >> 1) .. as D^T = W c^T (lane: row li, channels 8 j + 4 half ..),
+// the weight rows read straight from global memory (they stay in L2).  Every load of a workgroup
+// -- its weight chunks, condition rows and the LayerNorm affine -- is issued at its start: one
+// memory round trip (with the loads after one another, 19 us: a round trip each).
+// ---------------------------------------------------------------------------------------
+struct CondTermsArgs {
+  int64_t rows; int C, Cs;
+  const uint16_t* cond;                       // [rows, Cs]
+  const float *lnc_w, *lnc_b;                 // [Cs] (lnc_b may be null)
+  const uint16_t *w_scale, *w_shift, *w_zc;   // [C, Cs]
+  const float *b_scale, *b_zc;                // [C] or null
+  uint16_t *scale, *shift, *zgate;            // [rows, C]
+};
+constexpr int kCondMaxCs = 384;
+
+__global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t sA[];   // [64][Cs + 8], then lnc_w, lnc_b (f32)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
+  const int Cs = a.Cs, pitch = Cs + 8, nch = Cs / 8;
+  const int term = blockIdx.z;                                  // 0 scale, 1 shift, 2 zgate
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  const int n0 = blockIdx.y * 128;
+  float* sG = reinterpret_cast<float*>(sA + 64 * pitch);
+  float* sB = sG + Cs;
+  // the weight chunks first (they depend on nothing): A operand of D^T = W c^T, lane (half, li)
+  // channel nq + li, k = 16 kc + 8 half ..
+  const uint16_t* W = term == 0 ? a.w_scale : term == 1 ? a.w_shift : a.w_zc;
+  const int nq = n0 + 32 * (wave & 3), rq = 32 * (wave >> 2);
+  u32x4 wr[kCondMaxCs / 16];
+  {
+    const uint16_t* wp = W + (int64_t)(nq + li) * Cs + 8 * half;
+#pragma unroll
+    for (int kc = 0; kc < kCondMaxCs / 16; ++kc) wr[kc] = 16 * kc < Cs ? ld16(wp + 16 * kc) : u32x4{0, 0, 0, 0};
+  }
+  // thread (row tid / 8, part tid % 8): chunks of 8 channels part, part + 8, ...
+  const int rr = tid >> 3, q = tid & 7;
+  u32x4 v[kCondMaxCs / 64];
+  {
+    const uint16_t* cp = a.cond + min(r0 + rr, a.rows - 1) * Cs;
+#pragma unroll
+    for (int t = 0; t < kCondMaxCs / 64; ++t) v[t] = q + 8 * t < nch ? ld16(cp + 8 * (q + 8 * t)) : u32x4{0, 0, 0, 0};
+  }
+  if (term < 2)                                                 // the LayerNorm's affine, to LDS
+    for (int c = 4 * tid; c < Cs; c += 2048) {
+      *reinterpret_cast<f32x4*>(sG + c) = *reinterpret_cast<const f32x4*>(a.lnc_w + c);
+      *reinterpret_cast<f32x4*>(sB + c) = a.lnc_b ? *reinterpret_cast<const f32x4*>(a.lnc_b + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  __syncthreads();
+  {
+    float mean = 0.f, rstd = 1.f;
+    if (term < 2) {
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < kCondMaxCs / 64; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum += bflo(v[t][e]) + bfhi(v[t][e]);
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+      mean = sum / (float)Cs;
+      float sq = 0.f;
+#pragma unroll
+      for (int t = 0; t < kCondMaxCs / 64; ++t) {
+        if (q + 8 * t < nch) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float d0 = bflo(v[t][e]) - mean, d1 = bfhi(v[t][e]) - mean;
+            sq += d0 * d0 + d1 * d1;
+          }
+        }
+      }
+      sq += __shfl_xor(sq, 1);
+      sq += __shfl_xor(sq, 2);
+      sq += __shfl_xor(sq, 4);
+      rstd = rsqrtf(sq / (float)Cs + 1e-5f);
+    }
+#pragma unroll
+    for (int t = 0; t < kCondMaxCs / 64; ++t) {
+      const int ch = q + 8 * t;
+      if (ch >= nch) continue;
+      u32x4 y = v[t];
+      if (term < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 8 * ch + 2 * e;
+          y[e] = pack_bf2((bflo(v[t][e]) - mean) * rstd * sG[c] + sB[c],
+                          (bfhi(v[t][e]) - mean) * rstd * sG[c + 1] + sB[c + 1]);
+        }
+      }
+      st16(&sA[rr * pitch + 8 * ch], y);
+    }
+  }
+  __syncthreads();
+  const float* bias = term == 0 ? a.b_scale : term == 1 ? nullptr : a.b_zc;
+  const uint16_t* ap = sA + (rq + li) * pitch + 8 * half;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int kc = 0; kc < kCondMaxCs / 16; ++kc)
+    if (16 * kc < Cs) acc = mfma32(as_bf16x8(wr[kc]), as_bf16x8(ld16(ap + 16 * kc)), acc);
+  const int64_t row = r0 + rq + li;
+  if (row >= a.rows) return;
+  uint16_t* out = (term == 0 ? a.scale : term == 1 ? a.shift : a.zgate) + row * a.C;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = nq + 8 * j + 4 * half;
+    float v4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v4[e] = acc[4 * j + e] + (bias ? bias[n + e] : 0.f);
+      if (term != 1) v4[e] = sigmoidf_(v4[e]);
+    }
+    *reinterpret_cast<u32x2*>(out + n) = u32x2{pack_bf2(v4[0], v4[1]), pack_bf2(v4[2], v4[3])};
+  }
+}
+
+bool cond_terms_ok(int C, int Cs, const void* cond, const void* w_scale, const void* w_shift, const void* w_zc) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(cond) | reinterpret_cast<uintptr_t>(w_scale) |
+                       reinterpret_cast<uintptr_t>(w_shift) | reinterpret_cast<uintptr_t>(w_zc);
+  return Cs % 16 == 0 && Cs <= kCondMaxCs && C % 128 == 0 && (al & 15) == 0;   // (f32 vectors: torch-aligned)
+}
+
+int cond_terms(int64_t rows, int C, int Cs, const void* cond, const float* lnc_w, const float* lnc_b,
+               const void* w_scale, const float* b_scale, const void* w_shift, const void* w_zc, const float* b_zc,
+               void* scale, void* shift, void* zgate, hipStream_t st) {
+  CondTermsArgs t{};
+  t.rows = rows; t.C = C; t.Cs = Cs;
+  t.cond = static_cast<const uint16_t*>(cond); t.lnc_w = lnc_w; t.lnc_b = lnc_b;
+  t.w_scale = static_cast<const uint16_t*>(w_scale); t.w_shift = static_cast<const uint16_t*>(w_shift);
+  t.w_zc = static_cast<const uint16_t*>(w_zc); t.b_scale = b_scale; t.b_zc = b_zc;
+  t.scale = static_cast<uint16_t*>(scale); t.shift = static_cast<uint16_t*>(shift); t.zgate = static_cast<uint16_t*>(zgate);
+  const size_t lds = (size_t)64 * (Cs + 8) * 2 + (size_t)2 * Cs * 4;   // 53 KB at Cs = 384
+  hipLaunchKernelGGL(cond_terms_kernel, dim3((unsigned)((rows + 63) / 64), (unsigned)(C / 128), 3), dim3(512), lds, st, t);
+  return sf_check_launch("cond_terms_kernel");
+}
+
 // attention stage of the self-attention chain: q, k, v, g are column blocks of y [S*N, 4HD]
 sf_attention_args self_attn_args(const sf_self_attention_args* a, const void* y, void* o) {
   const int HD = a->H * a->D;
@@ -305,7 +450,10 @@ size_t self_ws(const sf_self_attention_args* a) {
   const int64_t rows = (int64_t)a->S * a->N;
   const int HD = a->H * a->D;
   const bool cond_gemms = a->cond && !a->pre_scale;   // AdaLN from cond (not precomputed)
-  if (cond_gemms) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
+  if (cond_gemms) {                          // LN(cond), scale, shift, zgate
+    ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2);
+    ws.take((size_t)a->N * a->C * 2);
+  }
   ws.take((size_t)rows * a->C * 2);          // h
   ws.take((size_t)rows * 4 * HD * 2);        // q k v g
   ws.take((size_t)rows * HD * 2);            // o
@@ -380,16 +528,28 @@ static int self_attention_run(const sf_self_attention_args* a, void* workspace, 
   const int HD = a->H * a->D;
   void* h = nullptr;
   int rc;
+  void *c_scale = nullptr, *c_shift = nullptr, *c_zgate = nullptr;
+  const bool fused_cond = a->cond && !pre && cond_terms_ok(a->C, a->Cs, a->cond, a->w_scale, a->w_shift, a->w_zc);
   {
     // the AdaLN workspace is taken first, as in self_ws
     Arena probe = ws;
-    if (a->cond && !pre) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
+    if (a->cond && !pre) {
+      probe.take((size_t)a->N * a->Cs * 2);
+      c_scale = probe.take((size_t)a->N * a->C * 2); c_shift = probe.take((size_t)a->N * a->C * 2);
+      c_zgate = probe.take((size_t)a->N * a->C * 2);
+    }
     h = probe.take((size_t)rows * a->C * 2);
-    if (pre) {
+    if (pre || fused_cond) {
+      // the conditioning terms of this layer in one launch (or given), then the modulated LayerNorm
+      if (fused_cond && (rc = cond_terms(a->N, a->C, a->Cs, a->cond, a->lnc_w, a->lnc_b, a->w_scale, a->b_scale,
+                                         a->w_shift, a->w_zc, a->b_zc, c_scale, c_shift, c_zgate, st))) {
+        return rc;
+      }
       sf_layer_norm_args ln{};
       ln.M = rows; ln.C = a->C; ln.eps = 1e-5f;
       ln.x = a->x; ln.x_rs = a->C; ln.y = h; ln.y_rs = a->C;
-      ln.scale = a->pre_scale; ln.shift = a->pre_shift; ln.cond_rows = a->N; ln.cond_rs = a->pre_rs;
+      ln.scale = pre ? a->pre_scale : c_scale; ln.shift = pre ? a->pre_shift : c_shift; ln.cond_rows = a->N;
+      ln.cond_rs = pre ? a->pre_rs : a->C;
       if ((rc = sf_hip_layer_norm_fwd(&ln, st))) return rc;
     } else if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b,
                            a->w_scale, a->b_scale, a->w_shift, ws, h, st))) {
@@ -407,8 +567,9 @@ static int self_attention_run(const sf_self_attention_args* a, void* workspace, 
   const size_t split = sf_attention_workspace_bytes(&t);
   void* split_ws = ws.take(split);
   if ((rc = sf_attention_run(&t, split_ws, split, st))) return rc;
-  return zero_init_out(rows, a->C, HD, o, pre ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w_t2,
-                       a->add_residual ? a->x : nullptr, a->out, ws, st, a->pre_zgate, a->pre_rs);
+  return zero_init_out(rows, a->C, HD, o, pre || fused_cond ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc,
+                       a->w_t2, a->add_residual ? a->x : nullptr, a->out, ws, st,
+                       pre ? a->pre_zgate : c_zgate, pre ? a->pre_rs : a->C);
 }
 
 extern "C" int sf_hip_self_attention_fwd(const sf_self_attention_args* a, void* workspace,
@@ -845,7 +1006,10 @@ size_t transition_ws(const sf_transition_args* a) {
   Arena ws{nullptr};
   const int64_t rows = (int64_t)a->S * a->N;
   const bool cond_gemms = a->cond && !a->pre_scale;
-  if (cond_gemms) { ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2); }
+  if (cond_gemms) {                          // LN(cond), scale, shift, zgate
+    ws.take((size_t)a->N * a->Cs * 2); ws.take((size_t)a->N * a->C * 2); ws.take((size_t)a->N * a->C * 2);
+    ws.take((size_t)a->N * a->C * 2);
+  }
   ws.take((size_t)rows * a->C * 2);          // h
   ws.take((size_t)rows * a->I * 2);          // gated intermediate
   if (cond_gemms) ws.take((size_t)a->N * a->C * 2);
@@ -885,15 +1049,27 @@ extern "C" int sf_hip_transition_fwd(const sf_transition_args* a, void* workspac
   const int64_t rows = (int64_t)a->S * a->N;
   int rc;
   void* h = nullptr;
+  void *c_scale = nullptr, *c_shift = nullptr, *c_zgate = nullptr;
+  const bool fused_cond = a->cond && !pre && cond_terms_ok(a->C, a->Cs, a->cond, a->w_scale, a->w_shift, a->w_zc);
   {
     Arena probe = ws;                        // the AdaLN scratch first, as in transition_ws
-    if (a->cond && !pre) { probe.take((size_t)a->N * a->Cs * 2); probe.take((size_t)a->N * a->C * 2); probe.take((size_t)a->N * a->C * 2); }
+    if (a->cond && !pre) {
+      probe.take((size_t)a->N * a->Cs * 2);
+      c_scale = probe.take((size_t)a->N * a->C * 2); c_shift = probe.take((size_t)a->N * a->C * 2);
+      c_zgate = probe.take((size_t)a->N * a->C * 2);
+    }
     h = probe.take((size_t)rows * a->C * 2);
-    if (pre) {
+    if (pre || fused_cond) {
+      // the conditioning terms of this layer in one launch (or given), then the modulated LayerNorm
+      if (fused_cond && (rc = cond_terms(a->N, a->C, a->Cs, a->cond, a->lnc_w, a->lnc_b, a->w_scale, a->b_scale,
+                                         a->w_shift, a->w_zc, a->b_zc, c_scale, c_shift, c_zgate, st))) {
+        return rc;
+      }
       sf_layer_norm_args ln{};
       ln.M = rows; ln.C = a->C; ln.eps = 1e-5f;
       ln.x = a->x; ln.x_rs = a->C; ln.y = h; ln.y_rs = a->C;
-      ln.scale = a->pre_scale; ln.shift = a->pre_shift; ln.cond_rows = a->N; ln.cond_rs = a->pre_rs;
+      ln.scale = pre ? a->pre_scale : c_scale; ln.shift = pre ? a->pre_shift : c_shift; ln.cond_rows = a->N;
+      ln.cond_rs = pre ? a->pre_rs : a->C;
       if ((rc = sf_hip_layer_norm_fwd(&ln, st))) return rc;
     } else if ((rc = adaln(rows, a->C, a->x, a->cond, a->N, a->Cs, a->ln_w, a->ln_b, a->lnc_w, a->lnc_b,
                            a->w_scale, a->b_scale, a->w_shift, ws, h, st))) {
@@ -906,8 +1082,9 @@ extern "C" int sf_hip_transition_fwd(const sf_transition_args* a, void* workspac
   g.M = rows; g.N = 2 * a->I; g.K = a->C; g.x = h; g.x_rs = a->C; g.wt = a->w1; g.mul_rows = 1;
   g.y = c; g.y_rs = a->I; g.glu = 1;
   if ((rc = sf_hip_linear_fwd(&g, st))) return rc;
-  return zero_init_out(rows, a->C, a->I, c, pre ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc, a->w2,
-                       a->add_residual ? a->x : nullptr, a->out, ws, st, a->pre_zgate, a->pre_rs);
+  return zero_init_out(rows, a->C, a->I, c, pre || fused_cond ? nullptr : a->cond, a->N, a->Cs, a->w_zc, a->b_zc,
+                       a->w2, a->add_residual ? a->x : nullptr, a->out, ws, st,
+                       pre ? a->pre_zgate : c_zgate, pre ? a->pre_rs : a->C);
 }
 
 namespace {
