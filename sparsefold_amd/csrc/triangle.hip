@@ -1393,7 +1393,7 @@ struct IbsArgs {
                                       // past N or masked (no valid row attends them) and tiles past T
   int32_t* index; float* weight;      // [N][H][T][S]
   uint16_t* o;                        // o_off blocks (per head, attention row, 32 queries), as the dense stage writes them
-  const uint8_t* flags;               // tri_ibs_attn_kernel: only (row, head) flagged here (null: all)
+  const uint8_t* flags;               // (row, head) pairs the tile kernel flagged, for tri_ibs_flagged_kernel
 };
 
 __device__ __forceinline__ unsigned long long ibs_mix64(unsigned long long x) {
@@ -1671,13 +1671,9 @@ __global__ __launch_bounds__(64 * kIbsIndexWaves) __attribute__((amdgpu_waves_pe
 // the fix-up kernel.  It recomputes the (row, head) pairs tri_ibs_tile_attn_kernel flagged (a
 // weight sum out of range of its fixed reference point), or every row where that kernel's
 // per-wave table cannot hold the key blocks (N > 4096).
-__global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
-  const int64_t task = (int64_t)blockIdx.x * 4 + wave;
-  if (task >= (int64_t)a.N * a.H * a.T) return;
-  const int t = (int)(task % a.T), h = (int)((task / a.T) % a.H), r = (int)(task / ((int64_t)a.T * a.H));
-  if (a.seq[r] == 0) return;
-  if (a.flags != nullptr && a.flags[r * a.H + h] == 0) return;   // uniform over the wave
+__device__ void ibs_exact_tile(const IbsArgs& a, int r, int h, int t) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, li = lane & 31;
+  const int64_t task = ((int64_t)r * a.H + h) * a.T + t;
   const int N = a.N, NP = a.NP, H = a.H;
   const int i = 32 * t + li;                                 // this lane's query (< NP)
   bf16x8 qb[2];
@@ -1743,6 +1739,42 @@ __global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) w4[e] = pack_bf2(o[8 * kk + 2 * e] * inv, o[8 * kk + 2 * e + 1] * inv);
     st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w4[0], w4[1], w4[2], w4[3]});
+  }
+}
+
+// Every (row, head, query tile) of the valid rows, one wave each (N > 4096: the attention itself).
+__global__ __launch_bounds__(256) void tri_ibs_attn_kernel(const IbsArgs a) {
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= (int64_t)a.N * a.H * a.T) return;
+  const int t = (int)(task % a.T), h = (int)((task / a.T) % a.H), r = (int)(task / ((int64_t)a.T * a.H));
+  if (a.seq[r] == 0) return;
+  ibs_exact_tile(a, r, h, t);
+}
+
+// The (row, head) pairs the tile kernel flagged: (row, head) items dealt over a fixed grid, a
+// workgroup's items checked at once (one per thread), its 4 waves then taking the query tiles of
+// each flagged pair.  (One wave per (row, head, tile) that checked its pair's flag and mostly
+// returned took 51 us at N = 1536 with nothing flagged: 295k waves dispatched for nothing.)
+constexpr int kIbsFlaggedGrid = 1024;
+__global__ __launch_bounds__(256) void tri_ibs_flagged_kernel(const IbsArgs a) {
+  __shared__ int list[256];
+  __shared__ int nlist;
+  const int tid = threadIdx.x, wave = tid >> 6, items = a.N * a.H;
+  const int K = (items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  for (int k0 = 0; k0 < K; k0 += 256) {
+    if (tid == 0) nlist = 0;
+    __syncthreads();
+    {
+      const int k = k0 + tid, item = (int)blockIdx.x + k * (int)gridDim.x;
+      if (k < K && a.seq[item / a.H] != 0 && a.flags[item] != 0) list[atomicAdd(&nlist, 1)] = item;
+    }
+    __syncthreads();
+    const int n = nlist;
+    for (int w = 0; w < n; ++w) {
+      const int item = list[w], r = item / a.H, h = item - r * a.H;
+      for (int t = wave; t < a.T; t += 4) ibs_exact_tile(a, r, h, t);
+    }
+    __syncthreads();                                       // nlist and list are read
   }
 }
 
@@ -2022,8 +2054,13 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
     if ((rc = sf_check_launch("tri_ibs_tile_attn_kernel"))) return rc;
     ia.flags = ws.flags;
   }
-  hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
-  if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
+  if (ia.flags != nullptr) {
+    hipLaunchKernelGGL(tri_ibs_flagged_kernel, dim3((unsigned)std::min(ia.N * ia.H, kIbsFlaggedGrid)), dim3(256), 0, st, ia);
+    if ((rc = sf_check_launch("tri_ibs_flagged_kernel"))) return rc;
+  } else {
+    hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
+    if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
+  }
   hipLaunchKernelGGL(tri_fixup_kernel, dim3(std::min(a->N * a->H, kFixupGrid)), dim3(256), 0, st, fa);   // masked rows: mean of V
   if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
   return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);
