@@ -663,7 +663,7 @@ struct WinFusedArgs {
   const uint16_t* zgate; int64_t zrs;   // [A] rows of 128, row stride zrs
   const uint16_t* x;                    // residual [S * A][128] (null: none)
   uint16_t* out;                        // [S * A][128]
-  float cs, inv_scale;                  // scale * log2 e, 1 / scale
+  float scale;                          // logits scale (q.k scale + bias)
 };
 constexpr int kWinOgPitch = 136;        // og rows in LDS (bf16): 272 bytes apart, conflict-free
 
@@ -708,38 +708,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
   }
   const uint16_t* qp = a.yq + (qrow + li) * 256 + h * 32 + 8 * half;
   const bf16x8 qb0 = as_bf16x8(ld16(qp)), qb1 = as_bf16x8(ld16(qp + 16));
-  // bias of query li, keys 32 kb + 8 j + 4 half .. + 3 (S^T registers 4 j .. 4 j + 3 of block kb)
-  u32x2 br[4][4];
+  // bias of query li, keys 16 c + 8 half .. + 7: the B operand of an MFMA that adds it to S^T
+  // through an identity A (16-byte loads: with the keys of the S^T registers, 8 bytes a lane, the
+  // loads were twice as many, each touching as many rows)
+  u32x4 br[8];
   if (a.bias != nullptr) {
-    const uint16_t* bp = a.bias + (((int64_t)u * 4 + h) * 32 + li) * 128 + 4 * half;
+    const uint16_t* bp = a.bias + (((int64_t)u * 4 + h) * 32 + li) * 128 + 8 * half;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) br[kb][j] = *reinterpret_cast<const u32x2*>(bp + 32 * kb + 8 * j);
-  } else {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) br[kb][j] = u32x2{0, 0};
+    for (int c = 0; c < 8; ++c) br[c] = ld16(bp + 16 * c);
   }
   const bool kvalid0 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane] != 0;
   const bool kvalid1 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane + 64] != 0;
   const uint64_t mk0 = __ballot(kvalid0), mk1 = __ballot(kvalid1);
   const bool qvalid = a.mask_q == nullptr || a.mask_q[(int64_t)u * 32 + li] != 0;
 
-  // ---- S^T = K Q^T + bias / scale, masks ----
+  // ---- S^T = scale K Q^T + bias, masks ----
+  // identity chunk c of a 32-key block: A row r, k = 8 half + e is 1 where r = 16 c + 8 half + e
+  bf16x8 idn[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) idn[c][e] = (__bf16)(li == 16 * c + 8 * half + e ? 1.0f : 0.0f);
   f32x16 sc[4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        sc[kb][4 * j + 2 * e] = bflo(br[kb][j][e]) * a.inv_scale;
-        sc[kb][4 * j + 2 * e + 1] = bfhi(br[kb][j][e]) * a.inv_scale;
-      }
+    for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
     sc[kb] = mfma32(as_bf16x8(kr[kb][0]), qb0, sc[kb]);
     sc[kb] = mfma32(as_bf16x8(kr[kb][1]), qb1, sc[kb]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[kb][r] *= a.scale;
+    if (a.bias != nullptr) {                                // uniform
+      sc[kb] = mfma32(idn[0], as_bf16x8(br[2 * kb]), sc[kb]);
+      sc[kb] = mfma32(idn[1], as_bf16x8(br[2 * kb + 1]), sc[kb]);
+    }
   }
   if ((mk0 & mk1) != ~0ull) {                               // uniform: some key masked
 #pragma unroll
@@ -764,15 +766,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
 #pragma unroll
     for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[kb][r]);
   m = fmaxf(m, __shfl_xor(m, 32));
-  const float mb = m * a.cs;
+  const float mb = m * SF_LOG2E;
   bf16x2 pw[32];
   float l0 = 0.f, l1 = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(sc[kb][2 * e], a.cs, -mb)),
-                               fast_exp2(__builtin_fmaf(sc[kb][2 * e + 1], a.cs, -mb)));
+      pw[8 * kb + e] = cvt_bf2(fast_exp2(__builtin_fmaf(sc[kb][2 * e], SF_LOG2E, -mb)),
+                               fast_exp2(__builtin_fmaf(sc[kb][2 * e + 1], SF_LOG2E, -mb)));
       if (e & 1) l1 = add_bf2(pw[8 * kb + e], l1); else l0 = add_bf2(pw[8 * kb + e], l0);
     }
   float l = l0 + l1;
@@ -783,22 +785,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
   asm volatile("" ::: "memory");
   // gate of query li, dims 8 j + 4 half .. + 3 (O^T registers 4 j .. 4 j + 3), and W_t2 rows
   // 32 h + li (A operand of the projection; L2-resident): in flight during P.V
-  u32x2 gr[4];
-  const uint16_t* gp = a.yq + (qrow + li) * 256 + 128 + h * 32 + 4 * half;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) gr[j] = *reinterpret_cast<const u32x2*>(gp + 8 * j);
+  const uint16_t* gp = a.yq + (qrow + li) * 256 + 128 + h * 32;
+  const u32x4 gl0 = ld16(gp + 8 * half), gl1 = ld16(gp + 16 + 8 * half);
   u32x4 wr[8];
   const uint16_t* wp = a.w_t2 + (int64_t)(32 * h + li) * 128 + 8 * half;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) wr[kk] = ld16(wp + 16 * kk);
   // zero-gate and residual of the output channels 32 h + 8 j + 4 half .. + 3 of query li
   const int64_t orow = qrow + li;
-  const uint16_t* zp = a.zgate + (int64_t)(32 * u + li) * a.zrs + 32 * h + 4 * half;
-  u32x2 zg[4], xr[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    zg[j] = *reinterpret_cast<const u32x2*>(zp + 8 * j);
-    xr[j] = a.x != nullptr ? *reinterpret_cast<const u32x2*>(a.x + orow * 128 + 32 * h + 8 * j + 4 * half) : u32x2{0, 0};
+  const uint16_t* zp = a.zgate + (int64_t)(32 * u + li) * a.zrs + 32 * h;
+  const u32x4 zl0 = ld16(zp + 8 * half), zl1 = ld16(zp + 16 + 8 * half);
+  u32x4 xl0 = u32x4{0, 0, 0, 0}, xl1 = u32x4{0, 0, 0, 0};
+  if (a.x != nullptr) {
+    xl0 = ld16(a.x + orow * 128 + 32 * h + 8 * half);
+    xl1 = ld16(a.x + orow * 128 + 32 * h + 16 + 8 * half);
   }
   f32x16 o;
 #pragma unroll
@@ -824,6 +824,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
       o = mfma32(as_bf16x8(u32x4{part[0][0], part[0][1], part[1][0], part[1][1]}), pb, o);
     }
   }
+  // 16-byte pieces of 8 dims (channels) per lane -> the 4-dim runs of the O^T registers: lane
+  // half 0 loaded dims 0..7 and 16..23, half 1 dims 8..15 and 24..31; run j = dims 8 j + 4 half
+  // .. + 3, half of them from the partner lane (l xor 32), exchanged by permlane32_swap
+  const uint32_t hm = half ? ~0u : 0u;
+  auto blend = [&](uint32_t if1, uint32_t if0) __attribute__((always_inline)) { return (if1 & hm) | (if0 & ~hm); };
+  auto runs = [&](const u32x4& p0, const u32x4& p1, u32x2 (&rj)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const u32x4& p = q ? p1 : p0;
+      const auto s0 = __builtin_amdgcn_permlane32_swap(p[0], p[2], false, false);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(p[1], p[3], false, false);
+      // half 0: run 2q = own words 0, 1; run 2q + 1 = the partner's words 0, 1 (s*[1])
+      // half 1: run 2q = the partner's words 2, 3 (s*[0]); run 2q + 1 = own words 2, 3
+      rj[2 * q] = u32x2{blend(s0[0], p[0]), blend(s1[0], p[1])};
+      rj[2 * q + 1] = u32x2{blend(p[2], s0[1]), blend(p[3], s1[1])};
+    }
+  };
+  u32x2 gr[4];
+  runs(gl0, gl1, gr);
   // ---- og = O / l * sigmoid(g) -> LDS (the V rows of every wave are then dead) ----
   const float inv = 1.0f / l;
   __syncthreads();
@@ -845,6 +864,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
     acc = mfma32(as_bf16x8(wr[kk]), as_bf16x8(ld16(og + li * kWinOgPitch + 16 * kk + 8 * half)), acc);
+  u32x2 zg[4], xr[4];
+  runs(zl0, zl1, zg);
+  runs(xl0, xl1, xr);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float v[4] = {acc[4 * j] * bflo(zg[j][0]), acc[4 * j + 1] * bfhi(zg[j][0]),
@@ -914,7 +936,7 @@ int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t s
     f.x = a->add_residual ? static_cast<const uint16_t*>(a->xq) : nullptr;
     f.out = static_cast<uint16_t*>(a->out);
     const float scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)a->D);
-    f.cs = scale * SF_LOG2E; f.inv_scale = 1.0f / scale;
+    f.scale = scale;
     hipLaunchKernelGGL(window_attn_out_kernel, dim3((unsigned)(a->S * a->U)), dim3(256), 0, st, f);
     return sf_check_launch("window_attn_out_kernel");
   }
