@@ -77,8 +77,11 @@ typedef struct sf_attention_args {
   const void* gate; int64_t g_s[4];             /* bf16 or NULL (sigmoid gate logits)      */
   void* out;        int64_t o_s[4];             /* bf16, strides [b0, b1, q, h]            */
   /* Work decomposition: 0 = chosen from the sizes (normal use); 1 = query blocks of one
-   * (batch, head) share their K/V tiles; 2 = every 32-query block is an independent task.
-   * Both give the same result up to fp32 summation order; tests select each explicitly. */
+   * (batch, head) share their K/V tiles; 2 = every 32-query block is an independent task;
+   * 3 = the shared-bias kernel: B0 = 5 samples, B1 = 1, D = Dv = 48, one bias for all samples
+   * (bias_s[0] = 0), no query mask, a key mask shared by the samples, Q % 64 == 0,
+   * K % 256 == 0, K <= 4096 (refused with an error otherwise; opt-in only, 0 never picks it).
+   * All give the same result up to fp32 summation order; tests select each explicitly. */
   int32_t schedule;
   /* Key / value rows gathered by index (the key windows of CrossAttTransformer read from
    * per-atom K / V, DiffusionCrossAttentionIndexed.cpp:376-411): with kv_index (int32), key j of

@@ -90,7 +90,8 @@ def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gat
   q ``[B0,B1,Q,H,D]``, k ``[B0,B1,K,H,D]``, v ``[B0,B1,K,H,Dv]``, gate like the output
   ``[B0,B1,Q,H,Dv]``; bias ``[B0,B1,H,Q,K]`` (zero strides allowed), masks ``[B0,B1,Q]`` /
   ``[B0,B1,K]`` uint8.  All bf16 with unit last stride.  ``schedule``: 0 chooses the work
-  decomposition from the sizes, 1 / 2 force shared-tile / per-wave tasks.  Returns ``out``.
+  decomposition from the sizes, 1 / 2 force shared-tile / per-wave tasks, 3 the shared-bias
+  kernel (5 samples, head dim 48, one bias for all samples; refused otherwise).  Returns ``out``.
   """
   dev = _require_cuda(q, k, v, bias, mask_q, mask_k, gate, out)
   _require(q.ndim == 5 and k.ndim == 5 and v.ndim == 5, "attention: q/k/v must be [B0,B1,L,H,D]")
@@ -124,7 +125,7 @@ def attention(q, k, v, *, scale: float, bias=None, mask_q=None, mask_k=None, gat
     _require(tuple(gate.shape) == (B0, B1, Q, H, Dv), f"attention: gate shape {tuple(gate.shape)}")
     a.gate, a.g_s = _vp(gate), (C.c_int64 * 4)(*gate.stride()[:4])
   a.out, a.o_s = _vp(out), (C.c_int64 * 4)(*out.stride()[:4])
-  _require(schedule in (0, 1, 2), f"attention: schedule {schedule} is not 0, 1 or 2")
+  _require(schedule in (0, 1, 2, 3), f"attention: schedule {schedule} is not 0, 1, 2 or 3")
   a.schedule = schedule
   lib = _lib.load()
   _lib.check(lib.sf_hip_attention_fwd(C.byref(a), _stream(q)), "sf_hip_attention_fwd")

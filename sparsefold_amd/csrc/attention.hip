@@ -839,6 +839,16 @@ size_t sf_attention_workspace_bytes(const sf_attention_args* a) {
 
 int sf_attention_run(const sf_attention_args* a, void* workspace, size_t workspace_bytes, hipStream_t st) {
   if (a == nullptr) { sf_set_error("attention: null args"); return 1; }
+  if (a->schedule == 3) {
+    // the shared-bias kernel, opt-in: on the diffusion shape it measured slower than the
+    // shared-tile kernel (51.5 against 45 us), so the automatic choice never takes it
+    const char* why = nullptr;
+    AttnRoute chk;
+    if (route(a, false, chk)) return 1;                      // argument checks first
+    if (sf_sb_attention_ok(a, &why)) return sf_sb_attention_launch(a, st);
+    sf_set_error("attention: schedule 3 (shared-bias kernel) refused: %s", why);
+    return 1;
+  }
   AttnRoute r;
   const bool can_split = workspace != nullptr;
   if (route(a, can_split, r)) return 1;

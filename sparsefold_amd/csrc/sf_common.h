@@ -132,3 +132,7 @@ int sf_resident_workgroups(const void* kernel, int threads);
 // split their key range into slices merged by a combine kernel.
 size_t sf_attention_workspace_bytes(const sf_attention_args* a);
 int sf_attention_run(const sf_attention_args* a, void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Shared-bias attention (5 samples, head dim 48, one bias for every sample): whether it serves
+// `a` (else *why names the first condition that fails), and its launch.
+bool sf_sb_attention_ok(const sf_attention_args* a, const char** why);
+int sf_sb_attention_launch(const sf_attention_args* a, hipStream_t stream);

@@ -141,3 +141,67 @@ def test_reference_point_moves_after_the_first_tile(mode):
   bias[2, :, :, 250:] += 70.0 / 1.4426950408889634
   out, ref = _run(q, k, v, mask_k=mk, bias=bias, schedule=1 if mode == "s" else 2)
   assert_close_bf16(out, ref, f"reference point moves ({mode})")
+
+
+# ---- shared-bias kernel (schedule 3): 5 samples, head dim 48, one bias for every sample ----
+
+def _sb_inputs(N, H, seed, *, mask_frac=0.0, gate=True):
+  g = torch.Generator().manual_seed(seed)
+  S, D = 5, 48
+  q, k, v = (torch.randn(S, N, H, D, generator=g) for _ in range(3))
+  bias = torch.randn(H, N, N, generator=g)                 # shared by the 5 samples (stride 0)
+  mk = None
+  if mask_frac:
+    mk = torch.rand(N, generator=g) > mask_frac            # one key mask for every sample
+  gt = torch.randn(S, N, H, D, generator=g) if gate else None
+  return q, k, v, bias, mk, gt
+
+
+@pytest.mark.parametrize("N,H,mask_frac,gate", [(256, 2, 0.0, True), (512, 3, 0.3, True), (768, 1, 0.0, False)])
+def test_shared_bias_kernel_matches_oracle(N, H, mask_frac, gate):
+  """Diffusion-transformer shape family (DiffusionSelfAttention.cpp:391,555: one pair bias for all
+  samples): the shared-bias kernel against the float32 oracle, with and without a key mask / gate."""
+  q, k, v, bias, mk, gt = _sb_inputs(N, H, 4000 + N + H, mask_frac=mask_frac, gate=gate)
+  out, ref = _run(q, k, v, bias=bias, mask_k=mk, gate=gt, schedule=3)
+  assert_close_bf16(out, ref, f"shared-bias N={N} H={H} mask={mask_frac} gate={gate}")
+
+
+def test_shared_bias_kernel_agrees_with_tile_kernels_at_diffusion_size():
+  """5 x 1024 tokens, 16 heads (the C4 block's attention): the shared-bias kernel against the
+  shared-tile kernel on the same GPU inputs (same arithmetic up to fp32 summation order and the
+  reference point of the softmax)."""
+  g = torch.Generator(device=DEV).manual_seed(77)
+  S, N, H, D = 5, 1024, 16, 48
+  bf = torch.bfloat16
+  q, k, v, gt = (torch.randn(S, N, H, D, device=DEV, generator=g).to(bf) for _ in range(4))
+  bias = torch.randn(H, N, N, device=DEV, generator=g).to(bf)
+  mk = torch.ones(N, dtype=torch.bool, device=DEV)
+  mk[-N // 10:] = False
+  outs = [hip_dpa(q, k, v, bias=bias, mask_k=mk, gate=gt, schedule=sch).float() for sch in (3, 1)]
+  torch.cuda.synchronize()
+  assert_close_bf16(outs[0].cpu(), outs[1].cpu(), "shared-bias vs shared-tile, 5x1024, H=16")
+
+
+def test_shared_bias_kernel_exact_path_for_flagged_rows():
+  """Rows the fast path cannot serve with its fixed reference point: every key masked (mean of V
+  over all keys) and logits 200 above the rest (weight sum past 2^100), recomputed exactly."""
+  N, H = 256, 2
+  q, k, v, bias, _, gt = _sb_inputs(N, H, 4242, gate=True)
+  bias[0, 5, 17] += 200.0                                  # one huge logit: row (h 0, q 5) overflows
+  bias[1, 70:90, :] += 120.0                               # rows whose sum passes 2^100 on every key
+  out, ref = _run(q, k, v, bias=bias, gate=gt, schedule=3)
+  assert_close_bf16(out, ref, "shared-bias flagged rows (overflow)")
+  mk = torch.zeros(N, dtype=torch.bool)                    # every key masked
+  out, ref = _run(q, k, v, bias=bias, mask_k=mk, schedule=3)
+  assert_close_bf16(out, ref, "shared-bias, every key masked")
+  mean = bf16_round(v).mean(1)                             # [5, H, 48]
+  diff = (out - mean[:, None]).abs().max().item()
+  assert diff <= 2 ** -8 * mean.abs().max().item() + 1e-6, diff
+
+
+def test_shared_bias_kernel_refuses_other_shapes():
+  q, k, v, bias, _, _ = _sb_inputs(256, 2, 1)
+  with pytest.raises(RuntimeError, match="schedule 3"):
+    _run(q[..., :32], k[..., :32], v[..., :32], bias=bias, schedule=3)   # head dim 32
+  with pytest.raises(RuntimeError, match="schedule 3"):
+    _run(q[:4], k[:4], v[:4], bias=bias, schedule=3)                     # 4 samples
