@@ -210,6 +210,105 @@ __global__ __launch_bounds__(256) void linear_kernel(const sf_linear_args a) {
   }
 }
 
+// Rows [0, nrows) of a staged fp32 output tile ct (pitch CP floats, BN columns from n0): bias,
+// sigmoid, gated pairs, row-broadcast multiplier, residual, bf16 stores of y.  Tile row rl is
+// output row m_first + rl; each thread finishes 8 consecutive columns of one row, so residual /
+// multiplier rows are read and y rows written as 16-byte pieces.  keep_final writes the final
+// values back into ct (for a transposed pass).
+template <int BN>
+__device__ __forceinline__ void linear_rows(const sf_linear_args& a, float* ct, int CP, int nrows, int64_t m_first,
+                                            int n0, int64_t bz, bool keep_final) {
+  uint16_t* yp = a.y ? (uint16_t*)a.y + bz * a.y_bs : nullptr;
+  const uint16_t* rp = (const uint16_t*)a.residual;
+  const uint16_t* mp = (const uint16_t*)a.mul;
+  const int ycols = a.ycols > 0 ? a.ycols : a.N;
+  const bool rvec = rp && (a.r_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0);
+  const bool mvec = mp && (a.mul_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(mp) & 15) == 0);
+  const bool yvec = yp && (a.y_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(yp) & 15) == 0);
+  constexpr int CPR = BN / 8;                                 // 8-column pieces per tile row
+  static_assert(256 % CPR == 0, "a thread keeps one column piece for all its rows");
+  const int tid = threadIdx.x;
+  const int cc = tid % CPR;
+  const int n = n0 + 8 * cc;                                  // this thread's columns n .. n+7
+  const bool full = n + 8 <= a.N;
+  float bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bv[e] = 0.f;
+  if (a.bias && n < a.N) {
+    if (full && ((reinterpret_cast<uintptr_t>(a.bias + n) & 15) == 0)) {
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.bias + n), b1 = *reinterpret_cast<const f32x4*>(a.bias + n + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { bv[e] = b0[e]; bv[4 + e] = b1[e]; }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bv[e] = n + e < a.N ? a.bias[n + e] : 0.f;
+    }
+  }
+  for (int rl = tid / CPR; rl < nrows; rl += 256 / CPR) {
+    const int64_t m = m_first + rl;
+    if (m >= a.M || n >= a.N) continue;
+    float* cv = &ct[rl * CP + 8 * cc];
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = cv[e] + bv[e];
+    if (a.glu) {
+      // gated pairs: columns 2j (swish) and 2j + 1 of the interleaved weight give output column j;
+      // N % 8 == 0 (checked on the host), so the 8 columns are 4 whole pairs
+      uint32_t w[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float g0 = v[4 * e] * sigmoidf_(v[4 * e]) * v[4 * e + 1];
+        const float g1 = v[4 * e + 2] * sigmoidf_(v[4 * e + 2]) * v[4 * e + 3];
+        w[e] = pack_bf2(g0, g1);
+      }
+      *reinterpret_cast<u32x2*>(yp + m * a.y_rs + n / 2) = u32x2{w[0], w[1]};
+      continue;
+    }
+    if (a.post_sigmoid) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = sigmoidf_(v[e]);
+    }
+    if (mp) {
+      const uint16_t* mrow = mp + (m % a.mul_rows) * a.mul_rs + n;
+      if (mvec && full) {
+        const u32x4 w = ld16(mrow);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[2 * e] *= bflo(w[e]); v[2 * e + 1] *= bfhi(w[e]); }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N) v[e] *= bf2f(mrow[e]);
+      }
+    }
+    if (rp) {
+      const uint16_t* rrow = rp + m * a.r_rs + n;
+      if (rvec && full) {
+        const u32x4 w = ld16(rrow);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[2 * e] += bflo(w[e]); v[2 * e + 1] += bfhi(w[e]); }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N) v[e] += bf2f(rrow[e]);
+      }
+    }
+    if (yp && n < ycols) {
+      uint16_t* yrow = yp + m * a.y_rs + n;
+      if (yvec && full && n + 8 <= ycols) {
+        st16(yrow, u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])});
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N && n + e < ycols) yrow[e] = f2bf(v[e]);
+      }
+    }
+    if (keep_final) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cv[e] = v[e];              // final values for the transposed pass
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // Linear, K % 64 == 0: BMxBN tile, 4 waves (2x2), K in steps of 64 double-buffered in LDS
 // through direct-to-LDS loads (global_load_lds_dwordx4: lane L fills bytes 16L..16L+15 of a
@@ -330,95 +429,8 @@ __global__ __launch_bounds__(256) void linear64_kernel(const sf_linear_args a) {
         *reinterpret_cast<f32x4*>(&ct[(wm * WR + 32 * mb + li) * CP + wn * WC + 32 * nb + 8 * c + 4 * half]) =
             f32x4{acc[mb][nb][4 * c], acc[mb][nb][4 * c + 1], acc[mb][nb][4 * c + 2], acc[mb][nb][4 * c + 3]};
   __syncthreads();
-  uint16_t* yp = a.y ? (uint16_t*)a.y + bz * a.y_bs : nullptr;
+  linear_rows<BN>(a, ct, CP, BM, m0, n0, bz, a.yt != nullptr);
   uint16_t* ytp = (uint16_t*)a.yt;
-  const uint16_t* rp = (const uint16_t*)a.residual;
-  const uint16_t* mp = (const uint16_t*)a.mul;
-  const int ycols = a.ycols > 0 ? a.ycols : a.N;
-  const bool rvec = rp && (a.r_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0);
-  const bool mvec = mp && (a.mul_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(mp) & 15) == 0);
-  const bool yvec = yp && (a.y_rs % 8 == 0) && ((reinterpret_cast<uintptr_t>(yp) & 15) == 0);
-  constexpr int CPR = BN / 8;                                 // 8-column pieces per tile row
-  static_assert(256 % CPR == 0, "a thread keeps one column piece for all its rows");
-  const int cc = tid % CPR;
-  const int n = n0 + 8 * cc;                                  // this thread's columns n .. n+7
-  const bool full = n + 8 <= a.N;
-  float bv[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) bv[e] = 0.f;
-  if (a.bias && n < a.N) {
-    if (full && ((reinterpret_cast<uintptr_t>(a.bias + n) & 15) == 0)) {
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.bias + n), b1 = *reinterpret_cast<const f32x4*>(a.bias + n + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { bv[e] = b0[e]; bv[4 + e] = b1[e]; }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bv[e] = n + e < a.N ? a.bias[n + e] : 0.f;
-    }
-  }
-  for (int rl = tid / CPR; rl < BM; rl += 256 / CPR) {
-    const int64_t m = m0 + rl;
-    if (m >= a.M || n >= a.N) continue;
-    float* cv = &ct[rl * CP + 8 * cc];
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = cv[e] + bv[e];
-    if (a.glu) {
-      // gated pairs: columns 2j (swish) and 2j + 1 of the interleaved weight give output column j;
-      // N % 8 == 0 (checked on the host), so the 8 columns are 4 whole pairs
-      uint32_t w[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float g0 = v[4 * e] * sigmoidf_(v[4 * e]) * v[4 * e + 1];
-        const float g1 = v[4 * e + 2] * sigmoidf_(v[4 * e + 2]) * v[4 * e + 3];
-        w[e] = pack_bf2(g0, g1);
-      }
-      *reinterpret_cast<u32x2*>(yp + m * a.y_rs + n / 2) = u32x2{w[0], w[1]};
-      continue;
-    }
-    if (a.post_sigmoid) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = sigmoidf_(v[e]);
-    }
-    if (mp) {
-      const uint16_t* mrow = mp + (m % a.mul_rows) * a.mul_rs + n;
-      if (mvec && full) {
-        const u32x4 w = ld16(mrow);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { v[2 * e] *= bflo(w[e]); v[2 * e + 1] *= bfhi(w[e]); }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < a.N) v[e] *= bf2f(mrow[e]);
-      }
-    }
-    if (rp) {
-      const uint16_t* rrow = rp + m * a.r_rs + n;
-      if (rvec && full) {
-        const u32x4 w = ld16(rrow);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { v[2 * e] += bflo(w[e]); v[2 * e + 1] += bfhi(w[e]); }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < a.N) v[e] += bf2f(rrow[e]);
-      }
-    }
-    if (yp && n < ycols) {
-      uint16_t* yrow = yp + m * a.y_rs + n;
-      if (yvec && full && n + 8 <= ycols) {
-        st16(yrow, u32x4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])});
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < a.N && n + e < ycols) yrow[e] = f2bf(v[e]);
-      }
-    }
-    if (ytp) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) cv[e] = v[e];              // final values for the transposed pass
-    }
-  }
   if (ytp) {
     // transposed columns [tcol0, tcol0 + tcols): each thread stores 8 consecutive rows of one column
     __syncthreads();
