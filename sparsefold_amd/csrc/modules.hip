@@ -101,12 +101,13 @@ int zero_init_out(int64_t rows, int C, int HD, const void* o, const void* cond, 
 // with LN(c) the LayerNorm of the condition rows (lnc_w / lnc_b, eps 1e-5), rounded to bf16 as
 // the LayerNorm kernel writes it.  It replaces a LayerNorm and three GEMM launches that each
 // fill a fraction of the GPU (1024 x 384 -> 768: 4.8 + 6.2 + 6.3 + 6.6 us in the diffusion
-// block).  Workgroup (64-row block, 64-channel block, term): the block's condition rows --
-// normalised unless term 2 -- staged in LDS, then wave w forms the 32 x 32 quadrant of channels
-// 32 (w & 1) .. and rows 32 (w >> 1) .. as D^T = W c^T (lane: row li, channels 8 j + 4 half ..),
-// the weight rows read straight from global memory (they stay in L2).  Every load of a workgroup
-// -- its weight chunks, condition rows and the LayerNorm affine -- is issued at its start: one
-// memory round trip (with the loads after one another, 19 us: a round trip each).
+// block).  Workgroup (64-row block, 128-channel block, term), 4 waves: the block's condition
+// rows -- normalised unless term 2 -- staged in LDS, then wave w forms channels 32 w .. of all 64
+// rows as D^T = W c^T (two 32-row accumulators; lane: row li, channels 8 j + 4 half ..), its
+// weight rows read once straight from global memory (they stay in L2).  Every load of a
+// workgroup -- its weight chunks, condition rows and the LayerNorm affine -- is issued at its
+// start: one memory round trip (with the loads after one another, 19 us: a round trip each).
+// With 8 waves of 32 x 32 quadrants every weight chunk was read twice per workgroup (21 us).
 // ---------------------------------------------------------------------------------------
 struct CondTermsArgs {
   int64_t rows; int C, Cs;
@@ -118,7 +119,7 @@ struct CondTermsArgs {
 };
 constexpr int kCondMaxCs = 384;
 
-__global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) {
+__global__ __launch_bounds__(256) void cond_terms_kernel(const CondTermsArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t sA[];   // [64][Cs + 8], then lnc_w, lnc_b (f32)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
   const int Cs = a.Cs, pitch = Cs + 8, nch = Cs / 8;
@@ -128,25 +129,27 @@ __global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) 
   float* sG = reinterpret_cast<float*>(sA + 64 * pitch);
   float* sB = sG + Cs;
   // the weight chunks first (they depend on nothing): A operand of D^T = W c^T, lane (half, li)
-  // channel nq + li, k = 16 kc + 8 half ..
+  // channel nq + li, k = 16 kc + 8 half ..; wave w takes channels 32 w .. for all 64 rows, so
+  // every weight chunk is read once per workgroup
   const uint16_t* W = term == 0 ? a.w_scale : term == 1 ? a.w_shift : a.w_zc;
-  const int nq = n0 + 32 * (wave & 3), rq = 32 * (wave >> 2);
+  const int nq = n0 + 32 * wave;
   u32x4 wr[kCondMaxCs / 16];
   {
     const uint16_t* wp = W + (int64_t)(nq + li) * Cs + 8 * half;
 #pragma unroll
     for (int kc = 0; kc < kCondMaxCs / 16; ++kc) wr[kc] = 16 * kc < Cs ? ld16(wp + 16 * kc) : u32x4{0, 0, 0, 0};
   }
-  // thread (row tid / 8, part tid % 8): chunks of 8 channels part, part + 8, ...
-  const int rr = tid >> 3, q = tid & 7;
-  u32x4 v[kCondMaxCs / 64];
+  // thread (row tid / 4, part tid % 4): chunks of 8 channels part, part + 4, ...
+  constexpr int kParts = 4, kChunks = kCondMaxCs / 8 / kParts;
+  const int rr = tid >> 2, q = tid & 3;
+  u32x4 v[kChunks];
   {
     const uint16_t* cp = a.cond + min(r0 + rr, a.rows - 1) * Cs;
 #pragma unroll
-    for (int t = 0; t < kCondMaxCs / 64; ++t) v[t] = q + 8 * t < nch ? ld16(cp + 8 * (q + 8 * t)) : u32x4{0, 0, 0, 0};
+    for (int t = 0; t < kChunks; ++t) v[t] = q + kParts * t < nch ? ld16(cp + 8 * (q + kParts * t)) : u32x4{0, 0, 0, 0};
   }
   if (term < 2)                                                 // the LayerNorm's affine, to LDS
-    for (int c = 4 * tid; c < Cs; c += 2048) {
+    for (int c = 4 * tid; c < Cs; c += 1024) {
       *reinterpret_cast<f32x4*>(sG + c) = *reinterpret_cast<const f32x4*>(a.lnc_w + c);
       *reinterpret_cast<f32x4*>(sB + c) = a.lnc_b ? *reinterpret_cast<const f32x4*>(a.lnc_b + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -156,17 +159,16 @@ __global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) 
     if (term < 2) {
       float sum = 0.f;
 #pragma unroll
-      for (int t = 0; t < kCondMaxCs / 64; ++t)
+      for (int t = 0; t < kChunks; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum += bflo(v[t][e]) + bfhi(v[t][e]);
       sum += __shfl_xor(sum, 1);
       sum += __shfl_xor(sum, 2);
-      sum += __shfl_xor(sum, 4);
       mean = sum / (float)Cs;
       float sq = 0.f;
 #pragma unroll
-      for (int t = 0; t < kCondMaxCs / 64; ++t) {
-        if (q + 8 * t < nch) {
+      for (int t = 0; t < kChunks; ++t) {
+        if (q + kParts * t < nch) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float d0 = bflo(v[t][e]) - mean, d1 = bfhi(v[t][e]) - mean;
@@ -176,12 +178,11 @@ __global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) 
       }
       sq += __shfl_xor(sq, 1);
       sq += __shfl_xor(sq, 2);
-      sq += __shfl_xor(sq, 4);
       rstd = rsqrtf(sq / (float)Cs + 1e-5f);
     }
 #pragma unroll
-    for (int t = 0; t < kCondMaxCs / 64; ++t) {
-      const int ch = q + 8 * t;
+    for (int t = 0; t < kChunks; ++t) {
+      const int ch = q + kParts * t;
       if (ch >= nch) continue;
       u32x4 y = v[t];
       if (term < 2) {
@@ -197,26 +198,40 @@ __global__ __launch_bounds__(512) void cond_terms_kernel(const CondTermsArgs a) 
   }
   __syncthreads();
   const float* bias = term == 0 ? a.b_scale : term == 1 ? nullptr : a.b_zc;
-  const uint16_t* ap = sA + (rq + li) * pitch + 8 * half;
-  f32x16 acc;
+  f32x16 acc[2];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 #pragma unroll
   for (int kc = 0; kc < kCondMaxCs / 16; ++kc)
-    if (16 * kc < Cs) acc = mfma32(as_bf16x8(wr[kc]), as_bf16x8(ld16(ap + 16 * kc)), acc);
-  const int64_t row = r0 + rq + li;
-  if (row >= a.rows) return;
-  uint16_t* out = (term == 0 ? a.scale : term == 1 ? a.shift : a.zgate) + row * a.C;
+    if (16 * kc < Cs) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = nq + 8 * j + 4 * half;
-    float v4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v4[e] = acc[4 * j + e] + (bias ? bias[n + e] : 0.f);
-      if (term != 1) v4[e] = sigmoidf_(v4[e]);
+      for (int i = 0; i < 2; ++i)                             // rows 32 i + li: two independent chains
+        acc[i] = mfma32(as_bf16x8(wr[kc]), as_bf16x8(ld16(sA + (32 * i + li) * pitch + 8 * half + 16 * kc)), acc[i]);
     }
-    *reinterpret_cast<u32x2*>(out + n) = u32x2{pack_bf2(v4[0], v4[1]), pack_bf2(v4[2], v4[3])};
+  float bn[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bn[j][e] = bias ? bias[nq + 8 * j + 4 * half + e] : 0.f;
+  uint16_t* outb = term == 0 ? a.scale : term == 1 ? a.shift : a.zgate;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t row = r0 + 32 * i + li;
+    if (row >= a.rows) continue;
+    uint16_t* out = outb + row * a.C;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = nq + 8 * j + 4 * half;
+      float v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v4[e] = acc[i][4 * j + e] + bn[j][e];
+        if (term != 1) v4[e] = sigmoidf_(v4[e]);
+      }
+      *reinterpret_cast<u32x2*>(out + n) = u32x2{pack_bf2(v4[0], v4[1]), pack_bf2(v4[2], v4[3])};
+    }
   }
 }
 
@@ -236,7 +251,7 @@ int cond_terms(int64_t rows, int C, int Cs, const void* cond, const float* lnc_w
   t.w_zc = static_cast<const uint16_t*>(w_zc); t.b_scale = b_scale; t.b_zc = b_zc;
   t.scale = static_cast<uint16_t*>(scale); t.shift = static_cast<uint16_t*>(shift); t.zgate = static_cast<uint16_t*>(zgate);
   const size_t lds = (size_t)64 * (Cs + 8) * 2 + (size_t)2 * Cs * 4;   // 53 KB at Cs = 384
-  hipLaunchKernelGGL(cond_terms_kernel, dim3((unsigned)((rows + 63) / 64), (unsigned)(C / 128), 3), dim3(512), lds, st, t);
+  hipLaunchKernelGGL(cond_terms_kernel, dim3((unsigned)((rows + 63) / 64), (unsigned)(C / 128), 3), dim3(256), lds, st, t);
   return sf_check_launch("cond_terms_kernel");
 }
 
