@@ -88,35 +88,40 @@ __device__ __forceinline__ u32x4 load8_guard(const uint16_t* row, int d0, int n,
 }
 
 // LayerNorm (eps 1e-5, no affine: gamma / beta are folded into the consuming weight) of 32
-// positions x 128 channels, straight into MFMA operand registers: lane (li, half)
-// holds channels 16*kk + 8*half .. +7 of position li for kk = 0..7 -- the same registers serve
-// as A operand (rows = positions) and as B operand (columns = positions).
-__device__ __forceinline__ void ln128_operands(const u32x4 (&x)[8], bool valid, bf16x8 (&xo)[8]) {
+// positions x 16*NC channels, straight into MFMA operand registers: lane (li, half)
+// holds channels 16*kk + 8*half .. +7 of position li for kk = 0..NC-1 -- the same registers
+// serve as A operand (rows = positions) and as B operand (columns = positions).
+template <int NC>
+__device__ __forceinline__ void ln_operands(const u32x4 (&x)[NC], bool valid, bf16x8 (&xo)[NC]) {
+  constexpr float kInvC = 1.0f / (16 * NC);
   float sum = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
+  for (int kk = 0; kk < NC; ++kk)
 #pragma unroll
     for (int e = 0; e < 4; ++e) sum += bflo(x[kk][e]) + bfhi(x[kk][e]);
   sum += __shfl_xor(sum, 32);
-  const float mean = sum * (1.0f / 128);
+  const float mean = sum * kInvC;
   float sq = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
+  for (int kk = 0; kk < NC; ++kk)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float d0 = bflo(x[kk][e]) - mean, d1 = bfhi(x[kk][e]) - mean;
       sq += d0 * d0 + d1 * d1;
     }
   sq += __shfl_xor(sq, 32);
-  const float rstd = valid ? rsqrtf(sq * (1.0f / 128) + 1e-5f) : 0.f;
+  const float rstd = valid ? rsqrtf(sq * kInvC + 1e-5f) : 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk)
+  for (int kk = 0; kk < NC; ++kk)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const bf16x2 v = cvt_bf2((bflo(x[kk][e]) - mean) * rstd, (bfhi(x[kk][e]) - mean) * rstd);
       xo[kk][2 * e] = v[0];
       xo[kk][2 * e + 1] = v[1];
     }
+}
+__device__ __forceinline__ void ln128_operands(const u32x4 (&x)[8], bool valid, bf16x8 (&xo)[8]) {
+  ln_operands<8>(x, valid, xo);
 }
 
 // Thread-local last-error plumbing shared by all C entry points.

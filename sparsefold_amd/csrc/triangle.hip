@@ -68,38 +68,53 @@ __host__ __device__ inline int64_t bias_off_stored(int h, int i, int js, int NP)
 __host__ __device__ inline int64_t bias_off(int h, int i, int j, int NP) {
   return bias_off_stored(h, i, (j & ~63) + bias_pos64(j & 63), NP);
 }
-// Attention output o of (head h, attention row r, query i): per (h, r, block of 32 queries) one
-// 2 KB block [piece 4][query 32][8 dims], piece 2 hf + kk holding the 8 dims the attention
+// The operand layouts below are written for KC = D / 16 k-chunks of 16 dims per head: KC = 2 for
+// head dim 32 (C = 128), KC = 1 for head dim 16 (C = 64).
+// Attention output o of (head h, attention row r, query i): per (h, r, block of 32 queries) a
+// block of KC KB [piece 2 KC][query 32][8 dims], piece KC hf + kk holding the 8 dims the attention
 // epilogue's lane half hf stores as its k-chunk kk (dims 16 kk + 8 (t/4) + 4 hf + t%4 of the
 // head, t = 0..7).  Each store
 // of the epilogue (a piece of 32 queries per lane half) and each load of the output stage (a
 // piece of 32 positions) then covers 512 contiguous bytes; with a query's 64 bytes contiguous,
 // consecutive lanes were 64 bytes apart.  Indexed by attention row and query, not by pair
 // position, so both nodes write whole blocks.
+template <int KC = 2>
 __host__ __device__ inline int64_t o_off(int h, int r, int i, int hf, int kk, int N, int NP) {
-  return ((((int64_t)h * N + r) * (NP >> 5) + (i >> 5)) << 10) + ((((2 * hf + kk) << 5) + (i & 31)) << 3);
+  return ((((int64_t)h * N + r) * (NP >> 5) + (i >> 5)) * (512 * KC)) + ((((KC * hf + kk) << 5) + (i & 31)) << 3);
 }
 // Q / K / G of (row r, head h): position p, k-chunk kk, lane half hf.  The 8 values at the
 // returned offset are dims 16*kk + 8*(t/4) + 4*hf + t%4 for t = 0..7 -- what lane (p%32, hf)
 // of a 32x32x16 MFMA holds for k-chunk kk, both as the A operand of S^T = K Q^T and, for Q,
 // as its B operand, and what the D^T accumulator of the projection holds in registers
 // 8*kk .. 8*kk+7.  The dot product q.k is invariant under this common dim permutation.
+template <int KC = 2>
 __host__ __device__ __forceinline__ int64_t ql_off(int r, int h, int H, int NP, int p, int kk, int hf) {
-  return ((((int64_t)r * H + h) * (NP >> 5) + (p >> 5)) * 4 + kk * 2 + hf) * 256 + (p & 31) * 8;
+  return ((((int64_t)r * H + h) * (NP >> 5) + (p >> 5)) * (2 * KC) + kk * 2 + hf) * 256 + (p & 31) * 8;
 }
-// V^T of (row r, head h): 16-key chunk c16, lane half hf, dim d.  The 8 values are keys
+// V^T of (row r, head h): 16-key chunk c16, lane half hf, dim d < 16 KC.  The 8 values are keys
 // 16*c16 + 8*(t/4) + 4*hf + t%4 (PV slot order: the keys whose weights lane half hf holds).
+template <int KC = 2>
 __host__ __device__ __forceinline__ int64_t vl_off(int r, int h, int H, int NP, int c16, int hf, int d) {
-  return ((((int64_t)r * H + h) * (NP >> 4) + c16) * 2 + hf) * 256 + d * 8;
+  return ((((int64_t)r * H + h) * (NP >> 4) + c16) * 2 + hf) * (128 * KC) + d * 8;
 }
 
-constexpr int kPC = 128;              // channels (C) handled by the fast path
+// Sizes of the fast paths: KC = 2 (C = 128, head dim 32) and KC = 1 (C = 64, head dim 16), four
+// heads each.
+template <int KC>
+struct TriDims {
+  static constexpr int C = 64 * KC;                   // channels
+  static constexpr int D = 16 * KC;                   // head dim
+  static constexpr int WP = C + 8;                    // LDS pitch (elements) of weight rows
+  static constexpr int NC = C / 16;                   // 16-channel k-chunks of a position
+  static constexpr int NB = C / 32;                   // blocks of 32 rows of each of W_q, W_k, W_v, W_g, W_o
+  static constexpr int Cols = (4 * NB + 1) * 32;      // folded rows: q k v g + bias block (32, 4 used)
+  // Blocks of 32 folded rows the projection keeps in LDS: q (0 .. NB-1), k, v and the bias block
+  // (folded block 4 NB, stored as LDS block 3 NB); the gate rows are used by the output kernel.
+  static constexpr int ProjBlocks = 3 * NB + 1;
+};
+constexpr int kPC = 128;              // channels (C) of the head-dim-32 path
 constexpr int kWP = kPC + 8;          // LDS pitch (elements) of weight rows
 constexpr int kPWaves = 8;            // waves per projection / output workgroup
-constexpr int kPCols = 17 * 32;       // folded rows: q k v g (4 x 128) + bias block (32, 4 used)
-// Blocks of 32 folded rows the projection keeps in LDS: q (0-3), k (4-7), v (8-11) and the bias
-// block (16, stored as LDS block 12); the gate rows (12-15) are used by the output kernel.
-constexpr int kProjBlocks = 13;
 
 struct FastWs {
   uint16_t *q, *k, *vt, *bias, *o, *wf;
@@ -119,8 +134,10 @@ int fused_groups(int32_t N) {
   return (NP / 4) * ((NP + 255) / 256);
 }
 
+template <int KC = 2>
 FastWs carve_fast(void* base, int32_t N, int32_t H) {
-  const size_t NP = (size_t)round_np(N), E = NP * NP * H * 32;
+  using TD = TriDims<KC>;
+  const size_t NP = (size_t)round_np(N), E = NP * NP * H * TD::D;
   FastWs w{};
   char* p = (char*)base;
   size_t off = 0;
@@ -128,9 +145,9 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
   w.k = (uint16_t*)(p + off); off += round_up(E * 2);
   w.vt = (uint16_t*)(p + off); off += round_up(E * 2);
   w.bias = (uint16_t*)(p + off); off += round_up(NP * NP * H * 2);
-  w.o = (uint16_t*)(p + off); off += round_up((size_t)N * NP * H * 32 * 2);   // o_off blocks
-  w.wf = (uint16_t*)(p + off); off += round_up((size_t)kPCols * kPC * 2);
-  w.off = (float*)(p + off); off += round_up((size_t)kPCols * 4);
+  w.o = (uint16_t*)(p + off); off += round_up((size_t)N * NP * H * TD::D * 2);   // o_off blocks
+  w.wf = (uint16_t*)(p + off); off += round_up((size_t)TD::Cols * TD::C * 2);
+  w.off = (float*)(p + off); off += round_up((size_t)TD::Cols * 4);
   w.flags = (uint8_t*)(p + off); off += round_up((size_t)N * H);
   w.nctr = fused_groups(N) + 4;
   w.ctr = (int*)(p + off); off += round_up((size_t)w.nctr * 4);
@@ -142,14 +159,14 @@ FastWs carve_fast(void* base, int32_t N, int32_t H) {
 
 // ---------------------------------------------------------------------------------------
 // 0. weight fold: wf[n][c] = bf16(w[n][c] * gamma[c]), off[n] = sum_c beta[c] w[n][c];
-//    rows 516..543 (padding of the bias block) are zero.  One wave per weight row.  Also clears
+//    rows 4 H D + H .. Cols-1 (padding of the bias block) are zero.  One wave per weight row.  Also clears
 //    the attention kernel's fix-up flags.
 // ---------------------------------------------------------------------------------------
 struct TriFoldArgs {
-  int nrows;                          // 4 * H * 32 + H
-  const uint16_t* w;                  // [nrows, 128]
+  int nrows;                          // 4 * H * D + H
+  const uint16_t* w;                  // [nrows, C]
   const float* ln_w; const float* ln_b;
-  uint16_t* wf; float* off;           // [544, 128], [544]
+  uint16_t* wf; float* off;           // [Cols, C], [Cols]
   uint8_t* flags; int nflags;         // [N * H], cleared
   int* ctr; int nctr;                 // fused epilogue counters, cleared
   uint8_t* defer; int ndefer;         // fused epilogue deferred rows, cleared
@@ -158,7 +175,9 @@ struct TriFoldArgs {
   int* rgl; int rg, N; const uint8_t* seq;
 };
 
+template <int KC>
 __global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
+  using TD = TriDims<KC>;
   const int lane = threadIdx.x & 63;
   if (blockIdx.x == gridDim.x - 1) {                       // the extra last workgroup compacts the row groups
     if (a.rgl == nullptr) return;
@@ -192,15 +211,23 @@ __global__ __launch_bounds__(256) void tri_fold_kernel(const TriFoldArgs a) {
   for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.nctr; f += zstride) a.ctr[f] = 0;
   for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < a.ndefer; f += zstride) a.defer[f] = 0;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= kPCols) return;
-  const int c = 2 * lane;
-  float w0 = 0.f, w1 = 0.f;
-  if (n < a.nrows) {
-    const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.w + (int64_t)n * kPC + c);
-    w0 = bflo(raw); w1 = bfhi(raw);
+  if (n >= TD::Cols) return;
+  float part;
+  if constexpr (KC == 2) {                                 // two channels per lane
+    const int c = 2 * lane;
+    float w0 = 0.f, w1 = 0.f;
+    if (n < a.nrows) {
+      const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.w + (int64_t)n * TD::C + c);
+      w0 = bflo(raw); w1 = bfhi(raw);
+    }
+    *reinterpret_cast<uint32_t*>(a.wf + (int64_t)n * TD::C + c) = pack_bf2(w0 * a.ln_w[c], w1 * a.ln_w[c + 1]);
+    part = a.ln_b != nullptr ? a.ln_b[c] * w0 + a.ln_b[c + 1] * w1 : 0.f;
+  } else {                                                 // one channel per lane
+    const int c = lane;
+    const float w0 = n < a.nrows ? bf2f(a.w[(int64_t)n * TD::C + c]) : 0.f;
+    a.wf[(int64_t)n * TD::C + c] = f2bf(w0 * a.ln_w[c]);
+    part = a.ln_b != nullptr ? a.ln_b[c] * w0 : 0.f;
   }
-  *reinterpret_cast<uint32_t*>(a.wf + (int64_t)n * kPC + c) = pack_bf2(w0 * a.ln_w[c], w1 * a.ln_w[c + 1]);
-  const float part = a.ln_b != nullptr ? a.ln_b[c] * w0 + a.ln_b[c + 1] * w1 : 0.f;
   const float tot = wave_sum(part);
   if (lane == 0) a.off[n] = tot;
 }
@@ -212,54 +239,60 @@ struct TriProjArgs {
   int N, NP, H, transpose;
   float qscale;                       // softmax scale * log2(e)
   const uint16_t* z; const uint8_t* seq;
-  const uint16_t* wf; const float* off;   // folded weight [544, 128] and column offsets
+  const uint16_t* wf; const float* off;   // folded weight [Cols, C] and column offsets
   uint16_t *q, *k, *vt, *bias;
   int items, items_per_wave;          // items = NP * NP / 32 position blocks
 };
 
 // Persistent: each workgroup keeps the folded weight in LDS and walks 32-position blocks;
 // positions of attention row r are z[r, p] (starting node) or z[p, r] (ending node).
+// A block of 32 projection rows is one head of 32 dims (KC = 2) or two heads of 16 (KC = 1,
+// rows 16 j .. 16 j + 15 = head 2 nb + j).
+template <int KC>
 __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[kProjBlocks * 32 * kWP];
-  __shared__ __attribute__((aligned(16))) float sOff[kProjBlocks * 32];
+  using TD = TriDims<KC>;
+  constexpr int C = TD::C, WP = TD::WP, NC = TD::NC, NB = TD::NB, PB = TD::ProjBlocks;
+  __shared__ __attribute__((aligned(16))) uint16_t sW[PB * 32 * WP];
+  __shared__ __attribute__((aligned(16))) float sOff[PB * 32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
 
   // every load is issued before the first LDS store: one memory latency for the whole staging
   // (a loop of load, wait, store paid it 13 times per workgroup)
-  constexpr int kStage = kProjBlocks * 32 * (kPC / 8) / (64 * kPWaves);
-  static_assert(kProjBlocks * 32 * (kPC / 8) % (64 * kPWaves) == 0, "whole staging rounds");
+  constexpr int kPieces = PB * 32 * (C / 8);                // 16-byte pieces of the staged rows
+  constexpr int kStage = (kPieces + 64 * kPWaves - 1) / (64 * kPWaves);
+  static_assert(KC != 2 || kPieces % (64 * kPWaves) == 0, "whole staging rounds");
   u32x4 wst[kStage];
 #pragma unroll
   for (int j = 0; j < kStage; ++j) {
-    const int t = tid + j * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    const int src = n < 12 * 32 ? n : n + 4 * 32;      // LDS block 12 <- folded block 16
-    wst[j] = ld16(a.wf + (int64_t)src * kPC + c8);
+    const int t = tid + j * 64 * kPWaves, n = t / (C / 8), c8 = (t % (C / 8)) * 8;
+    const int src = n < 3 * C ? n : n + C;                  // LDS block 3 NB <- folded bias block 4 NB
+    if (kPieces % (64 * kPWaves) == 0 || t < kPieces) wst[j] = ld16(a.wf + (int64_t)src * C + c8);
   }
 #pragma unroll
   for (int j = 0; j < kStage; ++j) {
-    const int t = tid + j * 64 * kPWaves, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    st16(&sW[n * kWP + c8], wst[j]);
+    const int t = tid + j * 64 * kPWaves, n = t / (C / 8), c8 = (t % (C / 8)) * 8;
+    if (kPieces % (64 * kPWaves) == 0 || t < kPieces) st16(&sW[n * WP + c8], wst[j]);
   }
-  for (int n = tid; n < kProjBlocks * 32; n += 64 * kPWaves) sOff[n] = a.off[n < 12 * 32 ? n : n + 4 * 32];
+  for (int n = tid; n < PB * 32; n += 64 * kPWaves) sOff[n] = a.off[n < 3 * C ? n : n + C];
   __syncthreads();
 
   const int bpr = NP / 32;                              // position blocks per attention row
-  auto block_load = [&](int item, u32x4 (&x)[8], bool& valid, int& r, int& p) {
+  auto block_load = [&](int item, u32x4 (&x)[NC], bool& valid, int& r, int& p) {
     r = item / bpr;
     p = (item - r * bpr) * 32 + li;
     const int za = a.transpose ? p : r, zb = a.transpose ? r : p;
     valid = za < N && zb < N;
-    const uint16_t* zp = a.z + ((int64_t)(valid ? za : 0) * N + (valid ? zb : 0)) * kPC + 8 * half;
+    const uint16_t* zp = a.z + ((int64_t)(valid ? za : 0) * N + (valid ? zb : 0)) * C + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < NC; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
   };
   auto pos_valid = [&](int r, int pe) { return a.transpose ? (pe < N && r < N) : (r < N && pe < N); };
 
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
-  u32x4 xn[8];
+  u32x4 xn[NC];
   bool vn = false;
   int rn = 0, pn = 0;
   if (first < last) block_load(first, xn, vn, rn, pn);
@@ -267,29 +300,32 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
     // the LDS weights are re-read every item: hoisted out of the loop they would not fit in
     // registers
     asm volatile("" ::: "memory");
-    bf16x8 xo[8];
+    bf16x8 xo[NC];
     const bool valid = vn;
     const int r = rn, p = pn;                            // this lane's position p (= p0 + li)
-    ln128_operands(xn, valid, xo);
+    ln_operands<NC>(xn, valid, xo);
     if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
     const int p0 = p - li;
 
     // q, k: D^T = W . X^T -> lane = position; registers 8*kk .. 8*kk+7 are the 16 bytes of
-    // k-chunk kk in the Q/K layout
+    // k-chunk kk (KC = 2) or of head 2 nb + kk (KC = 1) in the Q/K layout
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
       uint16_t* dst = which == 0 ? a.q : a.k;
       const float sc = which == 0 ? a.qscale : 1.0f;
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const int nb = 4 * which + hh;
+      for (int hh = 0; hh < NB; ++hh) {
+        const int nb = NB * which + hh;
         f32x16 acc;
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-          acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xo[kk], acc);
-        uint16_t* op = dst + ql_off(r, hh, H, NP, p, 0, half);
+        for (int kk = 0; kk < NC; ++kk)
+          acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * WP + 16 * kk + 8 * half])), xo[kk], acc);
+        // KC = 2: k-chunk kk of head hh, 512 elements apart; KC = 1: head 2 hh + kk (NP * 16 apart)
+        uint16_t* op = dst + ql_off<KC>(r, KC == 2 ? hh : 2 * hh, H, NP, p, 0, half);
+        constexpr int kStep = KC == 2 ? 512 : 0;
+        const int64_t step = KC == 2 ? kStep : (int64_t)NP * 16;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const f32x4 o0 = *reinterpret_cast<const f32x4*>(&sOff[32 * nb + 16 * kk + 4 * half]);
@@ -302,22 +338,24 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
             w[2 + e] = pack_bf2(valid ? (acc[8 * kk + 4 + 2 * e] + o1[2 * e]) * sc : 0.f,
                                 valid ? (acc[8 * kk + 4 + 2 * e + 1] + o1[2 * e + 1]) * sc : 0.f);
           }
-          st16_stream(op + kk * 512, u32x4{w[0], w[1], w[2], w[3]});
+          st16_stream(op + kk * step, u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
-    // v: D = X . W^T -> lane = dim li; registers 8*cc .. 8*cc+7 are keys of 16-key chunk cc of
-    // this block in PV slot order for lane half `half`
+    // v: D = X . W^T -> lane = projection row li (head hh, dim li for KC = 2; head 2 hh + li / 16,
+    // dim li % 16 for KC = 1); registers 8*cc .. 8*cc+7 are keys of 16-key chunk cc of this block
+    // in PV slot order for lane half `half`
 #pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const int nb = 8 + hh;
+    for (int hh = 0; hh < NB; ++hh) {
+      const int nb = 2 * NB + hh;
       f32x16 acc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
+      for (int kk = 0; kk < NC; ++kk)
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * WP + 16 * kk + 8 * half])), acc);
       const float off = sOff[32 * nb + li];
+      const int vh = KC == 2 ? hh : 2 * hh + (li >> 4), vd = KC == 2 ? li : li & 15;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
         uint32_t w[4];
@@ -329,18 +367,18 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
           w[e] = pack_bf2(pos_valid(r, k0) ? acc[8 * cc + t0] + off : 0.f,
                           pos_valid(r, k1) ? acc[8 * cc + t1] + off : 0.f);
         }
-        st16_stream(a.vt + vl_off(r, hh, H, NP, (p0 >> 4) + cc, half, li), u32x4{w[0], w[1], w[2], w[3]});
+        st16_stream(a.vt + vl_off<KC>(r, vh, H, NP, (p0 >> 4) + cc, half, vd), u32x4{w[0], w[1], w[2], w[3]});
       }
     }
     // bias planes: D = X . Wb^T, lane = head li (< H), 4 consecutive positions
     {
-      const int nb = 12;                                // LDS block of the folded bias rows
+      const int nb = 3 * NB;                            // LDS block of the folded bias rows
       f32x16 acc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), acc);
+      for (int kk = 0; kk < NC; ++kk)
+        acc = mfma32(xo[kk], as_bf16x8(ld16(&sW[(32 * nb + li) * WP + 16 * kk + 8 * half])), acc);
       if (li < H) {
         const float off = sOff[32 * nb + li];
 #pragma unroll
@@ -375,67 +413,72 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
 //      out[p] = z[p] + (o[p] * sigmoid(g)) . W_o^T
 //    The gate of pair position (za, zb) is the gate the attention row used there for both the
 //    starting and the ending node, so it is recomputed here from z instead of being stored.
-//    W_g and W_o are resident in LDS; lane = position.  Within each head, o holds its 32 dims
+//    W_g and W_o are resident in LDS; lane = position.  Within each head, o holds its D dims
 //    in the order the attention epilogue produces them (lane half hf, register group c,
 //    element e -> dim 8c + 4hf + e); W_o's columns are permuted to match when staged.
 // ---------------------------------------------------------------------------------------
 struct TriOutArgs {
   int N, NP, transpose;
   const uint16_t* o;                  // o_off blocks
-  const uint16_t* wo;                 // [128 out, 128 in]
-  const uint16_t* wg;                 // folded gate rows [128, 128]
-  const float* goff;                  // [128]
-  const uint16_t* z;                  // [P, 128]
+  const uint16_t* wo;                 // [C out, C in]
+  const uint16_t* wg;                 // folded gate rows [C, C]
+  const float* goff;                  // [C]
+  const uint16_t* z;                  // [P, C]
   int add_residual;
   uint16_t* out;
   int items, items_per_wave;          // blocks of 32 queries of one attention row: N * ceil(N / 32)
 };
 
 // W_o (its columns permuted to the attention epilogue's dim order) and the folded gate rows into
-// LDS rows of pitch kWP, by NTHR threads: every load first, then the stores (one memory latency).
-template <int NTHR>
+// LDS rows of pitch WP, by NTHR threads: every load first, then the stores (one memory latency).
+template <int NTHR, int KC = 2>
 __device__ __forceinline__ void stage_out_weights(uint16_t* sW, uint16_t* sG, float* sGoff, const uint16_t* wo,
                                                   const uint16_t* wg, const float* goff, int tid) {
-  constexpr int kStage = kPC * (kPC / 8) / NTHR;
-  static_assert(kPC * (kPC / 8) % NTHR == 0, "whole staging rounds");
+  constexpr int C = TriDims<KC>::C, WP = TriDims<KC>::WP;
+  constexpr int kStage = C * (C / 8) / NTHR;
+  static_assert(C * (C / 8) % NTHR == 0, "whole staging rounds");
   u32x2 wlo[kStage], whi[kStage];
   u32x4 gst[kStage];
 #pragma unroll
   for (int u = 0; u < kStage; ++u) {
-    const int t = tid + u * NTHR, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
+    const int t = tid + u * NTHR, n = t / (C / 8), c8 = (t % (C / 8)) * 8;
     // o feature c8 .. c8+7 = (head, lane half hf, groups 2j and 2j+1): natural dims
-    // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head
-    const int hd = c8 & ~31, hf = (c8 >> 4) & 1, j = (c8 >> 3) & 1;
-    const uint16_t* src = wo + (int64_t)n * kPC + hd + 16 * j + 4 * hf;
+    // 16j + 4hf + 0..3 and 16j + 8 + 4hf + 0..3 of the head (KC = 1: j = 0)
+    const int hd = KC == 2 ? c8 & ~31 : c8 & ~15;
+    const int hf = KC == 2 ? (c8 >> 4) & 1 : (c8 >> 3) & 1, j = KC == 2 ? (c8 >> 3) & 1 : 0;
+    const uint16_t* src = wo + (int64_t)n * C + hd + 16 * j + 4 * hf;
     wlo[u] = *reinterpret_cast<const u32x2*>(src);
     whi[u] = *reinterpret_cast<const u32x2*>(src + 8);
-    gst[u] = ld16(wg + (int64_t)n * kPC + c8);
+    gst[u] = ld16(wg + (int64_t)n * C + c8);
   }
 #pragma unroll
   for (int u = 0; u < kStage; ++u) {
-    const int t = tid + u * NTHR, n = t / (kPC / 8), c8 = (t % (kPC / 8)) * 8;
-    st16(&sW[n * kWP + c8], u32x4{wlo[u][0], wlo[u][1], whi[u][0], whi[u][1]});
-    st16(&sG[n * kWP + c8], gst[u]);
+    const int t = tid + u * NTHR, n = t / (C / 8), c8 = (t % (C / 8)) * 8;
+    st16(&sW[n * WP + c8], u32x4{wlo[u][0], wlo[u][1], whi[u][0], whi[u][1]});
+    st16(&sG[n * WP + c8], gst[u]);
   }
-  for (int n = tid; n < kPC; n += NTHR) sGoff[n] = goff[n];
+  for (int n = tid; n < C; n += NTHR) sGoff[n] = goff[n];
 }
 
 // Gate of 32 pair positions (lane = position li, half = channel half): from this lane's z
-// channels 16 kk + 8 half + 0..7 (zn) and o pieces (on: feature 16 kk + 8 half + 0..7 of o is head
-// kk/2, piece (hf = kk%2, k-chunk = half) of the epilogue's order) it forms the gated o operands
-// xg of the output projection and, with add_residual, the residual pieces zr its accumulator
-// layout needs (output features 8c + 4h + e of lane half h sit in z chunk 2nb + c/2 of lane half
-// c%2, elements 4h + e: two permlane32 swaps per chunk bring them over).
+// channels 16 kk + 8 half + 0..7 (zn) and o pieces (on: feature 16 kk + 8 half + 0..7 of o is,
+// for KC = 2, head kk/2, piece (hf = kk%2, k-chunk = half) of the epilogue's order; for KC = 1,
+// head kk, piece hf = half) it forms the gated o operands xg of the output projection and, with
+// add_residual, the residual pieces zr its accumulator layout needs (output features 8c + 4h + e
+// of lane half h sit in z chunk 2nb + c/2 of lane half c%2, elements 4h + e: two permlane32 swaps
+// per chunk bring them over).
 //   g = LN(z[p]) . W_g^T   (gamma folded into W_g, beta into its offset)
-__device__ __forceinline__ void out_gate(const u32x4 (&on)[8], const u32x4 (&zn)[8], bool ok, bool add_residual,
-                                         const uint16_t* sG, const float* sGoff, int lane, bf16x8 (&xg)[8],
-                                         uint32_t (&zr)[8][2][2]) {
+template <int KC = 2>
+__device__ __forceinline__ void out_gate(const u32x4 (&on)[TriDims<KC>::NC], const u32x4 (&zn)[TriDims<KC>::NC], bool ok,
+                                         bool add_residual, const uint16_t* sG, const float* sGoff, int lane,
+                                         bf16x8 (&xg)[TriDims<KC>::NC], uint32_t (&zr)[TriDims<KC>::NC][2][2]) {
+  constexpr int NC = TriDims<KC>::NC, NB = TriDims<KC>::NB, WP = TriDims<KC>::WP;
   const int half = lane >> 5, li = lane & 31;
-  bf16x8 zo[8];
-  ln128_operands(zn, ok, zo);
+  bf16x8 zo[NC];
+  ln_operands<NC>(zn, ok, zo);
   if (add_residual) {   // (add_residual false: the caller supplies the residual another way, or none)
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
+    for (int kk = 0; kk < NC; ++kk) {
       const auto s02 = __builtin_amdgcn_permlane32_swap(zn[kk][0], zn[kk][2], false, false);
       const auto s13 = __builtin_amdgcn_permlane32_swap(zn[kk][1], zn[kk][3], false, false);
 #pragma unroll
@@ -445,26 +488,31 @@ __device__ __forceinline__ void out_gate(const u32x4 (&on)[8], const u32x4 (&zn)
       }
     }
   }
-  // gate of head nb: D^T = W_g . X^T -> lane (position, half hf) holds natural dims
-  // 8c + 4hf + e in register 4c + e; o operand chunk kk = 2nb + j of lane half h needs the
-  // gate of half j, register 8h + t -- one permlane32 swap per register pair gets it
+  // gate block nb: D^T = W_g . X^T -> lane (position, half hf) holds gate row 8c + 4hf + e of the
+  // block in register 4c + e.
+  //  KC = 2 (block = head nb): o operand chunk kk = 2nb + j of lane half h needs the gate of
+  //    half j, register 8h + t -- one permlane32 swap per register pair gets it.
+  //  KC = 1 (block = heads 2nb, 2nb + 1): chunk kk = 2nb + j of lane half h needs dims
+  //    8(t/4) + 4h + t%4 of head 2nb + j: rows 16j + ..., register 8j + t of the same lane half.
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      acc = mfma32(as_bf16x8(ld16(&sG[(32 * nb + li) * kWP + 16 * kk + 8 * half])), zo[kk], acc);
+    for (int kk = 0; kk < NC; ++kk)
+      acc = mfma32(as_bf16x8(ld16(&sG[(32 * nb + li) * WP + 16 * kk + 8 * half])), zo[kk], acc);
     float sg[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) sg[r] = sigmoidf_(acc[r] + sGoff[32 * nb + 8 * (r >> 2) + 4 * half + (r & 3)]);
+    if constexpr (KC == 2) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(sg[t]), __float_as_uint(sg[t + 8]), false, false);
-      // sw[0]: gate for chunk 2nb (j = 0), sw[1]: for chunk 2nb + 1 (j = 1), element t
-      sg[t] = __uint_as_float(sw[0]);
-      sg[t + 8] = __uint_as_float(sw[1]);
+      for (int t = 0; t < 8; ++t) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(sg[t]), __float_as_uint(sg[t + 8]), false, false);
+        // sw[0]: gate for chunk 2nb (j = 0), sw[1]: for chunk 2nb + 1 (j = 1), element t
+        sg[t] = __uint_as_float(sw[0]);
+        sg[t + 8] = __uint_as_float(sw[1]);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -482,18 +530,19 @@ __device__ __forceinline__ void out_gate(const u32x4 (&on)[8], const u32x4 (&zn)
 // Output projection + residual of the 32 positions: out[p] = z[p] + (o[p] * g[p]) . W_o^T
 // (blocks.py:286-291, :366).  st(nb, c, v) receives output channels 32 nb + 8 c + 4 half .. +3 of
 // position li as two bf16 pairs; resid(nb, c) gives the same channels of z.
-template <class Store, class Resid>
-__device__ __forceinline__ void out_proj(const bf16x8 (&xg)[8], bool add_residual, const uint16_t* sW, int lane,
-                                         Resid resid, Store st) {
+template <int KC = 2, class Store, class Resid>
+__device__ __forceinline__ void out_proj(const bf16x8 (&xg)[TriDims<KC>::NC], bool add_residual, const uint16_t* sW,
+                                         int lane, Resid resid, Store st) {
+  constexpr int NC = TriDims<KC>::NC, NB = TriDims<KC>::NB, WP = TriDims<KC>::WP;
   const int half = lane >> 5, li = lane & 31;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * kWP + 16 * kk + 8 * half])), xg[kk], acc);
+    for (int kk = 0; kk < NC; ++kk)
+      acc = mfma32(as_bf16x8(ld16(&sW[(32 * nb + li) * WP + 16 * kk + 8 * half])), xg[kk], acc);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float v[4];
@@ -508,15 +557,25 @@ __device__ __forceinline__ void out_proj(const bf16x8 (&xg)[8], bool add_residua
   }
 }
 
+// o piece of feature chunk kk (16 features) for lane half `half`: head kk/2, piece (hf = kk%2,
+// k-chunk = half) for KC = 2; head kk, piece hf = half for KC = 1.
+template <int KC>
+__device__ __forceinline__ int64_t o_piece_off(int kk, int r, int i, int half, int N, int NP) {
+  return KC == 2 ? o_off<2>(kk >> 1, r, i, kk & 1, half, N, NP) : o_off<1>(kk, r, i, half, 0, N, NP);
+}
+
+template <int KC>
 __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[kPC * kWP];
-  __shared__ __attribute__((aligned(16))) uint16_t sG[kPC * kWP];
-  __shared__ __attribute__((aligned(16))) float sGoff[kPC];
-  __shared__ __attribute__((aligned(16))) uint16_t sOut[kPWaves][32 * kWP];   // per-wave output rows
+  using TD = TriDims<KC>;
+  constexpr int C = TD::C, WP = TD::WP, NC = TD::NC;
+  __shared__ __attribute__((aligned(16))) uint16_t sW[C * WP];
+  __shared__ __attribute__((aligned(16))) uint16_t sG[C * WP];
+  __shared__ __attribute__((aligned(16))) float sGoff[C];
+  __shared__ __attribute__((aligned(16))) uint16_t sOut[kPWaves][32 * WP];   // per-wave output rows
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, li = lane & 31;
   uint16_t* const so = sOut[wave];
-  stage_out_weights<64 * kPWaves>(sW, sG, sGoff, a.wo, a.wg, a.goff, tid);
+  stage_out_weights<64 * kPWaves, KC>(sW, sG, sGoff, a.wo, a.wg, a.goff, tid);
   __syncthreads();
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
@@ -524,43 +583,44 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   // position (r, i) (starting node) or (i, r) (ending node)
   const int IB = (a.N + 31) >> 5;
   auto pos = [&](int r, int i) -> int64_t { return a.transpose ? (int64_t)i * a.N + r : (int64_t)r * a.N + i; };
-  auto load = [&](int item, u32x4 (&xo)[8], u32x4 (&xz)[8], int& rn, int& in) {
+  auto load = [&](int item, u32x4 (&xo)[NC], u32x4 (&xz)[NC], int& rn, int& in) {
     rn = item / IB;
     in = (item - rn * IB) * 32 + li;
     const bool ok = in < a.N;
     const int i = ok ? in : 0;
-    const uint16_t* zp = a.z + pos(rn, i) * kPC + 8 * half;
+    const uint16_t* zp = a.z + pos(rn, i) * C + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      xo[kk] = ok ? ld16(a.o + o_off(kk >> 1, rn, i, kk & 1, half, a.N, a.NP)) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < NC; ++kk) {
+      xo[kk] = ok ? ld16(a.o + o_piece_off<KC>(kk, rn, i, half, a.N, a.NP)) : u32x4{0, 0, 0, 0};
       xz[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
     }
   };
-  u32x4 on[8], zn[8];
+  u32x4 on[NC], zn[NC];
   int rn = 0, in = 0;
   if (first < last) load(first, on, zn, rn, in);
   for (int item = first; item < last; ++item) {
     asm volatile("" ::: "memory");                      // LDS weights are re-read every item
     const int r = rn, i0 = in - li;
     const bool ok = in < a.N;                            // only a row's last block has idle lanes
-    bf16x8 xg[8];
-    uint32_t zr[8][2][2];
-    out_gate(on, zn, ok, a.add_residual, sG, sGoff, lane, xg, zr);
+    bf16x8 xg[NC];
+    uint32_t zr[NC][2][2];
+    out_gate<KC>(on, zn, ok, a.add_residual, sG, sGoff, lane, xg, zr);
     if (item + 1 < last) load(item + 1, on, zn, rn, in);   // lands during the output projection
-    out_proj(xg, a.add_residual, sW, lane,
-             [&](int nb, int c) { return u32x2{zr[2 * nb + (c >> 1)][c & 1][0], zr[2 * nb + (c >> 1)][c & 1][1]}; },
-             [&](int nb, int c, u32x2 v) { *reinterpret_cast<u32x2*>(so + li * kWP + 32 * nb + 4 * half + 8 * c) = v; });
-    // the wave's 32 output rows (8 KB of contiguous memory for the starting node, 32 rows of
-    // 256 bytes for the ending node): lane (row 4u + lane/16, chunk lane%16) stores 16 bytes,
-    // four whole 256-byte rows per streaming store (the LDS rows were written by other lanes of
-    // this wave; LDS executes a wave's accesses in order).  Against 8-byte stores straight from
-    // the MFMA layout: 0.128 -> 0.106 ms at N=768.
+    out_proj<KC>(xg, a.add_residual, sW, lane,
+                 [&](int nb, int c) { return u32x2{zr[2 * nb + (c >> 1)][c & 1][0], zr[2 * nb + (c >> 1)][c & 1][1]}; },
+                 [&](int nb, int c, u32x2 v) { *reinterpret_cast<u32x2*>(so + li * WP + 32 * nb + 4 * half + 8 * c) = v; });
+    // the wave's 32 output rows (2 KC KB of contiguous memory for the starting node, 32 rows of
+    // 2 C bytes for the ending node): lane (row, 16-byte chunk) stores 16 bytes, 512 / C whole
+    // rows per streaming store (the LDS rows were written by other lanes of this wave; LDS
+    // executes a wave's accesses in order).  Against 8-byte stores straight from the MFMA layout:
+    // 0.128 -> 0.106 ms at N=768, C = 128.
     asm volatile("" ::: "memory");
+    constexpr int kRows = 512 / C;                       // rows per store instruction
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int row = 4 * u + (lane >> 4), ch = lane & 15;
-      const u32x4 v = ld16(so + row * kWP + 8 * ch);
-      if (i0 + row < a.N) st16_stream(a.out + pos(r, i0 + row) * kPC + 8 * ch, v);
+    for (int u = 0; u < 32 / kRows; ++u) {
+      const int row = kRows * u + lane / (C / 8), ch = lane % (C / 8);
+      const u32x4 v = ld16(so + row * WP + 8 * ch);
+      if (i0 + row < a.N) st16_stream(a.out + pos(r, i0 + row) * C + 8 * ch, v);
     }
   }
 }
@@ -570,7 +630,7 @@ struct TriAttnArgs {
   float sum_limit;                    // weight sums outside [2^-100, sum_limit] flag the (row, head)
   const uint16_t *q, *k, *vt, *bias;
   const uint8_t* seq;
-  uint16_t* o;                        // o_off blocks: per (head, attention row, 32 queries), N * NP * H * 32
+  uint16_t* o;                        // o_off blocks: per (head, attention row, 32 queries), N * NP * H * D
   uint8_t* flags;                     // [N][H]: 1 = recomputed exactly (dense: tri_fixup_kernel)
   // block-sparse rows (tri_ibs_tile_attn_kernel): maps [N][H][T][S] of (key block, weight);
   // sparse != 0 also keeps tri_fixup_kernel to the masked rows (flagged rows are recomputed by
@@ -614,23 +674,26 @@ typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
 // One LDS tile buffer, all in 16-byte slots; every 1 KB of it is filled by one
 // global_load_lds_dwordx4 (lane L -> bytes 16L..16L+15):
-//   K    [row rr][key block 2][k-chunk 2][lane half 2][key 32]   copied as stored     16 KB
-//   V^T  [row rr][16-key chunk 4][lane half 2][dim 32]          copied as stored     16 KB
+//   K    [row rr][key block 2][k-chunk KC][lane half 2][key 32]   copied as stored     8 KC KB
+//   V^T  [row rr][16-key chunk 4][lane half 2][dim 16 KC]        copied as stored     8 KC KB
 // The operand reads of consecutive lanes are consecutive slots (bank-conflict free), and
 // every read of a lane is one per-lane base plus a compile-time offset.  The bias tile is not
 // staged here: each wave's 32 query rows of it are its own (no other wave reads them), so every
 // wave loads them a tile ahead straight into registers, which takes them off the LDS (a DMA
 // write and a read per byte) and out of the barrier's wait.
+template <int KC>
 struct TileLayout {
-  static constexpr int kKBytes = kTR * kKT * 32 * 2;
-  static constexpr int kVBytes = kTR * kKT * 32 * 2;
+  static constexpr int kRowBytes = kKT * 16 * KC * 2;       // K (or V^T) of one row
+  static constexpr int kKBytes = kTR * kRowBytes;
+  static constexpr int kVBytes = kTR * kRowBytes;
   static constexpr int kKVBytes = kKBytes + kVBytes;
   static constexpr int kBytes = kKVBytes;
   __device__ static constexpr int chunk_offset(int buf, int c) { return buf * kKVBytes + c * 1024; }
   static constexpr int kChunks = kBytes / 1024;
   static constexpr int kChunksPerWave = kChunks / kAW;
   static_assert(kChunks % kAW == 0, "tile chunks must split evenly over the waves");
-  static_assert(kChunksPerWave == 4 && kAW == 2 * kTR, "waves 0-3 copy K rows, waves 4-7 V^T rows, 4 chunks each");
+  static_assert(kChunksPerWave == 2 * KC && kAW == 2 * kTR,
+                "waves 0-3 copy K rows, waves 4-7 V^T rows, 2 KC chunks each");
 };
 
 // Task = (head, row group of 4 rows, block of 256 queries).  The grid is persistent: at most
@@ -647,10 +710,11 @@ struct TileLayout {
 // each wave fills its table from the maps; a unit (row rr, 32-key block b) whose weight w is 0 is
 // skipped (no S^T MFMAs, exponentials or P.V), and a selected one adds log2 w to its logits, so
 // that its weights are w 2^s.  Row sums, normalisation and the out-of-range flags are unchanged.
-template <bool SP, bool FUSED>
+template <bool SP, bool FUSED, int KC = 2>
 __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   static_assert(!(SP && FUSED), "the block-sparse rows use the separate output stage");
-  using TL = TileLayout;
+  static_assert(KC == 2 || (!SP && !FUSED), "head dim 16: dense rows, separate output stage");
+  using TL = TileLayout<KC>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * TL::kBytes + (SP ? kIbsTabBytes : 0) + (FUSED ? kFusedBytes : 0)];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar branches
@@ -688,24 +752,27 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   // ---- tile loader: this wave's 1 KB chunks of a tile, straight into LDS.  Wave w < 4 copies
   //      the K tile of row r0 + w, wave w >= 4 the V^T tile of row r0 + w - 4: four 1 KB quarters
   //      of 4 KB of contiguous memory. ----
-  const int64_t rstride = (int64_t)H * NP * 32;             // row stride of the Q/K/G and V^T layouts
+  const int64_t rstride = (int64_t)H * NP * 16 * KC;        // row stride of the Q/K/G and V^T layouts
   const uint32_t lane16 = (uint32_t)lane * 16u;
   auto loader_src = [&](int r0, int h) __attribute__((always_inline)) -> const char* {
-    return wave < 4 ? (const char*)(a.k + ql_off(r0 + wave, h, H, NP, 0, 0, 0))
-                    : (const char*)(a.vt + vl_off(r0 + wave - 4, h, H, NP, 0, 0, 0));
+    return wave < 4 ? (const char*)(a.k + ql_off<KC>(r0 + wave, h, H, NP, 0, 0, 0))
+                    : (const char*)(a.vt + vl_off<KC>(r0 + wave - 4, h, H, NP, 0, 0, 0));
   };
   auto load_tile = [&](const char* wsrc, int j0, int buf) __attribute__((always_inline)) {
-    const char* src = wsrc + (int64_t)j0 * 64;
+    const char* src = wsrc + (int64_t)j0 * (32 * KC);        // K / V^T bytes per key
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerWave; ++u)
       __builtin_amdgcn_global_load_lds(src + u * 1024 + lane16,
                                        (lds_u32*)(smem + TL::chunk_offset(buf, wave * TL::kChunksPerWave + u)), 16, 0, 0);
   };
   auto kslot = [&](int buf, int rr, int kb, int kk) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + buf * TL::kKVBytes + rr * 4096 + (kb * 4 + kk * 2 + half) * 512 + li * 16;
+    return smem + buf * TL::kKVBytes + rr * TL::kRowBytes + (kb * 2 * KC + kk * 2 + half) * 512 + li * 16;
   };
-  auto vslot = [&](int buf, int rr, int c2) __attribute__((always_inline)) -> const uint8_t* {
-    return smem + buf * TL::kKVBytes + TL::kKBytes + rr * 4096 + (c2 * 2 + half) * 512 + li * 16;
+  // V^T rows of the P.V MFMA's A operand: dims 0 .. 16 KC - 1 (KC = 1: lanes li >= 16 read dims
+  // li - 16 again; output rows 16..31 of that MFMA are not used)
+  auto vslot = [&](int buf, int rr, int c16) __attribute__((always_inline)) -> const uint8_t* {
+    return smem + buf * TL::kKVBytes + TL::kKBytes + rr * TL::kRowBytes + (c16 * 2 + half) * (256 * KC)
+           + (KC == 2 ? li : li & 15) * 16;
   };
   // ---- this lane's bias of a tile, straight into registers: piece k of the wave's 4 KB block
   //      (bias_off_stored) is pieces 4(k/2) + 2 half + k%2 of its query's 64 keys, 8 keys each:
@@ -722,14 +789,14 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   };
 
   // Q operands (B of S^T = K Q^T) of a task's 4 rows.  Rows past N hold zeros and are never stored.
-  bf16x8 qb8[kTR][2];
-  auto load_q = [&](int r0, int h, int qb, bf16x8 (&qd)[kTR][2]) __attribute__((always_inline)) {
+  bf16x8 qb8[kTR][KC];
+  auto load_q = [&](int r0, int h, int qb, bf16x8 (&qd)[kTR][KC]) __attribute__((always_inline)) {
     const int iq = min(qb * 32 * kAW + 32 * wave + li, NP - 1);   // operand row (results of i >= N unused)
-    const uint16_t* qbase = a.q + ql_off(r0, h, H, NP, iq, 0, half);
+    const uint16_t* qbase = a.q + ql_off<KC>(r0, h, H, NP, iq, 0, half);
 #pragma unroll
     for (int rr = 0; rr < kTR; ++rr)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) qd[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + kk * 512));
+      for (int kk = 0; kk < KC; ++kk) qd[rr][kk] = as_bf16x8(ld16(qbase + rr * rstride + kk * 512));
   };
   // Softmax against a fixed reference point of 0: the logits (log2 units, q carries
   // scale * log2 e) are exponentiated as they come out of the S^T MFMA, with no running maximum
@@ -764,17 +831,18 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       }
     }
   };
-  auto load_k = [&](int rr, int kb, int buf, bf16x8 (&kr)[2]) __attribute__((always_inline)) {
-    kr[0] = as_bf16x8(ld16(kslot(buf, rr, kb, 0)));
-    kr[1] = as_bf16x8(ld16(kslot(buf, rr, kb, 1)));
+  auto load_k = [&](int rr, int kb, int buf, bf16x8 (&kr)[KC]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < KC; ++kk) kr[kk] = as_bf16x8(ld16(kslot(buf, rr, kb, kk)));
   };
   auto load_v = [&](int rr, int kb, int buf, bf16x8 (&vr)[2]) __attribute__((always_inline)) {
     vr[0] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb)));
     vr[1] = as_bf16x8(ld16(vslot(buf, rr, 2 * kb + 1)));
   };
   // S^T half of unit (row rr, 32-key half kb) = K Q^T + bias, logits in log2 units
-  auto qk = [&](int rr, int kb, const bf16x8 (&kr)[2], f32x16& s) __attribute__((always_inline)) {
-    s = mfma32(kr[1], qb8[rr][1], mfma32(kr[0], qb8[rr][0], bseed[kb]));
+  auto qk = [&](int rr, int kb, const bf16x8 (&kr)[KC], f32x16& s) __attribute__((always_inline)) {
+    if constexpr (KC == 2) s = mfma32(kr[1], qb8[rr][1], mfma32(kr[0], qb8[rr][0], bseed[kb]));
+    else s = mfma32(kr[0], qb8[rr][0], bseed[kb]);
   };
 
   // The work of a tile is split into units (row rr, 32-key half kb): S^T half = 32 keys x 32
@@ -790,15 +858,16 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   // SP: wu[u] = weight of unit u of the current tile (wave-uniform scalars), 0 = skipped
   float wu[2 * kTR];
   auto on = [&](int u) __attribute__((always_inline)) { return !SP || wu[u] != 0.f; };
-  // ISSUE(u), u < 4: the next tile's loads, one K/V^T chunk and one bias piece per unit (see the
-  // tile below).  PRIO: the wave's raised issue priority is dropped at unit kPrioUnits.
+  // ISSUE(u), u < 4: the next tile's loads, one K/V^T chunk (units u < 2 KC) and one bias piece
+  // per unit (see the tile below).  PRIO: the wave's raised issue priority is dropped at unit
+  // kPrioUnits.
   // FIN(rr): row rr's result is final (its last P.V MFMA was issued a unit earlier): the last tile
   // of a task normalises and stores rows 0..2 there, spread over the tile, instead of all four
   // rows of all eight waves storing together after it.
   auto units = [&](int buf, auto reloadc, const uint16_t* nq, auto issue, auto fin) __attribute__((always_inline)) {
     constexpr bool RELOAD = decltype(reloadc)::value;
     f32x16 sc, sn;
-    bf16x8 kr[2], vr[2];
+    bf16x8 kr[KC], vr[2];
     if (on(0)) {
       load_k(0, 0, buf, kr);
       qk(0, 0, kr, sc);
@@ -808,7 +877,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
 #pragma unroll
     for (int u = 0; u < 2 * kTR; ++u) {
       const int rr = u >> 1;
-      if (u < TL::kChunksPerWave) {
+      if (u < 4) {
         issue(u);
         asm volatile("" ::: "memory");   // keeps the loads in issue order (the tile's waits count them)
       }
@@ -817,7 +886,7 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       if (u + 2 < 2 * kTR && on(u + 2)) load_k((u + 2) >> 1, (u + 2) & 1, buf, kr);
       if (RELOAD && (u & 1) == 0) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) qb8[rr][kk] = as_bf16x8(ld16(nq + rr * rstride + kk * 512));
+        for (int kk = 0; kk < KC; ++kk) qb8[rr][kk] = as_bf16x8(ld16(nq + rr * rstride + kk * 512));
       }
       __builtin_amdgcn_sched_barrier(0);
       if (on(u)) {
@@ -1028,14 +1097,14 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       if (!(lt >= 0x1p-100f && lt <= a.sum_limit) && a.seq[r] != 0) a.flags[r * H + h] = 1;
       const float inv = fast_rcp(lt);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+      for (int kk = 0; kk < KC; ++kk) {                    // O^T rows 16 kk .. 16 kk + 15 (dims)
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           w[e] = pack_bf2(o[rr][8 * kk + 2 * e] * inv, o[rr][8 * kk + 2 * e + 1] * inv);
         // FUSED: plain stores, so that the group's epilogue finds them in L2
-        if constexpr (FUSED) st16(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
-        else st16_stream(a.o + o_off(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        if constexpr (FUSED) st16(a.o + o_off<KC>(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+        else st16_stream(a.o + o_off<KC>(h, r, i, half, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
       }
     };
     if constexpr (SP) fill_table(r0, h, qb);
@@ -1057,8 +1126,8 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
     // wait for the tile loads just issued.  A plain __syncthreads would also wait for the Q loads
     // at the end of the last tile.
     // this lane's Q operands of the next task (of this task again on the last one: a harmless reload)
-    const uint16_t* nq = has_next ? a.q + ql_off(nr0, nh, H, NP, min(nqb * 32 * kAW + 32 * wave + li, NP - 1), 0, half)
-                                  : a.q + ql_off(r0, h, H, NP, min(qb * 32 * kAW + 32 * wave + li, NP - 1), 0, half);
+    const uint16_t* nq = has_next ? a.q + ql_off<KC>(nr0, nh, H, NP, min(nqb * 32 * kAW + 32 * wave + li, NP - 1), 0, half)
+                                  : a.q + ql_off<KC>(r0, h, H, NP, min(qb * 32 * kAW + 32 * wave + li, NP - 1), 0, half);
     auto tile = [&](int tt, auto firstc, auto lastc, auto bufc) __attribute__((always_inline)) {
       constexpr bool FIRST = decltype(firstc)::value, LAST = decltype(lastc)::value;
       constexpr int buf = decltype(bufc)::value;             // compile-time: the compiler then
@@ -1089,16 +1158,18 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       const char* tsrc = LAST ? nsrc : wsrc;
       const char* tbsrc = LAST ? nbsrc : bsrc;
       const int tj = LAST ? 0 : (tt + 1) * kKT;
-      // The end-of-tile waits `vmcnt(1)` / `vmcnt(5)` below are counts of this lambda's loads in
-      // the order they are issued: chunk D_u, then bias piece B_u, for u = 0..3 (plus the last
-      // tile's Q reloads).  The vector memory counter retires loads in issue order, so the wait
+      constexpr int kKeyBytes = 32 * KC;                     // K / V^T bytes per key
+      // The end-of-tile waits below (KC = 2: `vmcnt(1)` / `vmcnt(5)`) are counts of this lambda's
+      // loads in the order they are issued: chunk D_u (u < 2 KC), then bias piece B_u, for
+      // u = 0..3 (plus the last tile's Q reloads).  The vector memory counter retires loads in issue order, so the wait
       // covers every K/V^T chunk only if no chunk is issued after a load the wait leaves in
       // flight.  The compiler fence between D_u and B_u (and the one after each issue(u) in the
       // unit loop) is what fixes that order; without it the compiler may reorder the two loads
       // and the last chunk can still be in flight when the barrier releases the other waves.
       auto issue = [&](int u) __attribute__((always_inline)) {
-        __builtin_amdgcn_global_load_lds(tsrc + (int64_t)tj * 64 + u * 1024 + lane16,
-                                         (lds_u32*)(smem + TL::chunk_offset(buf ^ 1, wave * TL::kChunksPerWave + u)), 16, 0, 0);
+        if (u < TL::kChunksPerWave)
+          __builtin_amdgcn_global_load_lds(tsrc + (int64_t)tj * kKeyBytes + u * 1024 + lane16,
+                                           (lds_u32*)(smem + TL::chunk_offset(buf ^ 1, wave * TL::kChunksPerWave + u)), 16, 0, 0);
         asm volatile("" ::: "memory");   // the chunk before the bias piece (left alone, the compiler
                                          // put the bias load first, and the partial waits below
                                          // then let the last chunk stay in flight past the barrier)
@@ -1121,15 +1192,23 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
       };
       if (active) units(buf, lastc, nq, issue, fin);
       __builtin_amdgcn_s_setprio(0);
-      // this wave's chunks landed.  Issue order (unit: loads) is 0: D0 B0 [Q0 Q0], 1: D1 B1,
+      // this wave's chunks landed.  Issue order (unit: loads), KC = 2: 0: D0 B0 [Q0 Q0], 1: D1 B1,
       // 2: D2 B2 [Q1 Q1], 3: D3 B3, 4: [Q2 Q2], 6: [Q3 Q3] -- D chunk, B bias piece, [Q] the last
       // tile's reloads of the next task's Q operands -- so the bias piece of unit 3 and the Q
-      // reloads after it may stay in flight (idle waves issued no bias or Q loads: they wait for all)
-      static_assert(2 * kTR == 8 && TL::kChunksPerWave == 4 && kPrioUnits >= 0,
+      // reloads after it may stay in flight (idle waves issued no bias or Q loads: they wait for
+      // all).  KC = 1: 0: D0 B0 [Q0], 1: D1 B1, 2: B2 [Q1], 3: B3, 4: [Q2], 6: [Q3] -- the bias
+      // pieces of units 1-3 and the Q reloads after D1 may stay in flight.
+      static_assert(2 * kTR == 8 && TL::kChunksPerWave == 2 * KC && kPrioUnits >= 0,
                     "the partial waits below count the loads of the unit schedule above");
-      if (LAST && active) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)" ::: "memory");
-      else if (active) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      if constexpr (KC == 2) {
+        if (LAST && active) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)" ::: "memory");
+        else if (active) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      } else {
+        if (LAST && active) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
+        else if (active) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      }
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     };
@@ -1163,7 +1242,8 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
   __builtin_amdgcn_s_waitcnt(0);                           // the last task's Q reloads
 }
 
-__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) { tri_attn_body<false, false>(a); }
+template <int KC>
+__global__ __launch_bounds__(64 * kAW) void tri_attn_kernel(const TriAttnArgs a) { tri_attn_body<false, false, KC>(a); }
 
 __global__ __launch_bounds__(64 * kAW) void tri_ibs_tile_attn_kernel(const TriAttnArgs a) { tri_attn_body<true, false>(a); }
 
@@ -1173,25 +1253,27 @@ __global__ __launch_bounds__(64 * kAW) void tri_attn_fused_kernel(const TriAttnA
 // recomputed with an exact two-pass softmax (maximum first, then weights 2^(s - max)) in fp32 from
 // the same Q, K, V^T and bias operands, one query per thread of a 256-thread workgroup; each flag
 // is cleared afterwards.
+template <int KC = 2>
 __device__ void tri_exact_head(const TriAttnArgs& a, int r, int h, int tid) {
+  constexpr int D = 16 * KC;
   const int N = a.N, NP = a.NP, H = a.H;
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
   {
     if (a.flags[r * H + h] == 0) return;                 // same address for every thread: uniform
     for (int i = tid; i < N; i += 256) {
       // q.k is invariant under the common dim permutation of the Q / K layouts: dot in storage order
-      float q[32];
+      float q[D];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 v = ld16(a.q + ql_off(r, h, H, NP, i, c >> 1, c & 1));
+      for (int c = 0; c < 2 * KC; ++c) {
+        const u32x4 v = ld16(a.q + ql_off<KC>(r, h, H, NP, i, c >> 1, c & 1));
 #pragma unroll
         for (int e = 0; e < 4; ++e) { q[8 * c + 2 * e] = bflo(v[e]); q[8 * c + 2 * e + 1] = bfhi(v[e]); }
       }
       auto logit = [&](int j) {
         float s = bf2f(a.bias[bias_off(h, i, j, NP)]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32x4 v = ld16(a.k + ql_off(r, h, H, NP, j, c >> 1, c & 1));
+        for (int c = 0; c < 2 * KC; ++c) {
+          const u32x4 v = ld16(a.k + ql_off<KC>(r, h, H, NP, j, c >> 1, c & 1));
 #pragma unroll
           for (int e = 0; e < 4; ++e) s += q[8 * c + 2 * e] * bflo(v[e]) + q[8 * c + 2 * e + 1] * bfhi(v[e]);
         }
@@ -1199,27 +1281,27 @@ __device__ void tri_exact_head(const TriAttnArgs& a, int r, int h, int tid) {
       };
       float m = -INFINITY;
       for (int j = 0; j < N; ++j) m = fmaxf(m, logit(j));
-      float l = 0.f, acc[32];
+      float l = 0.f, acc[D];
 #pragma unroll
-      for (int d = 0; d < 32; ++d) acc[d] = 0.f;
+      for (int d = 0; d < D; ++d) acc[d] = 0.f;
       for (int j = 0; j < N; ++j) {
         const float w = exp2f(logit(j) - m);
         l += w;
         // V^T piece of key j: chunk j/16, lane half (j/4)%2, element 4((j%16)/8) + j%4
         const int c16 = j >> 4, hf = (j >> 2) & 1, t = 4 * ((j & 15) >> 3) + (j & 3);
 #pragma unroll
-        for (int d = 0; d < 32; ++d) acc[d] += w * bf2f(a.vt[vl_off(r, h, H, NP, c16, hf, d) + t]);
+        for (int d = 0; d < D; ++d) acc[d] += w * bf2f(a.vt[vl_off<KC>(r, h, H, NP, c16, hf, d) + t]);
       }
       const float inv = 1.0f / l;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KC; ++kk) {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             w[e] = pack_bf2(acc[slot_dim(hf, kk, 2 * e)] * inv, acc[slot_dim(hf, kk, 2 * e + 1)] * inv);
-          st16(a.o + o_off(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
+          st16(a.o + o_off<KC>(h, r, i, hf, kk, N, NP), u32x4{w[0], w[1], w[2], w[3]});
         }
       }
     }
@@ -1243,12 +1325,14 @@ __device__ void tri_exact_heads(const TriAttnArgs& a, int r, int tid) {
 //    Q, K, V^T and bias operands, one query per thread; the flag is cleared afterwards.
 // ---------------------------------------------------------------------------------------
 constexpr int kFixupGrid = 512;       // workgroups of tri_fixup_kernel (items strided over them)
+template <int KC>
 __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
+  constexpr int D = 16 * KC, NPART = 256 / D;
   const int H = a.H, tid = threadIdx.x, N = a.N, NP = a.NP, items = N * H;
-  // stored slot (lane half hf, k-chunk kk, element t) of a head's 32 outputs -> dim of V^T
+  // stored slot (lane half hf, k-chunk kk, element t) of a head's D outputs -> dim of V^T
   auto slot_dim = [](int hf, int kk, int t) { return 16 * kk + 8 * (t >> 2) + 4 * hf + (t & 3); };
-  __shared__ float part[8][32];
-  __shared__ float mean[32];
+  __shared__ float part[NPART][D];
+  __shared__ float mean[D];
   __shared__ int list[256];
   __shared__ int nlist;
   // this workgroup's items are blockIdx.x + k gridDim.x; 256 of them are checked at once, one per
@@ -1266,7 +1350,7 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
     for (int w = 0; w < n; ++w) {                          // (row r, head hb)
       const int item = list[w], r = item / H, hb = item - r * H;
       if (a.seq[r] != 0) {                               // a flagged (row, head): exact recompute
-        tri_exact_head(a, r, hb, tid);
+        tri_exact_head<KC>(a, r, hb, tid);
         continue;
       }
       // head hb of a masked row.  Sum over the keys: thread (part p, dim d), part p of the 16-key
@@ -1274,14 +1358,14 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
       // (One workgroup per row, all heads, took 8.5 us for the 38 padded rows of N = 384: a
       // single workgroup's load, reduce and store chain per row is the whole kernel.)
       {
-        const int d = tid & 31, pp = tid >> 5, nc = NP / 16;
+        const int d = tid % D, pp = tid / D, nc = NP / 16;
         float s0 = 0.f, s1 = 0.f;
-        for (int c0 = pp; c0 < nc; c0 += 8 * 4) {        // chunks c0 + 8u, u < 4: all loads issued together
+        for (int c0 = pp; c0 < nc; c0 += NPART * 4) {    // chunks c0 + NPART u, u < 4: all loads issued together
           u32x4 v[8];
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            const int c16 = c0 + 8 * (u >> 1);
-            v[u] = c16 < nc ? ld16(a.vt + vl_off(r, hb, H, NP, c16, u & 1, d)) : u32x4{0, 0, 0, 0};
+            const int c16 = c0 + NPART * (u >> 1);
+            v[u] = c16 < nc ? ld16(a.vt + vl_off<KC>(r, hb, H, NP, c16, u & 1, d)) : u32x4{0, 0, 0, 0};
           }
 #pragma unroll
           for (int u = 0; u < 8; ++u)
@@ -1291,10 +1375,10 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
         part[pp][d] = s0 + s1;
       }
       __syncthreads();
-      if (tid < 32) {
+      if (tid < D) {
         float t = 0.f;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) t += part[q][tid];
+        for (int q = 0; q < NPART; ++q) t += part[q][tid];
         mean[tid] = t / (float)N;
       }
       __syncthreads();
@@ -1303,11 +1387,11 @@ __global__ __launch_bounds__(256) void tri_fixup_kernel(const TriAttnArgs a) {
       for (int t = tid; t < N * 2; t += 256) {
         const int i = t % N, hf = t / N;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KC; ++kk) {
           uint32_t wv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) wv[e] = pack_bf2(mean[slot_dim(hf, kk, 2 * e)], mean[slot_dim(hf, kk, 2 * e + 1)]);
-          st16(a.o + o_off(hb, r, i, hf, kk, N, NP), u32x4{wv[0], wv[1], wv[2], wv[3]});
+          st16(a.o + o_off<KC>(hb, r, i, hf, kk, N, NP), u32x4{wv[0], wv[1], wv[2], wv[3]});
         }
       }
       __syncthreads();                                   // mean is read: the next item may refill it
@@ -1789,7 +1873,10 @@ struct TriWs {
   size_t bytes;
 };
 
+// The fast paths: head dim 32 with C = 128 (the trunk; also the block-sparse mode) and head dim
+// 16 with C = 64 (the template stack), four heads each.
 bool fast_path(int32_t C, int32_t H, int32_t D) { return C == kPC && D == 32 && H * D == kPC; }
+bool fast16_path(int32_t C, int32_t H, int32_t D) { return C == TriDims<1>::C && D == 16 && H == 4; }
 
 TriWs carve(void* base, int32_t N, int32_t C, int32_t H, int32_t D) {
   const size_t P = (size_t)N * N, HD = (size_t)H * D;  TriWs w{};
@@ -1806,7 +1893,9 @@ TriWs carve(void* base, int32_t N, int32_t C, int32_t H, int32_t D) {
 
 extern "C" size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t D) {
   if (N <= 0 || C <= 0 || H <= 0 || D <= 0) return 0;
-  return fast_path(C, H, D) ? carve_fast(nullptr, N, H).bytes : carve(nullptr, N, C, H, D).bytes;
+  if (fast_path(C, H, D)) return carve_fast<2>(nullptr, N, H).bytes;
+  if (fast16_path(C, H, D)) return carve_fast<1>(nullptr, N, H).bytes;
+  return carve(nullptr, N, C, H, D).bytes;
 }
 
 namespace {
@@ -1828,9 +1917,11 @@ float sum_limit(float requested) {
   return requested > 0.f && requested <= v ? requested : v;
 }
 
+template <int KC>
 int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_bytes, hipStream_t st, int stages) {
+  using TD = TriDims<KC>;
   const int32_t N = a->N, H = a->H;
-  const FastWs ws = carve_fast(workspace, N, H);
+  const FastWs ws = carve_fast<KC>(workspace, N, H);
   if (workspace == nullptr || workspace_bytes < ws.bytes) {
     sf_set_error("triangle: workspace too small (%zu < %zu bytes)", workspace_bytes, ws.bytes);
     return 1;
@@ -1838,25 +1929,25 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   const int NP = round_np(N);
   if (stages & SF_TRI_STAGE_PROJECT) {
     TriFoldArgs fa{};
-    fa.nrows = 4 * H * 32 + H;
+    fa.nrows = 4 * H * TD::D + H;
     fa.w = (const uint16_t*)a->w_qkvgb; fa.ln_w = a->ln_w; fa.ln_b = a->ln_b;
     fa.wf = ws.wf; fa.off = ws.off;
     fa.flags = ws.flags; fa.nflags = N * H;
     fa.ctr = ws.ctr; fa.nctr = ws.nctr;
     fa.defer = ws.defer; fa.ndefer = N;
     fa.rgl = ws.rgl; fa.rg = NP / 4; fa.N = N; fa.seq = a->seq_mask;
-    hipLaunchKernelGGL(tri_fold_kernel, dim3(kPCols / 4 + 1), dim3(256), 0, st, fa);
+    hipLaunchKernelGGL(tri_fold_kernel<KC>, dim3(TD::Cols / 4 + 1), dim3(256), 0, st, fa);
     if (int rc = sf_check_launch("tri_fold_kernel")) return rc;
 
     TriProjArgs pa{};
     pa.N = N; pa.NP = NP; pa.H = H; pa.transpose = a->transpose;
-    pa.qscale = (1.0f / sqrtf(32.0f)) * SF_LOG2E;
+    pa.qscale = (1.0f / sqrtf((float)TD::D)) * SF_LOG2E;
     pa.z = (const uint16_t*)a->z; pa.seq = a->seq_mask;
     pa.wf = ws.wf; pa.off = ws.off;
     pa.q = ws.q; pa.k = ws.k; pa.vt = ws.vt; pa.bias = ws.bias;
     pa.items = NP * (NP / 32);
     const int pgroups = persistent_groups(pa.items, &pa.items_per_wave);
-    hipLaunchKernelGGL(tri_proj_kernel, dim3(pgroups), dim3(64 * kPWaves), 0, st, pa);
+    hipLaunchKernelGGL(tri_proj_kernel<KC>, dim3(pgroups), dim3(64 * kPWaves), 0, st, pa);
     if (int rc = sf_check_launch("tri_proj_kernel")) return rc;
   }
 
@@ -1873,7 +1964,8 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
     // 32 (each XCD's share a multiple of 4) no larger than the resident count
     const int fgrid = std::min(std::min(total, 256),
                                sf_resident_workgroups((const void*)tri_attn_fused_kernel, 64 * kAW) / 32 * 32);
-    if ((stages & SF_TRI_STAGE_FUSE) && (stages & SF_TRI_STAGE_OUTPUT) && fgrid >= 32) {
+    // (head dim 16: the separate output stage; SF_TRI_STAGE_FUSE is ignored)
+    if (KC == 2 && (stages & SF_TRI_STAGE_FUSE) && (stages & SF_TRI_STAGE_OUTPUT) && fgrid >= 32) {
       aa.wo = (const uint16_t*)a->w_o;
       aa.wg = ws.wf + (size_t)12 * 32 * kPC; aa.goff = ws.off + 12 * 32;   // folded gate rows 384..511
       aa.z = (const uint16_t*)a->z; aa.out = (uint16_t*)a->out; aa.add_residual = a->add_residual;
@@ -1883,9 +1975,9 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
       hipLaunchKernelGGL(tri_post_kernel, dim3(std::min(N, 128)), dim3(256), 0, st, aa);
       return sf_check_launch("tri_post_kernel");
     }
-    hipLaunchKernelGGL(tri_attn_kernel, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
+    hipLaunchKernelGGL(tri_attn_kernel<KC>, dim3(std::min(total, 256)), dim3(64 * kAW), 0, st, aa);
     if (int rc = sf_check_launch("tri_attn_kernel")) return rc;
-    hipLaunchKernelGGL(tri_fixup_kernel, dim3(std::min(N * a->H, kFixupGrid)), dim3(256), 0, st, aa);
+    hipLaunchKernelGGL(tri_fixup_kernel<KC>, dim3(std::min(N * a->H, kFixupGrid)), dim3(256), 0, st, aa);
     if (int rc = sf_check_launch("tri_fixup_kernel")) return rc;
   }
   if (!(stages & SF_TRI_STAGE_OUTPUT)) return 0;
@@ -1893,12 +1985,12 @@ int triangle_fast(const sf_triangle_args* a, void* workspace, size_t workspace_b
   TriOutArgs oa{};
   oa.N = N; oa.NP = NP; oa.transpose = a->transpose;
   oa.o = ws.o; oa.wo = (const uint16_t*)a->w_o;
-  oa.wg = ws.wf + (size_t)12 * 32 * kPC; oa.goff = ws.off + 12 * 32;   // folded gate rows 384..511
+  oa.wg = ws.wf + (size_t)3 * TD::C * TD::C; oa.goff = ws.off + 3 * TD::C;   // folded gate rows 3C .. 4C-1
   oa.z = (const uint16_t*)a->z; oa.add_residual = a->add_residual;
   oa.out = (uint16_t*)a->out;
   oa.items = N * ((N + 31) / 32);
   const int ogroups = persistent_groups(oa.items, &oa.items_per_wave);
-  hipLaunchKernelGGL(tri_out_kernel, dim3(ogroups), dim3(64 * kPWaves), 0, st, oa);
+  hipLaunchKernelGGL(tri_out_kernel<KC>, dim3(ogroups), dim3(64 * kPWaves), 0, st, oa);
   return sf_check_launch("tri_out_kernel");
 }
 }  // namespace
@@ -1916,9 +2008,12 @@ static int triangle_run(const sf_triangle_args* a, void* workspace, size_t works
   if (N > 65535) { sf_set_error("triangle: N=%d exceeds the grid limit", N); return 1; }
   if (a->out == a->z) { sf_set_error("triangle: out must not alias z"); return 1; }
   if (fast_path(C, H, D))
-    return triangle_fast(a, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), stages);
+    return triangle_fast<2>(a, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), stages);
+  if (fast16_path(C, H, D))
+    return triangle_fast<1>(a, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), stages);
   if ((stages & SF_TRI_STAGE_ALL) != SF_TRI_STAGE_ALL) {
-    sf_set_error("triangle: single stages are available on the head-dim-32 path only (C=%d H=%d D=%d)", C, H, D);
+    sf_set_error("triangle: single stages are available on the fast paths only (C=128, H=4, D=32 or C=64, H=4, "
+                 "D=16; given C=%d H=%d D=%d)", C, H, D);
     return 1;
   }
   const TriWs ws = carve(workspace, N, C, H, D);
@@ -2061,7 +2156,7 @@ extern "C" int sf_hip_triangle_attn_ibs_fwd(const sf_triangle_args* a, const sf_
     hipLaunchKernelGGL(tri_ibs_attn_kernel, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, ia);
     if ((rc = sf_check_launch("tri_ibs_attn_kernel"))) return rc;
   }
-  hipLaunchKernelGGL(tri_fixup_kernel, dim3(std::min(a->N * a->H, kFixupGrid)), dim3(256), 0, st, fa);   // masked rows: mean of V
+  hipLaunchKernelGGL(tri_fixup_kernel<2>, dim3(std::min(a->N * a->H, kFixupGrid)), dim3(256), 0, st, fa);   // masked rows: mean of V
   if ((rc = sf_check_launch("tri_fixup_kernel"))) return rc;
   return triangle_run(a, workspace, workspace_bytes, stream, SF_TRI_STAGE_OUTPUT);
 }

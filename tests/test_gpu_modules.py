@@ -254,11 +254,13 @@ def test_triangle_fused_output_stage(transpose, N, limit):
 
 
 @pytest.mark.parametrize("transpose", [False, True])
-@pytest.mark.parametrize("N,padded,sharp", [(96, True, True), (200, True, False), (37, False, True)])
+@pytest.mark.parametrize("N,padded,sharp", [(96, True, True), (200, True, False), (37, False, True),
+                                            (1, False, True), (65, True, True), (257, False, True)])
 def test_triangle_template_stack_shape(transpose, N, padded, sharp):
   """The template stack's PairFormer triangle attention (model/embeddings/template.py:122-127,
-  304-313): C=64, H=4, so D=16 -- the generic path (LayerNorm, one projection GEMM, strided
-  attention with the gate in its epilogue, output GEMM with the residual)."""
+  304-313): C=64, H=4, so D=16 -- the head-dim-16 instance of the fast path (fold, projection
+  into the attention layouts, tile attention, fix-up, gate and output projection).  Includes the
+  tiling edges: one token, one key past a 64-key tile (65), one query past a 256-query block."""
   mod, z, seq = W.make_triangle(N, C=64, H=4, transpose=transpose, padded=padded, seed=23, sharp=sharp)
   hip = _prepared(mod)
   zd, sd = z.to(DEV), seq.to(DEV)
@@ -271,6 +273,75 @@ def test_triangle_template_stack_shape(transpose, N, padded, sharp):
   out = hip(zd, sd)
   ref = OM.grid_self_attention(z.float(), seq, p, transpose=transpose)
   assert_close_bf16(out, ref, f"template triangle N={N} transpose={transpose}")
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("masked", ["all", "leading"])
+def test_triangle_template_stack_masked_rows(transpose, masked):
+  """Head dim 16 with masked attention rows: every token masked (no attention task runs; the
+  fix-up writes the mean of V for every row) and a masked prefix."""
+  mod, z, seq = W.make_triangle(100, C=64, H=4, transpose=transpose, seed=43, sharp=True)
+  if masked == "all":
+    seq[:] = False
+  else:
+    seq[:37] = False
+  hip = _prepared(mod)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False)
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert torch.isfinite(upd).all()
+  assert_close_bf16(upd, ref, f"template triangle masked={masked} transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_template_stack_exact_fixup(transpose):
+  """Head dim 16 with a weight-sum limit of 1: every unmasked (row, head) is flagged and
+  recomputed by the exact two-pass softmax; the flags are cleared for the next call."""
+  mod, z, seq = W.make_triangle(200, C=64, H=4, transpose=transpose, padded=True, seed=11, sharp=True)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  upd_default = hip(zd, sd, add_residual=False)
+  upd = _triangle_update(hip, zd, sd, fixup_sum_limit=1.0)
+  rows = (upd != upd_default).transpose(0, 1) if transpose else (upd != upd_default)
+  changed = rows.flatten(1).any(1).cpu()
+  assert not changed[~seq].any()
+  assert changed[seq].all()
+  ref = OM.grid_self_attention(z.float(), seq, _params(hip), transpose=transpose, return_update=True)
+  assert_close_bf16(upd, ref, f"template triangle exact fix-up transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+  assert torch.equal(hip(zd, sd, add_residual=False), upd_default)
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_template_stack_n768(transpose):
+  """Head dim 16 at N=768, sharp weights, the last 76 tokens padded: the rows of every
+  persistent attention workgroup's first and last task against the oracle, two calls bit for
+  bit equal (9 tasks per workgroup: the next-task hand-off behind partial waits runs 8 times),
+  and the single stages run one after another against one workspace give the same bits."""
+  from oracle.primitives import layer_norm, linear
+  from sparsefold_amd import _lib
+  mod, z, seq = W.make_triangle(768, C=64, H=4, transpose=transpose, padded=True, seed=17, sharp=True)
+  hip = _prepared(mod)
+  zd, sd = z.to(DEV), seq.to(DEV)
+  print(f"[case] template triangle N=768 transpose={transpose}", flush=True)
+  first = hip(zd, sd, add_residual=False)
+  for _ in range(2):
+    assert torch.equal(hip(zd, sd, add_residual=False), first)
+  ws = torch.empty(_lib.load().sf_hip_triangle_workspace_bytes(768, 64, 4, 16), dtype=torch.uint8, device=DEV)
+  out = torch.empty_like(first)
+  for st in (_lib.TRI_STAGE_PROJECT, _lib.TRI_STAGE_ATTEND, _lib.TRI_STAGE_OUTPUT):
+    _triangle_update(hip, zd, sd, stages=st, workspace=ws, out=out)
+  assert torch.equal(out, first)
+  upd = (first.float().cpu().transpose(0, 1) if transpose else first.float().cpu())
+  p = _params(hip)
+  zf = z.float()
+  x = layer_norm(zf, p["act_norm.weight"], p.get("act_norm.bias"))
+  bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
+  sel = _N768_FIRST_LAST
+  ref = torch.cat([OM.grid_self_attention_rows(zf, seq, p, transpose=transpose, rows=sel[i:i + 32], bias=bias)
+                   for i in range(0, len(sel), 32)])
+  assert_close_bf16(upd[sel], ref, f"template triangle N=768 transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
 
 
 @pytest.mark.parametrize("transpose", [False, True])
