@@ -295,13 +295,13 @@ def _config_builders(side_timings: bool = True) -> dict:
         "ms_per_call": round(t, 4), "gbs": round(bytes_ / t / 1e6, 1),
         "frac_hbm_peak": round(bytes_ / t / 1e6 / PEAK_HBM_GBS, 4), "bound": "hbm"})
 
-  def dense(n, padded=False):  # triangle attention, starting node; all-ones mask (the block-sparse
-    # lines' baseline), or the last n//10 tokens padded
+  def dense(n, padded=False, c=C):  # triangle attention, starting node; all-ones mask (the block-sparse
+    # lines' baseline), or the last n//10 tokens padded; c=64: the template stack's shape (H=4, D=16)
     def build():
-      mod, z, seq = W.make_triangle(n, seed=9, padded=padded)
+      mod, z, seq = W.make_triangle(n, C=c, H=4, seed=9, padded=padded)
       mod = mod.to(dev); backends.prepare(mod)
       z, seq = z.to(dev), seq.to(dev)
-      f = module_flop(n)
+      f = module_flop(n, c, 4, c // 4)
       return (lambda: mod(z, seq)), (lambda t: {"ms_per_call": round(t, 4), "tflops": round(f / t / 1e9, 1),
                                                 "frac_bf16_peak": round(f / t / 1e9 / PEAK_BF16_TFLOPS, 4),
                                                 "bound": "mfma"})
@@ -330,7 +330,7 @@ def _config_builders(side_timings: bool = True) -> dict:
     return build
 
   return {"triangle_n20_fp32": c1, "triangle_n384_start": c2(False), "triangle_n384_end": c2(True),
-          "triangle_n768_padded": dense(768, padded=True),
+          "triangle_n768_padded": dense(768, padded=True), "triangle_template_n768": dense(768, c=64),
           "triangle_ibs_n768": ibs(768), "triangle_n1536_start": dense(1536), "triangle_ibs_n1536": ibs(1536),
           "single_n768": c3b, "diffusion_5x1024_block": c4,
           "diffusion_5x1024_24_blocks": c4_stack, "diffusion_transition_5x1024": c4_transition,

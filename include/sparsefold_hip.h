@@ -157,7 +157,10 @@ int sf_hip_linear_fwd(const sf_linear_args* a, void* stream);
  *   w_qkvgb [4*H*D + H, C]  rows: q (h,d), k (h,d), v (h,d), g (h,d), bias (h)
  *   w_o     [C, H*D]        (transposed output projection)
  * ln_w / ln_b f32 [C] (ln_b may be NULL).  Workspace from sf_hip_triangle_workspace_bytes.
- * out may not alias z.  Constraints: C % 8 == 0, H*D <= 1024, D <= 64.
+ * out may not alias z.  Constraints: C % 8 == 0, H*D <= 1024, D <= 64.  Fast paths (operands in
+ * the attention kernel's register layouts): C = 128, H = 4, D = 32 (the trunk) and C = 64, H = 4,
+ * D = 16 (the template stack); other shapes run LN, a projection GEMM, strided attention and
+ * an output GEMM.
  * ------------------------------------------------------------------------------------- */
 typedef struct sf_triangle_args {
   int32_t N, C, H, D;
@@ -169,7 +172,7 @@ typedef struct sf_triangle_args {
   const void* w_qkvgb;
   const void* w_o;
   void* out;
-  /* Weight-sum limit of the head-dim-32 path's fixed-reference-point softmax: a (row, head)
+  /* Weight-sum limit of the fast paths' fixed-reference-point softmax: a (row, head)
    * whose sum of weights leaves [2^-100, limit] is recomputed by an exact two-pass softmax.
    * 0 = 2^100 (normal use); a smaller positive value sends more rows through the exact path, so
    * that tests can reach it with ordinary logits.  The result does not depend on it beyond
@@ -181,7 +184,8 @@ size_t sf_hip_triangle_workspace_bytes(int32_t N, int32_t C, int32_t H, int32_t 
 int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t workspace_bytes,
                              void* stream);
 
-/* The same module as separate stages sharing one workspace (head dim 32 path), mirroring the
+/* The same module as separate stages sharing one workspace (the fast paths: C = 128, H = 4,
+ * D = 32 and C = 64, H = 4, D = 16), mirroring the
  * reference's projection / attention split of the row-sharded triangle attention
  * (backends/vecops/kernels/registry.py:1236-1309, grid_distributed_projection and
  * grid_distributed_attention):
@@ -193,7 +197,8 @@ int sf_hip_triangle_attn_fwd(const sf_triangle_args* a, void* workspace, size_t 
  * A stage reads what the earlier stages left in the same workspace.
  *   SF_TRI_STAGE_FUSE     with ATTEND and OUTPUT: one attention kernel whose epilogue runs the
  *                         output stage per (row group, 256 queries) once its four heads are done
- *                         (results identical; measured slower on MI355X, so not the default).
+ *                         (results identical; measured slower on MI355X, so not the default;
+ *                         head dim 32 only, ignored for head dim 16).
  *                         ATTEND needs a workspace a PROJECT stage has initialised. */
 #define SF_TRI_STAGE_PROJECT 1
 #define SF_TRI_STAGE_ATTEND 2

@@ -583,16 +583,20 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   // position (r, i) (starting node) or (i, r) (ending node)
   const int IB = (a.N + 31) >> 5;
   auto pos = [&](int r, int i) -> int64_t { return a.transpose ? (int64_t)i * a.N + r : (int64_t)r * a.N + i; };
+  const int64_t ohs = (int64_t)a.N * (a.NP >> 5) * (512 * KC);   // o elements of one head
   auto load = [&](int item, u32x4 (&xo)[NC], u32x4 (&xz)[NC], int& rn, int& in) {
     rn = item / IB;
     in = (item - rn * IB) * 32 + li;
-    const bool ok = in < a.N;
-    const int i = ok ? in : 0;
+    // lanes past N read query 0 of the row instead (no masked loads): their LN is zeroed and their
+    // outputs are never stored, and the MFMAs keep every position in its own column
+    const int i = in < a.N ? in : 0;
     const uint16_t* zp = a.z + pos(rn, i) * C + 8 * half;
+    const uint16_t* op = a.o + o_piece_off<KC>(0, rn, i, half, a.N, a.NP);
 #pragma unroll
     for (int kk = 0; kk < NC; ++kk) {
-      xo[kk] = ok ? ld16(a.o + o_piece_off<KC>(kk, rn, i, half, a.N, a.NP)) : u32x4{0, 0, 0, 0};
-      xz[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+      // o_piece_off(kk) = o_piece_off(0) + head * ohs (+ 512 for the second piece of a head, KC = 2)
+      xo[kk] = ld16(op + (kk / KC) * ohs + (KC == 2 ? (kk & 1) * 512 : 0));
+      xz[kk] = ld16(zp + 16 * kk);
     }
   };
   u32x4 on[NC], zn[NC];
