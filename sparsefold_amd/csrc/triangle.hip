@@ -254,7 +254,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
   constexpr int C = TD::C, WP = TD::WP, NC = TD::NC, NB = TD::NB, PB = TD::ProjBlocks;
   __shared__ __attribute__((aligned(16))) uint16_t sW[PB * 32 * WP];
   __shared__ __attribute__((aligned(16))) float sOff[PB * 32];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   const int N = a.N, NP = a.NP, H = a.H;
 
@@ -279,32 +279,43 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
   __syncthreads();
 
   const int bpr = NP / 32;                              // position blocks per attention row
-  auto block_load = [&](int item, u32x4 (&x)[NC], bool& valid, int& r, int& p) {
+  auto block_load = [&](int item, u32x4 (&x)[NC], bool& valid, int& r, int& p, int& sm) {
     r = item / bpr;
     p = (item - r * bpr) * 32 + li;
     const int za = a.transpose ? p : r, zb = a.transpose ? r : p;
     valid = za < N && zb < N;
+    // the key's sequence mask, loaded with z (the bias below reads it as a bit of a wave ballot):
+    // a byte load there, after the stores, had the compiler drain every store before each use
+    sm = a.seq[valid ? zb : 0];
+    // positions past N read position 0 instead: no branch around the loads, so that the compiler
+    // counts them and the stores after them precisely (the LN of an invalid lane is zeroed)
     const uint16_t* zp = a.z + ((int64_t)(valid ? za : 0) * N + (valid ? zb : 0)) * C + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < NC; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < NC; ++kk) x[kk] = ld16(zp + 16 * kk);
   };
   auto pos_valid = [&](int r, int pe) { return a.transpose ? (pe < N && r < N) : (r < N && pe < N); };
 
   const int first = (blockIdx.x * kPWaves + wave) * a.items_per_wave;
   const int last = min(first + a.items_per_wave, a.items);
-  u32x4 xn[NC];
-  bool vn = false;
-  int rn = 0, pn = 0;
-  if (first < last) block_load(first, xn, vn, rn, pn);
-  for (int item = first; item < last; ++item) {
+  if (first >= last) return;                            // uniform: no barrier follows
+  // z of the next two items is in flight while one computes: per item the loads of item + 2 are
+  // issued first, and item + 1 (loaded an item earlier) is normalised at the end, after the
+  // stores, so that its wait leaves them in flight.  Two register blocks alternate.
+  struct ZBlock { u32x4 x[NC]; bool v; int r, p, sm; };
+  ZBlock za_, zb_;
+  block_load(first, za_.x, za_.v, za_.r, za_.p, za_.sm);
+  if (first + 1 < last) block_load(first + 1, zb_.x, zb_.v, zb_.r, zb_.p, zb_.sm);
+  bf16x8 xo[NC];
+  bool valid = za_.v;
+  int r = za_.r, p = za_.p;                             // this lane's position p (= p0 + li)
+  ln_operands<NC>(za_.x, valid, xo);
+  // bit j: sequence mask of the key of position p0 + j (lanes j and 32 + j hold the same one)
+  uint32_t mbits = (uint32_t)__ballot(za_.sm != 0);
+  auto iteration = [&](int item, ZBlock& nxt, ZBlock& fut) __attribute__((always_inline)) {
     // the LDS weights are re-read every item: hoisted out of the loop they would not fit in
     // registers
     asm volatile("" ::: "memory");
-    bf16x8 xo[NC];
-    const bool valid = vn;
-    const int r = rn, p = pn;                            // this lane's position p (= p0 + li)
-    ln_operands<NC>(xn, valid, xo);
-    if (item + 1 < last) block_load(item + 1, xn, vn, rn, pn);
+    if (item + 2 < last) block_load(item + 2, fut.x, fut.v, fut.r, fut.p, fut.sm);
     const int p0 = p - li;
 
     // q, k: D^T = W . X^T -> lane = position; registers 8*kk .. 8*kk+7 are the 16 bytes of
@@ -392,7 +403,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
             float b = (acc[4 * c + e] + off) * SF_LOG2E;
             if (zb >= N) b = -INFINITY;
             else if (za >= N) b = 0.f;
-            else if (a.seq[zb] == 0) b = SF_MASKED_LOGIT;
+            else if (((mbits >> (pe - p0)) & 1u) == 0) b = SF_MASKED_LOGIT;
             v[e] = b;
           }
           if (!a.transpose) {   // za = r: four consecutive keys of one bias row (stored together)
@@ -404,6 +415,17 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_proj_kernel(const TriProjArg
         }
       }
     }
+    if (item + 1 < last) {
+      ln_operands<NC>(nxt.x, nxt.v, xo);
+      int smn = nxt.sm;
+      asm volatile("" : "+v"(smn));                    // the mask test stays here, after the stores
+      mbits = (uint32_t)__ballot(smn != 0);
+      valid = nxt.v; r = nxt.r; p = nxt.p;
+    }
+  };
+  for (int item = first; item < last; item += 2) {
+    iteration(item, zb_, za_);
+    if (item + 1 < last) iteration(item + 1, za_, zb_);
   }
 }
 
@@ -572,7 +594,7 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
   __shared__ __attribute__((aligned(16))) uint16_t sG[C * WP];
   __shared__ __attribute__((aligned(16))) float sGoff[C];
   __shared__ __attribute__((aligned(16))) uint16_t sOut[kPWaves][32 * WP];   // per-wave output rows
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   uint16_t* const so = sOut[wave];
   stage_out_weights<64 * kPWaves, KC>(sW, sG, sGoff, a.wo, a.wg, a.goff, tid);
@@ -599,17 +621,22 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
       xz[kk] = ld16(zp + 16 * kk);
     }
   };
+  if (first >= last) return;                            // uniform: no barrier follows
   u32x4 on[NC], zn[NC];
-  int rn = 0, in = 0;
-  if (first < last) load(first, on, zn, rn, in);
+  int r, in;
+  load(first, on, zn, r, in);
+  bf16x8 xg[NC];
+  uint32_t zr[NC][2][2];
+  out_gate<KC>(on, zn, in < a.N, a.add_residual, sG, sGoff, lane, xg, zr);
   for (int item = first; item < last; ++item) {
     asm volatile("" ::: "memory");                      // LDS weights are re-read every item
-    const int r = rn, i0 = in - li;
-    const bool ok = in < a.N;                            // only a row's last block has idle lanes
-    bf16x8 xg[NC];
-    uint32_t zr[NC][2][2];
-    out_gate<KC>(on, zn, ok, a.add_residual, sG, sGoff, lane, xg, zr);
-    if (item + 1 < last) load(item + 1, on, zn, rn, in);   // lands during the output projection
+    const int i0 = in - li;
+    // the next item's o and z land during this item's projection and stores; its gate is formed
+    // at the end of this iteration, after the stores, so the wait for them leaves the stores in
+    // flight
+    const bool more = item + 1 < last;
+    int rn = 0, inn = 0;
+    if (more) load(item + 1, on, zn, rn, inn);
     out_proj<KC>(xg, a.add_residual, sW, lane,
                  [&](int nb, int c) { return u32x2{zr[2 * nb + (c >> 1)][c & 1][0], zr[2 * nb + (c >> 1)][c & 1][1]}; },
                  [&](int nb, int c, u32x2 v) { *reinterpret_cast<u32x2*>(so + li * WP + 32 * nb + 4 * half + 8 * c) = v; });
@@ -622,9 +649,14 @@ __global__ __launch_bounds__(64 * kPWaves) void tri_out_kernel(const TriOutArgs 
     constexpr int kRows = 512 / C;                       // rows per store instruction
 #pragma unroll
     for (int u = 0; u < 32 / kRows; ++u) {
-      const int row = kRows * u + lane / (C / 8), ch = lane % (C / 8);
+      // rows past N store the block's last valid row again (identical bytes): no branch
+      const int row = min(kRows * u + lane / (C / 8), a.N - 1 - i0), ch = lane % (C / 8);
       const u32x4 v = ld16(so + row * WP + 8 * ch);
-      if (i0 + row < a.N) st16_stream(a.out + pos(r, i0 + row) * C + 8 * ch, v);
+      st16_stream(a.out + pos(r, i0 + row) * C + 8 * ch, v);
+    }
+    if (more) {
+      out_gate<KC>(on, zn, inn < a.N, a.add_residual, sG, sGoff, lane, xg, zr);
+      r = rn; in = inn;
     }
   }
 }

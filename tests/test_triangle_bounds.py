@@ -144,6 +144,12 @@ def test_fast_path_accesses_stay_in_bounds(KC, N):
   for ch in range(C // 16):
     hd, hf, k2 = (ch >> 1, ch & 1, 1) if KC == 2 else (ch, 1, 0)
     assert _o_off(KC, hd, N - 1, N - 1, hf, k2, N, NP) + 8 <= EO
+  # output stage: a block of 32 queries (i0 = 32 ib < N) stores rows i0 + min(row, N - 1 - i0),
+  # the rows past N storing the block's last valid row again (no branch around the stores)
+  for i0 in range(0, N, 32):
+    for row in range(32):
+      ro = i0 + min(row, N - 1 - i0)
+      assert 0 <= ro < N and (ro == i0 + row or i0 + row >= N)
   # fix-up: mean of V over every 16-key chunk (parts pp of 256 / D threads, 4 chunks per pass)
   npart = 256 // D
   chunks = set()
