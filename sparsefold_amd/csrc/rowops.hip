@@ -589,8 +589,18 @@ __device__ __forceinline__ void lds_only_barrier() {
 }
 
 // HB: 32-plane blocks per tile (NP = 32 HB planes); G2: tiles per workgroup (the normalised z
-// operands are reused for G2 * NP planes; H <= G2 * NP * hgroups); SEG: segmented output.
-template <int HB, int G2, bool SEG, int W>
+// operands are reused for G2 * NP planes; H <= G2 * NP * hgroups, and every tile holds a plane
+// h < H); SEG: segmented output; VEC: 16-byte stores (P and seg multiples of 8, out 16-byte
+// aligned), else 2-byte stores.
+//
+// No wait covers a store: the z loads are unconditional (positions past P read position 0, their
+// operands are zeroed and their planes never stored), the loop is rotated so that the next step's
+// rows are normalised after this step's stores, and with VEC the stores are unconditional too
+// (a lane whose plane or positions are past the end stores the last valid plane's or chunk's
+// bytes again, identical to what its owner stores).  With a branch around a load or a store, or
+// the normalisation at the top of the loop, the compiler waited for every store of the previous
+// step before normalising the next.
+template <int HB, int G2, bool SEG, bool VEC, int W>
 __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_logits_args a, int64_t steps, int hgroups) {
   constexpr int NP = 32 * HB;                 // planes per tile
   constexpr int TPOS = 32 * W;                // positions per tile (one 32-row step per wave)
@@ -602,7 +612,7 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
   __shared__ __attribute__((aligned(16))) uint16_t sW[G2 * NP * kPLWP];
   __shared__ __attribute__((aligned(16))) uint16_t sT[2][NP * TP];
   __shared__ float sOff[G2 * NP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   // grid = hgroups * workers, workers % 8 == 0
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -630,7 +640,6 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
   const uint16_t* z = (const uint16_t*)a.z;
   uint16_t* out = (uint16_t*)a.out;
   const int64_t P = a.P, seg = a.seg, grp = a.group;
-  const bool vec_out = (P % 8 == 0) && (seg % 8 == 0) && ((reinterpret_cast<uintptr_t>(out) & 15) == 0);
   // element offset of position p inside its plane (plane hp adds blk*grp*P + h*seg)
   auto pos_off = [&](int64_t p) -> int64_t {
     if (!SEG) return p;
@@ -642,20 +651,23 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
     valid = step < steps && p < P;
     const uint16_t* zp = z + (valid ? p : 0) * 128 + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) x[kk] = valid ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
+    for (int kk = 0; kk < 8; ++kk) x[kk] = ld16(zp + 16 * kk);
   };
   // the planes this wave stores: plane row pl = wave * PPW + PPI * i + lane / LPP, chunk lane % LPP
   const int ch = lane % LPP;
   const int64_t wstride = workers * W;
   int64_t base = worker * W;                  // first step of this workgroup's tile
+  if (base >= steps) return;                  // uniform over the workgroup
   u32x4 xn[8];
-  bool vn = false;
-  if (base < steps) load(base + wave, xn, vn);
+  bool vn;
+  load(base + wave, xn, vn);
+  bf16x8 xo[8];
+  ln128_operands(xn, vn, xo);
   int buf = 0;
   for (; base < steps; base += wstride) {
-    bf16x8 xo[8];
-    ln128_operands(xn, vn, xo);
-    load(base + wstride + wave, xn, vn);
+    const bool more = base + wstride < steps;   // uniform
+    bool vnn = false;
+    if (more) load(base + wstride + wave, xn, vnn);
 #pragma unroll
     for (int g = 0; g < G2; ++g, buf ^= 1) {
     uint16_t* T = sT[buf];
@@ -676,17 +688,29 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
     }
     lds_only_barrier();
     const int64_t p = base * 32 + 8 * ch;     // first of this lane's 8 positions
+    if constexpr (VEC) {
+      // the last valid chunk (P is a multiple of 8 and the tile holds a position below P) and the
+      // last valid plane of the tile (it holds one)
+      const int64_t pc = min(p, P - 8);
+      const int chc = (int)((pc - base * 32) >> 3);
+      const int plmax = H - 1 - h0 - g * NP;
 #pragma unroll
-    for (int i = 0; i < PPW / PPI; ++i) {
-      const int pl = wave * PPW + PPI * i + lane / LPP;
-      const u32x4 v = ld16(T + pl * TP + 8 * ch);
-      const int hh = h0 + g * NP + pl;
-      if (hh < H && p < P) {
+      for (int i = 0; i < PPW / PPI; ++i) {
+        const int pl = min(wave * PPW + PPI * i + lane / LPP, plmax);
+        const u32x4 v = ld16(T + pl * TP + 8 * chc);
+        const int hh = h0 + g * NP + pl;
         const int64_t blk = hh / grp;
-        uint16_t* op = out + blk * grp * P + (hh - blk * grp) * seg;
-        if (vec_out && p + 8 <= P) {
-          st16_stream(op + pos_off(p), v);
-        } else {
+        st16_stream(out + blk * grp * P + (hh - blk * grp) * seg + pos_off(pc), v);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PPW / PPI; ++i) {
+        const int pl = wave * PPW + PPI * i + lane / LPP;
+        const u32x4 v = ld16(T + pl * TP + 8 * ch);
+        const int hh = h0 + g * NP + pl;
+        if (hh < H && p < P) {
+          const int64_t blk = hh / grp;
+          uint16_t* op = out + blk * grp * P + (hh - blk * grp) * seg;
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             if (p + e < P) op[pos_off(p + e)] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
@@ -694,6 +718,7 @@ __global__ __launch_bounds__(64 * W) void pair_logits128_kernel(const sf_pair_lo
       }
     }
     }
+    if (more) ln128_operands(xn, vnn, xo);
   }
 }
 
@@ -804,9 +829,12 @@ extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream
   if (b.C == 128) {
     const int64_t steps = (b.P + 31) / 32;
     const int hb = b.H <= 32 ? 1 : 2;
-    const int g2 = b.H <= 64 ? 1 : 2;
+    // two 64-plane tiles per workgroup unless the last workgroup's second tile would hold no plane
+    // below H (every tile must hold one: the kernel's stores repeat its last valid plane)
+    const int g2 = (b.H <= 64 || (b.H - 1) % 128 < 64) ? 1 : 2;
     const int hgroups = (b.H + 32 * hb * g2 - 1) / (32 * hb * g2);
     const bool seg = b.seg != b.P;
+    const bool vec = (b.P % 8 == 0) && (b.seg % 8 == 0) && al16(b.out);
     auto launch = [&](auto kernel) {
       // position workers (a multiple of 8): enough for every tile, and no more workgroups than are
       // resident at once
@@ -816,12 +844,17 @@ extern "C" int sf_hip_pair_logits_fwd(const sf_pair_logits_args* a, void* stream
       const int64_t workers = std::min(want, cap);
       hipLaunchKernelGGL(kernel, dim3((unsigned)(workers * hgroups)), dim3(64 * kPLWaves), 0, st, b, steps, hgroups);
     };
-    if (hb == 1 && !seg) launch(pair_logits128_kernel<1, 1, false, kPLWaves>);
-    else if (hb == 1) launch(pair_logits128_kernel<1, 1, true, kPLWaves>);
-    else if (g2 == 1 && !seg) launch(pair_logits128_kernel<2, 1, false, kPLWaves>);
-    else if (g2 == 1) launch(pair_logits128_kernel<2, 1, true, kPLWaves>);
-    else if (!seg) launch(pair_logits128_kernel<2, 2, false, kPLWaves>);
-    else launch(pair_logits128_kernel<2, 2, true, kPLWaves>);
+    auto by_tile = [&](auto vc) {
+      constexpr bool V = decltype(vc)::value;
+      if (hb == 1 && !seg) launch(pair_logits128_kernel<1, 1, false, V, kPLWaves>);
+      else if (hb == 1) launch(pair_logits128_kernel<1, 1, true, V, kPLWaves>);
+      else if (g2 == 1 && !seg) launch(pair_logits128_kernel<2, 1, false, V, kPLWaves>);
+      else if (g2 == 1) launch(pair_logits128_kernel<2, 1, true, V, kPLWaves>);
+      else if (!seg) launch(pair_logits128_kernel<2, 2, false, V, kPLWaves>);
+      else launch(pair_logits128_kernel<2, 2, true, V, kPLWaves>);
+    };
+    if (vec) by_tile(std::true_type{});
+    else by_tile(std::false_type{});
     return sf_check_launch("pair_logits128_kernel");
   }
   auto launch = [&](auto kernel) {
