@@ -334,8 +334,12 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(u32x4* __restrict__ p, i
 //      linear chain would read) to LDS;
 //   2. wave w forms output columns 32w .. 32w+31 of both sides, D^T = W h^T: lane (li, half)
 //      keeps row li, registers 4g .. 4g+3 the columns 8g + 4 half .. +3.
-// The next block's rows are requested before step 2.  (With a wave per 32 rows, every load
-// instruction touched 32 rows in 16-byte pieces: the loads took half of the kernel's time.)
+// The next block's rows are requested before step 2 and normalised after its stores, and the
+// barriers wait for LDS only, so no wait covers a store: rows past the end load, normalise and
+// store the last row again (identical bytes) instead of branching around the stores, and a
+// __syncthreads (vmcnt 0) or the normalisation at the loop top made every block wait for the
+// previous block's stores.  (With a wave per 32 rows, every load instruction touched 32 rows in
+// 16-byte pieces: the loads took half of the kernel's time.)
 struct Adaln2Args {
   int64_t rows, A; int S, blocks;
   const uint16_t* x;
@@ -349,7 +353,8 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[2 * 256 * kA2Pitch];
   __shared__ __attribute__((aligned(16))) uint16_t sH[2 * 32 * kA2Pitch];   // hq, hk of the block
   __shared__ __attribute__((aligned(16))) float sB[256];   // b_qg (zeros without it)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, li = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, li = lane & 31;
   const int prow = tid >> 4, pc = tid & 15;           // step 1: this thread's row and 8 channels
   if (tid < 256) sB[tid] = a.bqg ? a.bqg[tid] : 0.f;
   {
@@ -378,9 +383,9 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
   };
   const int stride = gridDim.x;
   int blk = blockIdx.x;
-  if (blk < a.blocks) load_rows(blk);
-  for (; blk < a.blocks; blk += stride) {
-    // ---- step 1: LayerNorm statistics over the row's 16 lanes, modulation, hq / hk to LDS ----
+  // ---- step 1: LayerNorm statistics over the row's 16 lanes, modulation -> hq / hk ----
+  u32x4 hq, hk;
+  auto step1 = [&]() __attribute__((always_inline)) {
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) sum += bflo(lx[e]) + bfhi(lx[e]);
@@ -396,22 +401,28 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) sq += __shfl_xor(sq, m);
     const float rstd = rsqrtf(sq * (1.0f / 128) + 1e-5f);
-    u32x4 hq, hk;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float n0 = (bflo(lx[e]) - mean) * rstd, n1 = (bfhi(lx[e]) - mean) * rstd;
       hq[e] = pack_bf2(n0 * bflo(lsq[e]) + bflo(lhq[e]), n1 * bfhi(lsq[e]) + bfhi(lhq[e]));
       hk[e] = pack_bf2(n0 * bflo(lsk[e]) + bflo(lhk[e]), n1 * bfhi(lsk[e]) + bfhi(lhk[e]));
     }
-    __syncthreads();                                   // the previous block's step 2 is done with sH
+  };
+  if (blk >= a.blocks) return;                         // uniform over the workgroup
+  load_rows(blk);
+  step1();
+  for (; blk < a.blocks; blk += stride) {
+    lds_only_barrier();                                // the previous block's step 2 is done with sH
     st16(&sH[prow * kA2Pitch + 8 * pc], hq);
     st16(&sH[(32 + prow) * kA2Pitch + 8 * pc], hk);
-    __syncthreads();
-    if (blk + stride < a.blocks) load_rows(blk + stride);   // lands during step 2
+    lds_only_barrier();
+    const bool more = blk + stride < a.blocks;          // uniform
+    if (more) load_rows(blk + stride);                 // lands during step 2
     // ---- step 2: this wave's 32 columns of both sides ----
+    // rows past the end: sH holds the last row's hq / hk (load_rows clamps), so their lanes store
+    // that row's bytes again
     const int64_t row = (int64_t)blk * 32 + li;
-    const bool valid = row < a.rows;
-    const int64_t rr = valid ? row : a.rows - 1;
+    const int64_t rr = row < a.rows ? row : a.rows - 1;
     const int64_t at = rr % a.A, smp = rr / a.A;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
@@ -441,7 +452,7 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(blend(pk[j][w], pk[2 + j][w]), 32);
-      if (valid) {
+      {
         // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
         // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
         const u32x4 lo = {blend(rx[0][0], pk[0][0]), blend(rx[0][1], pk[0][1]), blend(pk[2][0], rx[0][0]), blend(pk[2][1], rx[0][1])};
@@ -452,6 +463,7 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
         st16(q + 8, hi);
       }
     }
+    if (more) step1();                                 // the next block's rows, after the stores
   }
 }
 

@@ -579,14 +579,6 @@ constexpr int kPLWP = 128 + 8;        // LDS pitch (elements) of folded weight r
 constexpr int kPL128MaxH = 1024;
 constexpr int kPLWaves = 4;           // waves per workgroup (4 and 8 measure the same)
 
-// LDS barrier that leaves global loads in flight: this wave's LDS accesses complete
-// (lgkmcnt 0; vmcnt / expcnt left at their maxima), then the workgroup barrier.
-__device__ __forceinline__ void lds_only_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // HB: 32-plane blocks per tile (NP = 32 HB planes); G2: tiles per workgroup (the normalised z
 // operands are reused for G2 * NP planes; H <= G2 * NP * hgroups, and every tile holds a plane

@@ -124,6 +124,16 @@ __device__ __forceinline__ void ln128_operands(const u32x4 (&x)[8], bool valid, 
   ln_operands<8>(x, valid, xo);
 }
 
+// LDS barrier that leaves global loads and stores in flight: this wave's LDS accesses complete
+// (lgkmcnt 0; vmcnt / expcnt left at their maxima), then the workgroup barrier.  __syncthreads()
+// also waits for every global access of the wave (vmcnt 0), stores included.
+__device__ __forceinline__ void lds_only_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Thread-local last-error plumbing shared by all C entry points.
 void sf_set_error(const char* fmt, ...);
 int sf_check_launch(const char* what);
