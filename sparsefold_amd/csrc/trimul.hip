@@ -78,10 +78,15 @@ struct ProjArgs {
 // D^T = W X^T per 32 channels x 32 positions: lane (li, half) ends with position li (plane column
 // 32 cb + li) at channels 32 nb + 8(r/4) + 4 half + r%4; each register is one 2-byte store, and
 // the 32 lanes of a half write 64 contiguous bytes of one plane row.
+// No wait covers a store: the next item's z rows and mask bytes are loaded before this item's
+// products, unconditionally (positions past N read position 0; their values are replaced by
+// zeros), and normalised after its stores.  With the loads predicated, the mask read between the
+// stores and the normalisation at the top of the loop, every item waited for the previous item's
+// stores.
 __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[kGlu * kWS];
   __shared__ float sOff[kGlu];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   constexpr int kStage = kGlu * (kC / 8) / (64 * kTW);
   u32x4 st[kStage];
@@ -103,26 +108,44 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
   // neighbouring column blocks, whose stores fill the two halves of each 128-byte plane line, are
   // written together (one wave walking consecutive items came back to a line too late for L2)
   const int base = blockIdx.x * kTW * a.items_per_wave;
-  for (int k = 0; k < a.items_per_wave; ++k) {
-    const int item = base + k * kTW + wave;
-    if (item >= a.items) break;
-    // plane row R, columns 32 cb .. 32 cb + 31; this lane's column col.  Outgoing: z position
-    // (R, col); incoming: (col, R), so that the planes hold a^T and b^T
-    const int R = item / cbs, cb = item - R * cbs, col = 32 * cb + li;
+  // item -> plane row R, columns 32 cb .. 32 cb + 31; this lane's column col.  Outgoing: z position
+  // (R, col); incoming: (col, R), so that the planes hold a^T and b^T
+  auto load_item = [&](int item, u32x4 (&zn)[8], bool& ok, int& R, int& col, int& m0, int& m1) __attribute__((always_inline)) {
+    R = item / cbs;
+    col = 32 * (item - R * cbs) + li;
     const int za = a.incoming ? col : R, zb = a.incoming ? R : col;
-    const bool ok = za < a.N && zb < a.N;
-    u32x4 zn[8];
+    ok = za < a.N && zb < a.N;
     const uint16_t* zp = a.z + (ok ? (int64_t)za * a.N + zb : 0) * kC + 8 * half;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) zn[kk] = ok ? ld16(zp + 16 * kk) : u32x4{0, 0, 0, 0};
-    const bool keep = ok && (a.mask == nullptr || (a.mask[za] && a.mask[zb]));
-    const float m = keep ? 1.f : 0.f;
-    bf16x8 xo[8];
-    ln128_operands(zn, ok, xo);
-    const int64_t pbase = (int64_t)R * a.Pn + col;
+    for (int kk = 0; kk < 8; ++kk) zn[kk] = ld16(zp + 16 * kk);
+    m0 = a.mask == nullptr ? 1 : a.mask[ok ? za : 0];
+    m1 = a.mask == nullptr ? 1 : a.mask[ok ? zb : 0];
+  };
+  int item = base + wave;
+  if (item >= a.items) return;                        // uniform: no barrier follows
+  u32x4 zn[8];
+  bool ok;
+  int R, col, m0, m1;
+  load_item(item, zn, ok, R, col, m0, m1);
+  bf16x8 xo[8];
+  ln128_operands(zn, ok, xo);
+  bool keep = ok && m0 != 0 && m1 != 0;
+  for (int k = 0;; ++k) {
+    asm volatile("" ::: "memory");                    // the LDS weights are re-read every item
+    const int nitem = item + kTW;
+    const bool more = k + 1 < a.items_per_wave && nitem < a.items;   // uniform
+    bool okn = false;
+    int Rn = 0, coln = 0, m0n = 0, m1n = 0;
+    if (more) load_item(nitem, zn, okn, Rn, coln, m0n, m1n);
+    // store address = a uniform base per channel (scalar registers, recomputed every item from an
+    // opaque plane stride; hoisted, the 16 channel offsets of each block took 32 VGPRs) plus this
+    // lane's 32-bit byte offset (half 4 planes in, plus the position)
+    int64_t pstride = plane;
+    asm volatile("" : "+s"(pstride));
+    const uint32_t lofs = (uint32_t)((4 * half * pstride + (int64_t)R * a.Pn + col) * 2);
 #pragma unroll
     for (int side = 0; side < 2; ++side) {              // 0: a (even channels), 1: b (odd)
-      uint16_t* dstp = side ? a.b : a.a;
+      char* dstp = reinterpret_cast<char*>(side ? a.b : a.a);
 #pragma unroll
       for (int nb = 0; nb < kC / 32; ++nb) {
         const int rg = side * kC + 32 * nb + li;        // gate row of this lane's channel
@@ -138,11 +161,17 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int ch = 32 * nb + 8 * (r >> 2) + 4 * half + (r & 3);   // this register's channel
-          const float v = sigmoidf_(ag[r] + sOff[side * kC + ch]) * (ap[r] + sOff[2 * kC + side * kC + ch]) * m;
-          dstp[(int64_t)ch * plane + pbase] = f2bf(v);
+          const float v = sigmoidf_(ag[r] + sOff[side * kC + ch]) * (ap[r] + sOff[2 * kC + side * kC + ch]);
+          char* cbase = dstp + (int64_t)(32 * nb + 8 * (r >> 2) + (r & 3)) * pstride * 2;   // uniform
+          *reinterpret_cast<uint16_t*>(cbase + lofs) = f2bf(keep ? v : 0.f);
         }
       }
     }
+    if (!more) break;
+    ln128_operands(zn, okn, xo);                      // the next item, after this item's stores
+    asm volatile("" : "+v"(m0n), "+v"(m1n));           // (its mask test stays here as well)
+    keep = okn && m0n != 0 && m1n != 0;
+    item = nitem; R = Rn; col = coln;
   }
 }
 
