@@ -1211,7 +1211,13 @@ __device__ __forceinline__ void tri_attn_body(const TriAttnArgs& a) {
                                          // then let the last chunk stay in flight past the barrier)
         breg[u] = ld16(tbsrc + (int64_t)tj * 64 + 1024 * u);
       };
-      if (!active) load_tile(tsrc, tj, buf ^ 1);
+      // An idle wave loads its bias pieces as well: on a task's last tile they are the next
+      // task's first-tile bias, which the wave needs if it is active there (a workgroup's tasks
+      // step through the query blocks when QB does not divide the task stride).
+      if (!active) {
+        load_tile(tsrc, tj, buf ^ 1);
+        load_bias_regs(tbsrc, tj);
+      }
       // On each SIMD the wave launched first (w < 4) has the older age, so it won every issue
       // slot it competed for, finished its units ~25% sooner and then waited at the barrier
       // while the younger one (w + 4) ran alone (19% of the kernel at the barrier).  The younger

@@ -215,6 +215,29 @@ def test_triangle_c3_n768_sharp_padded_rows(transpose, rows):
 
 
 @pytest.mark.parametrize("transpose", [False, True])
+def test_triangle_n600_idle_waves(transpose):
+  """N=600 pads to 640 positions: 3 blocks of 256 queries, the last with 128, so waves 4-7 of a
+  workgroup are idle in its tasks of the last block, and since a workgroup's tasks step through
+  the blocks (32 mod 3 != 0), they are active again in the next task.  Every row against the
+  oracle, sharp weights (a wrong bias tile in any task's first tile shows)."""
+  from oracle.primitives import layer_norm, linear
+  mod, z, seq = W.make_triangle(600, transpose=transpose, padded=True, seed=23, sharp=True)
+  hip = _prepared(mod)
+  print(f"[case] triangle N=600 sharp padded transpose={transpose}", flush=True)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False).float().cpu()
+  got_all = upd.transpose(0, 1) if transpose else upd
+  p = _params(hip)
+  zf = z.float()
+  x = layer_norm(zf, p["act_norm.weight"], p.get("act_norm.bias"))
+  bias = linear(x, p["pair_bias_projection.weight"]).movedim(-1, -3).contiguous()
+  sel = list(range(600))
+  ref = torch.cat([OM.grid_self_attention_rows(zf, seq, p, transpose=transpose, rows=sel[i:i + 40], bias=bias)
+                   for i in range(0, 600, 40)])
+  assert_close_bf16(got_all, ref, f"triangle N=600 sharp padded transpose={transpose}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
+@pytest.mark.parametrize("transpose", [False, True])
 def test_triangle_n768_sharp_padded_repeatable(transpose):
   """Two calls on the same inputs give the same bits.  At N=768 every persistent attention
   workgroup runs 9 tasks, so the last tile of each task -- which loads the next task's first tile
