@@ -237,6 +237,27 @@ def test_triangle_n600_idle_waves(transpose):
                     max_abs=2e-2 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("C,N,transpose", [(128, 70, False), (128, 300, True), (128, 520, False),
+                                            (128, 800, True), (128, 1100, False), (128, 1100, True),
+                                            (128, 1300, False), (64, 520, True), (64, 1100, False)])
+def test_triangle_schedule_classes(C, N, transpose):
+  """Sizes across the attention kernel's schedule classes: 1 to 6 query blocks of 256 (NP =
+  N rounded up to 128), a half-full last block whose waves 4-7 idle (70, 300, 520, 800, 1100,
+  1300), blocks that a workgroup's tasks step through (32 mod QB != 0: 520, 1100, 1300) or not
+  (300, 800), padded tokens, both nodes and both head dims.  Sampled rows: the first two row
+  groups, the middle and the last, against the oracle with sharp weights."""
+  mod, z, seq = W.make_triangle(N, C=C, H=4, transpose=transpose, padded=True, seed=29 + N, sharp=True)
+  hip = _prepared(mod)
+  print(f"[case] triangle C={C} N={N} transpose={transpose}", flush=True)
+  upd = hip(z.to(DEV), seq.to(DEV), add_residual=False).float().cpu()
+  got_all = upd.transpose(0, 1) if transpose else upd
+  rows = sorted({0, 3, 4, 7, N // 2, N // 2 + 1, N - 4, N - 1} & set(range(N)))
+  ref = OM.grid_self_attention_rows(z.float(), seq, _params(hip), transpose=transpose, rows=rows)
+  assert torch.isfinite(got_all[rows]).all()
+  assert_close_bf16(got_all[rows], ref, f"triangle C={C} N={N} transpose={transpose} rows {rows}",
+                    max_abs=2e-2 * ref.abs().max().item())
+
+
 @pytest.mark.parametrize("transpose", [False, True])
 def test_triangle_n768_sharp_padded_repeatable(transpose):
   """Two calls on the same inputs give the same bits.  At N=768 every persistent attention
@@ -278,12 +299,15 @@ def test_triangle_fused_output_stage(transpose, N, limit):
 
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("N,padded,sharp", [(96, True, True), (200, True, False), (37, False, True),
-                                            (1, False, True), (65, True, True), (257, False, True)])
+                                            (1, False, True), (65, True, True), (257, False, True),
+                                            (600, True, True)])
 def test_triangle_template_stack_shape(transpose, N, padded, sharp):
   """The template stack's PairFormer triangle attention (model/embeddings/template.py:122-127,
   304-313): C=64, H=4, so D=16 -- the head-dim-16 instance of the fast path (fold, projection
   into the attention layouts, tile attention, fix-up, gate and output projection).  Includes the
-  tiling edges: one token, one key past a 64-key tile (65), one query past a 256-query block."""
+  tiling edges: one token, one key past a 64-key tile (65), one query past a 256-query block,
+  and N=600, whose half-full last query block leaves waves idle in one task and active in the
+  next."""
   mod, z, seq = W.make_triangle(N, C=64, H=4, transpose=transpose, padded=padded, seed=23, sharp=sharp)
   hip = _prepared(mod)
   zd, sd = z.to(DEV), seq.to(DEV)
