@@ -106,11 +106,13 @@ def _synthetic_maps(N, H, S, seed):
   return im, wm
 
 
-@pytest.mark.parametrize("transpose,limit", [(False, 0.0), (True, 0.0), (False, 1.0)])
-def test_ibs_given_maps_match_oracle(transpose, limit):
+@pytest.mark.parametrize("N,transpose,limit", [(200, False, 0.0), (200, True, 0.0), (200, False, 1.0),
+                                              (520, False, 0.0), (520, True, 0.0)])
+def test_ibs_given_maps_match_oracle(N, transpose, limit):
   """limit 1 flags every (row, head) of the tile pipeline (weight sums exceed 1), so the exact
-  block-sparse kernel recomputes all of them."""
-  N, S = 200, 4
+  block-sparse kernel recomputes all of them.  N=520: 3 query blocks, the last half full, which a
+  workgroup's tasks step through (waves idle in one task and active in the next)."""
+  S = 4
   mod, z, seq = W.make_triangle(N, transpose=transpose, padded=True, seed=33, sharp=True)
   hip = _prepared(mod)
   im, wm = _synthetic_maps(N, 4, S, seed=3)
@@ -118,7 +120,7 @@ def test_ibs_given_maps_match_oracle(transpose, limit):
   upd, im_out, wm_out = _call(hip, z.to(DEV), seq.to(DEV), params, fixup_sum_limit=limit,
                               index_map=torch.from_numpy(im).to(DEV), weight_map=torch.from_numpy(wm).to(DEV))
   assert (im_out.cpu().numpy() == im).all() and (wm_out.cpu().numpy() == wm).all(), "given maps are not rewritten"
-  rows = [0, 1, 63, 64, 150, N - 1]                    # N - 1: a masked row
+  rows = [0, 1, 63, 64, 150, N // 2 + 1, N - 1]       # N - 1: a masked row
   assert not seq[N - 1]
   ref = ibs.grid_self_attention_ibs(z.float(), seq, _params(hip), transpose=transpose, params=params, seed=0,
                                     maps=(im, wm), rows=rows).float()
