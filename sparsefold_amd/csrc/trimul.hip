@@ -139,10 +139,11 @@ __global__ __launch_bounds__(64 * kTW) void trimul_proj_kernel(const ProjArgs a)
     if (more) load_item(nitem, zn, okn, Rn, coln, m0n, m1n);
     // store address = a uniform base per channel (scalar registers, recomputed every item from an
     // opaque plane stride; hoisted, the 16 channel offsets of each block took 32 VGPRs) plus this
-    // lane's 32-bit byte offset (half 4 planes in, plus the position)
+    // lane's byte offset (half 4 planes in, plus the position; 64-bit: four planes pass 4 GiB
+    // from N ~ 16k)
     int64_t pstride = plane;
     asm volatile("" : "+s"(pstride));
-    const uint32_t lofs = (uint32_t)((4 * half * pstride + (int64_t)R * a.Pn + col) * 2);
+    const int64_t lofs = (4 * half * pstride + (int64_t)R * a.Pn + col) * 2;
 #pragma unroll
     for (int side = 0; side < 2; ++side) {              // 0: a (even channels), 1: b (odd)
       char* dstp = reinterpret_cast<char*>(side ? a.b : a.a);
