@@ -107,12 +107,16 @@ def test_linear_large_epilogues():
   assert_close_bf16(yg, torch.nn.functional.silu(h[:, 0::2]) * h[:, 1::2], "linear large glu")
 
 
-# C = 128 runs the MFMA kernel (P = 1320: a ragged last 32-position step; P = 1517: P % 4 != 0,
-# scalar stores); other C the per-position kernel.
+# C = 128 runs the MFMA kernel (P = 1320: a ragged last 32-position step, 16-byte stores; P = 1517:
+# P % 8 != 0, 2-byte stores); other C the per-position kernel.  H = 100, 130, 200 with 16-byte
+# stores: tiles whose last planes lie past H (their lanes store the last valid plane again), and
+# the one-tile-per-workgroup layout where a second tile would hold no plane (H = 130).
 @pytest.mark.parametrize("H,C,with_b,shape", [(4, 128, True, (33, 40)), (16, 128, True, (33, 40)),
                                               (16, 128, True, (37, 41)), (12, 16, False, (33, 40)),
                                               (64, 128, False, (33, 40)), (40, 128, True, (37, 41)),
-                                              (100, 128, True, (37, 41)), (384, 128, False, (64, 64))])
+                                              (100, 128, True, (37, 41)), (384, 128, False, (64, 64)),
+                                              (100, 128, False, (33, 40)), (130, 128, True, (33, 40)),
+                                              (200, 128, False, (33, 40))])
 def test_pair_logits(H, C, with_b, shape):
   g = torch.Generator().manual_seed(H * C)
   z = torch.randn(*shape, C, generator=g).to(torch.bfloat16)
