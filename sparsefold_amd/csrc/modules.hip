@@ -322,24 +322,23 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(u32x4* __restrict__ p, i
   p[(int64_t)(t / words) * stride + t % words] = u32x4{0, 0, 0, 0};
 }
 
-// Per-atom AdaLN of both sides and the q/g and k/v projections of the key windows in one pass
-// (C = 128, 2HD = 256):
-//   hq = LN(x) * q_scale[a] + q_shift[a],   hk = LN(x) * k_scale[a] + k_shift[a]   (a = row % A)
-//   yq[row] = hq W_qg^T + b_qg,   ykv[s][a] = hk W_kv^T,   ykv[s][A] = 0
-// Persistent: every workgroup keeps both weights (512 rows, pitch 136) and b_qg in LDS and walks
-// blocks of 32 rows.  Per block:
+// Per-atom AdaLN and the q/g or k/v projection of the key windows (C = 128, 2HD = 256):
+//   side 0: hq = LN(x) * q_scale[a] + q_shift[a],  yq[row] = hq W_qg^T + b_qg
+//   side 1: hk = LN(x) * k_scale[a] + k_shift[a],  ykv[s][a] = hk W_kv^T,  ykv[s][A] = 0
+// (a = row % A, s = row / A).  Persistent: each workgroup serves one side, keeps that side's weight
+// (256 rows, pitch 136) and bias in LDS, and walks blocks of 32 rows.  Per block:
 //   1. all 512 threads read the block's x, scale and shift rows as contiguous 16-byte pieces
 //      (thread t: row t/16, channels 8 (t%16) .. +7; 4 rows per instruction), reduce each row's
-//      LayerNorm statistics over its 16 lanes and write hq, hk (bf16, the operand the LayerNorm +
-//      linear chain would read) to LDS;
-//   2. wave w forms output columns 32w .. 32w+31 of both sides, D^T = W h^T: lane (li, half)
-//      keeps row li, registers 4g .. 4g+3 the columns 8g + 4 half .. +3.
-// The next block's rows are requested before step 2 and normalised after its stores, and the
-// barriers wait for LDS only, so no wait covers a store: rows past the end load, normalise and
-// store the last row again (identical bytes) instead of branching around the stores, and a
-// __syncthreads (vmcnt 0) or the normalisation at the loop top made every block wait for the
-// previous block's stores.  (With a wave per 32 rows, every load instruction touched 32 rows in
-// 16-byte pieces: the loads took half of the kernel's time.)
+//      LayerNorm statistics over its 16 lanes and write the modulated row (bf16, the operand the
+//      LayerNorm + linear chain would read) to LDS;
+//   2. wave w forms output columns 32w .. 32w+31, D^T = W h^T: lane (li, half) keeps row li,
+//      registers 4g .. 4g+3 the columns 8g + 4 half .. +3.
+// One side per workgroup halves the weight staging and the LDS (79 KB), so two workgroups share a
+// CU; the two sides of a worker run on one XCD (workgroups b and b + 8), so the second reads the
+// block's x rows from that XCD's L2.  (Both sides in one workgroup: 20.5 us for 5 x 8192 atoms.)
+// No wait covers a store: the next block's rows are requested before step 2 and normalised after
+// its stores, the barriers wait for LDS only, and rows past the end load, normalise and store the
+// last row again (identical bytes) instead of branching around the stores.
 struct Adaln2Args {
   int64_t rows, A; int S, blocks;
   const uint16_t* x;
@@ -350,41 +349,47 @@ struct Adaln2Args {
 constexpr int kA2Pitch = 136;
 
 __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[2 * 256 * kA2Pitch];
-  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * 32 * kA2Pitch];   // hq, hk of the block
-  __shared__ __attribute__((aligned(16))) float sB[256];   // b_qg (zeros without it)
+  __shared__ __attribute__((aligned(16))) uint16_t sW[256 * kA2Pitch];     // this side's weight
+  __shared__ __attribute__((aligned(16))) uint16_t sH[32 * kA2Pitch];      // the block's modulated rows
+  __shared__ __attribute__((aligned(16))) float sB[256];                   // b_qg (side 0), else zeros
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, li = lane & 31;
   const int prow = tid >> 4, pc = tid & 15;           // step 1: this thread's row and 8 channels
-  if (tid < 256) sB[tid] = a.bqg ? a.bqg[tid] : 0.f;
+  // workgroup b: XCD x = b % 8, side (b / 8) % 2, worker 8 (b / 16) + x (grid = 2 x workers,
+  // workers a multiple of 8)
+  const int side = (blockIdx.x >> 3) & 1;
+  const int worker = (int)((blockIdx.x >> 4) << 3) + (int)(blockIdx.x & 7);
+  const int workers = (int)gridDim.x >> 1;
+  const uint16_t* const wsrc = side ? a.wkv : a.wqg;
+  const uint16_t* const scale = side ? a.k_scale : a.q_scale;
+  const uint16_t* const shift = side ? a.k_shift : a.q_shift;
+  if (tid < 256) sB[tid] = (side == 0 && a.bqg) ? a.bqg[tid] : 0.f;
   {
-    u32x4 st[16];                                      // 512 rows x 16 pieces: 16 per thread
+    u32x4 st[8];                                       // 256 rows x 16 pieces: 8 per thread
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int t = tid + 512 * j, n = t >> 4, c8 = (t & 15) * 8;
-      st[j] = ld16((n < 256 ? a.wqg + n * 128 : a.wkv + (n - 256) * 128) + c8);
+      st[j] = ld16(wsrc + n * 128 + c8);
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int t = tid + 512 * j, n = t >> 4, c8 = (t & 15) * 8;
       st16(&sW[n * kA2Pitch + c8], st[j]);
     }
   }
-  if (blockIdx.x == 0)                                 // the zero row of every sample's K/V block
+  if (side == 1 && worker == 0)                        // the zero row of every sample's K/V block
     for (int e = tid; e < a.S * 32; e += 512)
       st16(a.ykv + ((int64_t)(e >> 5) * (a.A + 1) + a.A) * 256 + 8 * (e & 31), u32x4{0, 0, 0, 0});
-  // step 1 loads of a block: x, q scale / shift, k scale / shift of row prow, channels 8 pc .. +7
-  u32x4 lx, lsq, lhq, lsk, lhk;
+  // step 1 loads of a block: x, this side's scale / shift of row prow, channels 8 pc .. +7
+  u32x4 lx, ls, lh;
   auto load_rows = [&](int blk) __attribute__((always_inline)) {
     const int64_t row = min((int64_t)blk * 32 + prow, a.rows - 1), at = row % a.A;
     lx = ld16(a.x + row * 128 + 8 * pc);
-    lsq = ld16(a.q_scale + at * a.prs + 8 * pc); lhq = ld16(a.q_shift + at * a.prs + 8 * pc);
-    lsk = ld16(a.k_scale + at * a.prs + 8 * pc); lhk = ld16(a.k_shift + at * a.prs + 8 * pc);
+    ls = ld16(scale + at * a.prs + 8 * pc);
+    lh = ld16(shift + at * a.prs + 8 * pc);
   };
-  const int stride = gridDim.x;
-  int blk = blockIdx.x;
-  // ---- step 1: LayerNorm statistics over the row's 16 lanes, modulation -> hq / hk ----
-  u32x4 hq, hk;
+  // ---- step 1: LayerNorm statistics over the row's 16 lanes, modulation -> hm ----
+  u32x4 hm;
   auto step1 = [&]() __attribute__((always_inline)) {
     float sum = 0.f;
 #pragma unroll
@@ -404,65 +409,59 @@ __global__ __launch_bounds__(512) void adaln2_proj_kernel(const Adaln2Args a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float n0 = (bflo(lx[e]) - mean) * rstd, n1 = (bfhi(lx[e]) - mean) * rstd;
-      hq[e] = pack_bf2(n0 * bflo(lsq[e]) + bflo(lhq[e]), n1 * bfhi(lsq[e]) + bfhi(lhq[e]));
-      hk[e] = pack_bf2(n0 * bflo(lsk[e]) + bflo(lhk[e]), n1 * bfhi(lsk[e]) + bfhi(lhk[e]));
+      hm[e] = pack_bf2(n0 * bflo(ls[e]) + bflo(lh[e]), n1 * bfhi(ls[e]) + bfhi(lh[e]));
     }
   };
+  int blk = worker;
   if (blk >= a.blocks) return;                         // uniform over the workgroup
   load_rows(blk);
   step1();
-  for (; blk < a.blocks; blk += stride) {
+  for (; blk < a.blocks; blk += workers) {
     lds_only_barrier();                                // the previous block's step 2 is done with sH
-    st16(&sH[prow * kA2Pitch + 8 * pc], hq);
-    st16(&sH[(32 + prow) * kA2Pitch + 8 * pc], hk);
+    st16(&sH[prow * kA2Pitch + 8 * pc], hm);
     lds_only_barrier();
-    const bool more = blk + stride < a.blocks;          // uniform
-    if (more) load_rows(blk + stride);                 // lands during step 2
-    // ---- step 2: this wave's 32 columns of both sides ----
-    // rows past the end: sH holds the last row's hq / hk (load_rows clamps), so their lanes store
-    // that row's bytes again
+    const bool more = blk + workers < a.blocks;         // uniform
+    if (more) load_rows(blk + workers);                // lands during step 2
+    // ---- step 2: this wave's 32 columns ----
+    // rows past the end: sH holds the last row's modulated row (load_rows clamps), so their
+    // lanes store that row's bytes again
     const int64_t row = (int64_t)blk * 32 + li;
     const int64_t rr = row < a.rows ? row : a.rows - 1;
     const int64_t at = rr % a.A, smp = rr / a.A;
+    f32x16 acc;
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-      f32x16 acc;
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    for (int kk = 0; kk < 8; ++kk)
+      acc = mfma32(as_bf16x8(ld16(&sW[(32 * wave + li) * kA2Pitch + 16 * kk + 8 * half])),
+                   as_bf16x8(ld16(&sH[li * kA2Pitch + 16 * kk + 8 * half])), acc);
+    // lane half h' holds columns 8g + 4h' .. +3; after one exchange with the partner lane
+    // (li, 1 - h') half 0 holds columns 0..15 and half 1 columns 16..31: 32 contiguous bytes
+    uint32_t pk[4][2];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        acc = mfma32(as_bf16x8(ld16(&sW[(side * 256 + 32 * wave + li) * kA2Pitch + 16 * kk + 8 * half])),
-                     as_bf16x8(ld16(&sH[(32 * side + li) * kA2Pitch + 16 * kk + 8 * half])), acc);
-      // lane half h' holds columns 8g + 4h' .. +3; after one exchange with the partner lane
-      // (li, 1 - h') half 0 holds columns 0..15 and half 1 columns 16..31: 32 contiguous bytes
-      uint32_t pk[4][2];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int c0 = 32 * wave + 8 * g + 4 * half;
-        const f32x4 b4 = side == 0 ? *reinterpret_cast<const f32x4*>(&sB[c0]) : f32x4{0.f, 0.f, 0.f, 0.f};
-        pk[g][0] = pack_bf2(acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1]);
-        pk[g][1] = pack_bf2(acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
-      }
-      // (selects by half as bitwise blends of values: a select between array elements became a
-      // run-time index into a stack copy of the array)
-      const uint32_t hm = half ? ~0u : 0u;
-      auto blend = [&](uint32_t if1, uint32_t if0) __attribute__((always_inline)) { return (if1 & hm) | (if0 & ~hm); };
-      uint32_t rx[2][2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(blend(pk[j][w], pk[2 + j][w]), 32);
-      {
-        // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
-        // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
-        const u32x4 lo = {blend(rx[0][0], pk[0][0]), blend(rx[0][1], pk[0][1]), blend(pk[2][0], rx[0][0]), blend(pk[2][1], rx[0][1])};
-        const u32x4 hi = {blend(rx[1][0], pk[1][0]), blend(rx[1][1], pk[1][1]), blend(pk[3][0], rx[1][0]), blend(pk[3][1], rx[1][1])};
-        uint16_t* dst = side ? a.ykv + (smp * (a.A + 1) + at) * 256 : a.yq + rr * 256;
-        uint16_t* q = dst + 32 * wave + 16 * half;
-        st16(q, lo);
-        st16(q + 8, hi);
-      }
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = 32 * wave + 8 * g + 4 * half;
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sB[c0]);
+      pk[g][0] = pack_bf2(acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1]);
+      pk[g][1] = pack_bf2(acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
     }
+    // (selects by half as bitwise blends of values: a select between array elements became a
+    // run-time index into a stack copy of the array)
+    const uint32_t hmask = half ? ~0u : 0u;
+    auto blend = [&](uint32_t if1, uint32_t if0) __attribute__((always_inline)) { return (if1 & hmask) | (if0 & ~hmask); };
+    uint32_t rx[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int w = 0; w < 2; ++w) rx[j][w] = __shfl_xor(blend(pk[j][w], pk[2 + j][w]), 32);
+    // half 0: groups 0, 1 = own columns 8g..8g+3, then the partner's 8g+4..8g+7
+    // half 1: groups 2, 3 = the partner's 8g..8g+3, then own 8g+4..8g+7
+    const u32x4 lo = {blend(rx[0][0], pk[0][0]), blend(rx[0][1], pk[0][1]), blend(pk[2][0], rx[0][0]), blend(pk[2][1], rx[0][1])};
+    const u32x4 hi = {blend(rx[1][0], pk[1][0]), blend(rx[1][1], pk[1][1]), blend(pk[3][0], rx[1][0]), blend(pk[3][1], rx[1][1])};
+    uint16_t* dst = side ? a.ykv + (smp * (a.A + 1) + at) * 256 : a.yq + rr * 256;
+    uint16_t* q = dst + 32 * wave + 16 * half;
+    st16(q, lo);
+    st16(q + 8, hi);
     if (more) step1();                                 // the next block's rows, after the stores
   }
 }
@@ -926,9 +925,11 @@ int cross_prepared_run(const sf_cross_attention_args* a, Arena ws, hipStream_t s
     f.prs = a->pre_rs;
     f.wqg = static_cast<const uint16_t*>(a->w_qg); f.wkv = static_cast<const uint16_t*>(a->w_kv); f.bqg = a->b_qg;
     f.yq = static_cast<uint16_t*>(yq); f.ykv = static_cast<uint16_t*>(ykv);
+    // two workgroups per worker (one per side), workers a multiple of 8: the resident workgroups
+    // or enough for every block, whichever is fewer
     const int resident = sf_resident_workgroups(reinterpret_cast<const void*>(adaln2_proj_kernel), 512);
-    const int grid = std::max(1, std::min(resident, f.blocks));
-    hipLaunchKernelGGL(adaln2_proj_kernel, dim3(grid), dim3(512), 0, st, f);
+    const int workers = std::max(8, std::min(resident / 2, (f.blocks + 7) / 8 * 8) / 8 * 8);
+    hipLaunchKernelGGL(adaln2_proj_kernel, dim3(2 * workers), dim3(512), 0, st, f);
     if ((rc = sf_check_launch("adaln2_proj_kernel"))) return rc;
   } else {
   for (int side = 0; side < 2; ++side) {

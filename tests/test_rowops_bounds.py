@@ -1,6 +1,7 @@
 """CPU model of the global stores of the pair-logit kernel for C = 128 (csrc/rowops.hip:
-pair_logits128_kernel with 16-byte stores) and of the window projection (csrc/modules.hip:
-adaln2_proj_kernel), both of which store unconditionally: a lane whose plane, positions or row lie
+pair_logits128_kernel with 16-byte stores) and of the loads and stores of the window projection
+(csrc/modules.hip: adaln2_proj_kernel, one workgroup per side and worker), both of which store
+unconditionally: a lane whose plane, positions or row lie
 past the end stores the last valid plane's, chunk's or row's bytes again.  The host's tile
 arithmetic and the kernels' index expressions are restated; nothing here runs on a GPU.  Checked:
 every store lies inside the output, every output element is written, and a lane that repeats a
@@ -86,31 +87,52 @@ def test_pair_logits_16_byte_stores(P, H, seg, grp, workers):
   assert (written >= 1).all(), "every (plane, position) written"
 
 
-@pytest.mark.parametrize("S,A", [(5, 256), (2, 96), (1, 32), (3, 8192)])
-def test_window_projection_stores(S, A):
-  """adaln2_proj_kernel: per block of 32 rows (row = sample * A + atom), wave w stores columns
-  32 w .. 32 w + 31 of yq [S*A, 256] and ykv [S][A+1][256] for row min(row, rows - 1); block 0
-  zeroes row A of every sample's K/V block."""
+def _window_workers(blocks, resident=512):
+  """The host's launch: two workgroups per worker (one per side), workers a multiple of 8."""
+  return max(8, min(resident // 2, (blocks + 7) // 8 * 8) // 8 * 8)
+
+
+@pytest.mark.parametrize("S,A", [(5, 256), (2, 96), (1, 32), (3, 8192), (5, 8192)])
+@pytest.mark.parametrize("resident", [512, 64])
+def test_window_projection_accesses(S, A, resident):
+  """adaln2_proj_kernel: workgroup b serves side (b / 8) % 2 for worker 8 (b / 16) + b % 8; a worker
+  takes blocks worker, worker + workers, ... of 32 rows (row = sample * A + atom); per block it
+  loads x[min(row, rows - 1)] and its side's scale / shift of atom row % A, and wave w stores
+  columns 32 w .. 32 w + 31 of yq [S*A, 256] (side 0) or ykv [S][A+1][256] (side 1) for row
+  min(row, rows - 1); the side-1 workgroup of worker 0 zeroes row A of every sample's K/V block."""
   rows = S * A
   blocks = (rows + 31) // 32
+  workers = _window_workers(blocks, resident)
+  grid = 2 * workers
+  seen = set()
+  for b in range(grid):
+    side, worker = (b >> 3) & 1, 8 * (b >> 4) + (b & 7)
+    assert worker < workers
+    seen.add((side, worker))
+  assert len(seen) == grid, "every (side, worker) pair exactly once"
   li = np.arange(64) & 31
   half = np.arange(64) >> 5
+  prow = np.arange(512) >> 4
+  pc = np.arange(512) & 15
   yq = np.zeros(rows * 256, np.int64)
   ykv = np.zeros(S * (A + 1) * 256, np.int64)
-  for blk in range(blocks):
-    row = blk * 32 + li
-    rr = np.minimum(row, rows - 1)
-    at, smp = rr % A, rr // A
-    for wave in range(8):
-      for side in range(2):
+  for side, worker in sorted(seen):
+    for blk in range(worker, blocks, workers):
+      lrow = np.minimum(blk * 32 + prow, rows - 1)      # step-1 loads: x and this side's terms
+      assert (lrow * 128 + 8 * pc + 7 < rows * 128).all() and ((lrow % A) < A).all()
+      row = blk * 32 + li
+      rr = np.minimum(row, rows - 1)
+      at, smp = rr % A, rr // A
+      for wave in range(8):
         dst = (smp * (A + 1) + at) * 256 if side else rr * 256
         q = dst + 32 * wave + 16 * half
         buf = ykv if side else yq
         for e in range(16):
           assert ((q + e) < buf.size).all()
           np.add.at(buf, q + e, 1)
-  for e in range(S * 32):
-    start = ((e >> 5) * (A + 1) + A) * 256 + 8 * (e & 31)
-    assert start + 7 < ykv.size
-    ykv[start:start + 8] += 1
+    if side == 1 and worker == 0:
+      for e in range(S * 32):
+        start = ((e >> 5) * (A + 1) + A) * 256 + 8 * (e & 31)
+        assert start + 7 < ykv.size
+        ykv[start:start + 8] += 1
   assert (yq >= 1).all() and (ykv >= 1).all()
