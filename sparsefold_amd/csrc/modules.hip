@@ -736,13 +736,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
   const bf16x8 qb0 = as_bf16x8(ld16(qp)), qb1 = as_bf16x8(ld16(qp + 16));
   // bias of query li, keys 16 c + 8 half .. + 7: the B operand of an MFMA that adds it to S^T
   // through an identity A (16-byte loads: with the keys of the S^T registers, 8 bytes a lane, the
-  // loads were twice as many, each touching as many rows)
-  u32x4 br[8];
-  if (a.bias != nullptr) {
-    const uint16_t* bp = a.bias + (((int64_t)u * 4 + h) * 32 + li) * 128 + 8 * half;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) br[c] = ld16(bp + 16 * c);
-  }
+  // loads were twice as many, each touching as many rows), loaded per key block
+  const int64_t boff = (((int64_t)u * 4 + h) * 32 + li) * 128 + 8 * half;   // element offset in bias
   const bool kvalid0 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane] != 0;
   const bool kvalid1 = a.mask_k == nullptr || a.mask_k[(int64_t)u * 128 + lane + 64] != 0;
   const uint64_t mk0 = __ballot(kvalid0), mk1 = __ballot(kvalid1);
@@ -765,8 +760,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[kb][r] *= a.scale;
     if (a.bias != nullptr) {                                // uniform
-      sc[kb] = mfma32(idn[0], as_bf16x8(br[2 * kb]), sc[kb]);
-      sc[kb] = mfma32(idn[1], as_bf16x8(br[2 * kb + 1]), sc[kb]);
+      sc[kb] = mfma32(idn[0], as_bf16x8(ld16(a.bias + boff + 32 * kb)), sc[kb]);
+      sc[kb] = mfma32(idn[1], as_bf16x8(ld16(a.bias + boff + 32 * kb + 16)), sc[kb]);
     }
   }
   if ((mk0 & mk1) != ~0ull) {                               // uniform: some key masked
@@ -809,23 +804,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
   // ---- O^T = V^T P^T ----
   __builtin_amdgcn_s_waitcnt(0);                            // this wave's V copies have landed
   asm volatile("" ::: "memory");
-  // gate of query li, dims 8 j + 4 half .. + 3 (O^T registers 4 j .. 4 j + 3), and W_t2 rows
-  // 32 h + li (A operand of the projection; L2-resident): in flight during P.V
-  const uint16_t* gp = a.yq + (qrow + li) * 256 + 128 + h * 32;
-  const u32x4 gl0 = ld16(gp + 8 * half), gl1 = ld16(gp + 16 + 8 * half);
-  u32x4 wr[8];
-  const uint16_t* wp = a.w_t2 + (int64_t)(32 * h + li) * 128 + 8 * half;
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk) wr[kk] = ld16(wp + 16 * kk);
-  // zero-gate and residual of the output channels 32 h + 8 j + 4 half .. + 3 of query li
-  const int64_t orow = qrow + li;
-  const uint16_t* zp = a.zgate + (int64_t)(32 * u + li) * a.zrs + 32 * h;
-  const u32x4 zl0 = ld16(zp + 8 * half), zl1 = ld16(zp + 16 + 8 * half);
-  u32x4 xl0 = u32x4{0, 0, 0, 0}, xl1 = u32x4{0, 0, 0, 0};
-  if (a.x != nullptr) {
-    xl0 = ld16(a.x + orow * 128 + 32 * h + 8 * half);
-    xl1 = ld16(a.x + orow * 128 + 32 * h + 16 + 8 * half);
-  }
   f32x16 o;
 #pragma unroll
   for (int r = 0; r < 16; ++r) o[r] = 0.f;
@@ -867,6 +845,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void w
       rj[2 * q + 1] = u32x2{blend(p[2], s0[1]), blend(p[3], s1[1])};
     }
   };
+  // gate of query li, dims 8 j + 4 half .. + 3 (O^T registers 4 j .. 4 j + 3), W_t2 rows 32 h +
+  // li (A operand of the projection; L2-resident), zero-gate and residual of the output channels
+  // 32 h + 8 j + 4 half .. + 3 of query li: issued after P.V, whose P registers they reuse (held
+  // through P.V these loads cost more than their latency hidden)
+  const uint16_t* gp = a.yq + (qrow + li) * 256 + 128 + h * 32;
+  const u32x4 gl0 = ld16(gp + 8 * half), gl1 = ld16(gp + 16 + 8 * half);
+  u32x4 wr[8];
+  const uint16_t* wp = a.w_t2 + (int64_t)(32 * h + li) * 128 + 8 * half;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) wr[kk] = ld16(wp + 16 * kk);
+  const int64_t orow = qrow + li;
+  const uint16_t* zp = a.zgate + (int64_t)(32 * u + li) * a.zrs + 32 * h;
+  const u32x4 zl0 = ld16(zp + 8 * half), zl1 = ld16(zp + 16 + 8 * half);
+  u32x4 xl0 = u32x4{0, 0, 0, 0}, xl1 = u32x4{0, 0, 0, 0};
+  if (a.x != nullptr) {
+    xl0 = ld16(a.x + orow * 128 + 32 * h + 8 * half);
+    xl1 = ld16(a.x + orow * 128 + 32 * h + 16 + 8 * half);
+  }
   u32x2 gr[4];
   runs(gl0, gl1, gr);
   // ---- og = O / l * sigmoid(g) -> LDS (the V rows of every wave are then dead) ----
